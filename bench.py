@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""Benchmark of the dequant-GEMV hot path on one MI355X.
+
+Workload (one "step"): the INT4 (g64) M = 1 projections of a Qwen2-0.5B-shaped
+decoder layer plus its lm_head -- q/o 896->896, k/v 896->128, gate/up 896->4864,
+down 4864->896, lm_head 896->151936 -- with x ~ N(0,1) fp32 and W ~ N(0, 0.02)
+quantized on the device by kt_quantize (the reference layout: qdata [K x N/2],
+fp32 scales and u8 zeros [K/64 x N]). Inputs are resident in HBM before timing.
+Each step uses a different copy of the weight set so that the timed loop streams
+more than twice the 256 MB Infinity Cache. A step's eight launches are captured
+in a HIP graph (one graph per weight copy) and replayed.
+
+value = algorithmic bytes of a step / measured step time (GB/s). Algorithmic bytes
+per GEMV = K*bytesPerRow + 4*groups*N + groups*N (zeros) + 4*K (x) + 4*N (y).
+
+The JSON line also carries:
+  roofline      -- the dominant kernel (the lm_head GEMV), timed per launch with
+                   HIP events on the launch stream, against 8 TB/s;
+  cpu_baseline  -- the oracle (C restatement of MatMul.multiplyQuantized, M == 1
+                   unit schedule, work-stealing threads) on the same workload;
+  extra         -- the two targets of the workload family: INT4 GEMV on the
+                   Llama-3-8B FFN shape (4096->14336) and the INT8 prefill GEMM at
+                   M = 512 (2048->8192), each with its roofline fraction.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "dequant-GEMV GB/s (% HBM peak) at M=1; dequant-GEMM TFLOP/s at M=512"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+MALL_BYTES = 256 << 20
+
+QWEN = [("q", 896, 896), ("k", 896, 128), ("v", 896, 128), ("o", 896, 896), ("gate", 896, 4864),
+        ("up", 896, 4864), ("down", 4864, 896), ("lm_head", 896, 151936)]
+
+
+def layout(k, n, bits, g):
+    groups = (k + g - 1) // g
+    bpr = (n + n % 2) // 2 if bits == 4 else n
+    return groups, bpr
+
+
+def gemv_bytes(m, k, n, bits, g):
+    groups, bpr = layout(k, n, bits, g)
+    return k * bpr + 4 * groups * n + (groups * n if bits == 4 else 0) + 4 * m * k + 4 * m * n
+
+
+class Weight:
+    """One quantized weight in torch-allocated device memory, passed through the C ABI."""
+
+    def __init__(self, torch, kt_lib, k, n, bits, g, seed, stream):
+        self.k, self.n, self.bits, self.g = k, n, bits, g
+        groups, bpr = layout(k, n, bits, g)
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        w = torch.randn((k, n), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+        self.q = torch.empty(k * bpr, dtype=torch.uint8, device="cuda")
+        self.s = torch.empty(groups * n, dtype=torch.float32, device="cuda")
+        self.z = torch.empty(groups * n, dtype=torch.uint8, device="cuda") if bits == 4 else None
+        torch.cuda.synchronize()
+        kt_lib.call("kt_quantize", w.data_ptr(), k, n, bits, g, self.q.data_ptr(), self.s.data_ptr(),
+                    self.z.data_ptr() if self.z is not None else None, stream)
+        del w
+        self.struct = None
+        self._bind(kt_lib)
+
+    def _bind(self, kt_lib):
+        self.struct = kt_lib.QWeight(self.q.data_ptr(), self.s.data_ptr(),
+                                     self.z.data_ptr() if self.z is not None else None,
+                                     self.k, self.n, self.bits, self.g)
+
+    def clone(self, kt_lib):
+        c = object.__new__(Weight)
+        c.k, c.n, c.bits, c.g = self.k, self.n, self.bits, self.g
+        c.q = self.q.clone()
+        c.s = self.s.clone()
+        c.z = self.z.clone() if self.z is not None else None
+        c._bind(kt_lib)
+        return c
+
+    @property
+    def nbytes(self):
+        return self.q.numel() + 4 * self.s.numel() + (self.z.numel() if self.z is not None else 0)
+
+
+def qmatmul(kt_lib, x, m, w, y, stream):
+    kt_lib.call("kt_qmatmul", x.data_ptr(), m, ctypes.byref(w.struct), y.data_ptr(), 0, ctypes.c_float(1.0), stream)
+
+
+def time_per_launch(torch, fn, copies, launches):
+    """Average duration of one launch, events recorded on the launch stream around each."""
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+    torch.cuda.synchronize()
+    for i in range(launches):
+        starts[i].record(stream)
+        fn(copies[i % len(copies)])
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    times = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return sum(times) / len(times), times[len(times) // 2]
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """The oracle's M == 1 kernel on the same Qwen set, on this host's cores."""
+    import numpy as np
+
+    import oracle
+
+    oracle.build()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(1)
+    weights = []
+    for _, k, n in QWEN:
+        w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        st, q = oracle.quantize(w, 4, 64)
+        weights.append((k, n, q))
+    xs = {k: np.random.default_rng(0).standard_normal((1, k), dtype=np.float32) for k in (896, 4864)}
+    step_bytes = sum(gemv_bytes(1, k, n, 4, 64) for _, k, n in QWEN)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for k, n, q in weights:
+            oracle.multiply_quantized(xs[k], q, 1, threads=threads)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(step_bytes * steps / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} passes of the 8 Qwen2-0.5B INT4 g64 M=1 projections ({elapsed:.1f} s), "
+                  "C restatement of MatMul.multiplyQuantized's M=1 unit schedule, -O3 -ffp-contract=off",
+    }
+
+
+def traffic_from_profiles():
+    """HBM bytes per lm_head launch measured with rocprofv3 --pmc (profiles/), if recorded."""
+    path = ROOT / "profiles" / "traffic_gemv_int4_lm_head.json"
+    if path.exists():
+        try:
+            return json.loads(path.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the 8B GEMV and M=512 GEMM figures")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    import kotensor_amd  # noqa: F401  (loads libkotensor_hip.so after torch's HIP runtime)
+    from kotensor_amd import _lib as kt_lib
+
+    torch.cuda.set_device(0)
+    # A dedicated stream: every launch, event and graph capture below runs on it.
+    stream_obj = torch.cuda.Stream()
+    with torch.cuda.stream(stream_obj):
+        return run(args, torch, kt_lib, stream_obj)
+
+
+def run(args, torch, kt_lib, stream_obj) -> int:
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    bits, g = 4, 64
+
+    # ---- weights: one quantized set, cloned until the rotation exceeds 2x the MALL
+    base = [Weight(torch, kt_lib, k, n, bits, g, seed=1 + i, stream=stream) for i, (_, k, n) in enumerate(QWEN)]
+    set_bytes = sum(w.nbytes for w in base)
+    copies = max(2, -(-2 * MALL_BYTES // set_bytes))
+    sets = [base] + [[w.clone(kt_lib) for w in base] for _ in range(copies - 1)]
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    xs = {k: torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32) for k in (896, 4864)}
+    ys = [torch.empty((1, n), device="cuda", dtype=torch.float32) for _, _, n in QWEN]
+    torch.cuda.synchronize()
+
+    def step(ws):
+        for i, (_, k, n) in enumerate(QWEN):
+            qmatmul(kt_lib, xs[k], 1, ws[i], ys[i], stream)
+
+    # eager warm-up (allocates the library's per-stream workspace before capture)
+    for r in range(copies):
+        step(sets[r])
+    torch.cuda.synchronize()
+    graphs = []
+    for r in range(copies):
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph, stream=stream_obj):
+            step(sets[r])
+        graphs.append(gph)
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream_obj)
+    for i in range(args.steps):
+        graphs[i % copies].replay()
+    t1.record(stream_obj)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    step_bytes = sum(gemv_bytes(1, k, n, bits, g) for _, k, n in QWEN)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: the lm_head GEMV, per launch
+    head = [s[-1] for s in sets]
+    head_y = ys[-1]
+    head_bytes = gemv_bytes(1, 896, 151936, bits, g)
+    avg_ms, med_ms = time_per_launch(torch, lambda w: qmatmul(kt_lib, xs[896], 1, w, head_y, stream), head, 100)
+    achieved = head_bytes / (avg_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                "kernel": "gemv_kernel<4,*> lm_head 896x151936 int4 g64",
+                "algorithmic_bytes": head_bytes, "avg_us": round(avg_ms * 1e3, 3), "median_us": round(med_ms * 1e3, 3)}
+
+    extra = {}
+    if not args.no_extra:
+        # INT4 GEMV on the Llama-3-8B FFN shape, 16 copies (> 2x MALL)
+        w8 = Weight(torch, kt_lib, 4096, 14336, 4, 64, seed=7, stream=stream)
+        n8 = max(2, -(-2 * MALL_BYTES // w8.nbytes))
+        c8 = [w8] + [w8.clone(kt_lib) for _ in range(n8 - 1)]
+        x8 = torch.randn((1, 4096), generator=gen, device="cuda", dtype=torch.float32)
+        y8 = torch.empty((1, 14336), device="cuda", dtype=torch.float32)
+        for w in c8:
+            qmatmul(kt_lib, x8, 1, w, y8, stream)
+        a8, m8 = time_per_launch(torch, lambda w: qmatmul(kt_lib, x8, 1, w, y8, stream), c8, 100)
+        b8 = gemv_bytes(1, 4096, 14336, 4, 64)
+        extra["int4_gemv_llama8b_ffn_4096x14336"] = {
+            "GB/s": round(b8 / (a8 * 1e-3) / 1e9, 1), "frac_hbm": round(b8 / (a8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "avg_us": round(a8 * 1e3, 3), "median_us": round(m8 * 1e3, 3), "bytes": b8, "copies": n8}
+        del c8, w8
+        # INT8 prefill GEMM at M = 512
+        for (k, n) in [(2048, 8192), (8192, 2048)]:
+            wg = Weight(torch, kt_lib, k, n, 8, 64, seed=9, stream=stream)
+            ng = max(2, -(-2 * MALL_BYTES // wg.nbytes))
+            cg = [wg] + [wg.clone(kt_lib) for _ in range(ng - 1)]
+            xg = torch.randn((512, k), generator=gen, device="cuda", dtype=torch.float32)
+            yg = torch.empty((512, n), device="cuda", dtype=torch.float32)
+            for w in cg:
+                qmatmul(kt_lib, xg, 512, w, yg, stream)
+            ag, mg = time_per_launch(torch, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 50)
+            tflops = 2.0 * 512 * k * n / (ag * 1e-3) / 1e12
+            extra[f"int8_gemm_m512_{k}x{n}"] = {
+                "TFLOP/s": round(tflops, 1), "frac_mfma": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                "avg_us": round(ag * 1e3, 3), "median_us": round(mg * 1e3, 3), "copies": ng}
+            del cg, wg
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0,1) fp32, W ~ N(0,0.02) fp32 quantized on device (seeded)",
+        "config": {"workload": "qwen2-0.5b int4 g64 M=1 projection GEMVs (q,k,v,o,gate,up,down,lm_head)",
+                   "weights": "uint4 + fp32 scales + u8 zeros, reference layout", "group_size": g, "m": 1,
+                   "step_bytes": step_bytes, "weight_copies": copies, "graph_replay": True},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,147 @@
+/*
+ * kotensor_hip.h -- C ABI of libkotensor_hip.so, the MI355X (gfx950) implementation
+ * of Kotensor's group-wise INT8/INT4 weight-only quantization path.
+ *
+ * Binding rules (what a JDK Foreign Function & Memory downcall needs):
+ *   - C linkage, fixed-width integer and float arguments, plain pointers, no C++ or
+ *     HIP types. A stream is an opaque pointer (a hipStream_t); NULL is the null stream.
+ *   - Every data pointer passed to a compute entry point is a DEVICE pointer owned
+ *     by the caller (kt_dev_alloc / kt_dev_free). The library never frees them.
+ *   - Entry points are stateless and reentrant. Compute entry points enqueue work on
+ *     the given stream and return before it finishes, except kt_quantize (see there).
+ *     The library keeps one internal workspace per (device, stream); calls that
+ *     share a stream are ordered by it, calls on different streams never share one.
+ *   - Return value: KT_OK (0) on success; a negative KT_ERR_* for an argument error
+ *     (the reference raises IllegalArgumentException for the same cases); a positive
+ *     value is a HIP runtime error code (the reference has no counterpart; a binding
+ *     maps it to IllegalStateException). kt_last_error() returns the message of the
+ *     last failure on the calling thread.
+ *
+ * Weight layout is the reference's, consumed without repacking:
+ *   qdata  [rows x bytes_per_row], row-major. 8-bit: bytes_per_row = columns, each
+ *          byte a two's-complement int8. 4-bit: bytes_per_row = (columns + columns%2)/2
+ *          and split-half packing: column c < bytes_per_row is the LOW nibble of byte c,
+ *          column c >= bytes_per_row the HIGH nibble of byte c - bytes_per_row; the
+ *          high nibble of the last byte is 0 when columns is odd.
+ *   scales [groups x columns] fp32, groups = ceil(rows / group_size).
+ *   zeros  [groups x columns] bytes read as signed int8 (a Kotlin ByteArray), required
+ *          for 4-bit, optional (NULL) for 8-bit.
+ * Reference: Engine/kotensor/src/main/kotlin/QuantizedTensor.kt:27-98 (K/ below).
+ */
+#ifndef KOTENSOR_HIP_H
+#define KOTENSOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KT_ABI_VERSION 1
+
+/* Status codes. */
+#define KT_OK 0
+#define KT_ERR_ARGUMENT (-1)   /* bad bits / group size / count / null pointer */
+#define KT_ERR_SHAPE (-2)      /* size or shape mismatch */
+#define KT_ERR_NAN (-3)        /* quantize met a value Float.roundToInt() rejects */
+#define KT_ERR_ZEROS (-4)      /* 4-bit tensor without zero points (K/QuantizedTensor.kt:69) */
+#define KT_ERR_RANGE (-5)      /* index out of range (row / column / token) */
+
+/* A quantized weight held in device memory. Mirrors the fields of
+ * QuantizedTensor (K/QuantizedTensor.kt:27-49): rows = K (in), columns = N (out). */
+typedef struct kt_qweight {
+    const void* qdata;
+    const float* scales;
+    const uint8_t* zeros;  /* NULL iff the tensor has no zero points */
+    int32_t rows;
+    int32_t columns;
+    int32_t bits;          /* 4 or 8 (Quantization.bits, K/QuantizedTensor.kt:10-17) */
+    int32_t group_size;    /* > 0 (Quantization.groupSize) */
+} kt_qweight;
+
+/* ---- library / errors --------------------------------------------------------- */
+int32_t kt_abi_version(void);
+/* Copies the calling thread's last error message (NUL-terminated, truncated to len). */
+int32_t kt_last_error(char* buf, size_t len);
+int32_t kt_device_count(int32_t* count);
+int32_t kt_set_device(int32_t device);
+
+/* Kernel selection knobs, the counterpart of MatMul's runtime knobs
+ * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they change how
+ * the M == 1 kernel splits its work, never its result beyond fp32 rounding order.
+ * gemv_vec: bytes per lane per row (4, 8 or 16; 0 = automatic);
+ * gemv_splits: workgroups along K per column tile (0 = automatic). Process-wide. */
+int32_t kt_set_kernel_config(int32_t gemv_vec, int32_t gemv_splits);
+
+/* ---- device memory and streams (the Kotlin side owns every buffer) ------------ */
+int32_t kt_dev_alloc(size_t bytes, void** ptr);
+int32_t kt_dev_free(void* ptr);
+int32_t kt_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int32_t kt_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int32_t kt_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int32_t kt_memset(void* dst, int32_t value, size_t bytes, void* stream);
+int32_t kt_stream_create(void** stream);
+int32_t kt_stream_destroy(void* stream);
+int32_t kt_stream_sync(void* stream);
+
+/* ---- format helpers (pure host arithmetic, no device work) -------------------- */
+/* groups, storedColumns, bytesPerRow and sizeInBytes of K/QuantizedTensor.kt:47-49,97-98. */
+int32_t kt_qweight_layout(int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
+                          int32_t has_zeros, int64_t* out4);
+/* Validates a weight the way the QuantizedTensor constructor does
+ * (K/QuantizedTensor.kt:63-70). */
+int32_t kt_qweight_check(const kt_qweight* w);
+
+/* ---- quantize + pack ---------------------------------------------------------- */
+/* QuantizedTensor.quantize(data, rows, columns, Quantization(bits, group_size)),
+ * K/QuantizedTensor.kt:256-324. data fp32 [rows x columns] row-major on the device.
+ * Writes qdata [rows x bytes_per_row], scales [groups x columns] and, for 4-bit,
+ * zeros [groups x columns]; zeros must be NULL for 8-bit. Bit-exact with the
+ * reference: scale = maxAbs/127 (8-bit) or (max-min)/15 with 0 inside [min,max]
+ * (4-bit), q = Math.round(x * (1/scale)) (ties toward +inf), clamped.
+ * SYNCHRONOUS: it waits for the stream, because a NaN in the rounding step makes
+ * the reference throw; that case returns KT_ERR_NAN (output contents unspecified). */
+int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bits,
+                    int32_t group_size, void* qdata, float* scales, uint8_t* zeros,
+                    void* stream);
+
+/* ---- dequantizing matmul -------------------------------------------------------- */
+/* MatMul.multiplyQuantized(a, weight, c, m, accumulate, alpha), K/MatMul.kt:460-486:
+ *   c[m x N] = (accumulate ? c : 0) + alpha * (a[m x K] . deq(W)),
+ * deq(W)[k][n] = scale[k/g][n] * (q[k][n] - zero[k/g][n]), applied per group after an
+ * integer-valued accumulation (K/MatMul.kt:804-828,942-952). fp32 in and out.
+ * m == 0 is a no-op (K/MatMul.kt:473). Asynchronous. */
+int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
+                   int32_t accumulate, float alpha, void* stream);
+
+/* QuantizedLinear.forwardInto(input, out), K/QuantizedLinear.kt:22-25 (with
+ * Tensor.matmulDequantInto K/Tensor.kt:180-188 and addInPlace K/Tensor.kt:201-221):
+ *   out[m x N] = a . deq(W) + bias (bias fp32 [N] broadcast over rows, or NULL). */
+int32_t kt_qlinear_forward(const float* a, int32_t m, const kt_qweight* w, const float* bias,
+                           float* out, void* stream);
+
+/* MatMul.multiplyByQuantizedTransposed(dy, weight, dx, m, accumulate),
+ * K/MatMul.kt:954-981:  dx[m x K] = (accumulate ? dx : 0) + dy[m x N] . deq(W)^T.
+ * 8-bit rows are dequantized without zero points, as dequantizeRow does
+ * (K/QuantizedTensor.kt:198-202). Asynchronous. */
+int32_t kt_qmatmul_transposed(const float* dy, int32_t m, const kt_qweight* w, float* dx,
+                              int32_t accumulate, void* stream);
+
+/* ---- dequant accessors ---------------------------------------------------------- */
+/* dequantizeRow for each index in rows[0..count) (device int32 array), writing
+ * out[i x N]; the row gather of QuantizedEmbedding.lookupInto/forward
+ * (K/Embedding.kt:73-113 -> K/QuantizedTensor.kt:188-213). Indices outside
+ * [0, rows) are not checked on the device; pass validated indices. */
+int32_t kt_dequantize_rows(const kt_qweight* w, const int32_t* rows, int32_t count, float* out,
+                           void* stream);
+/* dequantizeColumn for each index in columns[0..count), writing out[i x K]; the
+ * tied-embedding gather of TiedQuantizedEmbedding (K/Embedding.kt:115-136 ->
+ * K/QuantizedTensor.kt:235-241). An index outside [0, columns) produces NaN. */
+int32_t kt_dequantize_columns(const kt_qweight* w, const int32_t* columns, int32_t count,
+                              float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KOTENSOR_HIP_H */

@@ -1,0 +1,30 @@
+"""kotensor_amd: MI355X (gfx950) implementation of Kotensor's group-wise INT8/INT4
+weight-only quantization path.
+
+The product is ``libkotensor_hip.so`` (C ABI: ``include/kotensor_hip.h``). This
+package is a host-side mirror of the reference's API over that ABI:
+``Quantization``, ``QuantizedTensor``, ``MatMul.multiply_quantized``,
+``DeviceTensor.matmul_dequant(_into)`` and ``QuantizedLinear``.
+"""
+from ._lib import IllegalArgumentException, IllegalStateException, LibraryMissingError, LIBRARY_PATH
+from .device import DeviceBuffer, Stream, synchronize, device_count
+from .quantization import Quantization, QuantizedTensor
+from .matmul import MatMul, DeviceTensor
+from .linear import QuantizedLinear, projection
+
+__all__ = [
+    "IllegalArgumentException",
+    "IllegalStateException",
+    "LibraryMissingError",
+    "LIBRARY_PATH",
+    "DeviceBuffer",
+    "Stream",
+    "synchronize",
+    "device_count",
+    "Quantization",
+    "QuantizedTensor",
+    "MatMul",
+    "DeviceTensor",
+    "QuantizedLinear",
+    "projection",
+]

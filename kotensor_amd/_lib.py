@@ -1,0 +1,148 @@
+"""ctypes binding of libkotensor_hip.so (the C ABI in include/kotensor_hip.h).
+
+This is the Python counterpart of the JDK Foreign Function & Memory downcalls a
+Kotlin host makes: every entry point takes plain pointers and sizes and returns an
+int32 status. A negative status raises :class:`IllegalArgumentException`, a
+positive (HIP runtime) status :class:`IllegalStateException`, mirroring the
+reference's ``require`` / ``check`` failures.
+
+The library is loaded from the package directory and never replaced by anything
+else: if it is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import importlib.util
+import os
+import sys
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libkotensor_hip.so"
+
+
+class IllegalArgumentException(ValueError):
+    """An argument error (the reference's ``require`` failures)."""
+
+    def __init__(self, message: str, status: int = -1):
+        super().__init__(message)
+        self.status = status
+
+
+class IllegalStateException(RuntimeError):
+    """A runtime failure of the device (HIP error code in ``status``)."""
+
+    def __init__(self, message: str, status: int = 1):
+        super().__init__(message)
+        self.status = status
+
+
+class LibraryMissingError(RuntimeError):
+    """libkotensor_hip.so has not been built; there is no fallback path."""
+
+
+# status codes, include/kotensor_hip.h
+KT_OK = 0
+KT_ERR_ARGUMENT = -1
+KT_ERR_SHAPE = -2
+KT_ERR_NAN = -3
+KT_ERR_ZEROS = -4
+KT_ERR_RANGE = -5
+
+
+class _QWeight(ctypes.Structure):
+    _fields_ = [
+        ("qdata", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("zeros", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("columns", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+    ]
+
+
+QWeight = _QWeight
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+
+# name -> argument types (all return int32)
+SIGNATURES = {
+    "kt_abi_version": [],
+    "kt_last_error": [ctypes.c_char_p, _SZ],
+    "kt_device_count": [ctypes.POINTER(_I)],
+    "kt_set_device": [_I],
+    "kt_set_kernel_config": [_I, _I],
+    "kt_dev_alloc": [_SZ, ctypes.POINTER(_P)],
+    "kt_dev_free": [_P],
+    "kt_memcpy_h2d": [_P, _P, _SZ, _P],
+    "kt_memcpy_d2h": [_P, _P, _SZ, _P],
+    "kt_memcpy_d2d": [_P, _P, _SZ, _P],
+    "kt_memset": [_P, _I, _SZ, _P],
+    "kt_stream_create": [ctypes.POINTER(_P)],
+    "kt_stream_destroy": [_P],
+    "kt_stream_sync": [_P],
+    "kt_qweight_layout": [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
+    "kt_qweight_check": [ctypes.POINTER(_QWeight)],
+    "kt_quantize": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "kt_qmatmul": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],
+    "kt_qlinear_forward": [_P, _I, ctypes.POINTER(_QWeight), _P, _P, _P],
+    "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],
+    "kt_dequantize_rows": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
+    "kt_dequantize_columns": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _load():
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY_PATH.exists():
+            raise LibraryMissingError(
+                f"{LIBRARY_PATH} is not built; run `python -m kotensor_amd.build` "
+                "(there is no CPU fallback for the HIP path)"
+            )
+        # torch bundles its own HIP runtime under the same soname; loading it first
+        # makes this library bind to that copy, so a process never holds two runtimes.
+        if "torch" not in sys.modules and importlib.util.find_spec("torch") is not None \
+                and os.environ.get("KOTENSOR_NO_TORCH_PRELOAD") != "1":
+            import torch  # noqa: F401
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _I
+        _lib = lib
+        return lib
+
+
+def lib():
+    """The loaded library (loads it on first use)."""
+    return _load()
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(512)
+    lib().kt_last_error(buf, 512)
+    return buf.value.decode("utf-8", "replace")
+
+
+def check(status: int, what: str = "") -> None:
+    if status == KT_OK:
+        return
+    message = last_error() or what
+    if status < 0:
+        raise IllegalArgumentException(message, status)
+    raise IllegalStateException(message, status)
+
+
+def call(name: str, *args) -> None:
+    """Calls an entry point and raises on a non-zero status."""
+    check(getattr(lib(), name)(*args), name)

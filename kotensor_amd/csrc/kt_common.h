@@ -1,0 +1,74 @@
+// kt_common.h -- internals shared by the translation units of libkotensor_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kotensor_hip.h"
+
+namespace kt {
+
+// Records a message for kt_last_error() on the calling thread and returns status.
+int32_t fail(int32_t status, const char* fmt, ...);
+// Maps a HIP error to a positive status (and records its message).
+int32_t hip_fail(hipError_t err, const char* what);
+
+#define KT_HIP(call)                                             \
+    do {                                                         \
+        hipError_t kt_err_ = (call);                             \
+        if (kt_err_ != hipSuccess) return ::kt::hip_fail(kt_err_, #call); \
+    } while (0)
+
+// Checks the launch that was just enqueued.
+#define KT_LAUNCHED(name)                                        \
+    do {                                                         \
+        hipError_t kt_err_ = hipGetLastError();                  \
+        if (kt_err_ != hipSuccess) return ::kt::hip_fail(kt_err_, name); \
+    } while (0)
+
+// Device workspace owned by the library, one per (device, stream). Calls on one
+// stream are ordered by that stream, so they may reuse the same bytes. Growing it
+// waits for the stream before the old allocation is released.
+int32_t workspace(hipStream_t stream, size_t bytes, void** out);
+
+// Validated view of a kt_qweight, with the derived layout numbers.
+struct WeightView {
+    const uint8_t* q;
+    const float* s;
+    const int8_t* z;  // nullptr when the weight has no zero points
+    int32_t K, N, bits, g, G, bpr;
+};
+int32_t view_weight(const kt_qweight* w, WeightView* v);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+__host__ __device__ inline int32_t ceil_div(int32_t a, int32_t b) { return (a + b - 1) / b; }
+
+// Number of compute units of the current device (cached per device).
+int32_t cu_count();
+
+// Launch entry points implemented by the kernel translation units. All take
+// validated arguments. bias may be nullptr; partial results never leave the stream.
+int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, int32_t g,
+                        uint8_t* q, float* s, int8_t* z, int32_t* nan_flag, hipStream_t st);
+int32_t launch_gemv(const float* a, const WeightView& w, float* c, int32_t accumulate, float alpha,
+                    const float* bias, hipStream_t st);
+int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
+                    float alpha, const float* bias, hipStream_t st);
+int32_t launch_generic(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
+                       float alpha, const float* bias, hipStream_t st);
+int32_t launch_transposed(const float* dy, int32_t m, const WeightView& w, float* dx,
+                          int32_t accumulate, hipStream_t st);
+int32_t launch_dequantize_rows(const WeightView& w, const int32_t* rows, int32_t count, float* out,
+                               hipStream_t st);
+int32_t launch_dequantize_columns(const WeightView& w, const int32_t* cols, int32_t count, float* out,
+                                  hipStream_t st);
+
+// Forces the lane vector width and split count of the M == 1 kernel (0 = automatic).
+void set_gemv_config(int32_t vec, int32_t splits);
+
+// Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
+// otherwise the generic kernel runs.
+bool gemv_supported(const float* a, const WeightView& w, const float* c);
+bool gemm_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+
+}  // namespace kt

@@ -1,0 +1,310 @@
+// kt_runtime.hip -- errors, device memory, streams, the per-stream workspace and
+// the argument checks shared by every entry point of libkotensor_hip.so.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "kt_common.h"
+
+namespace kt {
+
+static thread_local char g_last_error[512] = "";
+
+int32_t fail(int32_t status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int32_t hip_fail(hipError_t err, const char* what) {
+    int32_t code = static_cast<int32_t>(err);
+    if (code <= 0) code = 1;
+    return fail(code, "%s failed: %s (%d)", what, hipGetErrorString(err), static_cast<int>(err));
+}
+
+namespace {
+struct Block {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, Block> g_ws;
+std::map<int, int32_t> g_cus;
+}  // namespace
+
+int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
+    int device = 0;
+    KT_HIP(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Block& b = g_ws[std::make_pair(device, stream)];
+    if (b.bytes < bytes) {
+        size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes + bytes / 4;
+        if (b.ptr) {
+            KT_HIP(hipStreamSynchronize(stream));
+            KT_HIP(hipFree(b.ptr));
+            b.ptr = nullptr;
+            b.bytes = 0;
+        }
+        KT_HIP(hipMalloc(&b.ptr, want));
+        b.bytes = want;
+    }
+    *out = b.ptr;
+    return KT_OK;
+}
+
+int32_t cu_count() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    auto it = g_cus.find(device);
+    if (it != g_cus.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+        cus = 256;
+    g_cus[device] = cus;
+    return cus;
+}
+
+int32_t view_weight(const kt_qweight* w, WeightView* v) {
+    if (!w) return fail(KT_ERR_ARGUMENT, "weight is NULL");
+    if (w->bits != 4 && w->bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", w->bits);
+    if (w->group_size <= 0) return fail(KT_ERR_ARGUMENT, "groupSize must be positive");
+    if (w->rows <= 0 || w->columns <= 0)
+        return fail(KT_ERR_SHAPE, "QuantizedTensor needs a 2-D shape, got [%d, %d]", w->rows, w->columns);
+    if (w->bits == 4 && !w->zeros) return fail(KT_ERR_ZEROS, "4-bit tensors need zero points");
+    if (!w->qdata || !w->scales) return fail(KT_ERR_ARGUMENT, "weight has a NULL qdata or scales pointer");
+    v->q = static_cast<const uint8_t*>(w->qdata);
+    v->s = w->scales;
+    v->z = reinterpret_cast<const int8_t*>(w->zeros);
+    v->K = w->rows;
+    v->N = w->columns;
+    v->bits = w->bits;
+    v->g = w->group_size;
+    v->G = (w->rows + w->group_size - 1) / w->group_size;
+    v->bpr = w->bits == 4 ? (w->columns + w->columns % 2) / 2 : w->columns;
+    int64_t qbytes = static_cast<int64_t>(v->K) * v->bpr;
+    int64_t sbytes = static_cast<int64_t>(v->G) * v->N * 4;
+    if (qbytes > INT32_MAX * 4LL || sbytes > INT32_MAX * 4LL)
+        return fail(KT_ERR_SHAPE, "weight [%d, %d] is too large", v->K, v->N);
+    return KT_OK;
+}
+
+}  // namespace kt
+
+using namespace kt;
+
+extern "C" {
+
+int32_t kt_abi_version(void) { return KT_ABI_VERSION; }
+
+int32_t kt_last_error(char* buf, size_t len) {
+    if (!buf || len == 0) return KT_ERR_ARGUMENT;
+    strncpy(buf, g_last_error, len - 1);
+    buf[len - 1] = '\0';
+    return KT_OK;
+}
+
+int32_t kt_device_count(int32_t* count) {
+    if (!count) return fail(KT_ERR_ARGUMENT, "count is NULL");
+    int n = 0;
+    KT_HIP(hipGetDeviceCount(&n));
+    *count = n;
+    return KT_OK;
+}
+
+int32_t kt_set_device(int32_t device) {
+    KT_HIP(hipSetDevice(device));
+    return KT_OK;
+}
+
+int32_t kt_set_kernel_config(int32_t gemv_vec, int32_t gemv_splits) {
+    if (gemv_vec != 0 && gemv_vec != 4 && gemv_vec != 8 && gemv_vec != 16)
+        return fail(KT_ERR_ARGUMENT, "gemv_vec must be 0, 4, 8 or 16, got %d", gemv_vec);
+    if (gemv_splits < 0) return fail(KT_ERR_ARGUMENT, "gemv_splits must be >= 0, got %d", gemv_splits);
+    set_gemv_config(gemv_vec, gemv_splits);
+    return KT_OK;
+}
+
+int32_t kt_dev_alloc(size_t bytes, void** ptr) {
+    if (!ptr) return fail(KT_ERR_ARGUMENT, "ptr is NULL");
+    *ptr = nullptr;
+    if (bytes == 0) return KT_OK;
+    KT_HIP(hipMalloc(ptr, bytes));
+    return KT_OK;
+}
+
+int32_t kt_dev_free(void* ptr) {
+    if (!ptr) return KT_OK;
+    KT_HIP(hipFree(ptr));
+    return KT_OK;
+}
+
+static int32_t copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, void* stream) {
+    if (bytes == 0) return KT_OK;
+    if (!dst || !src) return fail(KT_ERR_ARGUMENT, "copy with a NULL pointer");
+    KT_HIP(hipMemcpyAsync(dst, src, bytes, kind, static_cast<hipStream_t>(stream)));
+    if (kind == hipMemcpyDeviceToHost) KT_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return KT_OK;
+}
+
+int32_t kt_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    int32_t st = copy(dst, src, bytes, hipMemcpyHostToDevice, stream);
+    if (st) return st;
+    // The source is caller memory that may be reused once this returns.
+    KT_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return KT_OK;
+}
+
+int32_t kt_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy(dst, src, bytes, hipMemcpyDeviceToHost, stream);
+}
+
+int32_t kt_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream);
+}
+
+int32_t kt_memset(void* dst, int32_t value, size_t bytes, void* stream) {
+    if (bytes == 0) return KT_OK;
+    if (!dst) return fail(KT_ERR_ARGUMENT, "memset of a NULL pointer");
+    KT_HIP(hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(stream)));
+    return KT_OK;
+}
+
+int32_t kt_stream_create(void** stream) {
+    if (!stream) return fail(KT_ERR_ARGUMENT, "stream is NULL");
+    hipStream_t s = nullptr;
+    KT_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return KT_OK;
+}
+
+int32_t kt_stream_destroy(void* stream) {
+    if (!stream) return KT_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    KT_HIP(hipStreamSynchronize(s));
+    {
+        int device = 0;
+        KT_HIP(hipGetDevice(&device));
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        auto it = g_ws.find(std::make_pair(device, s));
+        if (it != g_ws.end()) {
+            if (it->second.ptr) KT_HIP(hipFree(it->second.ptr));
+            g_ws.erase(it);
+        }
+    }
+    KT_HIP(hipStreamDestroy(s));
+    return KT_OK;
+}
+
+int32_t kt_stream_sync(void* stream) {
+    KT_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return KT_OK;
+}
+
+int32_t kt_qweight_layout(int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
+                          int32_t has_zeros, int64_t* out4) {
+    if (!out4) return fail(KT_ERR_ARGUMENT, "out is NULL");
+    if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
+    if (group_size <= 0) return fail(KT_ERR_ARGUMENT, "groupSize must be positive");
+    if (rows <= 0 || columns <= 0) return fail(KT_ERR_SHAPE, "QuantizedTensor needs a 2-D shape, got [%d, %d]", rows, columns);
+    int64_t groups = (rows + static_cast<int64_t>(group_size) - 1) / group_size;
+    int64_t stored = bits == 4 ? columns + columns % 2 : columns;
+    int64_t bpr = bits == 4 ? stored / 2 : stored;
+    out4[0] = groups;
+    out4[1] = stored;
+    out4[2] = bpr;
+    out4[3] = rows * bpr + groups * columns * 4 + (has_zeros ? groups * columns : 0);
+    return KT_OK;
+}
+
+int32_t kt_qweight_check(const kt_qweight* w) {
+    WeightView v;
+    return view_weight(w, &v);
+}
+
+int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
+                    void* qdata, float* scales, uint8_t* zeros, void* stream) {
+    if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
+    if (group_size <= 0) return fail(KT_ERR_ARGUMENT, "groupSize must be positive");
+    if (rows <= 0 || columns <= 0) return fail(KT_ERR_SHAPE, "QuantizedTensor needs a 2-D shape, got [%d, %d]", rows, columns);
+    if (!data || !qdata || !scales) return fail(KT_ERR_ARGUMENT, "quantize with a NULL pointer");
+    if (bits == 4 && !zeros) return fail(KT_ERR_ZEROS, "4-bit tensors need zero points");
+    if (bits == 8 && zeros) return fail(KT_ERR_ARGUMENT, "8-bit quantize writes no zero points; pass NULL");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    int32_t status = workspace(st, 256, &ws);
+    if (status) return status;
+    int32_t* flag = static_cast<int32_t*>(ws);
+    status = launch_quantize(data, rows, columns, bits, group_size, static_cast<uint8_t*>(qdata), scales,
+                             reinterpret_cast<int8_t*>(zeros), flag, st);
+    if (status) return status;
+    int32_t host_flag = 0;
+    KT_HIP(hipMemcpyAsync(&host_flag, flag, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    KT_HIP(hipStreamSynchronize(st));
+    if (host_flag) return fail(KT_ERR_NAN, "Cannot round NaN value.");
+    return KT_OK;
+}
+
+static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
+                       float alpha, const float* bias, void* stream) {
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    if (m == 0) return KT_OK;
+    if (!a || !c) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (m == 1 && gemv_supported(a, v, c)) return launch_gemv(a, v, c, accumulate, alpha, bias, st);
+    if (m > 1 && gemm_supported(a, m, v, c)) return launch_gemm(a, m, v, c, accumulate, alpha, bias, st);
+    return launch_generic(a, m, v, c, accumulate, alpha, bias, st);
+}
+
+int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
+                   void* stream) {
+    return qmatmul(a, m, w, c, accumulate, alpha, nullptr, stream);
+}
+
+int32_t kt_qlinear_forward(const float* a, int32_t m, const kt_qweight* w, const float* bias, float* out,
+                           void* stream) {
+    return qmatmul(a, m, w, out, 0, 1.0f, bias, stream);
+}
+
+int32_t kt_qmatmul_transposed(const float* dy, int32_t m, const kt_qweight* w, float* dx, int32_t accumulate,
+                              void* stream) {
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    if (m == 0) return KT_OK;
+    if (!dy || !dx) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
+    return launch_transposed(dy, m, v, dx, accumulate, static_cast<hipStream_t>(stream));
+}
+
+int32_t kt_dequantize_rows(const kt_qweight* w, const int32_t* rows, int32_t count, float* out, void* stream) {
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (count < 0) return fail(KT_ERR_ARGUMENT, "Negative count %d", count);
+    if (count == 0) return KT_OK;
+    if (!rows || !out) return fail(KT_ERR_ARGUMENT, "dequantize with a NULL pointer");
+    return launch_dequantize_rows(v, rows, count, out, static_cast<hipStream_t>(stream));
+}
+
+int32_t kt_dequantize_columns(const kt_qweight* w, const int32_t* columns, int32_t count, float* out,
+                              void* stream) {
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (count < 0) return fail(KT_ERR_ARGUMENT, "Negative count %d", count);
+    if (count == 0) return KT_OK;
+    if (!columns || !out) return fail(KT_ERR_ARGUMENT, "dequantize with a NULL pointer");
+    return launch_dequantize_columns(v, columns, count, out, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

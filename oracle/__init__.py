@@ -1,0 +1,172 @@
+"""The oracle: a CPU restatement of Kotensor's group-wise INT8/INT4 quantization
+path (kt_oracle.c), with a numpy interface.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of bench.py use it, as the checker and the CPU baseline. The
+product (kotensor_amd / libkotensor_hip.so) never imports or links it.
+
+Pinning status of each function is listed in kt_oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY_PATH = HERE / "_build" / "libkt_oracle.so"
+
+KO_OK = 0
+KO_ERR_ARG = -1
+KO_ERR_NAN = -3
+
+
+class QW(ctypes.Structure):
+    _fields_ = [
+        ("qdata", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("zeros", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("columns", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def build() -> Path:
+    """Compiles the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    proc = subprocess.run(["make", "-s", "-C", str(HERE)], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{proc.stdout}\n{proc.stderr}")
+    return LIBRARY_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIBRARY_PATH))
+        P, I, F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
+        L.ko_groups.argtypes = [I, I]
+        L.ko_bytes_per_row.argtypes = [I, I]
+        L.ko_java_round.argtypes = [F, ctypes.POINTER(I)]
+        L.ko_quantize.argtypes = [P, I, I, I, I, P, P, P]
+        L.ko_raw_value.argtypes = [ctypes.POINTER(QW), I, I]
+        L.ko_value.argtypes = [ctypes.POINTER(QW), I, I]
+        L.ko_value.restype = F
+        L.ko_dequantize_row.argtypes = [ctypes.POINTER(QW), I, P]
+        L.ko_dequantize_row.restype = None
+        L.ko_dequantize_column.argtypes = [ctypes.POINTER(QW), I, P]
+        L.ko_dequantize_column.restype = None
+        L.ko_multiply_quantized.argtypes = [P, ctypes.POINTER(QW), P, I, I, F, I]
+        L.ko_multiply_by_quantized_transposed.argtypes = [P, ctypes.POINTER(QW), P, I, I, I]
+        L.ko_row_units.argtypes = [ctypes.POINTER(QW), P]
+        L.ko_row_units.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def groups(rows: int, group_size: int) -> int:
+    return lib().ko_groups(rows, group_size)
+
+
+def bytes_per_row(columns: int, bits: int) -> int:
+    return lib().ko_bytes_per_row(columns, bits)
+
+
+def java_round(x: float) -> tuple[int, bool]:
+    nan = ctypes.c_int32(0)
+    r = lib().ko_java_round(ctypes.c_float(x), ctypes.byref(nan))
+    return int(r), bool(nan.value)
+
+
+class Quantized:
+    """Host arrays of one quantized tensor in the reference layout."""
+
+    def __init__(self, qdata, scales, zeros, rows, columns, bits, group_size):
+        self.qdata = np.ascontiguousarray(qdata).view(np.uint8).reshape(-1)
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        self.zeros = None if zeros is None else np.ascontiguousarray(zeros).view(np.int8).reshape(-1)
+        self.rows, self.columns, self.bits, self.group_size = int(rows), int(columns), int(bits), int(group_size)
+        self.groups = groups(self.rows, self.group_size)
+        self.bytes_per_row = bytes_per_row(self.columns, self.bits)
+        self._qw = QW(_p(self.qdata).value, _p(self.scales).value,
+                      None if self.zeros is None else _p(self.zeros).value,
+                      self.rows, self.columns, self.bits, self.group_size)
+
+    @property
+    def qw(self) -> QW:
+        return self._qw
+
+    def raw_value(self, row, column) -> int:
+        return int(lib().ko_raw_value(ctypes.byref(self._qw), row, column))
+
+    def value(self, row, column) -> float:
+        return float(lib().ko_value(ctypes.byref(self._qw), row, column))
+
+    def dequantize_row(self, row) -> np.ndarray:
+        out = np.empty(self.columns, dtype=np.float32)
+        lib().ko_dequantize_row(ctypes.byref(self._qw), row, _p(out))
+        return out
+
+    def dequantize_column(self, column) -> np.ndarray:
+        out = np.empty(self.rows, dtype=np.float32)
+        lib().ko_dequantize_column(ctypes.byref(self._qw), column, _p(out))
+        return out
+
+    def dequantize(self) -> np.ndarray:
+        return np.stack([self.dequantize_row(r) for r in range(self.rows)])
+
+    def row_units(self) -> list[int]:
+        out = np.zeros(6, dtype=np.int32)
+        lib().ko_row_units(ctypes.byref(self._qw), _p(out))
+        return [int(v) for v in out]
+
+
+def quantize(data: np.ndarray, bits: int, group_size: int) -> tuple[int, Quantized]:
+    """(status, Quantized) for fp32 ``data`` ``[rows x columns]`` (QuantizedTensor.kt:261-324)."""
+    data = np.ascontiguousarray(data, dtype=np.float32)
+    rows, columns = data.shape
+    g = groups(rows, group_size)
+    bpr = bytes_per_row(columns, bits)
+    q = np.empty(rows * bpr, dtype=np.uint8)
+    s = np.empty(g * columns, dtype=np.float32)
+    z = np.empty(g * columns, dtype=np.int8) if bits == 4 else None
+    status = lib().ko_quantize(_p(data), rows, columns, bits, group_size, _p(q), _p(s), _p(z))
+    return int(status), Quantized(q, s, z, rows, columns, bits, group_size)
+
+
+def multiply_quantized(a: np.ndarray, w: Quantized, m: int, c: np.ndarray | None = None, accumulate: bool = False,
+                       alpha: float = 1.0, threads: int = 1) -> np.ndarray:
+    """MatMul.multiplyQuantized (MatMul.kt:460-486), returning c ``[m x N]``."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    if c is None:
+        c = np.zeros(m * w.columns, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32).reshape(-1).copy()
+    st = lib().ko_multiply_quantized(_p(a), ctypes.byref(w.qw), _p(c), m, int(accumulate), ctypes.c_float(alpha),
+                                     threads)
+    if st != KO_OK:
+        raise ValueError(f"oracle multiply_quantized status {st}")
+    return c.reshape(m, w.columns)
+
+
+def multiply_by_quantized_transposed(dy: np.ndarray, w: Quantized, m: int, dx: np.ndarray | None = None,
+                                     accumulate: bool = False, threads: int = 1) -> np.ndarray:
+    dy = np.ascontiguousarray(dy, dtype=np.float32).reshape(-1)
+    if dx is None:
+        dx = np.zeros(m * w.rows, dtype=np.float32)
+    dx = np.ascontiguousarray(dx, dtype=np.float32).reshape(-1).copy()
+    st = lib().ko_multiply_by_quantized_transposed(_p(dy), ctypes.byref(w.qw), _p(dx), m, int(accumulate), threads)
+    if st != KO_OK:
+        raise ValueError(f"oracle transposed status {st}")
+    return dx.reshape(m, w.rows)

@@ -1,0 +1,99 @@
+"""An independent numpy restatement of the quantize spec and of the packed format.
+
+Used only to cross-check the C oracle (a second implementation written from the
+same specification: QuantizedTensor.kt:256-324 and the JDK contract of
+Math.round). numpy float32 arithmetic is IEEE-754 binary32 with correct rounding
+and gradual underflow, like the JVM's.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32_MAX = np.float32(np.finfo(np.float32).max)
+
+
+class RoundNaN(Exception):
+    pass
+
+
+def java_round(x: np.ndarray) -> np.ndarray:
+    """Math.round for float32 arrays: nearest, ties toward +inf, saturating to int32.
+    Raises RoundNaN if any element is NaN (Float.roundToInt rejects NaN)."""
+    x = np.asarray(x, dtype=np.float32)
+    if np.isnan(x).any():
+        raise RoundNaN()
+    xd = x.astype(np.float64)  # exact
+    r = np.floor(xd + 0.5)     # exact in float64 for every float32
+    r = np.clip(r, -2147483648.0, 2147483647.0)
+    return r.astype(np.int64)
+
+
+def wrap_i32(v: np.ndarray) -> np.ndarray:
+    v = np.asarray(v, dtype=np.int64) & 0xFFFFFFFF
+    return np.where(v >= 2**31, v - 2**32, v)
+
+
+def quantize(data: np.ndarray, bits: int, group_size: int):
+    """Returns (qdata uint8 [K*bpr], scales f32 [G*N], zeros int8 [G*N] or None)."""
+    data = np.ascontiguousarray(data, dtype=np.float32)
+    K, N = data.shape
+    G = (K + group_size - 1) // group_size
+    bpr = (N + N % 2) // 2 if bits == 4 else N
+    scales = np.empty((G, N), dtype=np.float32)
+    zeros = np.empty((G, N), dtype=np.int8) if bits == 4 else None
+    qv = np.zeros((K, N), dtype=np.int64)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore", under="ignore"):
+        for gi in range(G):
+            blk = data[gi * group_size:(gi + 1) * group_size]
+            if bits == 8:
+                a = np.abs(blk)
+                mx = np.where(np.isnan(a), np.float32(0), a).max(axis=0).astype(np.float32)
+                scale = np.where(mx > 0, mx / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+                inv = (np.float32(1.0) / scale).astype(np.float32)
+                q = java_round((blk * inv).astype(np.float32))
+                qv[gi * group_size:gi * group_size + blk.shape[0]] = np.clip(q, -127, 127)
+                scales[gi] = scale
+            else:
+                mn = np.where(np.isnan(blk), F32_MAX, blk).min(axis=0).astype(np.float32)
+                mx = np.where(np.isnan(blk), -F32_MAX, blk).max(axis=0).astype(np.float32)
+                mn = np.where(mn > 0, np.float32(0), mn).astype(np.float32)
+                mx = np.where(mx < 0, np.float32(0), mx).astype(np.float32)
+                rng = (mx - mn).astype(np.float32)
+                scale = np.where(rng > 0, rng / np.float32(15.0), np.float32(1.0)).astype(np.float32)
+                zero = np.clip(java_round((-mn / scale).astype(np.float32)), 0, 15)
+                inv = (np.float32(1.0) / scale).astype(np.float32)
+                q = wrap_i32(java_round((blk * inv).astype(np.float32)) + zero)
+                qv[gi * group_size:gi * group_size + blk.shape[0]] = np.clip(q, 0, 15)
+                scales[gi] = scale
+                zeros[gi] = zero.astype(np.int8)
+    if bits == 8:
+        qdata = (qv & 0xFF).astype(np.uint8).reshape(-1)
+    else:
+        half = bpr
+        packed = np.zeros((K, bpr), dtype=np.int64)
+        packed[:, :half] |= qv[:, :half]
+        high = qv[:, half:]
+        packed[:, :high.shape[1]] |= high << 4
+        qdata = packed.astype(np.uint8).reshape(-1)
+    return qdata, scales.reshape(-1), None if zeros is None else zeros.reshape(-1)
+
+
+def decode(qdata, scales, zeros, K, N, bits, group_size) -> np.ndarray:
+    """fp32 [K x N] of value(r, c) = scale * (raw - zero) (QuantizedTensor.kt:172-186)."""
+    bpr = (N + N % 2) // 2 if bits == 4 else N
+    q = np.asarray(qdata).view(np.uint8).reshape(K, bpr)
+    if bits == 8:
+        raw = q.view(np.int8).astype(np.int32)
+    else:
+        half = bpr
+        raw = np.empty((K, N), dtype=np.int32)
+        raw[:, :half] = q[:, :half] & 0xF
+        raw[:, half:] = (q[:, :N - half] >> 4) & 0xF
+    G = (K + group_size - 1) // group_size
+    gidx = np.arange(K) // group_size
+    s = np.asarray(scales, dtype=np.float32).reshape(G, N)[gidx]
+    if zeros is None:
+        z = np.zeros((K, N), dtype=np.int32)
+    else:
+        z = np.asarray(zeros).view(np.int8).reshape(G, N)[gidx].astype(np.int32)
+    return (s * (raw - z).astype(np.float32)).astype(np.float32)
