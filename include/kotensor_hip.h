@@ -68,11 +68,17 @@ int32_t kt_device_count(int32_t* count);
 int32_t kt_set_device(int32_t device);
 
 /* Kernel selection knobs, the counterpart of MatMul's runtime knobs
- * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they change how
- * the M == 1 kernel splits its work, never its result beyond fp32 rounding order.
- * gemv_vec: bytes per lane per row (4, 8 or 16; 0 = automatic);
- * gemv_splits: workgroups along K per column tile (0 = automatic). Process-wide. */
-int32_t kt_set_kernel_config(int32_t gemv_vec, int32_t gemv_splits);
+ * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they choose how the
+ * small-M kernels split their work, never their result beyond fp32 rounding order.
+ * gemv_kind: 0 = automatic (MFMA kernel for 1..16 rows where the layout allows),
+ *            1 = vector-ALU kernel for M == 1, 2 = MFMA kernel;
+ * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic);
+ * gemv_splits: workgroups along K per column tile (0 = automatic);
+ * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic);
+ * gemv_reduce: how split sums meet (0 = automatic, 1 = a second kernel, 2 = inside the
+ * kernel). Process-wide. */
+int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits,
+                             int32_t gemv_waves, int32_t gemv_reduce);
 
 /* ---- device memory and streams (the Kotlin side owns every buffer) ------------ */
 int32_t kt_dev_alloc(size_t bytes, void** ptr);
@@ -120,6 +126,17 @@ int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
  *   out[m x N] = a . deq(W) + bias (bias fp32 [N] broadcast over rows, or NULL). */
 int32_t kt_qlinear_forward(const float* a, int32_t m, const kt_qweight* w, const float* bias,
                            float* out, void* stream);
+
+/* Several projections of the same input in one call: for i < count,
+ *   outputs[i] = (accumulate ? outputs[i] : 0) + alpha * a . deq(weights[i]) (+ biases[i]).
+ * Replaces consecutive QuantizedLinear.forwardInto calls on one input -- wQ/wK/wV in
+ * Attention.decodeInto (K/Attention.kt:220-222) and wGate/wUp in SwiGLU.forwardInto
+ * (K/SwiGLU.kt:19-25) -- with one launch per four weights when m == 1. The weights
+ * must share rows, bits and group size; columns may differ. biases may be NULL, or
+ * an array whose entries may be NULL. Asynchronous. */
+int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, int32_t count,
+                         float* const* outputs, const float* const* biases, int32_t accumulate,
+                         float alpha, void* stream);
 
 /* MatMul.multiplyByQuantizedTransposed(dy, weight, dx, m, accumulate),
  * K/MatMul.kt:954-981:  dx[m x K] = (accumulate ? dx : 0) + dy[m x N] . deq(W)^T.

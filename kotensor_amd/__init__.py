@@ -10,7 +10,7 @@ from ._lib import IllegalArgumentException, IllegalStateException, LibraryMissin
 from .device import DeviceBuffer, Stream, synchronize, device_count
 from .quantization import Quantization, QuantizedTensor
 from .matmul import MatMul, DeviceTensor
-from .linear import QuantizedLinear, projection
+from .linear import QuantizedLinear, projection, forward_into_group
 
 __all__ = [
     "IllegalArgumentException",
@@ -27,4 +27,5 @@ __all__ = [
     "DeviceTensor",
     "QuantizedLinear",
     "projection",
+    "forward_into_group",
 ]

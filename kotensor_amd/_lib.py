@@ -75,7 +75,7 @@ SIGNATURES = {
     "kt_last_error": [ctypes.c_char_p, _SZ],
     "kt_device_count": [ctypes.POINTER(_I)],
     "kt_set_device": [_I],
-    "kt_set_kernel_config": [_I, _I],
+    "kt_set_kernel_config": [_I, _I, _I, _I, _I],
     "kt_dev_alloc": [_SZ, ctypes.POINTER(_P)],
     "kt_dev_free": [_P],
     "kt_memcpy_h2d": [_P, _P, _SZ, _P],
@@ -90,6 +90,7 @@ SIGNATURES = {
     "kt_quantize": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "kt_qmatmul": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],
     "kt_qlinear_forward": [_P, _I, ctypes.POINTER(_QWeight), _P, _P, _P],
+    "kt_qmatmul_group": [_P, _I, ctypes.POINTER(_QWeight), _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _F, _P],
     "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],
     "kt_dequantize_rows": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
     "kt_dequantize_columns": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],

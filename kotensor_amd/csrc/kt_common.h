@@ -30,6 +30,10 @@ int32_t hip_fail(hipError_t err, const char* what);
 // stream are ordered by that stream, so they may reuse the same bytes. Growing it
 // waits for the stream before the old allocation is released.
 int32_t workspace(hipStream_t stream, size_t bytes, void** out);
+// The same workspace plus `count` uint32 counters that are zero on entry; a kernel
+// that takes them must leave every one at zero when it completes.
+int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters);
+constexpr size_t MAX_COUNTERS = (64 << 10) / sizeof(uint32_t);
 
 // Validated view of a kt_qweight, with the derived layout numbers.
 struct WeightView {
@@ -52,6 +56,9 @@ int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, i
                         uint8_t* q, float* s, int8_t* z, int32_t* nan_flag, hipStream_t st);
 int32_t launch_gemv(const float* a, const WeightView& w, float* c, int32_t accumulate, float alpha,
                     const float* bias, hipStream_t st);
+// One launch for up to four weights that share the input row (same K, bits, group size).
+int32_t launch_gemv_group(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                          int32_t count, int32_t accumulate, float alpha, hipStream_t st);
 int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
                     float alpha, const float* bias, hipStream_t st);
 int32_t launch_generic(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
@@ -63,8 +70,18 @@ int32_t launch_dequantize_rows(const WeightView& w, const int32_t* rows, int32_t
 int32_t launch_dequantize_columns(const WeightView& w, const int32_t* cols, int32_t count, float* out,
                                   hipStream_t st);
 
-// Forces the lane vector width and split count of the M == 1 kernel (0 = automatic).
-void set_gemv_config(int32_t vec, int32_t splits);
+// Forces the lane vector width, split count and waves per workgroup of the M == 1
+// kernel (0 = automatic).
+void set_gemv_config(int32_t vec, int32_t splits, int32_t waves);
+// How split sums are combined: 0 automatic, 1 reduction kernel, 2 inside the kernel.
+void set_gemv_reduce_mode(int32_t mode);
+
+// The MFMA GEMV for 1..16 rows: support check, launch (up to four weights sharing the
+// input) and its knobs (0 = automatic; disable routes M == 1 to the VALU GEMV).
+bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float* const* cs, const float* const* biases,
+                         int32_t count, int32_t accumulate, float alpha, hipStream_t st);
+void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t disable);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
 // otherwise the generic kernel runs.

@@ -38,13 +38,18 @@ std::map<std::pair<int, hipStream_t>, Block> g_ws;
 std::map<int, int32_t> g_cus;
 }  // namespace
 
-int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
+// Each workspace starts with a COUNTER_BYTES region of uint32 counters that is zeroed
+// when the allocation is made and that every kernel using it leaves at zero; the
+// general area follows it.
+constexpr size_t COUNTER_BYTES = 64 << 10;
+
+static int32_t ensure(hipStream_t stream, size_t bytes, Block** out) {
     int device = 0;
     KT_HIP(hipGetDevice(&device));
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block& b = g_ws[std::make_pair(device, stream)];
-    if (b.bytes < bytes) {
-        size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes + bytes / 4;
+    if (b.bytes < COUNTER_BYTES + bytes) {
+        const size_t need = COUNTER_BYTES + bytes;
+        size_t want = need < (size_t(1) << 20) ? (size_t(1) << 20) : need + need / 4;
         if (b.ptr) {
             KT_HIP(hipStreamSynchronize(stream));
             KT_HIP(hipFree(b.ptr));
@@ -52,9 +57,31 @@ int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
             b.bytes = 0;
         }
         KT_HIP(hipMalloc(&b.ptr, want));
+        KT_HIP(hipMemsetAsync(b.ptr, 0, COUNTER_BYTES, stream));
+        KT_HIP(hipStreamSynchronize(stream));
         b.bytes = want;
     }
-    *out = b.ptr;
+    *out = &b;
+    return KT_OK;
+}
+
+int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Block* b = nullptr;
+    int32_t status = ensure(stream, bytes, &b);
+    if (status) return status;
+    *out = static_cast<char*>(b->ptr) + COUNTER_BYTES;
+    return KT_OK;
+}
+
+int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters) {
+    if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Block* b = nullptr;
+    int32_t status = ensure(stream, bytes, &b);
+    if (status) return status;
+    *counters = static_cast<uint32_t*>(b->ptr);
+    *general = static_cast<char*>(b->ptr) + COUNTER_BYTES;
     return KT_OK;
 }
 
@@ -123,11 +150,19 @@ int32_t kt_set_device(int32_t device) {
     return KT_OK;
 }
 
-int32_t kt_set_kernel_config(int32_t gemv_vec, int32_t gemv_splits) {
-    if (gemv_vec != 0 && gemv_vec != 4 && gemv_vec != 8 && gemv_vec != 16)
-        return fail(KT_ERR_ARGUMENT, "gemv_vec must be 0, 4, 8 or 16, got %d", gemv_vec);
+int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits, int32_t gemv_waves,
+                             int32_t gemv_reduce) {
+    if (gemv_kind < 0 || gemv_kind > 2) return fail(KT_ERR_ARGUMENT, "gemv_kind must be 0, 1 or 2, got %d", gemv_kind);
+    if (gemv_vec != 0 && gemv_vec != 4 && gemv_vec != 8)
+        return fail(KT_ERR_ARGUMENT, "gemv_vec must be 0, 4 or 8, got %d", gemv_vec);
     if (gemv_splits < 0) return fail(KT_ERR_ARGUMENT, "gemv_splits must be >= 0, got %d", gemv_splits);
-    set_gemv_config(gemv_vec, gemv_splits);
+    if (gemv_waves != 0 && gemv_waves != 2 && gemv_waves != 4 && gemv_waves != 8)
+        return fail(KT_ERR_ARGUMENT, "gemv_waves must be 0, 2, 4 or 8, got %d", gemv_waves);
+    if (gemv_reduce < 0 || gemv_reduce > 2)
+        return fail(KT_ERR_ARGUMENT, "gemv_reduce must be 0, 1 or 2, got %d", gemv_reduce);
+    set_gemv_config(gemv_vec, gemv_splits, gemv_waves == 2 ? 4 : gemv_waves);
+    set_gemv_reduce_mode(gemv_reduce);
+    set_gemv_mfma_config(gemv_splits, gemv_waves, gemv_reduce, gemv_kind == 1);
     return KT_OK;
 }
 
@@ -260,9 +295,54 @@ static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
     if (m == 0) return KT_OK;
     if (!a || !c) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (m <= 16 && gemv_mfma_supported(a, m, v, c)) {
+        const float* biases[1] = {bias};
+        return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
+    }
     if (m == 1 && gemv_supported(a, v, c)) return launch_gemv(a, v, c, accumulate, alpha, bias, st);
     if (m > 1 && gemm_supported(a, m, v, c)) return launch_gemm(a, m, v, c, accumulate, alpha, bias, st);
     return launch_generic(a, m, v, c, accumulate, alpha, bias, st);
+}
+
+int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, int32_t count, float* const* outputs,
+                         const float* const* biases, int32_t accumulate, float alpha, void* stream) {
+    if (count < 0) return fail(KT_ERR_ARGUMENT, "Negative weight count %d", count);
+    if (count == 0) return KT_OK;
+    if (!weights || !outputs) return fail(KT_ERR_ARGUMENT, "group with a NULL weight or output array");
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    WeightView views[4];
+    for (int32_t start = 0; start < count; start += 4) {
+        const int32_t n = count - start < 4 ? count - start : 4;
+        bool fast = m == 1 && a != nullptr;
+        bool mfma = m >= 1 && m <= 16 && a != nullptr;
+        for (int32_t i = 0; i < n; ++i) {
+            int32_t status = view_weight(&weights[start + i], &views[i]);
+            if (status) return status;
+            const WeightView& v = views[i];
+            if (v.K != views[0].K || v.bits != views[0].bits || v.g != views[0].g)
+                return fail(KT_ERR_SHAPE, "grouped weights must share rows, bits and group size");
+            if (!outputs[start + i]) return fail(KT_ERR_ARGUMENT, "group output %d is NULL", start + i);
+            const float* b = biases ? biases[start + i] : nullptr;
+            fast = fast && gemv_supported(a, v, outputs[start + i]) && (!b || aligned(b, 16));
+            mfma = mfma && gemv_mfma_supported(a, m, v, outputs[start + i]);
+        }
+        if (m == 0) continue;
+        if (!a) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        int32_t status = KT_OK;
+        if (mfma) {
+            status = launch_gemv_mfma(a, m, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,
+                                      alpha, st);
+        } else if (fast) {
+            status = launch_gemv_group(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
+        } else {
+            for (int32_t i = 0; i < n && status == KT_OK; ++i)
+                status = qmatmul(a, m, &weights[start + i], outputs[start + i], accumulate, alpha,
+                                 biases ? biases[start + i] : nullptr, stream);
+        }
+        if (status) return status;
+    }
+    return KT_OK;
 }
 
 int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,

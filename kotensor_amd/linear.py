@@ -69,6 +69,22 @@ class QuantizedLinear:
         return layer
 
 
+def forward_into_group(layers, x: DeviceTensor, outs, stream: Stream | None = None):
+    """``outs[i] = x · deq(layers[i].weight) + layers[i].bias`` for projections of one input
+    (wQ/wK/wV, Attention.kt:220-222; wGate/wUp, SwiGLU.kt:19-25), one launch per four layers."""
+    from .matmul import MatMul
+
+    m, k = x.shape
+    for layer, out in zip(layers, outs):
+        if layer.in_size != k:
+            raise _lib.IllegalArgumentException(f"{k} != {layer.in_size}")
+        if out.shape != (m, layer.out_size):
+            raise _lib.IllegalArgumentException(f"out shape {list(out.shape)} != [{m}, {layer.out_size}]")
+    MatMul.multiply_quantized_group(x, [l.weight for l in layers], outs, m, accumulate=False, alpha=1.0,
+                                    biases=[l.bias for l in layers], stream=stream)
+    return outs
+
+
 def projection(in_size: int, out_size: int, quantization: Quantization | None):
     """QuantizedLinear.kt:44-46 (only the quantized branch lives on the device)."""
     if quantization is None:

@@ -104,6 +104,32 @@ class MatMul:
                   ctypes.c_float(alpha), (stream or default_stream()).handle)
 
     @staticmethod
+    def multiply_quantized_group(a, weights, outputs, m: int, accumulate: bool = False, alpha: float = 1.0,
+                                 biases=None, stream: Stream | None = None) -> None:
+        """Several projections of one input in one call (kt_qmatmul_group): for each i,
+        ``outputs[i] = (accumulate ? outputs[i] : 0) + alpha * a · deq(weights[i]) (+ biases[i])``.
+        The weights must share rows, bits and group size (q/k/v, gate/up)."""
+        count = len(weights)
+        if count != len(outputs) or (biases is not None and len(biases) != count):
+            raise _lib.IllegalArgumentException("weights, outputs and biases differ in length")
+        if count == 0:
+            return
+        k = weights[0].rows
+        na = _nbytes(a)
+        if na is not None and na < m * k * 4:
+            raise _lib.IllegalArgumentException(f"a has {na // 4} elements, needs {m} × {k}")
+        for w, c in zip(weights, outputs):
+            nc = _nbytes(c)
+            if nc is not None and nc < m * w.columns * 4:
+                raise _lib.IllegalArgumentException(f"output has {nc // 4} elements, needs {m} × {w.columns}")
+        structs = (_lib.QWeight * count)(*[w.qweight for w in weights])
+        outs = (ctypes.c_void_p * count)(*[_ptr(c) for c in outputs])
+        bias_arr = None if biases is None else (ctypes.c_void_p * count)(
+            *[None if b is None else _ptr(b) for b in biases])
+        _lib.call("kt_qmatmul_group", _ptr(a), int(m), structs, count, outs, bias_arr, int(bool(accumulate)),
+                  ctypes.c_float(alpha), (stream or default_stream()).handle)
+
+    @staticmethod
     def multiply_by_quantized_transposed(dy, weight: QuantizedTensor, dx, m: int, accumulate: bool = True,
                                          stream: Stream | None = None) -> None:
         """``dx[m x K] = (accumulate ? dx : 0) + dy[m x N] · deq(W)^T``, MatMul.kt:954-981."""
@@ -119,6 +145,8 @@ class MatMul:
                   int(bool(accumulate)), (stream or default_stream()).handle)
 
     @staticmethod
-    def set_kernel_config(gemv_vec: int = 0, gemv_splits: int = 0) -> None:
-        """Work-split knobs of the M == 1 kernel (the counterpart of MatMul.kt:30-82's knobs)."""
-        _lib.call("kt_set_kernel_config", int(gemv_vec), int(gemv_splits))
+    def set_kernel_config(gemv_kind: int = 0, gemv_vec: int = 0, gemv_splits: int = 0, gemv_waves: int = 0,
+                          gemv_reduce: int = 0) -> None:
+        """Work-split knobs of the small-M kernels (the counterpart of MatMul.kt:30-82's knobs)."""
+        _lib.call("kt_set_kernel_config", int(gemv_kind), int(gemv_vec), int(gemv_splits), int(gemv_waves),
+                  int(gemv_reduce))

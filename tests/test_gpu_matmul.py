@@ -145,14 +145,21 @@ def test_gemv_work_splits_agree(kt, oracle_lib):
             qt = upload_quantized(kt, q)
             x = rng.standard_normal((1, k), dtype=np.float32)
             want = oracle_lib.multiply_quantized(x, q, 1)
-            for vec in (4, 8, 16):
-                for splits in (1, 2, 3, 5, q.groups):
-                    banner("split", k, n, bits, vec, splits)
-                    kt.MatMul.set_kernel_config(vec, splits)
-                    got = gpu_matmul(kt, x, qt, 1)
-                    assert normwise_rel(got, want) <= 1e-5, (vec, splits)
+            configs = [(1, vec, waves, splits, reduce) for vec in (4, 8) for waves in (4, 8)
+                       for splits in (1, 2, 3, 5, q.groups) for reduce in (1, 2)]
+            configs += [(2, 0, waves, splits, reduce) for waves in (2, 4, 8) for splits in (1, 2, 3, 5, q.groups)
+                        for reduce in (1, 2)]
+            for kind, vec, waves, splits, reduce in configs:
+                banner("split", k, n, bits, kind, vec, waves, splits, reduce)
+                kt.MatMul.set_kernel_config(kind, vec, splits, waves, reduce)
+                got = gpu_matmul(kt, x, qt, 1)
+                # the VALU kernel accumulates in fp32 like the reference; the MFMA kernel
+                # within the product tolerance
+                assert normwise_rel(got, want) <= (1e-5 if kind == 1 else TOL), (kind, vec, waves, splits, reduce)
+                # the in-kernel reduction leaves its counters at zero: a repeat agrees
+                assert same_bits(got, gpu_matmul(kt, x, qt, 1))
     finally:
-        kt.MatMul.set_kernel_config(0, 0)
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
 
 def test_quantized_linear_forward_with_bias(kt, oracle_lib):
@@ -170,6 +177,34 @@ def test_quantized_linear_forward_with_bias(kt, oracle_lib):
         assert normwise_rel(out, want) <= TOL
         # the device weight is the reference's quantization of w, bit for bit
         assert same_bits(layer.weight.qdata.view(np.uint8), q.qdata)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_grouped_projections(kt, oracle_lib, m):
+    """kt_qmatmul_group: q/k/v and gate/up of one input in one call, with biases."""
+    rng = np.random.default_rng(17)
+    for (k, ns, bits, g) in [(896, (896, 128, 128), 4, 64), (896, (4864, 4864), 4, 64), (2048, (2048, 512, 512), 8, 64),
+                             (256, (64, 72, 1024, 8, 16), 4, 32)]:
+        banner("group", m, k, ns, bits, g)
+        qs = [_weights(oracle_lib, k, n, bits, g, 20 + i, std=0.02) for i, n in enumerate(ns)]
+        qts = [upload_quantized(kt, q) for q in qs]
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        biases = [rng.standard_normal(n).astype(np.float32) for n in ns]
+        outs = [kt.DeviceBuffer.from_numpy(np.full((m, n), 3.0, np.float32)) for n in ns]
+        dbias = [kt.DeviceBuffer.from_numpy(b) for b in biases]
+        kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(x), qts, outs, m, accumulate=True, alpha=0.75,
+                                           biases=dbias)
+        kt.synchronize()
+        for q, o, b, n in zip(qs, outs, biases, ns):
+            got = o.download(np.float32).reshape(m, n)
+            want = oracle_lib.multiply_quantized(x, q, m, c=np.full((m, n), 3.0, np.float32), accumulate=True,
+                                                 alpha=0.75) + b[None, :]
+            assert normwise_rel(got, want) <= TOL
+    with pytest.raises(kt.IllegalArgumentException):
+        a = _weights(oracle_lib, 64, 64, 4, 64, 1)
+        b = _weights(oracle_lib, 128, 64, 4, 64, 1)
+        kt.MatMul.multiply_quantized_group(kt.DeviceBuffer(128 * 4), [upload_quantized(kt, a), upload_quantized(kt, b)],
+                                           [kt.DeviceBuffer(256), kt.DeviceBuffer(256)], 1)
 
 
 def test_unaligned_operands_take_the_generic_kernel(kt, oracle_lib):
