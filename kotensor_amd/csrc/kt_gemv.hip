@@ -111,11 +111,12 @@ __global__ void __launch_bounds__(64 * WAVES)
     __shared__ float red[WAVES][NC][64];
 
     // Select the job (scalar: blockIdx is uniform).
-    int32_t ji = 0;
+    // The job of this block: every job is read at a constant kernarg offset and selected,
+    // so the scalar loads go out together instead of after a first dependent load.
+    Job jb = jobs.job[0];
 #pragma unroll
     for (int j = 1; j < MAX_JOBS; ++j)
-        if (j < jobs.count && static_cast<int32_t>(blockIdx.x) >= jobs.job[j].block_begin) ji = j;
-    const Job& jb = jobs.job[ji];
+        if (j < jobs.count && static_cast<int32_t>(blockIdx.x) >= jobs.job[j].block_begin) jb = jobs.job[j];
     const uint8_t* __restrict__ q = jb.q;
     const int32_t N = jb.N, bpr = jb.bpr, half = jb.bpr;
     const int32_t local = blockIdx.x - jb.block_begin;

@@ -1,27 +1,34 @@
-// kt_gemv_mfma.hip -- decode dequant-GEMV for M = 1..16 rows on gfx950 MFMA:
+// kt_gemv_mfma.hip -- decode dequant-GEMV for M = 1, 2 rows on gfx950 MFMA:
 //   c[M x N] = (accumulate ? c : 0) + alpha * x[M x K] . deq(W) (+ bias),
 // the small-M case of MatMul.multiplyQuantized (Engine/kotensor/src/main/kotlin/
 // MatMul.kt:460-486; M == 1 is multiplyQuantizedRow :494-536).
 //
-// The weights stream from HBM once, in the reference layout. The MFMA unit does the
-// multiply-adds, so the vector ALU only unpacks (about one instruction per weight):
+// The weights stream from HBM once, in the reference layout, and the matrix cores do
+// all multiply-adds exactly, so the vector ALU spends under one instruction per weight:
 //
 //   * v_mfma_f32_16x16x32_f16: lane l holds B[k = 8*(l/16) + i][n = l%16], i < 8. A lane
-//     (cl = l%16, kb = l/16) loads rows r0 + 8*kb + i of an 8-byte column strip, so its
-//     registers already hold, for each byte j of the strip, the 8 k-values of one
-//     column -- a B fragment. 16 lanes cover 128 contiguous bytes of a row (one cache
-//     line); a chunk is 32 rows (4 k-blocks);
-//   * a weight becomes an exact fp16 without arithmetic: v_perm_b32 puts the byte j of
-//     two consecutive rows into the low bytes of the two fp16 halves and a mask keeps
-//     the nibble, giving the fp16 subnormal q * 2^-24 (low nibble), 16*q * 2^-24 (high
-//     nibble) or, for INT8 after xor 0x80, (q + 128) * 2^-24 (bias folded into the zero);
-//   * x is split into fp16 hi + lo parts after an exact power-of-two scaling per row
-//     (largest |x| of the workgroup's K-range in [2^14, 2^15)), about 22 significant
-//     bits; A_hi and A_lo both multiply the same B into one fp32 accumulator;
-//   * rowSum for the zero-point term comes from the same MFMA against a constant B of
-//     2^-24 (one extra pair of MFMAs per chunk), in exactly the units of the weights';
-//   * per quantization group: res += scale * (acc - zero * rowSum) (the reference's
-//     combineGroup form), then one exact power-of-two factor per row at the end;
+//     (cl = l%16, kb = l/16) loads rows r0 + 8*kb + i of an 8-byte column strip, so for
+//     each byte j of the strip its registers hold the 8 k-values of one column. 16 lanes
+//     cover 128 contiguous bytes of a row; a chunk is 32 rows;
+//   * weight bytes become fp16 in two instructions per pair of k-values: v_perm_b32
+//     puts byte j of two consecutive rows into the low bytes of the two halves and an
+//     and-or keeps the nibble under the exponent of 1024, giving the exact integers
+//     1024 + q (low nibble), 1024 + 16q (high nibble) or, INT8 bytes biased by 128,
+//     1152 + q;
+//   * the constant 1024 (1152) and the zero point are removed exactly through the
+//     accumulator: per quantization group, x is split into three fp16 parts on fixed
+//     grids (hi + mid + lo, 2^13 / g steps each, about 21 bits below the group's
+//     largest |x|, which is scaled into [2^14, 2^15)), each part is an A row, and each
+//     accumulator starts the group at -(1024 + zero) * sum(part). Every partial sum of
+//     the group is then an fp32 integer multiple of the part's grid with at most 24
+//     bits, so the MFMA results are exact: sum(part * (q - zero)) per part;
+//   * for M == 1 the 16 A rows hold four copies of the three parts in four row blocks;
+//     the MFMA for column u uses block u % 4 only, so its result lands in lane group
+//     u % 4 and four MFMAs share one accumulator. The per-group combine
+//     res += scale * 2^e * (hi + mid + lo) then runs on all 64 lanes, four columns each
+//     (two blocks of two x rows for M == 2);
+//   * every wave prepares the x of its own groups in its own LDS area before its
+//     weight loads, then keeps NB chunks (16 KB) of weight loads in flight;
 //   * a workgroup is WAVES waves on one 128-byte column strip; its waves take the
 //     groups of its K-slice round-robin and meet through LDS in a fixed order; K-slices
 //     of one strip meet through the in-kernel counter reduction of kt_gemv.hip's
@@ -38,6 +45,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int MAX_JOBS = 4;
 constexpr int CHUNK = 32;  // rows per MFMA k-step (4 lanes groups x 8 rows)
 constexpr int STRIP = 128; // bytes of a row per wave (16 lanes x 8 bytes)
+constexpr int NB = 4;      // chunks of weight loads in flight per wave
+constexpr int MAX_M = 2;   // x rows: three parts (and a zero row) of each take 4 A rows
+constexpr int XB = 4;      // groups of x loaded per batch
 
 struct Job {
     const uint8_t* q;
@@ -47,7 +57,7 @@ struct Job {
     const float* bias;
     float* partials;     // [slices x M x N] or nullptr
     uint32_t* counters;  // [tiles] for the in-kernel slice reduction, or nullptr
-    int32_t N, bpr, tiles, slices, groups_per_slice, block_begin;
+    int32_t N, bpr, tiles, slices, groups_per_slice;
 };
 
 struct Jobs {
@@ -64,28 +74,82 @@ __device__ __forceinline__ uint32_t pair_bytes(uint32_t a, uint32_t b, int j) {
     return __builtin_amdgcn_perm(b, a, sel);
 }
 
-// R: rows per lane of the 16x16 result (min(M, 4)); WAVES per workgroup.
-template <int BITS, int R, int WAVES, bool ZP>
-__global__ void __launch_bounds__(64 * WAVES)
-    gemv_mfma_kernel(const float* __restrict__ x, int32_t M, int32_t K, int32_t g, Jobs jobs, float alpha,
-                     int32_t accumulate) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    constexpr int NCOL = BITS == 4 ? 16 : 8;  // columns per lane
+// A constant the compiler keeps in a VGPR: (v & mask) | bits and (v ^ a) + b with such
+// operands become one v_and_or_b32 / v_xad_u32 each instead of two instructions with
+// literals. Only vector ALU instructions read the result.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+    return r;
+}
 
-    int32_t ji = 0;
+// Max (or sum) over the SEG lanes of a segment (32 or 64), in every lane: a DPP
+// butterfly inside each 16-lane row (quad swaps, then half-row and row mirrors), then
+// the four row results through scalar registers. The values reduced here are exact
+// (maxima, or sums of numbers on one fixed-point grid), so the order does not matter.
+template <bool MAX>
+__device__ __forceinline__ float dpp_step(float v, int ctrl_tag) {
+    int o = 0;
+    switch (ctrl_tag) {  // dpp_ctrl must be a constant
+        case 0: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad [1,0,3,2]
+        case 1: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad [2,3,0,1]
+        case 2: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        default: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
+    }
+    return MAX ? fmaxf(v, __int_as_float(o)) : v + __int_as_float(o);
+}
+template <int SEG, bool MAX>
+__device__ __forceinline__ float segment_reduce(float v, int32_t ln) {
 #pragma unroll
-    for (int j = 1; j < MAX_JOBS; ++j)
-        if (j < jobs.count && static_cast<int32_t>(blockIdx.x) >= jobs.job[j].block_begin) ji = j;
-    const Job& jb = jobs.job[ji];
-    const uint8_t* __restrict__ q = jb.q;
+    for (int i = 0; i < 4; ++i) v = dpp_step<MAX>(v, i);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    const float a = MAX ? fmaxf(r0, r1) : r0 + r1;
+    const float b = MAX ? fmaxf(r2, r3) : r2 + r3;
+    if (SEG == 64) return MAX ? fmaxf(a, b) : a + b;
+    return ln < 32 ? a : b;
+}
+
+// Scales and zero points of one quantization group for a lane's NACC columns.
+template <int NACC>
+struct GroupScales {
+    float s[NACC];
+    int32_t z[NACC];
+};
+
+// MP: x rows per A row block (1 or 2; M <= MP); CPG: 32-row chunks per group.
+template <int BITS, int MP, int WAVES, int CPG, bool ZP>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+    gemv_mfma_kernel(const float* __restrict__ x, int32_t M, int32_t K, Jobs jobs, int32_t wave_groups,
+                     float alpha, int32_t accumulate) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int g = CPG * CHUNK;
+    constexpr int NCOL = BITS == 4 ? 16 : 8;  // columns per lane strip: (byte, nibble) pairs
+    constexpr int NR = 4 / MP;                 // A row blocks
+    constexpr int NACC = NCOL / NR;            // accumulators (columns) per lane
+    constexpr float OFF = BITS == 4 ? 1024.0f : 1152.0f;
+    // fixed-point parts: P steps each; grids 2^15 / P, 2^15 / P^2, 2^15 / P^3
+    constexpr int P = 8192 / g;
+    constexpr float GRID0 = 32768.0f / P, GRID1 = GRID0 / P, GRID2 = GRID1 / P;
+    static_assert(NB % CPG == 0, "a ring of NB chunks holds whole groups");
+
+    // The job is blockIdx.y: its fields load at an offset known at wave start. The empty
+    // asm takes every argument the kernel uses, so all scalar loads go out in one round
+    // instead of one round per use; then blocks past the job's own count leave.
+    Job jb = jobs.job[blockIdx.y];
+    asm volatile("" ::"s"(jb.q), "s"(jb.s), "s"(jb.z), "s"(jb.out), "s"(jb.bias), "s"(jb.partials), "s"(jb.counters),
+                 "s"(jb.N), "s"(jb.bpr), "s"(jb.tiles), "s"(jb.slices), "s"(jb.groups_per_slice), "s"(x), "s"(M), "s"(K),
+                 "s"(wave_groups), "s"(alpha), "s"(accumulate));
+    const int32_t local = blockIdx.x;
+    if (local >= jb.tiles * jb.slices) return;
     const int32_t N = jb.N, bpr = jb.bpr, half = jb.bpr;
-    const int32_t local = blockIdx.x - jb.block_begin;
     const int32_t tile = local % jb.tiles;
     const int32_t slice = local / jb.tiles;
     const int32_t G = K / g;
     const int32_t g_begin = slice * jb.groups_per_slice;
     const int32_t g_end = min(g_begin + jb.groups_per_slice, G);
-    const int32_t ra = g_begin * g, nrows = (g_end - g_begin) * g;
 
     const int32_t t = threadIdx.x;
     const int32_t ln = t & 63;
@@ -95,250 +159,291 @@ __global__ void __launch_bounds__(64 * WAVES)
     const bool active = col_off < bpr;
     const int32_t boff = active ? col_off : 0;  // lanes past the row end compute and discard
 
-    // ---- x in LDS as fp16 hi/lo, per-row exponent ---------------------------------
-    _Float16* xh = reinterpret_cast<_Float16*>(smem);
-    _Float16* xl = xh + M * nrows;
-    uint32_t* amax = reinterpret_cast<uint32_t*>(xl + M * nrows);  // [16]
-    if (t < 16) amax[t] = 0u;
-    __syncthreads();
-    for (int32_t idx = t; idx < M * nrows; idx += 64 * WAVES) {
-        const int32_t m = idx / nrows, k = idx - m * nrows;
-        const float v = x[static_cast<size_t>(m) * K + ra + k];
-        atomicMax(&amax[m], __float_as_uint(fabsf(v)));
-    }
-    __syncthreads();
-    for (int32_t idx = t; idx < M * nrows; idx += 64 * WAVES) {
-        const int32_t m = idx / nrows, k = idx - m * nrows;
-        const float mx = __uint_as_float(amax[m]);
-        int e = 0;
-        if (mx > 0.0f && isfinite(mx)) {
-            frexpf(mx, &e);
-            e -= 15;
-        }
-        const float v = ldexpf(x[static_cast<size_t>(m) * K + ra + k], -e);
-        const _Float16 h = static_cast<_Float16>(v);
-        xh[idx] = h;
-        xl[idx] = static_cast<_Float16>(v - static_cast<float>(h));
-    }
-    __syncthreads();
-
-    // Per result row (m = 4*kb + i): the power of two that undoes the x scaling, read now
-    // because the final reduction reuses this LDS.
-    float rowf[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const int32_t m = 4 * kb + i;
-        int e = 0;
-        const float mx = m < M ? __uint_as_float(amax[m]) : 0.0f;
-        if (mx > 0.0f && isfinite(mx)) {
-            frexpf(mx, &e);
-            e -= 15;
-        }
-        rowf[i] = ldexpf(1.0f, e);
-    }
-
-    // ---- main loop: this wave's groups, chunk by chunk, double-buffered ---------------
-    // res[c][i]: column c of this lane, result row m = 4*kb + i.
-    float res[NCOL][R];
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c)
-#pragma unroll
-        for (int i = 0; i < R; ++i) res[c][i] = 0.0f;
-
-    const int32_t chunks_per_group = g / CHUNK;
+    // This wave's quantization groups: g_begin + wave + k * WAVES, k < my_groups.
     const int32_t my_groups = g_end - g_begin > wave ? (g_end - g_begin - wave + WAVES - 1) / WAVES : 0;
-    const int32_t my_chunks = my_groups * chunks_per_group;
-    // k-th chunk of this wave -> absolute row of its first line
-    auto chunk_row = [&](int32_t c) {
-        const int32_t gg = c / chunks_per_group;
-        return (g_begin + wave + gg * WAVES) * g + (c - gg * chunks_per_group) * CHUNK;
-    };
-    auto load = [&](uint2* v, int32_t c) {
-        const int32_t r = chunk_row(c) + 8 * kb;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint2*>(q + static_cast<size_t>(r + i) * bpr + boff);
-    };
-    const u32x4 ones = {0x00010001u, 0x00010001u, 0x00010001u, 0x00010001u};  // fp16 2^-24 in every half
-    f32x4 acc[NCOL];
-    f32x4 racc;
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    racc = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int32_t my_chunks = my_groups * CPG;
 
-    auto compute = [&](const uint2* v, int32_t c) {
-        // A fragments: x rows m = cl (zero for m >= M), k = chunk rows 8*kb .. 8*kb+7.
-        const int32_t krow = chunk_row(c) - ra + 8 * kb;
-        half8 ah = {}, al = {};
-        if (cl < M) {
-            ah = *reinterpret_cast<const half8*>(xh + cl * nrows + krow);
-            al = *reinterpret_cast<const half8*>(xl + cl * nrows + krow);
-        }
-        racc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, as_half8(ones), racc, 0, 0, 0);
-        racc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, as_half8(ones), racc, 0, 0, 0);
+    // The wave's LDS area: parts [wave_groups][M][4][g] fp16 (hi, mid, lo, zeros), then
+    // [wave_groups][M] x {sum hi, sum mid, sum lo, 2^e}.
+    const int32_t parts_bytes = wave_groups * M * 8 * g;
+    const int32_t xw_bytes = parts_bytes + wave_groups * M * 16;
+    _Float16* xs = reinterpret_cast<_Float16*>(smem + wave * xw_bytes);
+    float4* sums = reinterpret_cast<float4*>(smem + wave * xw_bytes + parts_bytes);
+
+    // A role of this lane (A row cl): block cl / (4 MP), x row (cl / 4) % MP, part cl % 4.
+    const int32_t a_block = cl / (4 * MP);
+    const int32_t a_row = (cl >> 2) % MP;
+    const int32_t a_part = a_row < M ? (cl & 3) : 3;  // rows past M read the zero part
+    const int32_t a_off = ((a_row < M ? a_row : 0) * 4 + a_part) * g + 8 * kb;
+    // D role (result rows 4 kb .. 4 kb + 3): block kb / MP, x row kb % MP, part i.
+    const int32_t d_block = kb / MP;
+    const int32_t d_row = kb % MP;
+    const int32_t d_row_c = d_row < M ? d_row : 0;
+    // Accumulator a holds column u = a * NR + d_block: byte u & 7, high nibble if u >= 8.
+    int32_t col[NACC];
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {  // dword of the 8-byte strip
-            // B fragments of the dword's 4 byte columns first, then the hi products of all
-            // of them, then the lo ones: consecutive MFMAs write different accumulators.
-            u32x4 p[4];
+    for (int a = 0; a < NACC; ++a) {
+        const int u = a * NR + d_block;
+        col[a] = (u >= 8 ? half : 0) + boff + (u & 7);
+    }
+
+    float res[NACC];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
+    for (int a = 0; a < NACC; ++a) res[a] = 0.0f;
+    const uint32_t mask_lo = in_vgpr(0x000F000Fu), mask_hi = in_vgpr(0x00F000F0u);
+    const uint32_t flip = in_vgpr(0x00800080u), exp1024 = in_vgpr(0x64006400u);
+
+    if (my_groups > 0) {
+        // ---- x of this wave's groups as fixed-point fp16 parts ------------------------
+        // The first batch of x loads goes out before the weight loads (a wave's loads
+        // return in order), the parts are made while the weights are in flight.
+        constexpr int SEG = CPG >= 2 ? 64 : 32;       // lanes per group
+        constexpr int VPL = CPG >= 2 ? CPG / 2 : 1;   // x values per lane per group and row
+        constexpr int GPI = 64 / SEG;                 // groups per wave instruction
+        const int32_t sub = SEG == 32 ? (ln >> 5) : 0;
+        const int32_t kk0 = ln & (SEG - 1);
+        float xv[XB][MP][VPL];
+        auto load_x = [&](int32_t k0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    uint32_t a = w ? v[2 * i].y : v[2 * i].x;
-                    uint32_t b = w ? v[2 * i + 1].y : v[2 * i + 1].x;
-                    if (BITS == 8) {
-                        a ^= 0x80808080u;
-                        b ^= 0x80808080u;
+            for (int b = 0; b < XB; ++b) {
+                int32_t k = k0 + b * GPI + sub;
+                k = k < my_groups ? k : my_groups - 1;
+                const float* px = x + static_cast<size_t>(g_begin + wave + k * WAVES) * g + kk0;
+#pragma unroll
+                for (int m = 0; m < MP; ++m)
+#pragma unroll
+                    for (int v = 0; v < VPL; ++v) xv[b][m][v] = px[static_cast<size_t>(m < M ? m : 0) * K + 64 * v];
+            }
+        };
+        // Every loaded slot is processed (slots past my_groups only skip their stores):
+        // a conditional use would let the compiler sink the slot's load behind the
+        // weight loads, and waiting for it would then wait for all of them.
+        auto prep_x = [&](int32_t k0) {
+#pragma unroll
+            for (int b = 0; b < XB; ++b) {
+                const int32_t k = k0 + b * GPI + sub;
+#pragma unroll
+                for (int m = 0; m < MP; ++m) {  // MP == M
+                    float mx = 0.0f;
+#pragma unroll
+                    for (int v = 0; v < VPL; ++v) mx = fmaxf(mx, fabsf(xv[b][m][v]));
+                    mx = segment_reduce<SEG, true>(mx, ln);
+                    int e = 0;
+                    if (mx > 0.0f && mx <= 3.402823466e38f) {
+                        frexpf(mx, &e);
+                        e -= 15;
                     }
-                    p[jj][i] = pair_bytes(a, b, jj);
-                }
+                    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+                    _Float16* dst = xs + (k * M + m) * 4 * g + kk0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const half8 xa = h ? al : ah;
+                    for (int v = 0; v < VPL; ++v) {
+                        const float xp = ldexpf(xv[b][m][v], -e);
+                        const float hi = rintf(xp * (1.0f / GRID0)) * GRID0;
+                        const float r1 = xp - hi;
+                        const float mid = rintf(r1 * (1.0f / GRID1)) * GRID1;
+                        const float lo = rintf((r1 - mid) * (1.0f / GRID2)) * GRID2;
+                        s0 += hi;
+                        s1 += mid;
+                        s2 += lo;
+                        if (k < my_groups) {
+                            dst[64 * v] = static_cast<_Float16>(hi);
+                            dst[g + 64 * v] = static_cast<_Float16>(mid);
+                            dst[2 * g + 64 * v] = static_cast<_Float16>(lo);
+                            dst[3 * g + 64 * v] = static_cast<_Float16>(0.0f);
+                        }
+                    }
+                    s0 = segment_reduce<SEG, false>(s0, ln);
+                    s1 = segment_reduce<SEG, false>(s1, ln);
+                    s2 = segment_reduce<SEG, false>(s2, ln);
+                    if (k < my_groups && kk0 == 0) sums[k * M + m] = make_float4(s0, s1, s2, ldexpf(1.0f, e));
+                }
+            }
+        };
+        load_x(0);
+        __builtin_amdgcn_sched_barrier(0);  // the x loads go out first: they are waited for first
+
+        // ---- weight loads: NB chunks in flight -------------------------------------
+        uint32_t roff[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) roff[i] = static_cast<uint32_t>((8 * kb + i) * bpr + boff);
+        auto chunk_base = [&](int32_t c) {
+            const int32_t k = c / CPG, cc = c - k * CPG;
+            return jb.q + static_cast<size_t>((g_begin + wave + k * WAVES) * g + cc * CHUNK) * bpr;
+        };
+        auto load = [&](uint2* v, int32_t c) {
+            const uint8_t* base = chunk_base(c < my_chunks ? c : my_chunks - 1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint2*>(base + roff[i]);
+        };
+        uint2 buf[NB][8];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(buf[b], b);
+
+        auto load_scales = [&](int32_t k) {
+            GroupScales<NACC> sc;
+            const size_t gi = static_cast<size_t>(g_begin + wave + k * WAVES);
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                sc.s[a] = jb.s[gi * N + col[a]];
+                sc.z[a] = ZP ? static_cast<int32_t>(jb.z[gi * N + col[a]]) : 0;
+            }
+            return sc;
+        };
+        // Scales of the next SR groups are in flight with the weights (slot = group % SR).
+        constexpr int SR = NB / CPG >= 2 ? 2 : 1;
+        GroupScales<NACC> scales[SR];
+#pragma unroll
+        for (int i = 0; i < SR; ++i) scales[i] = load_scales(i < my_groups ? i : my_groups - 1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        prep_x(0);
+        for (int32_t k0 = XB * GPI; k0 < my_groups; k0 += XB * GPI) {
+            load_x(k0);
+            prep_x(k0);
+        }
+
+        // ---- main loop --------------------------------------------------------------
+        f32x4 acc[NACC];
+        // Accumulators start group k at -(OFF + zero) * sum(part) for D rows (parts) 0..2.
+        auto start_group = [&](int32_t k, const GroupScales<NACC>& gs) {
+            const float4 sm = sums[k * M + d_row_c];
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                const int u = a * NR + d_block;
+                const float zs = (BITS == 4 && u >= 8) ? 16.0f : 1.0f;
+                const float off = -(OFF + zs * static_cast<float>(gs.z[a]));
+                acc[a] = f32x4{off * sm.x, off * sm.y, off * sm.z, 0.0f};
+            }
+        };
+        auto compute = [&](const uint2* v, int32_t c) {
+            const int32_t k = c / CPG, cc = c - k * CPG;
+            const half8 a = *reinterpret_cast<const half8*>(xs + k * M * 4 * g + a_off + cc * CHUNK);
+            half8 ab[NR];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) ab[r] = a_block == r ? a : half8{};
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {  // dword of the 8-byte strip
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
                     const int j = 4 * w + jj;
+                    u32x4 p;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        p[i] = pair_bytes(w ? v[2 * i].y : v[2 * i].x, w ? v[2 * i + 1].y : v[2 * i + 1].x, jj);
                     if (BITS == 8) {
-                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, as_half8(p[jj]), acc[j], 0, 0, 0);
+                        u32x4 bq;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) bq[i] = (p[i] ^ flip) + exp1024;  // 1152 + q
+                        acc[j / NR] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ab[j % NR], as_half8(bq), acc[j / NR], 0, 0, 0);
                     } else {
-                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, as_half8(p[jj] & 0x000F000Fu), acc[j], 0, 0, 0);
-                        acc[8 + j] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, as_half8(p[jj] & 0x00F000F0u), acc[8 + j], 0, 0, 0);
+                        u32x4 blo, bhi;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            blo[i] = (p[i] & mask_lo) | exp1024;  // 1024 + q
+                            bhi[i] = (p[i] & mask_hi) | exp1024;  // 1024 + 16 q
+                        }
+                        acc[j / NR] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ab[j % NR], as_half8(blo), acc[j / NR], 0, 0, 0);
+                        acc[(8 + j) / NR] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(ab[(8 + j) % NR], as_half8(bhi), acc[(8 + j) / NR], 0, 0, 0);
                     }
                 }
             }
-        }
-    };
-    // res += scale * (acc - zero * rowSum) for group gi; then clear the accumulators.
-    auto combine = [&](int32_t gi) {
-        const float* srow = jb.s + static_cast<size_t>(gi) * N;
-        float sc[NCOL];
-        int32_t zr[NCOL];
+        };
+        // res += scale * 2^e * (hi + mid + lo) of local group k.
+        auto combine = [&](int32_t k, const GroupScales<NACC>& gs) {
+            const float f = sums[k * M + d_row_c].w;
 #pragma unroll
-        for (int side = 0; side < NCOL / 8; ++side) {
-            const int32_t col = (side ? half : 0) + boff;
-            const float4 s0 = *reinterpret_cast<const float4*>(srow + col);
-            const float4 s1 = *reinterpret_cast<const float4*>(srow + col + 4);
-            sc[8 * side + 0] = s0.x; sc[8 * side + 1] = s0.y; sc[8 * side + 2] = s0.z; sc[8 * side + 3] = s0.w;
-            sc[8 * side + 4] = s1.x; sc[8 * side + 5] = s1.y; sc[8 * side + 6] = s1.z; sc[8 * side + 7] = s1.w;
-            uint2 zz = make_uint2(0u, 0u);
-            if constexpr (ZP) zz = *reinterpret_cast<const uint2*>(jb.z + static_cast<size_t>(gi) * N + col);
-#pragma unroll
-            for (int b = 0; b < 8; ++b)
-                zr[8 * side + b] = static_cast<int8_t>(((b < 4 ? zz.x : zz.y) >> (8 * (b & 3))) & 0xFFu);
-        }
-#pragma unroll
-        for (int c = 0; c < NCOL; ++c) {
-            // low nibble / INT8 columns: acc and rowSum in units of 2^-24; high nibble
-            // columns carry an extra 16 in acc, matched by 16 * zero.
-            float zf = static_cast<float>(zr[c]) + (BITS == 8 ? 128.0f : 0.0f);
-            if (BITS == 4 && c >= 8) zf *= 16.0f;
-#pragma unroll
-            for (int i = 0; i < R; ++i) res[c][i] = fmaf(sc[c], fmaf(-zf, racc[i], acc[c][i]), res[c][i]);
-            acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        racc = f32x4{0.f, 0.f, 0.f, 0.f};
-    };
+            for (int a = 0; a < NACC; ++a) {
+                const int u = a * NR + d_block;
+                const float sc = (BITS == 4 && u >= 8) ? gs.s[a] * 0.0625f : gs.s[a];
+                res[a] = fmaf(sc * f, (acc[a][0] + acc[a][1]) + acc[a][2], res[a]);
+            }
+        };
 
-    if (my_chunks > 0) {
-        uint2 va[8], vb[8];
-        load(va, 0);
-        int32_t c = 0;
-        for (;;) {
-            load(vb, c + 1 < my_chunks ? c + 1 : c);
-            compute(va, c);
-            if ((c + 1) % chunks_per_group == 0) combine(g_begin + wave + (c / chunks_per_group) * WAVES);
-            if (++c >= my_chunks) break;
-            load(va, c + 1 < my_chunks ? c + 1 : c);
-            compute(vb, c);
-            if ((c + 1) % chunks_per_group == 0) combine(g_begin + wave + (c / chunks_per_group) * WAVES);
-            if (++c >= my_chunks) break;
-        }
-    }
-
-    // ---- waves of the workgroup meet in LDS (reusing the x area), in wave order ---------
-    // Results are in units of 2^-24 (low nibble, INT8) or 2^-20 (high nibble) times 2^-e_m.
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);  // [64 lanes][NCOL][R]
-    for (int w = 0; w < WAVES; ++w) {
-        if (wave == w) {
+        start_group(0, scales[0]);
+        for (int32_t c0 = 0; c0 < my_chunks; c0 += NB) {
 #pragma unroll
-            for (int c = 0; c < NCOL; ++c)
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    float* slot = red + (ln * NCOL + c) * R + i;
-                    *slot = w == 0 ? res[c][i] : *slot + res[c][i];
+            for (int b = 0; b < NB; ++b) {
+                const int32_t c = c0 + b;
+                if (c < my_chunks) {
+                    compute(buf[b], c);
+                    if (b % CPG == CPG - 1) {
+                        const int32_t k = c / CPG;  // k % SR == (b / CPG) % SR: NB / CPG is a multiple of SR
+                        const int slot = (b / CPG) % SR;  // a constant once the loop is unrolled
+                        const int next = (slot + 1) % SR;
+                        combine(k, scales[slot]);
+                        scales[slot] = load_scales(k + SR < my_groups ? k + SR : my_groups - 1);
+                        if (k + 1 < my_groups) start_group(k + 1, scales[next]);
+                    }
                 }
+                load(buf[b], c + NB);
+            }
         }
-        __syncthreads();
     }
+
+    // ---- waves of the workgroup meet in LDS (reusing the x areas), in wave order -------
+    float* red = reinterpret_cast<float*>(smem);  // [WAVES - 1][NACC][64 lanes]
+    __syncthreads();
+    if (wave > 0)
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) red[((wave - 1) * NACC + a) * 64 + ln] = res[a];
+    __syncthreads();
     if (wave != 0) return;
+    for (int w = 1; w < WAVES; ++w)
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c)
-#pragma unroll
-        for (int i = 0; i < R; ++i) res[c][i] = red[(ln * NCOL + c) * R + i];
+        for (int a = 0; a < NACC; ++a) res[a] += red[((w - 1) * NACC + a) * 64 + ln];
 
-    // Back to real units: 2^(24 or 20) and 2^e_m per row.
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-        const float unit = (BITS == 4 && c >= 8) ? 1048576.0f : 16777216.0f;  // 2^20 : 2^24
-#pragma unroll
-        for (int i = 0; i < R; ++i) res[c][i] *= unit * rowf[i];
-    }
-
-    auto column = [&](int c) { return (c >= 8 ? half : 0) + boff + (c & 7); };
+    const bool live = active && d_row < M;
     if (jb.partials && jb.counters) {
         // In-kernel slice reduction (write-through sums + tile counter), as in kt_gemv.hip.
-        float* part = jb.partials + static_cast<size_t>(slice) * M * N;
-        if (active)
+        float* part = jb.partials + (static_cast<size_t>(slice) * M + d_row_c) * N;
+        if (live)
 #pragma unroll
-            for (int c = 0; c < NCOL; ++c)
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    const int32_t m = 4 * kb + i;
-                    if (m < M)
-                        __hip_atomic_store(part + static_cast<size_t>(m) * N + column(c), res[c][i], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_SYSTEM);
-                }
+            for (int a = 0; a < NACC; ++a)
+                __hip_atomic_store(part + col[a], res[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __builtin_amdgcn_s_waitcnt(0);
         uint32_t old = 0;
         if (ln == 0) old = __hip_atomic_fetch_add(jb.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __builtin_amdgcn_readfirstlane(old);
         if (old != static_cast<uint32_t>(jb.slices - 1)) return;
+        // The last workgroup of the strip: every slice's sums (write-through, read past
+        // the caches), all loads in flight together, added in slice order.
+        constexpr int MAXS = 8;  // the host takes this path for at most 8 slices
+        float v[MAXS][NACC];
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c)
+        for (int sp = 0; sp < MAXS; ++sp)
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int32_t m = 4 * kb + i;
-                float sum = 0.0f;
-                if (active && m < M)
-                    for (int32_t sp = 0; sp < jb.slices; ++sp) {
-                        const float v = sp == slice ? res[c][i]
-                                                    : __hip_atomic_load(jb.partials + (static_cast<size_t>(sp) * M + m) * N + column(c),
-                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                        sum = sp == 0 ? v : sum + v;
-                    }
-                res[c][i] = sum;
+            for (int a = 0; a < NACC; ++a) {
+                v[sp][a] = 0.0f;
+                if (live && sp < jb.slices && sp != slice)
+                    v[sp][a] = __hip_atomic_load(jb.partials + (static_cast<size_t>(sp) * M + d_row_c) * N + col[a],
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < MAXS; ++sp)
+                if (sp < jb.slices) {
+                    const float vv = sp == slice ? res[a] : v[sp][a];
+                    sum = sp == 0 ? vv : sum + vv;
+                }
+            res[a] = sum;
+        }
         if (ln == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (!active) return;
+    if (!live) return;
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-        const int32_t n = column(c);
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const int32_t m = 4 * kb + i;
-            if (m >= M) continue;
-            if (jb.partials && !jb.counters) {
-                jb.partials[(static_cast<size_t>(slice) * M + m) * N + n] = res[c][i];
-            } else {
-                float* dst = jb.out + static_cast<size_t>(m) * N + n;
-                float o = accumulate ? *dst : 0.0f;
-                o = fmaf(alpha, res[c][i], o);
-                if (jb.bias) o += jb.bias[n];
-                *dst = o;
-            }
+    for (int a = 0; a < NACC; ++a) {
+        const int32_t n = col[a];
+        if (jb.partials && !jb.counters) {
+            jb.partials[(static_cast<size_t>(slice) * M + d_row) * N + n] = res[a];
+        } else {
+            float* dst = jb.out + static_cast<size_t>(d_row) * N + n;
+            float o = accumulate ? *dst : 0.0f;
+            o = fmaf(alpha, res[a], o);
+            if (jb.bias) o += jb.bias[n];
+            *dst = o;
         }
     }
 }
@@ -376,34 +481,51 @@ struct Forced {
 };
 Forced g_forced;
 
-constexpr size_t LDS_X_BYTES = 40 << 10;  // x hi/lo of a K-slice: 4 bytes per (row of x, k)
+// x areas of a workgroup: every wave keeps four fp16 parts of its groups (8 bytes per x
+// value and row) plus four floats per group and row.
+constexpr size_t LDS_X_BYTES = 64 << 10;
 
-template <int BITS, int R, int WAVES, bool ZP>
-void launch_kernel(dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K, int32_t g,
-                   const Jobs& jobs, float alpha, int32_t accumulate) {
-    gemv_mfma_kernel<BITS, R, WAVES, ZP><<<grid, dim3(64 * WAVES), lds, st>>>(a, M, K, g, jobs, alpha, accumulate);
+template <int BITS, int MP, int WAVES, int CPG, bool ZP>
+void launch_kernel(dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K, const Jobs& jobs,
+                   int32_t wave_groups, float alpha, int32_t accumulate) {
+    gemv_mfma_kernel<BITS, MP, WAVES, CPG, ZP>
+        <<<grid, dim3(64 * WAVES), lds, st>>>(a, M, K, jobs, wave_groups, alpha, accumulate);
 }
 
-template <int BITS, int R, int WAVES>
-void launch_zp(bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K, int32_t g,
-               const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (BITS == 4 || zp) launch_kernel<BITS, R, WAVES, true>(grid, lds, st, a, M, K, g, jobs, alpha, accumulate);
-    else launch_kernel<BITS, R, WAVES, false>(grid, lds, st, a, M, K, g, jobs, alpha, accumulate);
+template <int BITS, int MP, int WAVES, int CPG>
+void launch_zp(bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K, const Jobs& jobs,
+               int32_t wave_groups, float alpha, int32_t accumulate) {
+    if (BITS == 4 || zp) launch_kernel<BITS, MP, WAVES, CPG, true>(grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else launch_kernel<BITS, MP, WAVES, CPG, false>(grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
 }
 
-template <int BITS, int WAVES>
-void launch_r(int r, bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K, int32_t g,
-              const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (r == 1) launch_zp<BITS, 1, WAVES>(zp, grid, lds, st, a, M, K, g, jobs, alpha, accumulate);
-    else if (r == 2) launch_zp<BITS, 2, WAVES>(zp, grid, lds, st, a, M, K, g, jobs, alpha, accumulate);
-    else launch_zp<BITS, 4, WAVES>(zp, grid, lds, st, a, M, K, g, jobs, alpha, accumulate);
+template <int BITS, int MP, int WAVES>
+void launch_cpg(int cpg, bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K,
+                const Jobs& jobs, int32_t wave_groups, float alpha, int32_t accumulate) {
+    if (cpg == 1) launch_zp<BITS, MP, WAVES, 1>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else if (cpg == 2) launch_zp<BITS, MP, WAVES, 2>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else launch_zp<BITS, MP, WAVES, 4>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+}
+
+template <int BITS, int MP>
+void launch_waves(int waves, int cpg, bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M,
+                  int32_t K, const Jobs& jobs, int32_t wave_groups, float alpha, int32_t accumulate) {
+    if (waves == 8) launch_cpg<BITS, MP, 8>(cpg, zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else launch_cpg<BITS, MP, 4>(cpg, zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+}
+
+template <int BITS>
+void launch_bits(int mp, int waves, int cpg, bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M,
+                 int32_t K, const Jobs& jobs, int32_t wave_groups, float alpha, int32_t accumulate) {
+    if (mp == 1) launch_waves<BITS, 1>(waves, cpg, zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else launch_waves<BITS, 2>(waves, cpg, zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
 }
 
 }  // namespace
 
 void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t disable) {
     g_forced.slices = slices > 0 ? slices : 0;
-    g_forced.waves = (waves == 2 || waves == 4 || waves == 8) ? waves : 0;
+    g_forced.waves = (waves == 4 || waves == 8) ? waves : 0;
     g_forced.reduce = (reduce == 1 || reduce == 2) ? reduce : 0;
     g_forced.disable = disable ? 1 : 0;
 }
@@ -412,11 +534,16 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
     (void)a;
     (void)c;
     if (g_forced.disable) return false;
-    if (m < 1 || m > 16) return false;
-    if (w.g % CHUNK != 0 || w.K % w.g != 0) return false;  // whole 32-row chunks in whole groups
+    if (m < 1 || m > MAX_M) return false;
+    if (w.g != 32 && w.g != 64 && w.g != 128) return false;  // whole 32-row chunks, up to 4 per group
+    if (w.K % w.g != 0) return false;
     if (w.bpr % 8 != 0 || !aligned(w.q, 8)) return false;  // 8-byte lane strips
     if (w.N % 8 != 0 || !aligned(w.s, 16) || (w.z && !aligned(w.z, 8))) return false;
     if (w.bits == 4 && w.N % 16 != 0) return false;        // high-nibble columns start 8-aligned
+    // lane row offsets within a chunk are 32-bit
+    if (static_cast<int64_t>(CHUNK) * w.bpr >= (static_cast<int64_t>(1) << 31)) return false;
+    // one x group of every row must fit a wave's LDS area
+    if (static_cast<size_t>(8) * m * (8 * w.g + 16) > LDS_X_BYTES) return false;
     return true;
 }
 
@@ -434,18 +561,16 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     for (int32_t i = 0; i < count; ++i) tiles_total += ceil_div(ws[i].bpr, STRIP);
     const int32_t target_waves = cu_count() * 8;
     // Waves per workgroup (each takes whole groups), then K-slices until the GPU is
-    // covered; the x area in LDS bounds the rows of a slice.
-    int32_t waves = 4;
-    if (G < 4) waves = G >= 2 ? 2 : 1;
-    if (waves == 1) waves = 2;  // the smallest instantiation; an idle wave costs little
+    // covered; the x areas in LDS bound the groups of a slice.
+    int32_t waves = g_forced.waves ? g_forced.waves : 4;
     int32_t slices = static_cast<int32_t>((target_waves + tiles_total * waves - 1) / (tiles_total * waves));
     const int32_t max_slices = G / waves > 1 ? G / waves : 1;
     if (slices > max_slices) slices = max_slices;
     if (slices < 1) slices = 1;
-    const int32_t rows_cap = static_cast<int32_t>(LDS_X_BYTES / (4 * static_cast<size_t>(M)));
-    const int32_t min_slices = ceil_div(w0.K, rows_cap > w0.g ? rows_cap - rows_cap % w0.g : w0.g);
+    const size_t per_group = static_cast<size_t>(M) * (8 * w0.g + 16);
+    const int32_t cap_groups = static_cast<int32_t>(LDS_X_BYTES / (waves * per_group));  // per wave, >= 1
+    const int32_t min_slices = ceil_div(G, cap_groups * waves);
     if (slices < min_slices) slices = min_slices;
-    if (g_forced.waves) waves = g_forced.waves;
     if (g_forced.slices) slices = g_forced.slices > min_slices ? g_forced.slices : min_slices;
     if (slices > G) slices = G;
     constexpr int32_t MAX_INKERNEL_SLICES = 8;
@@ -456,7 +581,7 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     // Every slice takes gps whole groups; the last may take fewer.
     const int32_t gps = ceil_div(G, slices);
     slices = ceil_div(G, gps);
-    const int32_t rows = gps * w0.g;
+    const int32_t wave_groups = ceil_div(gps, waves);
     size_t ws_floats = 0, n_counters = 0;
     if (slices > 1)
         for (int32_t i = 0; i < count; ++i) {
@@ -465,7 +590,7 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
         }
     bool inkernel = slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS;
     if (g_forced.reduce == 1) inkernel = false;
-    if (g_forced.reduce == 2 && slices > 1 && n_counters <= MAX_COUNTERS) inkernel = true;
+    if (g_forced.reduce == 2 && slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS) inkernel = true;
     float* partials = nullptr;
     uint32_t* counters = nullptr;
     if (ws_floats) {
@@ -477,7 +602,7 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     }
     Jobs jobs{};
     jobs.count = count;
-    int32_t blocks = 0, widest = 0;
+    int32_t blocks = 0, widest = 0;  // blocks of the largest job: the grid is blocks x count
     size_t offset = 0, coffset = 0;
     for (int32_t i = 0; i < count; ++i) {
         Job& jb = jobs.job[i];
@@ -491,30 +616,25 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
         jb.tiles = ceil_div(ws[i].bpr, STRIP);
         jb.slices = slices;
         jb.groups_per_slice = gps;
-        jb.block_begin = blocks;
         jb.partials = slices > 1 ? partials + offset : nullptr;
         jb.counters = inkernel ? counters + coffset : nullptr;
         offset += static_cast<size_t>(slices) * M * ws[i].N;
         coffset += jb.tiles;
-        blocks += jb.tiles * slices;
+        if (jb.tiles * slices > blocks) blocks = jb.tiles * slices;
         if (M * ws[i].N > widest) widest = M * ws[i].N;
     }
-    // LDS: x hi/lo for the slice rows, the 16 row maxima; the wave reduction reuses it.
-    const int r = M >= 3 ? 4 : M;
+    // LDS: the waves' x areas; the cross-wave reduction reuses them.
+    const int mp = M == 1 ? 1 : 2;
     const int ncol = ws[0].bits == 4 ? 16 : 8;
-    const size_t lds_x = static_cast<size_t>(4) * M * rows + 16 * sizeof(uint32_t);
-    const size_t lds_red = static_cast<size_t>(64) * ncol * r * sizeof(float);
+    const int nacc = ncol / (4 / mp);
+    const size_t xw = static_cast<size_t>(wave_groups) * per_group;
+    const size_t lds_x = waves * xw;
+    const size_t lds_red = static_cast<size_t>(waves - 1) * nacc * 64 * sizeof(float);
     const size_t lds = lds_x > lds_red ? lds_x : lds_red;
-    const dim3 grid(static_cast<uint32_t>(blocks));
-    if (ws[0].bits == 4) {
-        if (waves == 8) launch_r<4, 8>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-        else if (waves == 2) launch_r<4, 2>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-        else launch_r<4, 4>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-    } else {
-        if (waves == 8) launch_r<8, 8>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-        else if (waves == 2) launch_r<8, 2>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-        else launch_r<8, 4>(r, zp, grid, lds, st, a, M, w0.K, w0.g, jobs, alpha, accumulate);
-    }
+    const int cpg = w0.g / CHUNK;
+    const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
+    if (ws[0].bits == 4) launch_bits<4>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+    else launch_bits<8>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
     KT_LAUNCHED("qmatmul: mfma gemv kernel");
     if (slices > 1 && !inkernel) {
         gemv_mfma_reduce<<<ceil_div(widest, 256), 256, 0, st>>>(jobs, M, alpha, accumulate);

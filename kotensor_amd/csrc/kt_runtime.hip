@@ -295,7 +295,7 @@ static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
     if (m == 0) return KT_OK;
     if (!a || !c) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (m <= 16 && gemv_mfma_supported(a, m, v, c)) {
+    if (m <= 2 && gemv_mfma_supported(a, m, v, c)) {
         const float* biases[1] = {bias};
         return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
     }
@@ -314,7 +314,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
     for (int32_t start = 0; start < count; start += 4) {
         const int32_t n = count - start < 4 ? count - start : 4;
         bool fast = m == 1 && a != nullptr;
-        bool mfma = m >= 1 && m <= 16 && a != nullptr;
+        bool mfma = m >= 1 && m <= 2 && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
             if (status) return status;

@@ -147,15 +147,13 @@ def test_gemv_work_splits_agree(kt, oracle_lib):
             want = oracle_lib.multiply_quantized(x, q, 1)
             configs = [(1, vec, waves, splits, reduce) for vec in (4, 8) for waves in (4, 8)
                        for splits in (1, 2, 3, 5, q.groups) for reduce in (1, 2)]
-            configs += [(2, 0, waves, splits, reduce) for waves in (2, 4, 8) for splits in (1, 2, 3, 5, q.groups)
+            configs += [(2, 0, waves, splits, reduce) for waves in (4, 8) for splits in (1, 2, 3, 5, q.groups)
                         for reduce in (1, 2)]
             for kind, vec, waves, splits, reduce in configs:
                 banner("split", k, n, bits, kind, vec, waves, splits, reduce)
                 kt.MatMul.set_kernel_config(kind, vec, splits, waves, reduce)
                 got = gpu_matmul(kt, x, qt, 1)
-                # the VALU kernel accumulates in fp32 like the reference; the MFMA kernel
-                # within the product tolerance
-                assert normwise_rel(got, want) <= (1e-5 if kind == 1 else TOL), (kind, vec, waves, splits, reduce)
+                assert normwise_rel(got, want) <= 1e-5, (kind, vec, waves, splits, reduce)
                 # the in-kernel reduction leaves its counters at zero: a repeat agrees
                 assert same_bits(got, gpu_matmul(kt, x, qt, 1))
     finally:
