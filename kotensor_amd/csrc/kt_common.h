@@ -82,6 +82,13 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
 int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float* const* cs, const float* const* biases,
                          int32_t count, int32_t accumulate, float alpha, hipStream_t st);
 void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t disable);
+// The M == 1 MFMA kernel on 512-byte row strips (kt_gemv_wide.hip).
+bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
+                         int32_t accumulate, float alpha, hipStream_t st);
+void set_gemv_wide_config(int32_t slices);
+// Whether the automatic choice takes the wide-strip kernel for these weights.
+bool gemv_wide_preferred(const WeightView* ws, int32_t count);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
 // otherwise the generic kernel runs.

@@ -1,0 +1,526 @@
+// kt_gemv_wide.hip -- the decode dequant-GEMV at M == 1 on gfx950 MFMA:
+//   c[1 x N] = (accumulate ? c : 0) + alpha * x[1 x K] . deq(W) (+ bias),
+// MatMul.multiplyQuantizedRow (Engine/kotensor/src/main/kotlin/MatMul.kt:494-536) for
+// the reference layout of the weights.
+//
+// HBM is the bound, so the kernel is built around the load stream:
+//
+//   * a wave owns a 512-byte strip of the packed rows (a tile) and one load instruction
+//     reads 512 contiguous bytes of one row: lane (cl = l % 16, kb = l / 16) reads bytes
+//     128 kb + 8 cl .. + 7. A chunk is 8 rows (4 KB per wave); every wave keeps NB
+//     chunks in flight and issues exactly the loads it needs;
+//   * v_mfma_f32_16x16x32_f16 with a block-diagonal A: k-block kb of B (lanes kb) holds
+//     the 8 rows of sub-strip kb, and A row block kb (rows 4 kb .. 4 kb + 3) holds x for
+//     those 8 rows only, so one MFMA gives all four sub-strips at once, each in the
+//     result rows of its own lanes;
+//   * weight bytes become exact fp16 integers in two instructions per pair of rows
+//     (v_perm_b32 pairs the byte of two rows, an and-or sets the exponent of 1024:
+//     1024 + q, 1024 + 16 q for the high nibble, 1152 + q for INT8 after a bias of 128);
+//   * x is split per 32-row unit into three fp16 parts on fixed grids (256 steps each,
+//     the unit's largest |x| scaled into [2^14, 2^15), 24 bits below it); the three
+//     parts are A rows 0..2 of the block. Every partial sum of part * (1024 + q) over a
+//     unit is an integer multiple of the part's grid below 2^24 grids, so the MFMA sums
+//     are exact, and so is sum(part * (q - z)) = fma(-(1024 + z), sum(part), that sum);
+//   * per unit: res += scale * 2^e * (hi + mid + lo), on every lane (16 columns each);
+//   * a workgroup is 8 waves on one tile; its waves take the units of its K-slice
+//     round-robin, meet in LDS and, with several K-slices, meet the other slices through
+//     write-through partial sums and a per-tile counter (the last workgroup adds them in
+//     slice order), so results do not depend on timing.
+#include "kt_common.h"
+
+namespace kt {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int MAX_JOBS = 4;
+constexpr int UNIT = 32;          // rows per x unit (exponent, parts, sums)
+constexpr int CROWS = 8;          // rows per chunk
+constexpr int CPU_ = UNIT / CROWS;  // chunks per unit
+constexpr int TILE = 512;         // bytes of a row per wave
+constexpr int WAVES = 8;          // waves per workgroup
+constexpr int THREADS = 64 * WAVES;
+constexpr int MAX_SLICES = 32;    // K-slices met inside the kernel
+constexpr int XB = 2;             // x load instructions per batch (2 units each)
+
+struct Job {
+    const uint8_t* q;
+    const float* s;
+    const int8_t* z;
+    float* out;
+    const float* bias;
+    float* partials;     // [slices x N] when slices > 1
+    uint32_t* counters;  // [tiles] when slices > 1
+    int32_t N, bpr, tiles, slices, units_per_slice;
+};
+
+struct Jobs {
+    Job job[MAX_JOBS];
+    int32_t count;
+};
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+
+// Byte j (0..3) of rows (a, b) into the low bytes of the two halves of a word.
+__device__ __forceinline__ uint32_t pair_bytes(uint32_t a, uint32_t b, int j) {
+    // v_perm_b32(S0 = b, S1 = a): selector bytes 0..3 pick a's bytes, 4..7 pick b's, 0x0c is 0.
+    const uint32_t sel = 0x0c000c00u | (static_cast<uint32_t>(4 + j) << 16) | static_cast<uint32_t>(j);
+    return __builtin_amdgcn_perm(b, a, sel);
+}
+
+// A constant held in a VGPR: (v & mask) | bits and (v ^ a) + b with such operands are
+// one v_and_or_b32 / v_xad_u32 each. Only vector ALU instructions read the result.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+    return r;
+}
+
+// Max (or sum) over each 32-lane half of the wave, in every lane: a DPP butterfly in
+// each 16-lane row, then the row results through scalar registers. The values reduced
+// are exact (maxima, sums on one fixed-point grid), so the order does not matter.
+template <bool MAX>
+__device__ __forceinline__ float dpp_step(float v, int tag) {
+    int o;
+    switch (tag) {  // dpp_ctrl must be a constant
+        case 0: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad [1,0,3,2]
+        case 1: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad [2,3,0,1]
+        case 2: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        default: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
+    }
+    return MAX ? fmaxf(v, __int_as_float(o)) : v + __int_as_float(o);
+}
+template <bool MAX>
+__device__ __forceinline__ float half_reduce(float v, int32_t ln) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v = dpp_step<MAX>(v, i);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    const float a = MAX ? fmaxf(r0, r1) : r0 + r1;
+    const float b = MAX ? fmaxf(r2, r3) : r2 + r3;
+    return ln < 32 ? a : b;
+}
+
+// Scales and zero points of one unit's group for a lane's columns: for each nibble side
+// (INT8: one), 8 consecutive columns.
+template <int BITS>
+struct UnitScales {
+    float4 s[BITS == 4 ? 4 : 2];
+    uint2 z[BITS == 4 ? 2 : 1];
+};
+
+template <int BITS, int NB, bool ZP>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+    gemv_wide_kernel(const float* __restrict__ x, int32_t K, int32_t g, Jobs jobs, float alpha, int32_t accumulate) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int SIDES = BITS == 4 ? 2 : 1;
+    constexpr int NACC = 8 * SIDES;  // accumulators (columns) per lane
+    constexpr float OFF = BITS == 4 ? 1024.0f : 1152.0f;
+    constexpr float GRID0 = 128.0f, GRID1 = 0.5f, GRID2 = 1.0f / 512.0f;  // 256 steps each below 2^15
+    static_assert(NB == CPU_, "the load ring is one unit");
+
+    // The job is blockIdx.y; the empty asm makes the arguments of the load stream load in
+    // one round (the output's are needed only at the end).
+    Job jb = jobs.job[blockIdx.y];
+    asm volatile("" ::"s"(jb.q), "s"(jb.s), "s"(jb.z), "s"(jb.N), "s"(jb.bpr), "s"(jb.tiles), "s"(jb.slices),
+                 "s"(jb.units_per_slice), "s"(x), "s"(K), "s"(g));
+    if (static_cast<int32_t>(blockIdx.x) >= jb.tiles * jb.slices) return;
+    const int32_t N = jb.N, bpr = jb.bpr, half = jb.bpr;
+    const int32_t tile = blockIdx.x % jb.tiles;
+    const int32_t slice = blockIdx.x / jb.tiles;
+    const int32_t units = K / UNIT;
+    const int32_t u_begin = slice * jb.units_per_slice;
+    const int32_t u_end = min(u_begin + jb.units_per_slice, units);
+
+    const int32_t t = threadIdx.x;
+    const int32_t ln = t & 63;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int32_t cl = ln & 15, kb = ln >> 4;
+    const int32_t col_off = tile * TILE + kb * 128 + cl * 8;  // first byte of this lane in a row
+    const bool active = col_off < bpr;
+    const int32_t boff = active ? col_off : 0;  // lanes past the row end compute and discard
+
+    // This wave's units: u_begin + wave + k * WAVES, k < my_units.
+    const int32_t my_units = u_end - u_begin > wave ? (u_end - u_begin - wave + WAVES - 1) / WAVES : 0;
+    const int32_t wave_units = (jb.units_per_slice + WAVES - 1) / WAVES;
+
+    // LDS: per wave, parts [wave_units][4][UNIT] fp16 (hi, mid, lo, zeros) and
+    // [wave_units] x {sum hi, sum mid, sum lo, 2^e}; the cross-wave sums reuse it.
+    const int32_t xw_bytes = wave_units * (4 * UNIT * 2 + 16);
+    _Float16* xs = reinterpret_cast<_Float16*>(smem + wave * xw_bytes);
+    float4* sums = reinterpret_cast<float4*>(smem + wave * xw_bytes + wave_units * 4 * UNIT * 2);
+    // A role: row cl of the block-diagonal A is x-part cl % 4 for k-block cl / 4.
+    const int32_t a_off = ((cl >> 2) == kb ? (cl & 3) : 3) * UNIT;
+
+    const uint32_t mask_lo = in_vgpr(0x000F000Fu), mask_hi = in_vgpr(0x00F000F0u);
+    const uint32_t flip = in_vgpr(0x00800080u), exp1024 = in_vgpr(0x64006400u);
+
+    float res[NACC];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) res[a] = 0.0f;
+
+    if (my_units > 0) {
+        // ---- x: first batch of loads, before the weight loads --------------------------
+        const int32_t sub = ln >> 5;  // two units per x instruction
+        const int32_t kk = ln & 31;
+        float xv[XB];
+        auto load_x = [&](int32_t k0) {
+#pragma unroll
+            for (int b = 0; b < XB; ++b) {
+                int32_t k = k0 + 2 * b + sub;
+                k = k < my_units ? k : my_units - 1;
+                xv[b] = x[static_cast<size_t>(u_begin + wave + k * WAVES) * UNIT + kk];
+            }
+        };
+        // Every loaded slot is processed (slots past my_units only skip their stores): a
+        // conditional use would let the compiler sink the load behind the weight loads.
+        auto prep_x = [&](int32_t k0) {
+#pragma unroll
+            for (int b = 0; b < XB; ++b) {
+                const int32_t k = k0 + 2 * b + sub;
+                const float mx = half_reduce<true>(fabsf(xv[b]), ln);
+                int e = 0;
+                if (mx > 0.0f && mx <= 3.402823466e38f) {
+                    frexpf(mx, &e);
+                    e -= 15;
+                }
+                const float xp = ldexpf(xv[b], -e);
+                const float hi = rintf(xp * (1.0f / GRID0)) * GRID0;
+                const float r1 = xp - hi;
+                const float mid = rintf(r1 * (1.0f / GRID1)) * GRID1;
+                const float lo = rintf((r1 - mid) * (1.0f / GRID2)) * GRID2;
+                const float s0 = half_reduce<false>(hi, ln);
+                const float s1 = half_reduce<false>(mid, ln);
+                const float s2 = half_reduce<false>(lo, ln);
+                if (k < my_units) {
+                    _Float16* dst = xs + k * 4 * UNIT + kk;
+                    dst[0] = static_cast<_Float16>(hi);
+                    dst[UNIT] = static_cast<_Float16>(mid);
+                    dst[2 * UNIT] = static_cast<_Float16>(lo);
+                    dst[3 * UNIT] = static_cast<_Float16>(0.0f);
+                    if (kk == 0) sums[k] = make_float4(s0, s1, s2, ldexpf(1.0f, e));
+                }
+            }
+        };
+        load_x(0);
+        __builtin_amdgcn_sched_barrier(0);  // the x loads go out first: they are waited for first
+
+        // ---- weight loads: the first unit (NB chunks) ---------------------------------
+        uint32_t roff[CROWS];
+#pragma unroll
+        for (int i = 0; i < CROWS; ++i) roff[i] = static_cast<uint32_t>(i * bpr + boff);
+        auto load = [&](uint2* v, int32_t k, int32_t cc) {
+            const uint8_t* base =
+                jb.q + static_cast<size_t>((u_begin + wave + k * WAVES) * UNIT + cc * CROWS) * bpr;
+#pragma unroll
+            for (int i = 0; i < CROWS; ++i) v[i] = *reinterpret_cast<const uint2*>(base + roff[i]);
+        };
+        uint2 buf[NB][CROWS];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(buf[b], 0, b);
+
+        const int32_t scol = tile * TILE + kb * 128 + cl * 8;  // first column of the lane, low side
+        const int32_t scol_c = active ? scol : 0;
+        auto load_scales = [&](int32_t k) {
+            UnitScales<BITS> sc;
+            const size_t gi = static_cast<size_t>((u_begin + wave + k * WAVES) * UNIT / g);
+#pragma unroll
+            for (int side = 0; side < SIDES; ++side) {
+                const int32_t col = (side ? half : 0) + scol_c;
+                sc.s[2 * side] = *reinterpret_cast<const float4*>(jb.s + gi * N + col);
+                sc.s[2 * side + 1] = *reinterpret_cast<const float4*>(jb.s + gi * N + col + 4);
+                if constexpr (ZP) sc.z[side] = *reinterpret_cast<const uint2*>(jb.z + gi * N + col);
+                else sc.z[side] = make_uint2(0u, 0u);
+            }
+            return sc;
+        };
+        // A unit's scales go out with its first chunk computations and are used at its end.
+        UnitScales<BITS> sc = load_scales(0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        prep_x(0);
+        for (int32_t k0 = 2 * XB; k0 < my_units; k0 += 2 * XB) {
+            load_x(k0);
+            prep_x(k0);
+        }
+
+        // ---- main loop ----------------------------------------------------------------
+        f32x4 acc[NACC];
+        const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // Chunk cc of unit k; the unit's first chunk starts the accumulators at zero.
+        auto compute = [&](const uint2* v, int32_t k, int cc) {
+            const half8 a = *reinterpret_cast<const half8*>(xs + k * 4 * UNIT + a_off + cc * CROWS);
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {  // dword of the 8-byte strip
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * w + jj;
+                    u32x4 p;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        p[i] = pair_bytes(w ? v[2 * i].y : v[2 * i].x, w ? v[2 * i + 1].y : v[2 * i + 1].x, jj);
+                    if (BITS == 8) {
+                        u32x4 bq;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) bq[i] = (p[i] ^ flip) + exp1024;  // 1152 + q
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(bq), cc ? acc[j] : zero4, 0, 0, 0);
+                    } else {
+                        u32x4 blo, bhi;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            blo[i] = (p[i] & mask_lo) | exp1024;  // 1024 + q
+                            bhi[i] = (p[i] & mask_hi) | exp1024;  // 1024 + 16 q
+                        }
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(blo), cc ? acc[j] : zero4, 0, 0, 0);
+                        acc[8 + j] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(bhi), cc ? acc[8 + j] : zero4, 0, 0, 0);
+                    }
+                }
+            }
+        };
+        // res += scale * 2^e * sum over parts of (D_p - (OFF + zero) * S_p), each term exact.
+        auto combine = [&](int32_t k, const UnitScales<BITS>& us) {
+            const float4 sm = sums[k];
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                const int side = a >> 3, j = a & 7;
+                const float4 s4 = us.s[2 * side + (j >> 2)];
+                float scl = (j & 3) == 0 ? s4.x : (j & 3) == 1 ? s4.y : (j & 3) == 2 ? s4.z : s4.w;
+                float off = OFF;
+                if constexpr (ZP) {
+                    const uint32_t zw = j < 4 ? us.z[side].x : us.z[side].y;
+                    off += (side ? 16.0f : 1.0f) * static_cast<float>(static_cast<int8_t>((zw >> (8 * (j & 3))) & 0xFFu));
+                }
+                if (side) scl *= 0.0625f;  // high nibble columns carry 16 q
+                const float d = (fmaf(-off, sm.x, acc[a][0]) + fmaf(-off, sm.y, acc[a][1])) + fmaf(-off, sm.z, acc[a][2]);
+                res[a] = fmaf(scl * sm.w, d, res[a]);
+            }
+        };
+
+        int32_t k = 0;
+        // Every unit but the last loads the next unit behind its own chunks; the last
+        // loads nothing, so no wave reads past its range.
+        for (; k + 1 < my_units; ++k) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                compute(buf[b], k, b);
+                load(buf[b], k + 1, b);
+            }
+            combine(k, sc);
+            sc = load_scales(k + 1);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) compute(buf[b], k, b);
+        combine(k, sc);
+    }
+
+    // ---- the workgroup's waves meet in LDS (reusing the x areas) ------------------------
+    // red[wave][column] with column = side * 512 + (kb * 128 + cl * 8 + j) of the tile.
+    float* red = reinterpret_cast<float*>(smem);
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) {
+        const int side = a >> 3, j = a & 7;
+        red[wave * (SIDES * TILE) + side * TILE + kb * 128 + cl * 8 + j] = res[a];
+    }
+    __syncthreads();
+    // Thread t owns tile columns t and t + 512 (INT4) or t (INT8), summed in wave order.
+    constexpr int PER_THREAD = SIDES * TILE / THREADS;
+    float sum[PER_THREAD];
+    int32_t colg[PER_THREAD];
+    bool live[PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int c = t + i * THREADS;  // tile column: side = c / 512, byte = c % 512
+        float v = red[c];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) v += red[w * (SIDES * TILE) + c];
+        sum[i] = v;
+        const int32_t byte = tile * TILE + (c & (TILE - 1));
+        live[i] = byte < bpr;
+        colg[i] = (c >= TILE ? half : 0) + (live[i] ? byte : 0);
+    }
+
+    if (jb.slices > 1) {
+        // Slices meet through write-through partial sums and a per-tile counter; the last
+        // workgroup of the tile adds them in slice order.
+        const int32_t S = jb.slices;
+        // A workgroup's sums are contiguous columns of its slice's row: full-line writes.
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i)
+            if (live[i])
+                __hip_atomic_store(jb.partials + static_cast<size_t>(slice) * N + colg[i], sum[i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        __shared__ uint32_t last;
+        if (t == 0)
+            last = __hip_atomic_fetch_add(jb.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   static_cast<uint32_t>(jb.slices - 1);
+        __syncthreads();
+        if (!last) return;
+        // All loads in flight together; the pointer steps by a row per slice in a VGPR.
+        float v[PER_THREAD][MAX_SLICES];
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const float* pp = jb.partials + colg[i];
+#pragma unroll
+            for (int sp = 0; sp < MAX_SLICES; ++sp) {
+                v[i][sp] = 0.0f;
+                if (sp < S && sp != slice && live[i]) v[i][sp] = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                pp += N;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            float s = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < MAX_SLICES; ++sp)
+                if (sp < S) {
+                    const float vv = sp == slice ? sum[i] : v[i][sp];
+                    s = sp == 0 ? vv : s + vv;
+                }
+            sum[i] = s;
+        }
+        if (t == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        if (!live[i]) continue;
+        float* dst = jb.out + colg[i];
+        float o = accumulate ? *dst : 0.0f;
+        o = fmaf(alpha, sum[i], o);
+        if (jb.bias) o += jb.bias[colg[i]];
+        *dst = o;
+    }
+}
+
+struct Forced {
+    int slices = 0;
+};
+Forced g_forced;
+
+// x areas: 4 fp16 parts per x value plus 16 bytes per unit, per wave.
+constexpr size_t LDS_X_BYTES = 96 << 10;
+
+template <int BITS>
+void launch_bits(bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs,
+                 float alpha, int32_t accumulate) {
+    if (BITS == 4 || zp)
+        gemv_wide_kernel<BITS, CPU_, true><<<grid, dim3(THREADS), lds, st>>>(a, K, g, jobs, alpha, accumulate);
+    else
+        gemv_wide_kernel<BITS, CPU_, false><<<grid, dim3(THREADS), lds, st>>>(a, K, g, jobs, alpha, accumulate);
+}
+
+}  // namespace
+
+void set_gemv_wide_config(int32_t slices) { g_forced.slices = slices > 0 ? slices : 0; }
+
+bool gemv_wide_preferred(const WeightView* ws, int32_t count) {
+    // The wide strips pay off once they give enough workgroups to keep the GPU's loads
+    // in flight; smaller products run better as more, narrower workgroups.
+    int64_t tiles = 0;
+    for (int32_t i = 0; i < count; ++i) tiles += ceil_div(ws[i].bpr, TILE);
+    int32_t slices = ws[0].K / UNIT / WAVES;
+    if (slices > MAX_SLICES) slices = MAX_SLICES;
+    if (slices < 1) slices = 1;
+    return tiles * slices >= 128;
+}
+
+bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
+    (void)a;
+    (void)c;
+    if (m != 1) return false;
+    if (w.g % UNIT != 0 || w.K % UNIT != 0) return false;  // units of 32 rows inside one group
+    if (w.bpr % 8 != 0 || !aligned(w.q, 8)) return false;  // 8-byte lane strips
+    if (w.N % 8 != 0 || !aligned(w.s, 16) || (w.z && !aligned(w.z, 8))) return false;
+    if (w.bits == 4 && w.N % 16 != 0) return false;        // high-nibble scales and zeros stay aligned
+    if (static_cast<int64_t>(CROWS) * w.bpr >= (static_cast<int64_t>(1) << 31)) return false;
+    return true;
+}
+
+int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
+                         int32_t accumulate, float alpha, hipStream_t st) {
+    const WeightView& w0 = ws[0];
+    const int32_t units = w0.K / UNIT;
+    bool zp = false;
+    for (int32_t i = 0; i < count; ++i) zp = zp || ws[i].z != nullptr;
+    if (zp)
+        for (int32_t i = 0; i < count; ++i)
+            if (!ws[i].z) return fail(KT_ERR_ARGUMENT, "grouped weights must all have zero points or none");
+
+    int64_t tiles_total = 0;
+    for (int32_t i = 0; i < count; ++i) tiles_total += ceil_div(ws[i].bpr, TILE);
+    // One workgroup of 8 waves per CU keeps about 128 KB of loads in flight there; aim for
+    // two per CU, each wave taking at least one unit.
+    const int64_t target = 2 * static_cast<int64_t>(cu_count());
+    int32_t slices = static_cast<int32_t>((target + tiles_total - 1) / tiles_total);
+    const int32_t max_slices = units / WAVES > 1 ? units / WAVES : 1;
+    if (slices > max_slices) slices = max_slices;
+    if (slices > MAX_SLICES) slices = MAX_SLICES;
+    if (slices < 1) slices = 1;
+    // the x areas bound the units of a slice
+    const int32_t cap_units = static_cast<int32_t>(LDS_X_BYTES / (WAVES * (4 * UNIT * 2 + 16))) * WAVES;
+    if (ceil_div(units, slices) > cap_units) slices = ceil_div(units, cap_units);
+    if (g_forced.slices) slices = g_forced.slices;
+    if (slices > units) slices = units;
+    if (slices > MAX_SLICES) return fail(KT_ERR_ARGUMENT, "wide gemv: at most %d K-slices", MAX_SLICES);
+    const int32_t ups = ceil_div(units, slices);
+    slices = ceil_div(units, ups);
+    const int32_t wave_units = ceil_div(ups, WAVES);
+    if (static_cast<size_t>(wave_units) * WAVES * (4 * UNIT * 2 + 16) > LDS_X_BYTES)
+        return fail(KT_ERR_ARGUMENT, "wide gemv: K-slice too long for the x area");
+
+    size_t ws_floats = 0, n_counters = 0;
+    if (slices > 1)
+        for (int32_t i = 0; i < count; ++i) {
+            ws_floats += static_cast<size_t>(slices) * ws[i].N;
+            n_counters += ceil_div(ws[i].bpr, TILE);
+        }
+    float* partials = nullptr;
+    uint32_t* counters = nullptr;
+    if (ws_floats) {
+        if (n_counters > MAX_COUNTERS) return fail(KT_ERR_ARGUMENT, "wide gemv: too many tiles for the counters");
+        void* p = nullptr;
+        const int32_t status = workspace_counters(st, ws_floats * sizeof(float), n_counters, &p, &counters);
+        if (status) return status;
+        partials = static_cast<float*>(p);
+    }
+    Jobs jobs{};
+    jobs.count = count;
+    int32_t blocks = 0;
+    size_t offset = 0, coffset = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        Job& jb = jobs.job[i];
+        jb.q = ws[i].q;
+        jb.s = ws[i].s;
+        jb.z = ws[i].z;
+        jb.out = cs[i];
+        jb.bias = biases ? biases[i] : nullptr;
+        jb.N = ws[i].N;
+        jb.bpr = ws[i].bpr;
+        jb.tiles = ceil_div(ws[i].bpr, TILE);
+        jb.slices = slices;
+        jb.units_per_slice = ups;
+        jb.partials = slices > 1 ? partials + offset : nullptr;
+        jb.counters = slices > 1 ? counters + coffset : nullptr;
+        offset += static_cast<size_t>(slices) * ws[i].N;
+        coffset += jb.tiles;
+        if (jb.tiles * slices > blocks) blocks = jb.tiles * slices;
+    }
+    const int sides = ws[0].bits == 4 ? 2 : 1;
+    const size_t lds_x = static_cast<size_t>(wave_units) * WAVES * (4 * UNIT * 2 + 16);
+    const size_t lds_red = static_cast<size_t>(WAVES) * sides * TILE * sizeof(float);
+    const size_t lds = lds_x > lds_red ? lds_x : lds_red;
+    const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
+    if (ws[0].bits == 4) launch_bits<4>(zp, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
+    else launch_bits<8>(zp, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
+    KT_LAUNCHED("qmatmul: wide gemv kernel");
+    return KT_OK;
+}
+
+}  // namespace kt
