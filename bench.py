@@ -6,21 +6,27 @@ decoder layer plus its lm_head -- q/o 896->896, k/v 896->128, gate/up 896->4864,
 down 4864->896, lm_head 896->151936 -- with x ~ N(0,1) fp32 and W ~ N(0, 0.02)
 quantized on the device by kt_quantize (the reference layout: qdata [K x N/2],
 fp32 scales and u8 zeros [K/64 x N]). Inputs are resident in HBM before timing.
-Each step uses a different copy of the weight set so that the timed loop streams
-more than twice the 256 MB Infinity Cache. A step's eight launches are captured
-in a HIP graph (one graph per weight copy) and replayed.
+q/k/v (one input) and gate/up (one input) each go out as one grouped launch
+(kt_qmatmul_group), o, down and lm_head as one launch each. Each step uses a
+different copy of the weight set so that the timed loop streams more than twice
+the 256 MB Infinity Cache; a step's launches are captured in a HIP graph (one graph
+per weight copy) and replayed.
 
 value = algorithmic bytes of a step / measured step time (GB/s). Algorithmic bytes
 per GEMV = K*bytesPerRow + 4*groups*N + groups*N (zeros) + 4*K (x) + 4*N (y).
 
 The JSON line also carries:
-  roofline      -- the dominant kernel (the lm_head GEMV), timed per launch with
-                   HIP events on the launch stream, against 8 TB/s;
+  roofline      -- the dominant kernel (the lm_head GEMV): back-to-back launches in a
+                   graph on the launch stream, HIP events around the timed replays,
+                   against 8 TB/s; traffic from rocprofv3 PMC runs (profiles/);
   cpu_baseline  -- the oracle (C restatement of MatMul.multiplyQuantized, M == 1
                    unit schedule, work-stealing threads) on the same workload;
   extra         -- the two targets of the workload family: INT4 GEMV on the
                    Llama-3-8B FFN shape (4096->14336) and the INT8 prefill GEMM at
-                   M = 512 (2048->8192), each with its roofline fraction.
+                   M = 512 (2048->8192, 8192->2048), each with its roofline fraction.
+
+--only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
+calibration of the HBM byte counters) for rocprofv3 PMC runs.
 """
 from __future__ import annotations
 
@@ -96,19 +102,31 @@ def qmatmul(kt_lib, x, m, w, y, stream):
     kt_lib.call("kt_qmatmul", x.data_ptr(), m, ctypes.byref(w.struct), y.data_ptr(), 0, ctypes.c_float(1.0), stream)
 
 
-def time_per_launch(torch, fn, copies, launches):
-    """Average duration of one launch, events recorded on the launch stream around each."""
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+def qmatmul_group(kt_lib, x, m, ws, ys, stream):
+    """Products of one input with up to four weights in one launch (kt_qmatmul_group)."""
+    n = len(ws)
+    structs = (kt_lib.QWeight * n)(*[w.struct for w in ws])
+    outs = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    kt_lib.call("kt_qmatmul_group", x.data_ptr(), m, structs, n, outs, None, 0, ctypes.c_float(1.0), stream)
+
+
+def time_graph_launches(torch, stream_obj, fn, copies, launches, replays=3):
+    """Average duration of one launch: `launches` back-to-back launches (rotating weight
+    copies) captured in one graph, HIP events on the launch stream around the replays."""
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph, stream=stream_obj):
+        for i in range(launches):
+            fn(copies[i % len(copies)])
+    gph.replay()
     torch.cuda.synchronize()
-    for i in range(launches):
-        starts[i].record(stream)
-        fn(copies[i % len(copies)])
-        ends[i].record(stream)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream_obj)
+    for _ in range(replays):
+        gph.replay()
+    t1.record(stream_obj)
     torch.cuda.synchronize()
-    times = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return sum(times) / len(times), times[len(times) // 2]
+    return t0.elapsed_time(t1) / (replays * launches)
 
 
 def cpu_baseline(seconds: float = 10.0):
@@ -165,6 +183,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 8B GEMV and M=512 GEMM figures")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=["dominant", "copy"], help="run one kernel for a rocprofv3 PMC run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -183,7 +202,35 @@ def main() -> int:
     # A dedicated stream: every launch, event and graph capture below runs on it.
     stream_obj = torch.cuda.Stream()
     with torch.cuda.stream(stream_obj):
+        if args.only:
+            return run_only(args, torch, kt_lib, stream_obj)
         return run(args, torch, kt_lib, stream_obj)
+
+
+def run_only(args, torch, kt_lib, stream_obj) -> int:
+    """One kernel, args.steps times, for hardware-counter runs (one dispatch per launch)."""
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    if args.only == "copy":
+        # calibration: 256 MiB read + 256 MiB written per launch
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
+                          "launches": args.steps}), flush=True)
+        return 0
+    w = Weight(torch, kt_lib, 896, 151936, 4, 64, seed=8, stream=stream)
+    copies = [w] + [w.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // w.nbytes)) - 1)]
+    x = torch.randn((1, 896), device="cuda", dtype=torch.float32)
+    y = torch.empty((1, 151936), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        qmatmul(kt_lib, x, 1, copies[i % len(copies)], y, stream)
+    torch.cuda.synchronize()
+    print(json.dumps({"only": "dominant", "kernel": "lm_head 896x151936 int4 g64 M=1",
+                      "algorithmic_bytes": gemv_bytes(1, 896, 151936, 4, 64), "launches": args.steps}), flush=True)
+    return 0
 
 
 def run(args, torch, kt_lib, stream_obj) -> int:
@@ -201,8 +248,12 @@ def run(args, torch, kt_lib, stream_obj) -> int:
     torch.cuda.synchronize()
 
     def step(ws):
-        for i, (_, k, n) in enumerate(QWEN):
-            qmatmul(kt_lib, xs[k], 1, ws[i], ys[i], stream)
+        # q, k, v share x; gate, up share x: one grouped launch each
+        qmatmul_group(kt_lib, xs[896], 1, ws[0:3], ys[0:3], stream)
+        qmatmul(kt_lib, xs[896], 1, ws[3], ys[3], stream)
+        qmatmul_group(kt_lib, xs[896], 1, ws[4:6], ys[4:6], stream)
+        qmatmul(kt_lib, xs[4864], 1, ws[6], ys[6], stream)
+        qmatmul(kt_lib, xs[896], 1, ws[7], ys[7], stream)
 
     # eager warm-up (allocates the library's per-stream workspace before capture)
     for r in range(copies):
@@ -230,16 +281,16 @@ def run(args, torch, kt_lib, stream_obj) -> int:
     step_bytes = sum(gemv_bytes(1, k, n, bits, g) for _, k, n in QWEN)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- dominant kernel: the lm_head GEMV, per launch
+    # ---- dominant kernel: the lm_head GEMV, back-to-back launches on the launch stream
     head = [s[-1] for s in sets]
     head_y = ys[-1]
     head_bytes = gemv_bytes(1, 896, 151936, bits, g)
-    avg_ms, med_ms = time_per_launch(torch, lambda w: qmatmul(kt_lib, xs[896], 1, w, head_y, stream), head, 100)
+    avg_ms = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xs[896], 1, w, head_y, stream), head, 60)
     achieved = head_bytes / (avg_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "gemv_kernel<4,*> lm_head 896x151936 int4 g64",
-                "algorithmic_bytes": head_bytes, "avg_us": round(avg_ms * 1e3, 3), "median_us": round(med_ms * 1e3, 3)}
+                "kernel": "gemv_wide_kernel<4,4,true> (lm_head 896x151936 int4 g64 M=1)",
+                "algorithmic_bytes": head_bytes, "avg_us": round(avg_ms * 1e3, 3)}
 
     extra = {}
     if not args.no_extra:
@@ -251,11 +302,11 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         y8 = torch.empty((1, 14336), device="cuda", dtype=torch.float32)
         for w in c8:
             qmatmul(kt_lib, x8, 1, w, y8, stream)
-        a8, m8 = time_per_launch(torch, lambda w: qmatmul(kt_lib, x8, 1, w, y8, stream), c8, 100)
+        a8 = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, x8, 1, w, y8, stream), c8, 64)
         b8 = gemv_bytes(1, 4096, 14336, 4, 64)
         extra["int4_gemv_llama8b_ffn_4096x14336"] = {
             "GB/s": round(b8 / (a8 * 1e-3) / 1e9, 1), "frac_hbm": round(b8 / (a8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "avg_us": round(a8 * 1e3, 3), "median_us": round(m8 * 1e3, 3), "bytes": b8, "copies": n8}
+            "avg_us": round(a8 * 1e3, 3), "bytes": b8, "copies": n8}
         del c8, w8
         # INT8 prefill GEMM at M = 512
         for (k, n) in [(2048, 8192), (8192, 2048)]:
@@ -266,11 +317,11 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             yg = torch.empty((512, n), device="cuda", dtype=torch.float32)
             for w in cg:
                 qmatmul(kt_lib, xg, 512, w, yg, stream)
-            ag, mg = time_per_launch(torch, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 50)
+            ag = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 32)
             tflops = 2.0 * 512 * k * n / (ag * 1e-3) / 1e12
             extra[f"int8_gemm_m512_{k}x{n}"] = {
                 "TFLOP/s": round(tflops, 1), "frac_mfma": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                "avg_us": round(ag * 1e3, 3), "median_us": round(mg * 1e3, 3), "copies": ng}
+                "avg_us": round(ag * 1e3, 3), "copies": ng}
             del cg, wg
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -288,6 +339,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         "dtype": "f32",
         "data": "synthetic: x ~ N(0,1) fp32, W ~ N(0,0.02) fp32 quantized on device (seeded)",
         "config": {"workload": "qwen2-0.5b int4 g64 M=1 projection GEMVs (q,k,v,o,gate,up,down,lm_head)",
+                   "launches_per_step": 5,
                    "weights": "uint4 + fp32 scales + u8 zeros, reference layout", "group_size": g, "m": 1,
                    "step_bytes": step_bytes, "weight_copies": copies, "graph_replay": True},
         "roofline": roofline,
