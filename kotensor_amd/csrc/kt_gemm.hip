@@ -1,4 +1,4 @@
-// kt_gemm.hip -- prefill dequant-GEMM (M >= 2) on gfx950 MFMA:
+// kt_gemm.hip -- prefill dequant-GEMM (M >= 3) on gfx950 MFMA:
 //   c[M x N] = (accumulate ? c : 0) + alpha * a[M x K] . deq(W) (+ bias),
 // the M > 1 branch of MatMul.multiplyQuantized (Engine/kotensor/src/main/kotlin/
 // MatMul.kt:479-485 -> computeQuantizedTile :830-881).
@@ -6,38 +6,59 @@
 // Numerics. The operands go to v_mfma_f32_32x32x16_f16 as fp16 with fp32
 // accumulation. Two exact power-of-two rescalings keep fp16 in its normal range
 // whatever the data: row m of a is multiplied by 2^-er[m] so its largest magnitude
-// lies in [2^14, 2^15), and column n of the weight by 2^-ec[n] so its largest
-// group scale lies in [1/2, 1). A weight element enters the MFMA as
-// fp16((q - zero) * scale * 2^-ec[n]) (q and zero exact integers), and the fp32
-// result is multiplied back by 2^(er[m] + ec[n]). The rounding of a and of the
-// dequantized weight to fp16 (relative 2^-11 each) keeps the normwise error far
-// below the 2e-3 the path is held to.
+// lies in [2^14, 2^15), and every scale of the weight by 2^-ew so that the largest
+// scale lies in [2^6, 2^7) (so |q - zero| <= 255 times it stays below 2^15). A
+// weight element enters the MFMA as (q - zero) * fp16(scale * 2^-ew) rounded once to
+// fp16 (q - zero is an exact small integer), and the fp32 result is multiplied back
+// by 2^(er[m] + ew). The roundings of a, of the scale and of the product to fp16
+// (relative 2^-11 each) keep the normwise error far below the 2e-3 the path is held
+// to; scales more than 2^20 below the largest one become fp16 subnormals and lose
+// relative precision, but their products are that much below the largest ones.
 //
-// Work layout. A pre-pass kernel writes the fp16 copy of a (zero-padded to whole
-// tiles, so tile loads need no bounds checks) and the two exponent vectors. The
-// GEMM kernel computes a 128 x 128 output tile per 256-thread workgroup (four waves
-// in a 2 x 2 arrangement, 64 x 64 each as 2 x 2 MFMA 32x32 blocks) over K in steps
-// of 32: a's tile is copied to LDS; the weight tile's packed bytes are loaded
-// (INT8: 128 bytes x 32 rows; INT4: 64 bytes x 32 rows = 64 low-nibble plus 64
-// high-nibble columns, so every packed byte is read once per row tile),
-// dequantized in registers and stored to LDS transposed (k contiguous) in the
-// order the MFMA B operand reads it.
+// Pre-pass. One kernel writes the fp16 copy of a (zero-padded to whole tiles, so tile
+// loads need no bounds checks) and er, one block per row reading the row once, and
+// the largest scale magnitude of each slice of the scale array.
+//
+// GEMM. A 256-thread workgroup computes a 128 x 128 output tile (four waves in a
+// 2 x 2 arrangement, 64 x 64 each as 2 x 2 MFMA 32x32 blocks) over K in steps of 64.
+// Two LDS stages hold a and the dequantized weights of two steps; the global loads
+// run two steps ahead in two register sets, so a step's data has two steps of MFMA
+// time to arrive. Dequantization works on pairs of rows of one column: v_perm_b32
+// puts the two bytes in the low bytes of the two halves of a word, and OR-ing (INT4
+// nibble) or XOR-adding (INT8 byte + 128) the fp16 exponent of 1024 turns each half
+// into the exact fp16 integer B + q; one packed fp16 add of -(B + zero) and one packed
+// multiply by the scale give two weights, stored k-contiguous as the MFMA B operand
+// reads them. INT8 tiles are 128 byte columns; INT4 tiles are 64 bytes = 64
+// low-nibble plus 64 high-nibble columns, so every packed byte is read once per row
+// tile. Workgroups that share a weight tile are numbered to land on one XCD (blocks
+// are dealt to the eight XCDs round-robin), so the weight tile is fetched into one
+// L2. When the tile grid is smaller than the GPU, K is split and a second kernel adds
+// the slices in slice order.
+#include <type_traits>
+
 #include "kt_common.h"
 
 namespace kt {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 32;
-constexpr int PITCH = BK + 8;  // halfs per LDS row (16-byte pad)
+constexpr int BK = 64;
+constexpr int PITCH = BK + 8;  // halfs per LDS row (16-byte pad: conflict-free fragment reads)
+constexpr int STAGE = (BM + BN) * PITCH;  // halfs per LDS stage
+constexpr int XCDS = 8;
+constexpr int MAX_SPLITS = 8;
+constexpr int DEPTH = 4;  // K steps whose loads are in flight
+constexpr int ROW_CHUNKS = 16;       // float4 chunks of a row each pre-pass thread keeps in registers
+constexpr int MAX_SCALE_BLOCKS = 256;  // pre-pass blocks over the scales (one maximum each)
 
-// Largest-magnitude based exponent: returns e with max * 2^-e in [2^(top-1), 2^top).
+// e such that max_abs * 2^-e lies in [2^(top-1), 2^top); 0 for zero or non-finite input.
 __device__ __forceinline__ int32_t scale_exponent(float max_abs, int32_t top) {
     if (!(max_abs > 0.0f) || !isfinite(max_abs)) return 0;
     int e = 0;
@@ -45,189 +66,462 @@ __device__ __forceinline__ int32_t scale_exponent(float max_abs, int32_t top) {
     return e - top;
 }
 
-// Blocks [0, Mp): fp16 rows of a. Blocks [Mp, Mp + ceil(N/256)): column exponents.
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+    const half2v h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Maximum over the threads of a block of WAVES waves, returned to every thread.
+template <int WAVES>
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < WAVES; ++i) m = fmaxf(m, red[i]);
+    return m;
+}
+
+// Chunk c (4 floats) of a row of K floats; zero past the end.
+__device__ __forceinline__ f32x4 row_chunk(const float* row, int32_t c, int32_t K, bool vec) {
+    const int32_t k = 4 * c;
+    if (vec) return k < K ? *reinterpret_cast<const f32x4*>(row + k) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = k + i < K ? row[k + i] : 0.0f;
+    return v;
+}
+
+// Blocks [0, Mp): row m of a as fp16 times 2^-er[m] (zeros for m >= M and k >= K).
+// Blocks [Mp, Mp + nsb): the largest |scale| over one slice of the G * N scales.
 __global__ void __launch_bounds__(256)
-    gemm_prep(const float* __restrict__ a, int32_t M, int32_t K, int32_t Mp, int32_t Kp, const float* __restrict__ s,
-              int32_t G, int32_t N, _Float16* __restrict__ a16, int32_t* __restrict__ er, int32_t* __restrict__ ec) {
-    __shared__ float red[256];
+    gemm_prep(const float* __restrict__ a, int32_t M, int32_t K, int32_t Kp, int32_t vec_rows, int32_t Mp,
+              const float* __restrict__ s, int64_t scale_quads, int32_t nsb, _Float16* __restrict__ a16,
+              int32_t* __restrict__ er, float* __restrict__ smax) {
+    __shared__ float red[4];
     const int32_t t = threadIdx.x;
-    if (static_cast<int32_t>(blockIdx.x) < Mp) {
-        const int32_t m = blockIdx.x;
-        _Float16* dst = a16 + static_cast<size_t>(m) * Kp;
+    const int32_t b = blockIdx.x;
+    if (b < Mp) {
+        const int32_t m = b;
+        const int32_t chunks = Kp / 4;
+        uint2* dst = reinterpret_cast<uint2*>(a16 + static_cast<size_t>(m) * Kp);
         if (m >= M) {
-            for (int32_t k = t; k < Kp; k += 256) dst[k] = static_cast<_Float16>(0.0f);
+            for (int32_t cc = t; cc < chunks; cc += 256) dst[cc] = make_uint2(0, 0);
             if (t == 0) er[m] = 0;
             return;
         }
         const float* row = a + static_cast<size_t>(m) * K;
+        const bool vec = vec_rows != 0;  // K % 4 == 0 and a 16-byte aligned
+        f32x4 v[ROW_CHUNKS];
         float mx = 0.0f;
-        for (int32_t k = t; k < K; k += 256) mx = fmaxf(mx, fabsf(row[k]));
-        red[t] = mx;
-        __syncthreads();
-        for (int32_t w = 128; w > 0; w >>= 1) {
-            if (t < w) red[t] = fmaxf(red[t], red[t + w]);
-            __syncthreads();
+#pragma unroll
+        for (int i = 0; i < ROW_CHUNKS; ++i) {
+            const int32_t cc = t + 256 * i;
+            v[i] = cc < chunks ? row_chunk(row, cc, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
         }
-        const int32_t e = scale_exponent(red[0], 15);
-        const float mul = ldexpf(1.0f, -e);
-        for (int32_t k = t; k < Kp; k += 256) dst[k] = static_cast<_Float16>(k < K ? row[k] * mul : 0.0f);
+        for (int32_t cc = t + 256 * ROW_CHUNKS; cc < chunks; cc += 256) {  // rows longer than 16384
+            const f32x4 u = row_chunk(row, cc, K, vec);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3]))));
+        }
+        const int32_t e = scale_exponent(block_max<4>(mx, red), 15);
+#pragma unroll
+        for (int i = 0; i < ROW_CHUNKS; ++i) {
+            const int32_t cc = t + 256 * i;
+            if (cc < chunks)
+                dst[cc] = make_uint2(pack_half2(ldexpf(v[i][0], -e), ldexpf(v[i][1], -e)),
+                                     pack_half2(ldexpf(v[i][2], -e), ldexpf(v[i][3], -e)));
+        }
+        for (int32_t cc = t + 256 * ROW_CHUNKS; cc < chunks; cc += 256) {
+            const f32x4 u = row_chunk(row, cc, K, vec);
+            dst[cc] = make_uint2(pack_half2(ldexpf(u[0], -e), ldexpf(u[1], -e)),
+                                 pack_half2(ldexpf(u[2], -e), ldexpf(u[3], -e)));
+        }
         if (t == 0) er[m] = e;
         return;
     }
-    const int32_t n = (blockIdx.x - Mp) * 256 + t;
-    if (n >= N) return;
+    // Scales: G * N is a multiple of 4 and s is 16-byte aligned (checked by gemm_supported).
+    const int32_t sb = b - Mp;
+    const int64_t per = (scale_quads + nsb - 1) / nsb;
+    const int64_t begin = per * sb;
+    const int64_t end = begin + per < scale_quads ? begin + per : scale_quads;
     float mx = 0.0f;
-    for (int32_t gi = 0; gi < G; ++gi) mx = fmaxf(mx, fabsf(s[static_cast<size_t>(gi) * N + n]));
-    ec[n] = scale_exponent(mx, 0);
+#pragma unroll 8
+    for (int64_t i = begin + t; i < end; i += 256) {
+        const f32x4 u = reinterpret_cast<const f32x4*>(s)[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3]))));
+    }
+    mx = block_max<4>(mx, red);
+    if (t == 0) smax[sb] = mx;
 }
 
+// Work split of the 512 threads per K step: a is 1024 chunks of 8 halfs (two per
+// thread); the weight tile is 64 rows x 32 lanes of column bytes (INT8: 4 bytes =
+// 4 columns; INT4: 2 bytes = 2 low-nibble + 2 high-nibble columns), each thread
+// taking 4 consecutive rows of one lane's bytes, which lie in one scale group
+// (g % 4 == 0).
+constexpr int THREADS = 512;
+constexpr int WROWS = 4;
+
 template <int BITS>
-__global__ void __launch_bounds__(256)
+struct WTile {
+    static constexpr int BYTES = BITS == 8 ? 4 : 2;  // weight bytes per row and thread
+    static constexpr int COLS = BITS == 8 ? 4 : 2;   // byte columns per thread
+    static constexpr int SIDES = BITS == 8 ? 1 : 2;
+};
+
+// The global data of one K step held by a thread.
+template <int BITS>
+struct StepRegs {
+    u32x4 a[2];                     // 2 x 8 fp16 of a
+    uint32_t w[WROWS];              // the thread's weight bytes of each row
+    f32x4 s[WTile<BITS>::SIDES];    // scales of the thread's columns (per side)
+    uint32_t z[WTile<BITS>::SIDES]; // zero points of the thread's columns (per side)
+};
+
+// Bytes j of words lo and hi in the low bytes of the two halves of a word.
+__device__ __forceinline__ uint32_t pair_bytes(uint32_t lo, uint32_t hi, int j) {
+    // v_perm_b32(S0 = hi, S1 = lo): selector bytes 0..3 pick lo's bytes, 4..7 hi's, 0x0c is 0.
+    const uint32_t sel = 0x0c000c00u | (static_cast<uint32_t>(4 + j) << 16) | static_cast<uint32_t>(j);
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// A constant held in a VGPR: (v & mask) | bits and (v ^ a) + b with such operands are
+// one v_and_or_b32 / v_xad_u32 each. Only vector ALU instructions read the result.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+    return r;
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+template <int N_>
+__device__ __forceinline__ f32x4 load_scales(const float* p) {
+    if constexpr (N_ == 4) return *reinterpret_cast<const f32x4*>(p);
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    return f32x4{v.x, v.y, 0.0f, 0.0f};
+}
+
+template <int N_>
+__device__ __forceinline__ uint32_t load_bytes(const void* p) {
+    if constexpr (N_ == 4) return *reinterpret_cast<const uint32_t*>(p);
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// The 8 waves split each K step: waves 0-3 multiply k 0..31 of it, waves 4-7 k 32..63,
+// each wave a 64 x 64 block of the tile (2 x 2 waves per half). The two halves' sums
+// are added through LDS at the end. Two waves per SIMD let one wave's dequantization
+// and waits overlap the other's MFMAs.
+// FAST: K % BK == 0 and the group size divides BK or is a multiple of it, so every
+// load of a step is a uniform base plus an offset fixed per lane (no per-step address
+// arithmetic and no clamping); otherwise rows and groups are computed per step.
+template <int BITS, bool ZP, bool FAST>
+__global__ void __launch_bounds__(THREADS, 1)
     gemm_kernel(const _Float16* __restrict__ a16, int32_t Kp, const int32_t* __restrict__ er,
-                const int32_t* __restrict__ ec, const uint8_t* __restrict__ q, const float* __restrict__ s,
-                const int8_t* __restrict__ z, int32_t M, int32_t K, int32_t N, int32_t bpr, int32_t g,
-                int32_t tiles_n, float* __restrict__ c, const float* __restrict__ bias, float alpha,
+                const float* __restrict__ smax, int32_t nsb, const uint8_t* __restrict__ q,
+                const float* __restrict__ s, const int8_t* __restrict__ z, int32_t M, int32_t K, int32_t N,
+                int32_t bpr, int32_t g, int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t steps_per_split,
+                float* __restrict__ c, float* __restrict__ partials, const float* __restrict__ bias, float alpha,
                 int32_t accumulate) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[BM * PITCH];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * PITCH];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * STAGE];
+    __shared__ int32_t er_s[BM];
+    __shared__ float red[THREADS / 64];
+    constexpr int BYTES = WTile<BITS>::BYTES;
+    constexpr int COLS = WTile<BITS>::COLS;
+    constexpr int SIDES = WTile<BITS>::SIDES;
+
+    // Block -> (tile_n, tile_m, slice): blocks d, d + 8, d + 16, ... run on XCD d, and
+    // consecutive ones of them take the row tiles and K slices of one weight tile.
+    const int32_t pid = blockIdx.x;
+    const int32_t j = pid / XCDS;
+    const int32_t per_n = tiles_m * splits;
+    const int32_t tile_n = (j / per_n) * XCDS + pid % XCDS;
+    if (tile_n >= tiles_n) return;
+    const int32_t rem = j % per_n;
+    const int32_t tile_m = rem % tiles_m;
+    const int32_t sp = rem / tiles_m;
+    const int32_t k_steps = (K + BK - 1) / BK;
+    const int32_t ks0 = sp * steps_per_split;
+    const int32_t n_steps = min(steps_per_split, k_steps - ks0);  // >= 1 by the host's split count
 
     const int32_t t = threadIdx.x;
     const int32_t ln = t & 63;
     const int32_t wave = t >> 6;
-    const int32_t wm = wave >> 1, wn = wave & 1;
-    const int32_t tile_m = blockIdx.x / tiles_n;
-    const int32_t tile_n = blockIdx.x % tiles_n;
+    const int32_t kh = __builtin_amdgcn_readfirstlane(wave >> 2);  // which half of each K step this wave multiplies
+    const int32_t wm = (wave >> 1) & 1, wn = wave & 1;
     const int32_t m0 = tile_m * BM;
-    const int32_t half = bpr;
-    // Byte columns of this tile: INT8 [b0, b0 + 128); INT4 [b0, b0 + 64) holding
-    // low-nibble columns b0.. and high-nibble columns half + b0.. .
-    const int32_t b0 = tile_n * (BITS == 8 ? BN : BN / 2);
+    const int32_t b0 = tile_n * (BITS == 8 ? BN : BN / 2);  // first byte column of the tile
 
-    // Weight-tile assignment: INT8 thread -> 4 byte columns x 4 rows; INT4 -> 4 bytes x 2 rows.
-    constexpr int ROWS_PER_T = BITS == 8 ? 4 : 2;
-    constexpr int COLQ = BITS == 8 ? 32 : 16;  // 4-byte column quads per tile row
-    const int32_t cq = t % COLQ;
-    const int32_t rg = t / COLQ;
-    const int32_t bcol = b0 + cq * 4;  // first byte column of this thread
-    const bool bvalid = bcol < bpr;
+    // Lane l of wave w takes byte group cq = l % 16 + 16 (l / 32) of rows rg * 4 .. rg * 4 + 3,
+    // rg = 2 w + (l / 16) % 2. Its column j of the group goes to row 32 j + cq of the
+    // dequantized tile (64 + ... for INT4 high nibbles), so the 32 lanes of a half-wave
+    // write 16 consecutive rows at two k offsets: the 64 LDS banks exactly once.
+    const int32_t cq = (t & 15) + ((t >> 1) & 16);
+    const int32_t rg = ((t >> 6) << 1) + ((t >> 4) & 1);
+    const int32_t bcol = b0 + cq * BYTES < bpr ? b0 + cq * BYTES : 0;  // bpr % 4 == 0: byte groups are whole
+
+    // Byte offsets fixed per lane.
+    uint32_t a_off[2], w_off[WROWS];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) a_off[i] = (static_cast<uint32_t>((t >> 3) + 64 * i) * Kp + (t & 7) * 8) * 2u;
+#pragma unroll
+    for (int i = 0; i < WROWS; ++i) w_off[i] = static_cast<uint32_t>(rg * WROWS + i) * bpr + bcol;
+    const uint32_t s_idx = static_cast<uint32_t>(g < BK ? (rg * WROWS) / g : 0) * N + bcol;
+    const char* a_tile = reinterpret_cast<const char*>(a16 + static_cast<size_t>(m0) * Kp);
+
+    auto load_step = [&](StepRegs<BITS>& r, int32_t step) {
+        const int32_t k0 = (ks0 + step) * BK;
+        const char* ab = a_tile + static_cast<size_t>(k0) * 2;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) r.a[i] = *reinterpret_cast<const u32x4*>(ab + a_off[i]);
+        if constexpr (FAST) {
+            const uint8_t* wb = q + static_cast<size_t>(k0) * bpr;
+#pragma unroll
+            for (int i = 0; i < WROWS; ++i) r.w[i] = load_bytes<BYTES>(wb + w_off[i]);
+            const size_t gbase = static_cast<size_t>(k0 / g) * N;
+#pragma unroll
+            for (int side = 0; side < SIDES; ++side) {
+                r.s[side] = load_scales<COLS>(s + gbase + s_idx + (side ? bpr : 0));
+                if constexpr (ZP) r.z[side] = load_bytes<BYTES>(z + gbase + s_idx + (side ? bpr : 0));
+            }
+        } else {
+            const int32_t kr = k0 + rg * WROWS;
+#pragma unroll
+            for (int i = 0; i < WROWS; ++i) {
+                const int32_t row = kr + i < K ? kr + i : K - 1;  // a is zero on rows >= K
+                r.w[i] = load_bytes<BYTES>(q + static_cast<size_t>(row) * bpr + bcol);
+            }
+            const size_t at = static_cast<size_t>((kr < K ? kr : K - 1) / g) * N + bcol;
+#pragma unroll
+            for (int side = 0; side < SIDES; ++side) {
+                r.s[side] = load_scales<COLS>(s + at + (side ? bpr : 0));
+                if constexpr (ZP) r.z[side] = load_bytes<BYTES>(z + at + (side ? bpr : 0));
+            }
+        }
+    };
+
+    // The slice maxima of the scales and the row exponents are loaded first, then the
+    // first DEPTH steps: loads complete in order, so waiting for the former does not
+    // wait for the latter.
+    const float smx = t < nsb ? smax[t] : 0.0f;  // nsb <= 256
+    const int32_t erv = t < BM && m0 + t < M ? er[m0 + t] : 0;
+    __builtin_amdgcn_sched_barrier(0);
+    StepRegs<BITS> r[DEPTH];
+    const int32_t last = n_steps - 1;
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load_step(r[d], min(d, last));
+    __builtin_amdgcn_sched_barrier(0);
+    if (t < BM) er_s[t] = erv;
+    const int32_t ew = scale_exponent(block_max<THREADS / 64>(smx, red), 7);
+
+    const uint32_t flip = in_vgpr(0x00800080u), exp1024 = in_vgpr(0x64006400u);
+    const uint32_t mask_lo = in_vgpr(0x000F000Fu), mask_hi = in_vgpr(0x00F000F0u);
+
+    auto store_a = [&](const StepRegs<BITS>& rs, int32_t stage) {
+        _Float16* As = lds + stage * STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(As + ((t >> 3) + 64 * i) * PITCH + (t & 7) * 8) = rs.a[i];
+    };
+    // Dequantizes piece p (0..3) of the thread's weight bytes into a stage: INT8 column
+    // p; INT4 byte column p / 2, low nibbles for even p and high nibbles for odd p.
+    auto store_piece = [&](const StepRegs<BITS>& rs, int32_t stage, int p) {
+        _Float16* Bs = lds + stage * STAGE + BM * PITCH;
+        const int jq = BITS == 8 ? p : p >> 1;
+        const int side = BITS == 8 ? 0 : p & 1;
+        const uint32_t pr0 = pair_bytes(rs.w[0], rs.w[1], jq), pr1 = pair_bytes(rs.w[2], rs.w[3], jq);
+        // INT4 high nibbles enter as 1024 + 16 q: the offset is -(1024 + 16 zero) and the
+        // scale is divided by 16, which is exact, so the product is the same.
+        const float sc = ldexpf(rs.s[side][jq], side ? -ew - 4 : -ew);
+        const half2v scv = {static_cast<_Float16>(sc), static_cast<_Float16>(sc)};
+        // -(B + zero) in both halves: the zero byte under the fp16 bits of -1024 (INT4,
+        // zero in [0, 15]) or of -1024 - (zero + 128) (INT8, signed zero).
+        uint32_t off;
+        if constexpr (!ZP) {
+            off = 0xE480E480u;  // -1152
+        } else {
+            const uint32_t zz = pair_bytes(rs.z[side], rs.z[side], jq);
+            if constexpr (BITS == 8) off = (zz ^ flip) + 0xE400E400u;
+            else off = side ? (zz << 4) | 0xE400E400u : zz | 0xE400E400u;
+        }
+        const half2v ofv = as_h2(off);
+        uint32_t x0, x1;
+        if constexpr (BITS == 8) {
+            x0 = (pr0 ^ flip) + exp1024;
+            x1 = (pr1 ^ flip) + exp1024;
+        } else {
+            x0 = (pr0 & (side ? mask_hi : mask_lo)) | exp1024;
+            x1 = (pr1 & (side ? mask_hi : mask_lo)) | exp1024;
+        }
+        const uint32_t h0 = __builtin_bit_cast(uint32_t, (as_h2(x0) + ofv) * scv);
+        const uint32_t h1 = __builtin_bit_cast(uint32_t, (as_h2(x1) + ofv) * scv);
+        const int32_t nl = side * (BN / 2) + jq * 32 + cq;
+        *reinterpret_cast<uint2*>(Bs + nl * PITCH + rg * WROWS) = make_uint2(h0, h1);
+    };
 
     float16v acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int e = 0; e < 16; ++e) acc[i][jj][e] = 0.0f;
 
-    for (int32_t k0 = 0; k0 < K; k0 += BK) {
-        // a tile: 128 rows x 32 halfs; thread -> row t/2, 16 halfs at (t&1)*16.
-        {
-            const int32_t r = t >> 1;
-            const int32_t kc = (t & 1) * 16;
-            const uint4* src = reinterpret_cast<const uint4*>(a16 + static_cast<size_t>(m0 + r) * Kp + k0 + kc);
-            uint4 v0 = src[0], v1 = src[1];
-            uint4* dst = reinterpret_cast<uint4*>(As + r * PITCH + kc);
-            dst[0] = v0;
-            dst[1] = v1;
-        }
-        // weight tile: load, dequantize, store transposed.
-        {
-            const int32_t kr = k0 + rg * ROWS_PER_T;  // all ROWS_PER_T rows share one group (g % 4 == 0)
-            uint32_t w[ROWS_PER_T];
+    // One step: the MFMAs of stage `cur` (this wave's half of the step's K) alternate
+    // with the dequantization of the next step's registers into stage `nxt`, in a fixed
+    // order (sched_barrier) so the matrix and vector units work at the same time.
+    auto step = [&](int32_t cur, const StepRegs<BITS>& rs, int32_t nxt, auto dequant) {
+        constexpr bool DQ = decltype(dequant)::value;
+        const _Float16* As = lds + cur * STAGE;
+        const _Float16* Bs = As + BM * PITCH;
+        half8 af[2][2], bf[2][2];
 #pragma unroll
-            for (int i = 0; i < ROWS_PER_T; ++i)
-                w[i] = (bvalid && kr + i < K) ? *reinterpret_cast<const uint32_t*>(q + static_cast<size_t>(kr + i) * bpr + bcol) : 0u;
-            const int32_t gi = (kr < K ? kr : K - 1) / g;
-            const float* srow = s + static_cast<size_t>(gi) * N;
-            const int8_t* zrow = z ? z + static_cast<size_t>(gi) * N : nullptr;
-#pragma unroll
-            for (int side = 0; side < (BITS == 4 ? 2 : 1); ++side) {
-                const int32_t col = side ? half + bcol : bcol;
-                float sc[4] = {0.f, 0.f, 0.f, 0.f};
-                int32_t zr[4] = {0, 0, 0, 0};
-                if (bvalid && kr < K) {
-                    const float4 s4 = *reinterpret_cast<const float4*>(srow + col);
-                    const int4 e4 = *reinterpret_cast<const int4*>(ec + col);
-                    sc[0] = ldexpf(s4.x, -e4.x);
-                    sc[1] = ldexpf(s4.y, -e4.y);
-                    sc[2] = ldexpf(s4.z, -e4.z);
-                    sc[3] = ldexpf(s4.w, -e4.w);
-                    if (zrow) {
-                        const uint32_t zw = *reinterpret_cast<const uint32_t*>(zrow + col);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) zr[j] = static_cast<int8_t>((zw >> (8 * j)) & 0xFFu);
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    _Float16 hv[ROWS_PER_T];
-#pragma unroll
-                    for (int i = 0; i < ROWS_PER_T; ++i) {
-                        const uint32_t byte = (w[i] >> (8 * j)) & 0xFFu;
-                        int32_t qv;
-                        if (BITS == 8) qv = static_cast<int8_t>(byte);
-                        else qv = side ? static_cast<int32_t>(byte >> 4) : static_cast<int32_t>(byte & 0xFu);
-                        hv[i] = static_cast<_Float16>(static_cast<float>(qv - zr[j]) * sc[j]);
-                    }
-                    const int32_t nl = (BITS == 8 ? 0 : side * (BN / 2)) + cq * 4 + j;
-                    _Float16* dst = Bs + nl * PITCH + rg * ROWS_PER_T;
-                    if constexpr (ROWS_PER_T == 4) {
-                        half4 hv4 = {hv[0], hv[1], hv[2], hv[3]};
-                        *reinterpret_cast<half4*>(dst) = hv4;
-                    } else {
-                        half2v hv2 = {hv[0], hv[1]};
-                        *reinterpret_cast<half2v*>(dst) = hv2;
-                    }
-                }
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            half8 af[2], bf[2];
+        for (int kq = 0; kq < 2; ++kq) {
+            const int32_t kk = kh * (BK / 2) + kq * 16 + (ln >> 5) * 8;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int32_t row = wm * 64 + i * 32 + (ln & 31);
-                af[i] = *reinterpret_cast<const half8*>(As + row * PITCH + kk + (ln >> 5) * 8);
-                const int32_t col = wn * 64 + i * 32 + (ln & 31);
-                bf[i] = *reinterpret_cast<const half8*>(Bs + col * PITCH + kk + (ln >> 5) * 8);
+                af[kq][i] = *reinterpret_cast<const half8*>(As + (wm * 64 + i * 32 + (ln & 31)) * PITCH + kk);
+                bf[kq][i] = *reinterpret_cast<const half8*>(Bs + (wn * 64 + i * 32 + (ln & 31)) * PITCH + kk);
             }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
+        if constexpr (DQ) store_a(rs, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int kq = p >> 1, i = p & 1;
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kq][i], bf[kq][0], acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kq][i], bf[kq][1], acc[i][1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (DQ) store_piece(rs, nxt, p);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Pipeline: LDS stage (step & 1) holds the step being multiplied; meanwhile the next
+    // step is dequantized into the other stage, and the register set it came from
+    // receives the loads of the step DEPTH steps after that one, so loads have DEPTH
+    // steps to arrive. Loads past the last step repeat the last step and are never used.
+    // sched_barrier(0) keeps the compiler from moving loads across the phases, which
+    // would make them wait on registers still in flight. The main loop body has no
+    // branches, so the compiler's load waits stay exact; the last (at most DEPTH) steps,
+    // whose loads are all issued, run in the tail.
+    store_a(r[0], 0);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) store_piece(r[0], 0, p);
+    __syncthreads();
+    load_step(r[0], min(DEPTH, last));
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t i = 0;
+    for (; i + DEPTH < n_steps; i += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            step(u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{});  // step i + u
+            __syncthreads();
+            load_step(r[(u + 1) % DEPTH], min(i + u + 1 + DEPTH, last));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) {
+        if (i + u < n_steps) {
+            if (i + u + 1 < n_steps) step(u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{});
+            else step(u & 1, r[0], 0, std::false_type{});
+            __syncthreads();
+        }
     }
 
-    // Epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%2), register (i/8)*4 + i%4.
+    // The two K halves meet: wave (kh, quad) hands its sums of row block 1 - kh to its
+    // partner (1 - kh, quad) through LDS and adds the partner's sums of row block kh,
+    // so each wave ends with the full sums of 32 rows x 64 columns.
+    float16v fin[2];
+    {
+        float* xch = reinterpret_cast<float*>(lds);  // 8 regions of 2 x 16 x 64 floats = 64 KiB
+        const int32_t quad = wave & 3;
+        float* mine = xch + (quad * 2 + (1 - kh)) * 2 * 16 * 64;
+        const float* theirs = xch + (quad * 2 + kh) * 2 * 16 * 64;
+        if (kh == 0) {
+            fin[0] = acc[1][0];
+            fin[1] = acc[1][1];
+        } else {
+            fin[0] = acc[0][0];
+            fin[1] = acc[0][1];
+        }
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-        const int32_t nl = wn * 64 + jb * 32 + (ln & 31);
-        int32_t n;
-        if (BITS == 8) n = b0 + nl;
-        else n = nl < BN / 2 ? b0 + nl : half + b0 + (nl - BN / 2);
-        const bool nvalid = BITS == 8 ? n < N : ((nl < BN / 2 ? b0 + nl : b0 + nl - BN / 2) < bpr && n < N);
-        if (!nvalid) continue;
-        const int32_t en = ec[n];
-        const float bn = bias ? bias[n] : 0.0f;
+        for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-        for (int ib = 0; ib < 2; ++ib) {
+            for (int e = 0; e < 16; ++e) mine[(jb * 16 + e) * 64 + ln] = fin[jb][e];
+        if (kh == 0) {
+            fin[0] = acc[0][0];
+            fin[1] = acc[0][1];
+        } else {
+            fin[0] = acc[1][0];
+            fin[1] = acc[1][1];
+        }
+        __syncthreads();
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int32_t i = (r >> 2) * 8 + (ln >> 5) * 4 + (r & 3);
-                const int32_t m = m0 + wm * 64 + ib * 32 + i;
-                if (m >= M) continue;
-                float* dst = c + static_cast<size_t>(m) * N + n;
-                const float v = ldexpf(acc[ib][jb][r], er[m] + en);
-                float o = accumulate ? *dst : 0.0f;
-                o = fmaf(alpha, v, o);
-                if (bias) o += bn;
-                *dst = o;
-            }
+        for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) fin[jb][e] += theirs[(jb * 16 + e) * 64 + ln];
+    }
+
+    // Epilogue: the tile goes through LDS in output-column order and leaves in rows of
+    // 16-byte stores. Element (i, j) of a 32x32 MFMA block sits in lane
+    // j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4; tile row nl holds byte column
+    // COLS (nl % 32) + (nl / 32) % COLS of the tile (INT4: high nibbles when nl >= 64).
+    constexpr int OPITCH = BN + 4;  // floats per staged row
+    float* tile_out = reinterpret_cast<float*>(lds);  // BM x OPITCH floats
+    __syncthreads();                                  // the exchange area is read
+    {
+        const int32_t mrow = wm * 64 + kh * 32 + (ln >> 5) * 4;  // tile row of register 0
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+            const int32_t nl = wn * 64 + jb * 32 + (ln & 31);
+            const int32_t col = (nl & BN / 2) * (BITS == 4) + COLS * (nl & 31) + ((nl >> 5) & (COLS - 1));
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tile_out[(mrow + (e >> 2) * 8 + (e & 3)) * OPITCH + col] = fin[jb][e];
         }
     }
+    __syncthreads();
+    float* out = partials ? partials + static_cast<size_t>(sp) * M * N : c;
+    const bool add = !partials && accumulate;
+    const float* bs = partials ? nullptr : bias;
+    const float al = partials ? 1.0f : alpha;
+#pragma unroll
+    for (int it = 0; it < BM * BN / 4 / THREADS; ++it) {
+        const int32_t idx = t + THREADS * it;
+        const int32_t ml = idx / (BN / 4), cv = (idx % (BN / 4)) * 4;  // tile row, first tile column
+        const int32_t tc = BITS == 4 && cv >= BN / 2 ? cv - BN / 2 : cv;  // byte column within the tile
+        const int32_t n = (BITS == 4 && cv >= BN / 2 ? bpr : 0) + b0 + tc;
+        if (m0 + ml >= M || b0 + tc >= bpr) continue;  // bpr % 4 == 0: the 4 columns are valid together
+        f32x4 v = *reinterpret_cast<const f32x4*>(tile_out + ml * OPITCH + cv);
+        const int32_t e = er_s[ml] + ew;
+        f32x4* dst = reinterpret_cast<f32x4*>(out + static_cast<size_t>(m0 + ml) * N + n);
+        const f32x4 old = add ? *dst : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4 bv = bs ? *reinterpret_cast<const f32x4*>(bs + n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[q4] = fmaf(al, ldexpf(v[q4], e), old[q4]) + bv[q4];
+        *dst = v;
+    }
+}
+
+// Adds the K slices of every output in slice order, then alpha, accumulate, bias.
+__global__ void __launch_bounds__(256)
+    gemm_reduce(const float* __restrict__ partials, int32_t splits, int32_t M, int32_t N, float* __restrict__ c,
+                const float* __restrict__ bias, float alpha, int32_t accumulate) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const size_t total = static_cast<size_t>(M) * N;
+    if (idx >= total) return;
+    float v[MAX_SPLITS];
+#pragma unroll
+    for (int i = 0; i < MAX_SPLITS; ++i) v[i] = i < splits ? partials[i * total + idx] : 0.0f;
+    float sum = v[0];
+#pragma unroll
+    for (int i = 1; i < MAX_SPLITS; ++i)
+        if (i < splits) sum += v[i];
+    const float o = fmaf(alpha, sum, accumulate ? c[idx] : 0.0f);
+    c[idx] = bias ? o + bias[idx % N] : o;
 }
 
 }  // namespace
@@ -235,37 +529,76 @@ __global__ void __launch_bounds__(256)
 bool gemm_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
     (void)a;
     (void)m;
-    (void)c;
-    if (w.g % 4 != 0) return false;  // a thread's 2 or 4 weight rows share one group
-    if (w.N % (w.bits == 4 ? 8 : 4) != 0) return false;
-    return aligned(w.q, 4) && aligned(w.s, 16) && (!w.z || aligned(w.z, 4));
+    if (w.g % WROWS != 0) return false;  // a thread's weight rows share one group
+    if (w.N % (w.bits == 4 ? 8 : 4) != 0) return false;  // whole 4-byte column quads
+    return aligned(w.q, 4) && aligned(w.s, 16) && (!w.z || aligned(w.z, 4)) && aligned(c, 16);
 }
 
 int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate, float alpha,
                     const float* bias, hipStream_t st) {
     const int32_t Mp = ceil_div(m, BM) * BM;
     const int32_t Kp = ceil_div(w.K, BK) * BK;
-    const size_t a16_bytes = (static_cast<size_t>(Mp) * Kp * sizeof(_Float16) + 255) & ~size_t(255);
-    const size_t er_bytes = (static_cast<size_t>(Mp) * 4 + 255) & ~size_t(255);
-    const size_t ec_bytes = (static_cast<size_t>(w.N) * 4 + 255) & ~size_t(255);
-    void* ws = nullptr;
-    int32_t status = workspace(st, a16_bytes + er_bytes + ec_bytes, &ws);
-    if (status) return status;
-    _Float16* a16 = static_cast<_Float16*>(ws);
-    int32_t* er = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + a16_bytes);
-    int32_t* ec = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + a16_bytes + er_bytes);
-    gemm_prep<<<Mp + ceil_div(w.N, 256), 256, 0, st>>>(a, m, w.K, Mp, Kp, w.s, w.G, w.N, a16, er, ec);
-    KT_LAUNCHED("qmatmul: gemm prep");
     const int32_t tiles_n = ceil_div(w.bpr, w.bits == 8 ? BN : BN / 2);
     const int32_t tiles_m = Mp / BM;
-    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n));
-    if (w.bits == 8)
-        gemm_kernel<8><<<grid, 256, 0, st>>>(a16, Kp, er, ec, w.q, w.s, w.z, m, w.K, w.N, w.bpr, w.g, tiles_n, c,
-                                             bias, alpha, accumulate);
+    const int32_t k_steps = Kp / BK;
+    // Split K when the tile grid leaves CUs idle, keeping at least 4 steps per slice.
+    int32_t splits = 1;
+    const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+    const int32_t cus = cu_count();
+    if (tiles < cus) splits = static_cast<int32_t>((cus + tiles - 1) / tiles);
+    const int32_t cap = k_steps / 4 > 1 ? k_steps / 4 : 1;
+    if (splits > cap) splits = cap;
+    if (splits > MAX_SPLITS) splits = MAX_SPLITS;
+    const int32_t steps_per_split = ceil_div(k_steps, splits);
+    splits = ceil_div(k_steps, steps_per_split);  // every slice has at least one step
+
+    const int64_t scale_quads = static_cast<int64_t>(w.G) * w.N / 4;
+    int64_t nsb64 = (scale_quads + 2047) / 2048;  // at least 8 quads per thread
+    if (nsb64 < 1) nsb64 = 1;
+    if (nsb64 > MAX_SCALE_BLOCKS) nsb64 = MAX_SCALE_BLOCKS;
+    const int32_t nsb = static_cast<int32_t>(nsb64);
+
+    auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t a16_bytes = round256(static_cast<size_t>(Mp) * Kp * sizeof(_Float16));
+    const size_t er_bytes = round256(static_cast<size_t>(Mp) * 4);
+    const size_t smax_bytes = round256(static_cast<size_t>(nsb) * 4);
+    const size_t part_bytes = splits > 1 ? static_cast<size_t>(splits) * m * w.N * sizeof(float) : 0;
+    void* ws = nullptr;
+    int32_t status = workspace(st, a16_bytes + er_bytes + smax_bytes + part_bytes, &ws);
+    if (status) return status;
+    char* base = static_cast<char*>(ws);
+    _Float16* a16 = reinterpret_cast<_Float16*>(base);
+    int32_t* er = reinterpret_cast<int32_t*>(base + a16_bytes);
+    float* smax = reinterpret_cast<float*>(base + a16_bytes + er_bytes);
+    float* partials = splits > 1 ? reinterpret_cast<float*>(base + a16_bytes + er_bytes + smax_bytes) : nullptr;
+
+    const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
+    gemm_prep<<<Mp + nsb, 256, 0, st>>>(a, m, w.K, Kp, vec_rows, Mp, w.s, scale_quads, nsb, a16, er, smax);
+    KT_LAUNCHED("qmatmul: gemm prep");
+    // Weight tiles dealt to the XCDs (padded to a multiple of 8), each with its row tiles
+    // and K slices.
+    const uint32_t blocks = static_cast<uint32_t>(ceil_div(tiles_n, XCDS) * XCDS * tiles_m * splits);
+#define KT_GEMM_ARGS                                                                                                 \
+    a16, Kp, er, smax, nsb, w.q, w.s, w.z, m, w.K, w.N, w.bpr, w.g, tiles_m, tiles_n, splits, steps_per_split, c, \
+        partials, bias, alpha, accumulate
+    const bool fast = w.K % BK == 0 && (BK % w.g == 0 || w.g % BK == 0);
+    if (w.bits == 4)
+        fast ? gemm_kernel<4, true, true><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS)
+             : gemm_kernel<4, true, false><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS);
+    else if (w.z)
+        fast ? gemm_kernel<8, true, true><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS)
+             : gemm_kernel<8, true, false><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS);
     else
-        gemm_kernel<4><<<grid, 256, 0, st>>>(a16, Kp, er, ec, w.q, w.s, w.z, m, w.K, w.N, w.bpr, w.g, tiles_n, c,
-                                             bias, alpha, accumulate);
+        fast ? gemm_kernel<8, false, true><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS)
+             : gemm_kernel<8, false, false><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS);
+#undef KT_GEMM_ARGS
     KT_LAUNCHED("qmatmul: gemm kernel");
+    if (splits > 1) {
+        const size_t total = static_cast<size_t>(m) * w.N;
+        gemm_reduce<<<static_cast<uint32_t>((total + 255) / 256), 256, 0, st>>>(partials, splits, m, w.N, c, bias,
+                                                                             alpha, accumulate);
+        KT_LAUNCHED("qmatmul: gemm reduce");
+    }
     return KT_OK;
 }
 

@@ -305,7 +305,8 @@ static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
         return launch_gemv_wide(a, &v, &c, biases, 1, accumulate, alpha, st);
     if (m <= 2 && gemv_mfma_supported(a, m, v, c)) return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
     if (m == 1 && gemv_supported(a, v, c)) return launch_gemv(a, v, c, accumulate, alpha, bias, st);
-    if (m > 1 && gemm_supported(a, m, v, c)) return launch_gemm(a, m, v, c, accumulate, alpha, bias, st);
+    if (m > 1 && gemm_supported(a, m, v, c) && (!bias || aligned(bias, 16)))
+        return launch_gemm(a, m, v, c, accumulate, alpha, bias, st);
     return launch_generic(a, m, v, c, accumulate, alpha, bias, st);
 }
 
