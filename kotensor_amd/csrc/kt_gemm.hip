@@ -51,10 +51,21 @@ constexpr int BM = 128;
 constexpr int BN = 128;
 constexpr int BK = 64;
 constexpr int PITCH = BK + 8;  // halfs per LDS row (16-byte pad: conflict-free fragment reads)
-constexpr int STAGE = (BM + BN) * PITCH;  // halfs per LDS stage
+constexpr int STAGE = BN * PITCH;  // halfs per weight stage (the dequantized weight tile)
+constexpr int ASTAGE = BM * BK;    // halfs per a stage (rows of 128 bytes, chunks swizzled)
+constexpr int ADEPTH = 4;          // a stages: K steps whose a tiles are loaded or in flight
 constexpr int XCDS = 8;
 constexpr int MAX_SPLITS = 8;
-constexpr int DEPTH = 4;  // K steps whose loads are in flight
+constexpr int DEPTH = 4;  // K steps whose weight loads are in flight
+// LDS: the a stages and two weight stages; after the K loop the same array holds the
+// exchange of the K halves (8 x 2 x 16 x 64 floats) and then the output tile
+// (BM x (BN + 4) floats).
+constexpr int LDS_HALFS = ADEPTH * ASTAGE + 2 * STAGE;
+static_assert(LDS_HALFS >= 2 * 16384 && LDS_HALFS >= 2 * BM * (BN + 4), "LDS array holds the epilogue");
+
+// s_waitcnt immediate that waits until at most n vector memory operations are
+// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at max).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int ROW_CHUNKS = 16;       // float4 chunks of a row each pre-pass thread keeps in registers
 constexpr int MAX_SCALE_BLOCKS = 256;  // pre-pass blocks over the scales (one maximum each)
 
@@ -106,9 +117,10 @@ __global__ void __launch_bounds__(256)
     if (b < Mp) {
         const int32_t m = b;
         const int32_t chunks = Kp / 4;
-        uint2* dst = reinterpret_cast<uint2*>(a16 + static_cast<size_t>(m) * Kp);
+        uint2* row16 = reinterpret_cast<uint2*>(a16 + static_cast<size_t>(m) * Kp);
+        auto dst = [&](int32_t cc) -> uint2& { return row16[cc]; };
         if (m >= M) {
-            for (int32_t cc = t; cc < chunks; cc += 256) dst[cc] = make_uint2(0, 0);
+            for (int32_t cc = t; cc < chunks; cc += 256) dst(cc) = make_uint2(0, 0);
             if (t == 0) er[m] = 0;
             return;
         }
@@ -131,12 +143,12 @@ __global__ void __launch_bounds__(256)
         for (int i = 0; i < ROW_CHUNKS; ++i) {
             const int32_t cc = t + 256 * i;
             if (cc < chunks)
-                dst[cc] = make_uint2(pack_half2(ldexpf(v[i][0], -e), ldexpf(v[i][1], -e)),
+                dst(cc) = make_uint2(pack_half2(ldexpf(v[i][0], -e), ldexpf(v[i][1], -e)),
                                      pack_half2(ldexpf(v[i][2], -e), ldexpf(v[i][3], -e)));
         }
         for (int32_t cc = t + 256 * ROW_CHUNKS; cc < chunks; cc += 256) {
             const f32x4 u = row_chunk(row, cc, K, vec);
-            dst[cc] = make_uint2(pack_half2(ldexpf(u[0], -e), ldexpf(u[1], -e)),
+            dst(cc) = make_uint2(pack_half2(ldexpf(u[0], -e), ldexpf(u[1], -e)),
                                  pack_half2(ldexpf(u[2], -e), ldexpf(u[3], -e)));
         }
         if (t == 0) er[m] = e;
@@ -157,11 +169,10 @@ __global__ void __launch_bounds__(256)
     if (t == 0) smax[sb] = mx;
 }
 
-// Work split of the 512 threads per K step: a is 1024 chunks of 8 halfs (two per
-// thread); the weight tile is 64 rows x 32 lanes of column bytes (INT8: 4 bytes =
-// 4 columns; INT4: 2 bytes = 2 low-nibble + 2 high-nibble columns), each thread
-// taking 4 consecutive rows of one lane's bytes, which lie in one scale group
-// (g % 4 == 0).
+// Work split of the 512 threads per K step: the weight tile is 64 rows x 32 lanes of
+// column bytes (INT8: 4 bytes = 4 columns; INT4: 2 bytes = 2 low-nibble + 2
+// high-nibble columns), each thread taking 4 consecutive rows of one lane's bytes,
+// which lie in one scale group (g % 4 == 0).
 constexpr int THREADS = 512;
 constexpr int WROWS = 4;
 
@@ -172,10 +183,9 @@ struct WTile {
     static constexpr int SIDES = BITS == 8 ? 1 : 2;
 };
 
-// The global data of one K step held by a thread.
+// The weight data of one K step held by a thread.
 template <int BITS>
-struct StepRegs {
-    u32x4 a[2];                     // 2 x 8 fp16 of a
+struct WRegs {
     uint32_t w[WROWS];              // the thread's weight bytes of each row
     f32x4 s[WTile<BITS>::SIDES];    // scales of the thread's columns (per side)
     uint32_t z[WTile<BITS>::SIDES]; // zero points of the thread's columns (per side)
@@ -198,6 +208,16 @@ __device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
 
 __device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
 
+// One global_load_lds_dwordx4: lane l's 16 bytes at g land at LDS byte address lds + 16 l
+// (lds wave-uniform). Written as inline assembly so the compiler neither reorders LDS
+// accesses around it ("memory") nor waits for it on its own: the kernel waits for these
+// loads itself with explicit vmcnt counts. The compiler's own waits for register loads
+// stay correct, only stricter than needed, since it does not count these operations.
+// Nothing else in the kernel uses m0.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory");
+}
+
 template <int N_>
 __device__ __forceinline__ f32x4 load_scales(const float* p) {
     if constexpr (N_ == 4) return *reinterpret_cast<const f32x4*>(p);
@@ -212,12 +232,14 @@ __device__ __forceinline__ uint32_t load_bytes(const void* p) {
 }
 
 // The 8 waves split each K step: waves 0-3 multiply k 0..31 of it, waves 4-7 k 32..63,
-// each wave a 64 x 64 block of the tile (2 x 2 waves per half). The two halves' sums
-// are added through LDS at the end. Two waves per SIMD let one wave's dequantization
-// and waits overlap the other's MFMAs.
+// each wave a 64 x 64 block of the tile (2 x 2 waves per half). The a tile of a step
+// goes from global memory straight into an LDS stage (global_load_lds, 16 bytes per
+// lane, no registers), ADEPTH steps ahead; the weights come through registers and are
+// dequantized into LDS. The two halves' sums are added through LDS at the end. Two
+// waves per SIMD let one wave's dequantization and waits overlap the other's MFMAs.
 // FAST: K % BK == 0 and the group size divides BK or is a multiple of it, so every
-// load of a step is a uniform base plus an offset fixed per lane (no per-step address
-// arithmetic and no clamping); otherwise rows and groups are computed per step.
+// weight load of a step is a uniform base plus an offset fixed per lane (no per-step
+// address arithmetic and no clamping); otherwise rows and groups are computed per step.
 template <int BITS, bool ZP, bool FAST>
 __global__ void __launch_bounds__(THREADS, 1)
     gemm_kernel(const _Float16* __restrict__ a16, int32_t Kp, const int32_t* __restrict__ er,
@@ -226,9 +248,10 @@ __global__ void __launch_bounds__(THREADS, 1)
                 int32_t bpr, int32_t g, int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t steps_per_split,
                 float* __restrict__ c, float* __restrict__ partials, const float* __restrict__ bias, float alpha,
                 int32_t accumulate) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[LDS_HALFS];
     __shared__ int32_t er_s[BM];
     __shared__ float red[THREADS / 64];
+    _Float16* const wstage = lds + ADEPTH * ASTAGE;  // the two weight stages
     constexpr int BYTES = WTile<BITS>::BYTES;
     constexpr int COLS = WTile<BITS>::COLS;
     constexpr int SIDES = WTile<BITS>::SIDES;
@@ -264,71 +287,85 @@ __global__ void __launch_bounds__(THREADS, 1)
     const int32_t bcol = b0 + cq * BYTES < bpr ? b0 + cq * BYTES : 0;  // bpr % 4 == 0: byte groups are whole
 
     // Byte offsets fixed per lane.
-    uint32_t a_off[2], w_off[WROWS];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) a_off[i] = (static_cast<uint32_t>((t >> 3) + 64 * i) * Kp + (t & 7) * 8) * 2u;
+    uint32_t w_off[WROWS];
 #pragma unroll
     for (int i = 0; i < WROWS; ++i) w_off[i] = static_cast<uint32_t>(rg * WROWS + i) * bpr + bcol;
     const uint32_t s_idx = static_cast<uint32_t>(g < BK ? (rg * WROWS) / g : 0) * N + bcol;
-    const char* a_tile = reinterpret_cast<const char*>(a16 + static_cast<size_t>(m0) * Kp);
+    // a tile: row r of a stage is 128 bytes = 8 chunks of 16 bytes; chunk c of row r sits
+    // in slot c ^ ((r / 2) % 8), so 16 lanes reading one chunk column of 16 rows hit all
+    // 64 banks once. A load instruction fills 1 KiB = rows 8 b .. 8 b + 7 (b = 8 j + wave,
+    // j = 0, 1), lane l writing slot l % 8 of row 8 b + l / 8: it loads the chunk that
+    // belongs there.
+    uint32_t a_off[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int32_t r = (jj * 8 + wave) * 8 + (ln >> 3);
+        a_off[jj] = static_cast<uint32_t>(r) * Kp + (((ln & 7) ^ ((r >> 1) & 7)) << 3);
+    }
+    const _Float16* a_tile = a16 + static_cast<size_t>(m0) * Kp;
 
-    auto load_step = [&](StepRegs<BITS>& r, int32_t step) {
+    // Loads part `part` of a step's weight data: 0 rows 0-1, 1 rows 2-3, 2 scales and
+    // zero points (-1: all), so the loads can be spread over a step.
+    auto load_w = [&](WRegs<BITS>& r, int32_t step, int part = -1) {
         const int32_t k0 = (ks0 + step) * BK;
-        const char* ab = a_tile + static_cast<size_t>(k0) * 2;
+        const int32_t kr = k0 + rg * WROWS;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) r.a[i] = *reinterpret_cast<const u32x4*>(ab + a_off[i]);
-        if constexpr (FAST) {
-            const uint8_t* wb = q + static_cast<size_t>(k0) * bpr;
-#pragma unroll
-            for (int i = 0; i < WROWS; ++i) r.w[i] = load_bytes<BYTES>(wb + w_off[i]);
-            const size_t gbase = static_cast<size_t>(k0 / g) * N;
-#pragma unroll
-            for (int side = 0; side < SIDES; ++side) {
-                r.s[side] = load_scales<COLS>(s + gbase + s_idx + (side ? bpr : 0));
-                if constexpr (ZP) r.z[side] = load_bytes<BYTES>(z + gbase + s_idx + (side ? bpr : 0));
-            }
-        } else {
-            const int32_t kr = k0 + rg * WROWS;
-#pragma unroll
-            for (int i = 0; i < WROWS; ++i) {
+        for (int i = 0; i < WROWS; ++i) {
+            if (part >= 0 && part != i / 2) continue;
+            if constexpr (FAST) {
+                r.w[i] = load_bytes<BYTES>(q + static_cast<size_t>(k0) * bpr + w_off[i]);
+            } else {
                 const int32_t row = kr + i < K ? kr + i : K - 1;  // a is zero on rows >= K
                 r.w[i] = load_bytes<BYTES>(q + static_cast<size_t>(row) * bpr + bcol);
             }
-            const size_t at = static_cast<size_t>((kr < K ? kr : K - 1) / g) * N + bcol;
+        }
+        if (part >= 0 && part != 2) return;
+        const size_t at = FAST ? static_cast<size_t>(k0 / g) * N + s_idx
+                               : static_cast<size_t>((kr < K ? kr : K - 1) / g) * N + bcol;
 #pragma unroll
-            for (int side = 0; side < SIDES; ++side) {
-                r.s[side] = load_scales<COLS>(s + at + (side ? bpr : 0));
-                if constexpr (ZP) r.z[side] = load_bytes<BYTES>(z + at + (side ? bpr : 0));
-            }
+        for (int side = 0; side < SIDES; ++side) {
+            r.s[side] = load_scales<COLS>(s + at + (side ? bpr : 0));
+            if constexpr (ZP) r.z[side] = load_bytes<BYTES>(z + at + (side ? bpr : 0));
         }
     };
+    auto load_a = [&](int32_t step) {
+        const _Float16* ab = a_tile + static_cast<size_t>(ks0 + step) * BK;
+        const uint32_t st = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds + (step % ADEPTH) * ASTAGE));
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+            lds_dma16(ab + a_off[jj], __builtin_amdgcn_readfirstlane(st + (jj * 8 + wave) * 1024));
+    };
+    // Vector memory operations a thread issues per step after its a loads: the weight
+    // bytes, scales and zero points.
+    constexpr int NW = WROWS + SIDES * (ZP ? 2 : 1);
 
     // The slice maxima of the scales and the row exponents are loaded first, then the
-    // first DEPTH steps: loads complete in order, so waiting for the former does not
-    // wait for the latter.
+    // first steps: loads complete in order, so waiting for the former does not wait
+    // for the latter.
     const float smx = t < nsb ? smax[t] : 0.0f;  // nsb <= 256
     const int32_t erv = t < BM && m0 + t < M ? er[m0 + t] : 0;
     __builtin_amdgcn_sched_barrier(0);
-    StepRegs<BITS> r[DEPTH];
+    WRegs<BITS> r[DEPTH];
     const int32_t last = n_steps - 1;
+    static_assert(ADEPTH == DEPTH, "a stage and weight set indices both follow step % 4");
+    // a tiles of steps 0..2 and weights of steps 0..3, a first in each pair.
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load_step(r[d], min(d, last));
-    __builtin_amdgcn_sched_barrier(0);
+    for (int d = 0; d < DEPTH; ++d) {
+        if (d < ADEPTH - 1) load_a(min(d, last));
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(r[d], min(d, last));
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if (t < BM) er_s[t] = erv;
     const int32_t ew = scale_exponent(block_max<THREADS / 64>(smx, red), 7);
 
     const uint32_t flip = in_vgpr(0x00800080u), exp1024 = in_vgpr(0x64006400u);
     const uint32_t mask_lo = in_vgpr(0x000F000Fu), mask_hi = in_vgpr(0x00F000F0u);
 
-    auto store_a = [&](const StepRegs<BITS>& rs, int32_t stage) {
-        _Float16* As = lds + stage * STAGE;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(As + ((t >> 3) + 64 * i) * PITCH + (t & 7) * 8) = rs.a[i];
-    };
     // Dequantizes piece p (0..3) of the thread's weight bytes into a stage: INT8 column
     // p; INT4 byte column p / 2, low nibbles for even p and high nibbles for odd p.
-    auto store_piece = [&](const StepRegs<BITS>& rs, int32_t stage, int p) {
-        _Float16* Bs = lds + stage * STAGE + BM * PITCH;
+    auto store_piece = [&](const WRegs<BITS>& rs, int32_t stage, int p) {
+        _Float16* Bs = wstage + stage * STAGE;
         const int jq = BITS == 8 ? p : p >> 1;
         const int side = BITS == 8 ? 0 : p & 1;
         const uint32_t pr0 = pair_bytes(rs.w[0], rs.w[1], jq), pr1 = pair_bytes(rs.w[2], rs.w[3], jq);
@@ -369,24 +406,31 @@ __global__ void __launch_bounds__(THREADS, 1)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][jj][e] = 0.0f;
 
-    // One step: the MFMAs of stage `cur` (this wave's half of the step's K) alternate
-    // with the dequantization of the next step's registers into stage `nxt`, in a fixed
-    // order (sched_barrier) so the matrix and vector units work at the same time.
-    auto step = [&](int32_t cur, const StepRegs<BITS>& rs, int32_t nxt, auto dequant) {
+    // One step: the MFMAs of a stage `as` and weight stage `cur` (this wave's half of
+    // the step's K) alternate with the dequantization of the next step's weights into
+    // weight stage `nxt`, in a fixed order (sched_barrier) so the matrix and vector
+    // units work at the same time.
+    // With loads (main loop), the a tile of step `la` goes into a stage `las` and the
+    // weights of step `lw` into `rl` between the MFMA pairs, so the memory pipeline
+    // works while the MFMAs run instead of after the barrier.
+    auto step = [&](int32_t as, int32_t cur, const WRegs<BITS>& rs, int32_t nxt, auto dequant, auto loads,
+                    WRegs<BITS>& rl, int32_t la, int32_t lw) {
         constexpr bool DQ = decltype(dequant)::value;
-        const _Float16* As = lds + cur * STAGE;
-        const _Float16* Bs = As + BM * PITCH;
+        constexpr bool LD = decltype(loads)::value;
+        const _Float16* As = lds + as * ASTAGE;
+        const _Float16* Bs = wstage + cur * STAGE;
         half8 af[2][2], bf[2][2];
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) {
             const int32_t kk = kh * (BK / 2) + kq * 16 + (ln >> 5) * 8;
+            const int32_t kc = kk >> 3;  // chunk of the a row
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                af[kq][i] = *reinterpret_cast<const half8*>(As + (wm * 64 + i * 32 + (ln & 31)) * PITCH + kk);
+                const int32_t ra = wm * 64 + i * 32 + (ln & 31);
+                af[kq][i] = *reinterpret_cast<const half8*>(As + ra * BK + ((kc ^ ((ra >> 1) & 7)) << 3));
                 bf[kq][i] = *reinterpret_cast<const half8*>(Bs + (wn * 64 + i * 32 + (ln & 31)) * PITCH + kk);
             }
         }
-        if constexpr (DQ) store_a(rs, nxt);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -395,39 +439,51 @@ __global__ void __launch_bounds__(THREADS, 1)
             acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kq][i], bf[kq][1], acc[i][1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (DQ) store_piece(rs, nxt, p);
+            if constexpr (LD) {
+                if (p == 0) load_a(la);
+                else load_w(rl, lw, p - 1);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Pipeline: LDS stage (step & 1) holds the step being multiplied; meanwhile the next
-    // step is dequantized into the other stage, and the register set it came from
-    // receives the loads of the step DEPTH steps after that one, so loads have DEPTH
-    // steps to arrive. Loads past the last step repeat the last step and are never used.
-    // sched_barrier(0) keeps the compiler from moving loads across the phases, which
-    // would make them wait on registers still in flight. The main loop body has no
-    // branches, so the compiler's load waits stay exact; the last (at most DEPTH) steps,
-    // whose loads are all issued, run in the tail.
-    store_a(r[0], 0);
+    // Pipeline: weight stage (step & 1) holds the weights of the step being multiplied
+    // while the next step is dequantized into the other stage. During step s the a tile
+    // of step s + 3 loads into the a stage step s - 1 used and the weights of step s + 4
+    // into the register set step s - 1 dequantized. Loads past the last step repeat the
+    // last step and are never used. sched_barrier(0) keeps the compiler from moving
+    // loads across the phases. The compiler waits for register loads itself; the a loads
+    // write LDS behind its back, so before the barrier that precedes reading a stage each
+    // thread waits until only the loads issued after that stage's are outstanding: in
+    // the steady state the weights of its own step and two later steps (3 NW + 4). The
+    // main loop body has no branches, so the compiler's waits stay exact; the last (at
+    // most DEPTH) steps, whose loads are all issued, run in the tail.
 #pragma unroll
     for (int p = 0; p < 4; ++p) store_piece(r[0], 0, p);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * NW + 4));  // a tile of step 0
     __syncthreads();
-    load_step(r[0], min(DEPTH, last));
-    __builtin_amdgcn_sched_barrier(0);
     int32_t i = 0;
     for (; i + DEPTH < n_steps; i += DEPTH) {
 #pragma unroll
         for (int u = 0; u < DEPTH; ++u) {
-            step(u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{});  // step i + u
+            // step i + u
+            step(u, u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{}, std::true_type{}, r[u],
+                 min(i + u + ADEPTH - 1, last), min(i + u + DEPTH, last));
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * NW + 4));  // a tile of step i + u + 1
             __syncthreads();
-            load_step(r[(u + 1) % DEPTH], min(i + u + 1 + DEPTH, last));
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // The tail issues the same loads (the a tile of step i + 3 may not be loaded yet) and
+    // waits for all of them before each barrier.
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u) {
         if (i + u < n_steps) {
-            if (i + u + 1 < n_steps) step(u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{});
-            else step(u & 1, r[0], 0, std::false_type{});
+            if (i + u + 1 < n_steps)
+                step(u, u & 1, r[(u + 1) % DEPTH], (u + 1) & 1, std::true_type{}, std::true_type{}, r[u],
+                     min(i + u + ADEPTH - 1, last), min(i + u + DEPTH, last));
+            else
+                step(u, u & 1, r[0], 0, std::false_type{}, std::false_type{}, r[0], 0, 0);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
         }
     }
