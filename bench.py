@@ -22,8 +22,10 @@ The JSON line also carries:
   cpu_baseline  -- the oracle (C restatement of MatMul.multiplyQuantized, M == 1
                    unit schedule, work-stealing threads) on the same workload;
   extra         -- the two targets of the workload family: INT4 GEMV on the
-                   Llama-3-8B FFN shape (4096->14336) and the INT8 prefill GEMM at
-                   M = 512 (2048->8192, 8192->2048), each with its roofline fraction.
+                   Llama-3-8B FFN shape (4096->14336) and the INT8 group-32 prefill
+                   GEMM at M = 512 on the 2048-wide layer's four projection shapes
+                   (2048->2048, 2048->512, 2048->8192, 8192->2048) and their sum, each
+                   with its fraction of the MFMA peak.
 
 --only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
 calibration of the HBM byte counters) for rocprofv3 PMC runs.
@@ -308,9 +310,11 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             "GB/s": round(b8 / (a8 * 1e-3) / 1e9, 1), "frac_hbm": round(b8 / (a8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "avg_us": round(a8 * 1e3, 3), "bytes": b8, "copies": n8}
         del c8, w8
-        # INT8 prefill GEMM at M = 512
-        for (k, n) in [(2048, 8192), (8192, 2048)]:
-            wg = Weight(torch, kt_lib, k, n, 8, 64, seed=9, stream=stream)
+        # INT8 prefill GEMM at M = 512, group 32, on the four projection shapes of a
+        # 2048-wide layer; "layer" is their flops over their summed time (one of each).
+        tot_flops = tot_ms = 0.0
+        for (k, n) in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
+            wg = Weight(torch, kt_lib, k, n, 8, 32, seed=9, stream=stream)
             ng = max(2, -(-2 * MALL_BYTES // wg.nbytes))
             cg = [wg] + [wg.clone(kt_lib) for _ in range(ng - 1)]
             xg = torch.randn((512, k), generator=gen, device="cuda", dtype=torch.float32)
@@ -318,11 +322,17 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             for w in cg:
                 qmatmul(kt_lib, xg, 512, w, yg, stream)
             ag = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 32)
-            tflops = 2.0 * 512 * k * n / (ag * 1e-3) / 1e12
-            extra[f"int8_gemm_m512_{k}x{n}"] = {
+            flops = 2.0 * 512 * k * n
+            tflops = flops / (ag * 1e-3) / 1e12
+            tot_flops += flops
+            tot_ms += ag
+            extra[f"int8_g32_gemm_m512_{k}x{n}"] = {
                 "TFLOP/s": round(tflops, 1), "frac_mfma": round(tflops / MFMA_PEAK_TFLOPS, 4),
                 "avg_us": round(ag * 1e3, 3), "copies": ng}
             del cg, wg
+        layer = tot_flops / (tot_ms * 1e-3) / 1e12
+        extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
+                                             "avg_us": round(tot_ms * 1e3, 3)}
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
