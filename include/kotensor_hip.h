@@ -160,6 +160,65 @@ int32_t kt_dequantize_rows(const kt_qweight* w, const int32_t* rows, int32_t cou
 int32_t kt_dequantize_columns(const kt_qweight* w, const int32_t* columns, int32_t count,
                               float* out, void* stream);
 
+/* ---- saveQuantized files (safetensors) -------------------------------------------
+ * The reference stores quantized models as safetensors (SafeTensors.kt:12-249): an
+ * 8-byte little-endian header size, a JSON header (tensor name -> dtype, shape,
+ * data_offsets; "__metadata__" -> string map), then the tensor bytes. saveQuantized
+ * (Transformer.kt:402-430) writes each quantized weight NAME as NAME.qweight (I8 for
+ * 8-bit, U8 for 4-bit) [rows x bytes_per_row], NAME.scales F32 [groups x columns] and,
+ * with zero points, NAME.zeros U8 [groups x columns], plus kotensor.* metadata. These
+ * entry points read such files into device buffers without repacking (the kernels
+ * consume the file layout) and write them back byte for byte. Host-side; only
+ * kt_st_load_qweight and kt_st_writer_save touch the device. */
+typedef struct kt_st_file kt_st_file;      /* a read-only mapping of one file */
+typedef struct kt_st_writer kt_st_writer;  /* entries and metadata of a file to write */
+
+typedef struct kt_st_entry {
+    char dtype[8];       /* "F32", "I8", "U8", ... (NUL-terminated) */
+    int32_t rank;        /* number of dimensions, at most 8 */
+    int64_t shape[8];
+    int64_t offset;      /* byte offset of the data from the start of the file */
+    int64_t nbytes;      /* data_offsets[1] - data_offsets[0] */
+} kt_st_entry;
+
+/* SafeTensorsFile(file) (SafeTensors.kt:37-67): maps the file read-only and parses the
+ * header with the reference's checks (header size in 1 .. 100 MiB, every tensor with a
+ * dtype and data_offsets inside the file). KT_ERR_ARGUMENT with the reference's
+ * message on a malformed file. */
+int32_t kt_st_open(const char* path, kt_st_file** file);
+int32_t kt_st_close(kt_st_file* file);
+/* names (:69-70): entry count and the index-th name in header order. */
+int32_t kt_st_count(const kt_st_file* file, int32_t* count);
+int32_t kt_st_name(const kt_st_file* file, int32_t index, char* buf, size_t len);
+/* entry(name) (:74-75); KT_ERR_ARGUMENT "No tensor named ..." when absent. */
+int32_t kt_st_find(const kt_st_file* file, const char* name, kt_st_entry* entry);
+/* metadata[key] (:40, :51-55) as text; KT_ERR_ARGUMENT when the key is absent. */
+int32_t kt_st_metadata(const kt_st_file* file, const char* key, char* buf, size_t len);
+/* The index-th metadata key in header order; KT_ERR_RANGE past the last one. */
+int32_t kt_st_metadata_key(const kt_st_file* file, int32_t index, char* buf, size_t len);
+/* map(name) (:101-107): the entry's bytes inside the mapping (valid until kt_st_close). */
+int32_t kt_st_data(const kt_st_file* file, const char* name, const void** data, int64_t* nbytes);
+/* QuantizedTensor.mapFrom (QuantizedTensor.kt:109-125) onto the device: checks
+ * NAME.qweight, NAME.scales (F32) and NAME.zeros against w's layout with the reference's
+ * messages, then copies them into w's device buffers (w->zeros is written when NAME.zeros
+ * is required, i.e. when w has zero points). Returns when the copies are done. */
+int32_t kt_st_load_qweight(const kt_st_file* file, const char* name, const kt_qweight* w, void* stream);
+
+/* SafeTensors.saveEntries (SafeTensors.kt:204-249): entries and metadata are written in
+ * the order added, with the reference's header text, padding and data order, so a file
+ * loaded and saved again is identical byte for byte (MappedModelTest.kt:108-119). */
+int32_t kt_st_writer_create(kt_st_writer** writer);
+int32_t kt_st_writer_destroy(kt_st_writer* writer);
+int32_t kt_st_writer_metadata(kt_st_writer* writer, const char* key, const char* value);
+/* One entry: nbytes of data at `data` (device memory when on_device != 0, else host
+ * memory), kept by reference until kt_st_writer_save. */
+int32_t kt_st_writer_add(kt_st_writer* writer, const char* name, const char* dtype, int32_t rank,
+                         const int64_t* shape, const void* data, int64_t nbytes, int32_t on_device);
+/* The entries saveQuantized writes for one quantized weight (Transformer.kt:425-428):
+ * NAME.qweight, NAME.scales and (with zero points) NAME.zeros, from w's device buffers. */
+int32_t kt_st_writer_add_qweight(kt_st_writer* writer, const char* name, const kt_qweight* w);
+int32_t kt_st_writer_save(kt_st_writer* writer, const char* path, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,13 +4,15 @@ weight-only quantization path.
 The product is ``libkotensor_hip.so`` (C ABI: ``include/kotensor_hip.h``). This
 package is a host-side mirror of the reference's API over that ABI:
 ``Quantization``, ``QuantizedTensor``, ``MatMul.multiply_quantized``,
-``DeviceTensor.matmul_dequant(_into)`` and ``QuantizedLinear``.
+``DeviceTensor.matmul_dequant(_into)``, ``QuantizedLinear`` and the saveQuantized
+file format (``SafeTensorsFile``, ``save_quantized``, ``load_quantized``).
 """
 from ._lib import IllegalArgumentException, IllegalStateException, LibraryMissingError, LIBRARY_PATH
 from .device import DeviceBuffer, Stream, synchronize, device_count
 from .quantization import Quantization, QuantizedTensor
 from .matmul import MatMul, DeviceTensor
 from .linear import QuantizedLinear, projection, forward_into_group
+from .safetensors import SafeTensorsFile, save_entries, save_quantized, load_quantized
 
 __all__ = [
     "IllegalArgumentException",
@@ -28,4 +30,8 @@ __all__ = [
     "QuantizedLinear",
     "projection",
     "forward_into_group",
+    "SafeTensorsFile",
+    "save_entries",
+    "save_quantized",
+    "load_quantized",
 ]

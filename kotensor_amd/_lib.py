@@ -64,6 +64,20 @@ class _QWeight(ctypes.Structure):
 
 QWeight = _QWeight
 
+
+class _StEntry(ctypes.Structure):
+    """kt_st_entry: one tensor of a safetensors header."""
+    _fields_ = [
+        ("dtype", ctypes.c_char * 8),
+        ("rank", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 8),
+        ("offset", ctypes.c_int64),
+        ("nbytes", ctypes.c_int64),
+    ]
+
+
+StEntry = _StEntry
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
 _SZ = ctypes.c_size_t
@@ -94,6 +108,21 @@ SIGNATURES = {
     "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],
     "kt_dequantize_rows": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
     "kt_dequantize_columns": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
+    "kt_st_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "kt_st_close": [_P],
+    "kt_st_count": [_P, ctypes.POINTER(_I)],
+    "kt_st_name": [_P, _I, ctypes.c_char_p, _SZ],
+    "kt_st_find": [_P, ctypes.c_char_p, ctypes.POINTER(_StEntry)],
+    "kt_st_metadata": [_P, ctypes.c_char_p, ctypes.c_char_p, _SZ],
+    "kt_st_metadata_key": [_P, _I, ctypes.c_char_p, _SZ],
+    "kt_st_data": [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_int64)],
+    "kt_st_load_qweight": [_P, ctypes.c_char_p, ctypes.POINTER(_QWeight), _P],
+    "kt_st_writer_create": [ctypes.POINTER(_P)],
+    "kt_st_writer_destroy": [_P],
+    "kt_st_writer_metadata": [_P, ctypes.c_char_p, ctypes.c_char_p],
+    "kt_st_writer_add": [_P, ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(ctypes.c_int64), _P, ctypes.c_int64, _I],
+    "kt_st_writer_add_qweight": [_P, ctypes.c_char_p, ctypes.POINTER(_QWeight)],
+    "kt_st_writer_save": [_P, ctypes.c_char_p, _P],
 }
 
 _lock = threading.Lock()
