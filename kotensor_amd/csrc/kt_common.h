@@ -34,6 +34,9 @@ int32_t workspace(hipStream_t stream, size_t bytes, void** out);
 // that takes them must leave every one at zero when it completes.
 int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters);
 constexpr size_t MAX_COUNTERS = (64 << 10) / sizeof(uint32_t);
+// The counters plus `doubles` fp64 accumulators that are zero on entry; a kernel that
+// uses them leaves them at zero.
+int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs);
 
 // Validated view of a kt_qweight, with the derived layout numbers.
 struct WeightView {
@@ -86,7 +89,7 @@ void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t
 bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c);
 int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
                          int32_t accumulate, float alpha, hipStream_t st);
-void set_gemv_wide_config(int32_t slices);
+void set_gemv_wide_config(int32_t slices, int32_t waves);
 // Whether the automatic choice takes the wide-strip kernel for these weights.
 bool gemv_wide_preferred(const WeightView* ws, int32_t count);
 

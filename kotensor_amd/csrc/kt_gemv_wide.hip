@@ -22,10 +22,18 @@
 //     unit is an integer multiple of the part's grid below 2^24 grids, so the MFMA sums
 //     are exact, and so is sum(part * (q - z)) = fma(-(1024 + z), sum(part), that sum);
 //   * per unit: res += scale * 2^e * (hi + mid + lo), on every lane (16 columns each);
-//   * a workgroup is 8 waves on one tile; its waves take the units of its K-slice
-//     round-robin, meet in LDS and, with several K-slices, meet the other slices through
-//     write-through partial sums and a per-tile counter (the last workgroup adds them in
-//     slice order), so results do not depend on timing.
+//   * a workgroup is 2, 4 or 8 waves on one tile; its waves take the units of its
+//     K-slice round-robin and meet in LDS. With several K-slices, every workgroup adds its
+//     column sums into fp64 accumulators with atomics and the last one of the tile (a
+//     per-tile counter) takes the totals, resetting them to zero. fp32 sums whose
+//     magnitudes lie within 2^(29 - log2 slices) of each other add exactly in fp64, so
+//     the result does not depend on the order of arrival; otherwise the fp64 total can
+//     differ in its last bit, which reaches the fp32 result only when the total lies
+//     within that bit of an fp32 rounding boundary.
+//
+// Grid shape: one workgroup is one tile x one K-slice. A workgroup's bandwidth is
+// limited (about 45 GB/s for 8 waves on MI355X), so the launcher takes as many K-slices
+// as keep one round of 8-wave workgroups on the CUs with a unit for every wave.
 #include "kt_common.h"
 
 namespace kt {
@@ -40,9 +48,7 @@ constexpr int UNIT = 32;          // rows per x unit (exponent, parts, sums)
 constexpr int CROWS = 8;          // rows per chunk
 constexpr int CPU_ = UNIT / CROWS;  // chunks per unit
 constexpr int TILE = 512;         // bytes of a row per wave
-constexpr int WAVES = 8;          // waves per workgroup
-constexpr int THREADS = 64 * WAVES;
-constexpr int MAX_SLICES = 32;    // K-slices met inside the kernel
+constexpr int MAX_WAVES = 8;      // waves per workgroup: 2, 4 or 8
 constexpr int XB = 2;             // x load instructions per batch (2 units each)
 
 struct Job {
@@ -51,7 +57,7 @@ struct Job {
     const int8_t* z;
     float* out;
     const float* bias;
-    float* partials;     // [slices x N] when slices > 1
+    double* accum;       // [N] fp64 column totals, zero on entry and exit, when slices > 1
     uint32_t* counters;  // [tiles] when slices > 1
     int32_t N, bpr, tiles, slices, units_per_slice;
 };
@@ -113,9 +119,10 @@ struct UnitScales {
     uint2 z[BITS == 4 ? 2 : 1];
 };
 
-template <int BITS, int NB, bool ZP>
-__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+template <int BITS, int NB, bool ZP, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
     gemv_wide_kernel(const float* __restrict__ x, int32_t K, int32_t g, Jobs jobs, float alpha, int32_t accumulate) {
+    constexpr int THREADS = 64 * WAVES;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int SIDES = BITS == 4 ? 2 : 1;
     constexpr int NACC = 8 * SIDES;  // accumulators (columns) per lane
@@ -210,6 +217,8 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
         __builtin_amdgcn_sched_barrier(0);  // the x loads go out first: they are waited for first
 
         // ---- weight loads: the first unit (NB chunks) ---------------------------------
+        // The first chunk goes out with x; the others follow once x is prepared, so the
+        // x loads do not queue behind the whole unit.
         uint32_t roff[CROWS];
 #pragma unroll
         for (int i = 0; i < CROWS; ++i) roff[i] = static_cast<uint32_t>(i * bpr + boff);
@@ -220,8 +229,12 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
             for (int i = 0; i < CROWS; ++i) v[i] = *reinterpret_cast<const uint2*>(base + roff[i]);
         };
         uint2 buf[NB][CROWS];
+        load(buf[0], 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        prep_x(0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) load(buf[b], 0, b);
+        for (int b = 1; b < NB; ++b) load(buf[b], 0, b);
 
         const int32_t scol = tile * TILE + kb * 128 + cl * 8;  // first column of the lane, low side
         const int32_t scol_c = active ? scol : 0;
@@ -242,7 +255,6 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
         UnitScales<BITS> sc = load_scales(0);
         __builtin_amdgcn_sched_barrier(0);
 
-        prep_x(0);
         for (int32_t k0 = 2 * XB; k0 < my_units; k0 += 2 * XB) {
             load_x(k0);
             prep_x(k0);
@@ -346,15 +358,15 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
     }
 
     if (jb.slices > 1) {
-        // Slices meet through write-through partial sums and a per-tile counter; the last
-        // workgroup of the tile adds them in slice order.
-        const int32_t S = jb.slices;
-        // A workgroup's sums are contiguous columns of its slice's row: full-line writes.
+        // The slices of the tile meet in the fp64 accumulators; the adds are complete
+        // (s_waitcnt) before the counter is taken, and the last workgroup's exchanges
+        // follow its counter read, so it sees every add. Each column is added by one
+        // thread per workgroup: the workgroup's sums are contiguous columns.
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i)
             if (live[i])
-                __hip_atomic_store(jb.partials + static_cast<size_t>(slice) * N + colg[i], sum[i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_fetch_add(jb.accum + colg[i], static_cast<double>(sum[i]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ uint32_t last;
@@ -363,29 +375,11 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
                    static_cast<uint32_t>(jb.slices - 1);
         __syncthreads();
         if (!last) return;
-        // All loads in flight together; the pointer steps by a row per slice in a VGPR.
-        float v[PER_THREAD][MAX_SLICES];
 #pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            const float* pp = jb.partials + colg[i];
-#pragma unroll
-            for (int sp = 0; sp < MAX_SLICES; ++sp) {
-                v[i][sp] = 0.0f;
-                if (sp < S && sp != slice && live[i]) v[i][sp] = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                pp += N;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            float s = 0.0f;
-#pragma unroll
-            for (int sp = 0; sp < MAX_SLICES; ++sp)
-                if (sp < S) {
-                    const float vv = sp == slice ? sum[i] : v[i][sp];
-                    s = sp == 0 ? vv : s + vv;
-                }
-            sum[i] = s;
-        }
+        for (int i = 0; i < PER_THREAD; ++i)
+            sum[i] = live[i] ? static_cast<float>(__hip_atomic_exchange(jb.accum + colg[i], 0.0, __ATOMIC_RELAXED,
+                                                                        __HIP_MEMORY_SCOPE_AGENT))
+                             : 0.0f;
         if (t == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
@@ -401,34 +395,76 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)
 
 struct Forced {
     int slices = 0;
+    int waves = 0;
 };
 Forced g_forced;
 
 // x areas: 4 fp16 parts per x value plus 16 bytes per unit, per wave.
 constexpr size_t LDS_X_BYTES = 96 << 10;
+constexpr size_t X_UNIT_BYTES = 4 * UNIT * 2 + 16;
 
-template <int BITS>
-void launch_bits(bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs,
-                 float alpha, int32_t accumulate) {
-    if (BITS == 4 || zp)
-        gemv_wide_kernel<BITS, CPU_, true><<<grid, dim3(THREADS), lds, st>>>(a, K, g, jobs, alpha, accumulate);
-    else
-        gemv_wide_kernel<BITS, CPU_, false><<<grid, dim3(THREADS), lds, st>>>(a, K, g, jobs, alpha, accumulate);
+template <int BITS, bool ZP, int WAVES>
+void launch_one(dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs, float alpha,
+                int32_t accumulate) {
+    gemv_wide_kernel<BITS, CPU_, ZP, WAVES><<<grid, dim3(64 * WAVES), lds, st>>>(a, K, g, jobs, alpha, accumulate);
+}
+
+template <int BITS, bool ZP>
+void launch_waves(int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs,
+                  float alpha, int32_t accumulate) {
+    if (waves == 8) launch_one<BITS, ZP, 8>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
+    else if (waves == 4) launch_one<BITS, ZP, 4>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
+    else launch_one<BITS, ZP, 2>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
+}
+
+void launch_kernel(int bits, bool zp, int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g,
+                   const Jobs& jobs, float alpha, int32_t accumulate) {
+    if (bits == 4) launch_waves<4, true>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
+    else if (zp) launch_waves<8, true>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
+    else launch_waves<8, false>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
+}
+
+struct Plan {
+    int32_t slices, waves, ups;
+};
+
+size_t lds_bytes(int32_t ups, int32_t waves, int sides) {
+    const size_t lds_x = static_cast<size_t>(ceil_div(ups, waves)) * waves * X_UNIT_BYTES;
+    const size_t lds_red = static_cast<size_t>(waves) * sides * TILE * sizeof(float);
+    return lds_x > lds_red ? lds_x : lds_red;
+}
+
+// Eight waves per workgroup and the most K-slices that keep one round of workgroups
+// (one per CU) with at least one unit for every wave: measured on MI355X, a second round
+// or idle waves cost more than the longer slices.
+Plan choose_plan(int64_t tiles, int32_t units) {
+    constexpr int32_t W = MAX_WAVES;
+    if (units < 1 || tiles < 1) return Plan{1, W, 1};  // no unit of 32 rows: the kernel does not apply
+    const int64_t cus = cu_count();
+    int32_t slices = static_cast<int32_t>(cus / tiles);
+    if (slices > units / W) slices = units / W;
+    if (slices < 1) slices = 1;
+    int32_t ups = ceil_div(units, slices);
+    if (static_cast<size_t>(ceil_div(ups, W)) * W * X_UNIT_BYTES > LDS_X_BYTES)
+        ups = static_cast<int32_t>(LDS_X_BYTES / (W * X_UNIT_BYTES)) * W;
+    return Plan{ceil_div(units, ups), W, ups};
 }
 
 }  // namespace
 
-void set_gemv_wide_config(int32_t slices) { g_forced.slices = slices > 0 ? slices : 0; }
+void set_gemv_wide_config(int32_t slices, int32_t waves) {
+    g_forced.slices = slices > 0 ? slices : 0;
+    g_forced.waves = waves == 2 || waves == 4 || waves == 8 ? waves : 0;
+}
 
 bool gemv_wide_preferred(const WeightView* ws, int32_t count) {
     // The wide strips pay off once they give enough workgroups to keep the GPU's loads
     // in flight; smaller products run better as more, narrower workgroups.
     int64_t tiles = 0;
     for (int32_t i = 0; i < count; ++i) tiles += ceil_div(ws[i].bpr, TILE);
-    int32_t slices = ws[0].K / UNIT / WAVES;
-    if (slices > MAX_SLICES) slices = MAX_SLICES;
-    if (slices < 1) slices = 1;
-    return tiles * slices >= 128;
+    if (ws[0].K < UNIT) return false;
+    const Plan p = choose_plan(tiles, ws[0].K / UNIT);
+    return tiles * p.slices >= 128;
 }
 
 bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
@@ -452,43 +488,32 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
     if (zp)
         for (int32_t i = 0; i < count; ++i)
             if (!ws[i].z) return fail(KT_ERR_ARGUMENT, "grouped weights must all have zero points or none");
+    const int sides = w0.bits == 4 ? 2 : 1;
 
     int64_t tiles_total = 0;
     for (int32_t i = 0; i < count; ++i) tiles_total += ceil_div(ws[i].bpr, TILE);
-    // One workgroup of 8 waves per CU keeps about 128 KB of loads in flight there; aim for
-    // two per CU, each wave taking at least one unit.
-    const int64_t target = 2 * static_cast<int64_t>(cu_count());
-    int32_t slices = static_cast<int32_t>((target + tiles_total - 1) / tiles_total);
-    const int32_t max_slices = units / WAVES > 1 ? units / WAVES : 1;
-    if (slices > max_slices) slices = max_slices;
-    if (slices > MAX_SLICES) slices = MAX_SLICES;
-    if (slices < 1) slices = 1;
-    // the x areas bound the units of a slice
-    const int32_t cap_units = static_cast<int32_t>(LDS_X_BYTES / (WAVES * (4 * UNIT * 2 + 16))) * WAVES;
-    if (ceil_div(units, slices) > cap_units) slices = ceil_div(units, cap_units);
-    if (g_forced.slices) slices = g_forced.slices;
-    if (slices > units) slices = units;
-    if (slices > MAX_SLICES) return fail(KT_ERR_ARGUMENT, "wide gemv: at most %d K-slices", MAX_SLICES);
-    const int32_t ups = ceil_div(units, slices);
-    slices = ceil_div(units, ups);
-    const int32_t wave_units = ceil_div(ups, WAVES);
-    if (static_cast<size_t>(wave_units) * WAVES * (4 * UNIT * 2 + 16) > LDS_X_BYTES)
-        return fail(KT_ERR_ARGUMENT, "wide gemv: K-slice too long for the x area");
+    Plan plan = choose_plan(tiles_total, units);
+    if (g_forced.slices || g_forced.waves) {
+        const int32_t waves = g_forced.waves ? g_forced.waves : plan.waves;
+        int32_t slices = g_forced.slices ? g_forced.slices : plan.slices;
+        if (slices > units) slices = units;
+        const int32_t ups = ceil_div(units, slices);
+        plan = Plan{ceil_div(units, ups), waves, ups};
+    }
+    if (static_cast<size_t>(ceil_div(plan.ups, plan.waves)) * plan.waves * X_UNIT_BYTES > LDS_X_BYTES)
+        return fail(KT_ERR_ARGUMENT, "wide gemv: K-slice of %d units too long for the x area", plan.ups);
+    const int32_t slices = plan.slices;
 
-    size_t ws_floats = 0, n_counters = 0;
+    size_t n_accs = 0;
     if (slices > 1)
-        for (int32_t i = 0; i < count; ++i) {
-            ws_floats += static_cast<size_t>(slices) * ws[i].N;
-            n_counters += ceil_div(ws[i].bpr, TILE);
-        }
-    float* partials = nullptr;
+        for (int32_t i = 0; i < count; ++i) n_accs += static_cast<size_t>(ws[i].N);
+    double* accs = nullptr;
     uint32_t* counters = nullptr;
-    if (ws_floats) {
-        if (n_counters > MAX_COUNTERS) return fail(KT_ERR_ARGUMENT, "wide gemv: too many tiles for the counters");
-        void* p = nullptr;
-        const int32_t status = workspace_counters(st, ws_floats * sizeof(float), n_counters, &p, &counters);
+    if (slices > 1) {
+        if (static_cast<size_t>(tiles_total) > MAX_COUNTERS)
+            return fail(KT_ERR_ARGUMENT, "wide gemv: too many tiles for the counters");
+        const int32_t status = workspace_accumulators(st, static_cast<size_t>(tiles_total), n_accs, &counters, &accs);
         if (status) return status;
-        partials = static_cast<float*>(p);
     }
     Jobs jobs{};
     jobs.count = count;
@@ -505,20 +530,16 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
         jb.bpr = ws[i].bpr;
         jb.tiles = ceil_div(ws[i].bpr, TILE);
         jb.slices = slices;
-        jb.units_per_slice = ups;
-        jb.partials = slices > 1 ? partials + offset : nullptr;
+        jb.units_per_slice = plan.ups;
+        jb.accum = slices > 1 ? accs + offset : nullptr;
         jb.counters = slices > 1 ? counters + coffset : nullptr;
-        offset += static_cast<size_t>(slices) * ws[i].N;
+        offset += static_cast<size_t>(ws[i].N);
         coffset += jb.tiles;
         if (jb.tiles * slices > blocks) blocks = jb.tiles * slices;
     }
-    const int sides = ws[0].bits == 4 ? 2 : 1;
-    const size_t lds_x = static_cast<size_t>(wave_units) * WAVES * (4 * UNIT * 2 + 16);
-    const size_t lds_red = static_cast<size_t>(WAVES) * sides * TILE * sizeof(float);
-    const size_t lds = lds_x > lds_red ? lds_x : lds_red;
+    const size_t lds = lds_bytes(plan.ups, plan.waves, sides);
     const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
-    if (ws[0].bits == 4) launch_bits<4>(zp, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
-    else launch_bits<8>(zp, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
+    launch_kernel(w0.bits, zp, plan.waves, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
     KT_LAUNCHED("qmatmul: wide gemv kernel");
     return KT_OK;
 }

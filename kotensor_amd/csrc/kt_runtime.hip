@@ -31,35 +31,39 @@ int32_t hip_fail(hipError_t err, const char* what) {
 namespace {
 struct Block {
     void* ptr = nullptr;
-    size_t bytes = 0;
+    size_t bytes = 0;   // whole allocation
+    size_t zbytes = 0;  // the zeroed accumulator region after the counters
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Block> g_ws;
 std::map<int, int32_t> g_cus;
 }  // namespace
 
-// Each workspace starts with a COUNTER_BYTES region of uint32 counters that is zeroed
-// when the allocation is made and that every kernel using it leaves at zero; the
-// general area follows it.
+// Each workspace starts with a COUNTER_BYTES region of uint32 counters and a region of
+// fp64 accumulators, both zeroed when the allocation is made and left at zero by every
+// kernel that uses them; the general area follows.
 constexpr size_t COUNTER_BYTES = 64 << 10;
 
-static int32_t ensure(hipStream_t stream, size_t bytes, Block** out) {
+static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** out) {
     int device = 0;
     KT_HIP(hipGetDevice(&device));
     Block& b = g_ws[std::make_pair(device, stream)];
-    if (b.bytes < COUNTER_BYTES + bytes) {
-        const size_t need = COUNTER_BYTES + bytes;
+    const size_t zcap = zbytes > b.zbytes ? zbytes + zbytes / 4 : b.zbytes;
+    if (zbytes > b.zbytes || b.bytes < COUNTER_BYTES + zcap + bytes) {
+        const size_t need = COUNTER_BYTES + zcap + bytes;
         size_t want = need < (size_t(1) << 20) ? (size_t(1) << 20) : need + need / 4;
         if (b.ptr) {
             KT_HIP(hipStreamSynchronize(stream));
             KT_HIP(hipFree(b.ptr));
             b.ptr = nullptr;
             b.bytes = 0;
+            b.zbytes = 0;
         }
         KT_HIP(hipMalloc(&b.ptr, want));
-        KT_HIP(hipMemsetAsync(b.ptr, 0, COUNTER_BYTES, stream));
+        KT_HIP(hipMemsetAsync(b.ptr, 0, COUNTER_BYTES + zcap, stream));
         KT_HIP(hipStreamSynchronize(stream));
         b.bytes = want;
+        b.zbytes = zcap;
     }
     *out = &b;
     return KT_OK;
@@ -68,9 +72,9 @@ static int32_t ensure(hipStream_t stream, size_t bytes, Block** out) {
 int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block* b = nullptr;
-    int32_t status = ensure(stream, bytes, &b);
+    int32_t status = ensure(stream, 0, bytes, &b);
     if (status) return status;
-    *out = static_cast<char*>(b->ptr) + COUNTER_BYTES;
+    *out = static_cast<char*>(b->ptr) + COUNTER_BYTES + b->zbytes;
     return KT_OK;
 }
 
@@ -78,10 +82,21 @@ int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void*
     if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block* b = nullptr;
-    int32_t status = ensure(stream, bytes, &b);
+    int32_t status = ensure(stream, 0, bytes, &b);
     if (status) return status;
     *counters = static_cast<uint32_t*>(b->ptr);
-    *general = static_cast<char*>(b->ptr) + COUNTER_BYTES;
+    *general = static_cast<char*>(b->ptr) + COUNTER_BYTES + b->zbytes;
+    return KT_OK;
+}
+
+int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs) {
+    if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Block* b = nullptr;
+    int32_t status = ensure(stream, doubles * sizeof(double), 0, &b);
+    if (status) return status;
+    *counters = static_cast<uint32_t*>(b->ptr);
+    *accs = reinterpret_cast<double*>(static_cast<char*>(b->ptr) + COUNTER_BYTES);
     return KT_OK;
 }
 
@@ -166,7 +181,7 @@ int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_s
     set_gemv_config(gemv_vec, gemv_splits, gemv_waves == 2 ? 4 : gemv_waves);
     set_gemv_reduce_mode(gemv_reduce);
     set_gemv_mfma_config(gemv_splits, gemv_waves, gemv_reduce, gemv_kind == 1);
-    set_gemv_wide_config(gemv_splits);
+    set_gemv_wide_config(gemv_splits, gemv_waves);
     g_gemv_kind = gemv_kind;
     return KT_OK;
 }
