@@ -68,6 +68,17 @@ def lib():
         L.ko_multiply_by_quantized_transposed.argtypes = [P, ctypes.POINTER(QW), P, I, I, I]
         L.ko_row_units.argtypes = [ctypes.POINTER(QW), P]
         L.ko_row_units.restype = None
+        L.ko_rope_inv_freq.argtypes = [I, F, F, F, F, I, P]
+        L.ko_rope_inv_freq.restype = None
+        L.ko_rmsnorm.argtypes = [P, I, I, P, F, P]
+        L.ko_rmsnorm.restype = None
+        L.ko_rope_rows.argtypes = [P, I, I, I, P, I]
+        L.ko_rope_rows.restype = None
+        L.ko_attend.argtypes = [P, I, I, P, P, I, I, I, I, I, P, P]
+        L.ko_attend.restype = None
+        L.ko_silu_mul.argtypes = [P, P, I]
+        L.ko_silu_mul.restype = None
+        L.ko_argmax.argtypes = [P, I]
         _lib = L
     return _lib
 
@@ -170,3 +181,54 @@ def multiply_by_quantized_transposed(dy: np.ndarray, w: Quantized, m: int, dx: n
     if st != KO_OK:
         raise ValueError(f"oracle transposed status {st}")
     return dx.reshape(m, w.rows)
+
+
+# ---- decoder pieces (kt_oracle_decoder.c) ------------------------------------------
+
+
+def rope_inv_freq(head_dim: int, base: float, scaling: tuple | None = None) -> np.ndarray:
+    """RoPE.invFreq; scaling = (factor, low, high, original_max) or None."""
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    f, lo, hi, om = scaling if scaling else (0.0, 1.0, 4.0, 8192)
+    lib().ko_rope_inv_freq(head_dim, ctypes.c_float(base), ctypes.c_float(f), ctypes.c_float(lo), ctypes.c_float(hi),
+                           int(om), _p(out))
+    return out
+
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, dim = x.reshape(-1, weight.size).shape
+    out = np.empty_like(x)
+    lib().ko_rmsnorm(_p(x), rows, dim, _p(np.ascontiguousarray(weight, dtype=np.float32)), ctypes.c_float(eps), _p(out))
+    return out
+
+
+def rope_rows(rows: np.ndarray, head_dim: int, inv_freq: np.ndarray, start: int) -> np.ndarray:
+    """A rotated copy of rows [tokens x width]."""
+    out = np.array(rows, dtype=np.float32, copy=True, order="C")
+    tokens, width = out.shape
+    lib().ko_rope_rows(_p(out), tokens, width, head_dim, _p(np.ascontiguousarray(inv_freq, dtype=np.float32)), start)
+    return out
+
+
+def attend(q: np.ndarray, start: int, keys: np.ndarray, values: np.ndarray, layer: int, num_heads: int,
+           num_kv_heads: int, head_dim: int, max_seq: int) -> np.ndarray:
+    """attendCached for q [tokens x num_heads*head_dim] over caches in the KVCache layout."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    tokens = q.shape[0]
+    context = np.empty_like(q)
+    scores = np.empty(start + tokens, dtype=np.float32)
+    lib().ko_attend(_p(q), tokens, start, _p(keys), _p(values), layer, num_heads, num_kv_heads, head_dim, max_seq,
+                    _p(context), _p(scores))
+    return context
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    out = np.array(gate, dtype=np.float32, copy=True, order="C")
+    lib().ko_silu_mul(_p(out), _p(np.ascontiguousarray(up, dtype=np.float32)), out.size)
+    return out
+
+
+def argmax(logits: np.ndarray) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    return int(lib().ko_argmax(_p(x), x.size))

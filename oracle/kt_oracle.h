@@ -26,6 +26,22 @@
  *       which is below the 2e-3 normwise criterion the GPU path is held to.
  *   ko_multiply_by_quantized_transposed  pinned to fp64 brute force
  *       (QuantizationTest.kt:98-105 tolerance 1e-3); bit order unpinned as above.
+ *
+ * Decoder pieces (kt_oracle_decoder.c, tests/test_oracle_decoder.py):
+ *   ko_rope_inv_freq ... pinned: closed form 1/base^(2i/d) in fp64, and the scaled
+ *       frequencies' three regimes worked by hand (unchanged, divided by the factor,
+ *       the smooth blend at its two ends).
+ *   ko_rmsnorm ......... pinned: fp64 closed form, zero rows, a constant row (exact
+ *       answer 1/sqrt(1+eps) per unit weight), scaling invariance.
+ *   ko_rope_rows ....... pinned: position 0 is the identity, each pair keeps its norm,
+ *       fp64 closed form, rotating by p1 then p2 equals p1 + p2, every head rotates
+ *       alike (RegressionTest.kt:57-76), rows agree with one row at a time.
+ *   ko_attend .......... pinned: fp64 brute-force softmax attention (causal, GQA
+ *       head mapping), one position gives v, equal scores give the mean of v.
+ *   ko_silu_mul, ko_argmax  pinned: fp64 closed form; first index of the maximum,
+ *       the -1e9 floor and NaN skipping by hand.
+ *   The summation orders follow the reference loops by reading; their bits are
+ *   "parity unpinned" (no JVM), far below the tolerances the GPU path is held to.
  */
 #ifndef KT_ORACLE_H
 #define KT_ORACLE_H
@@ -84,6 +100,23 @@ int32_t ko_multiply_by_quantized_transposed(const float* dy, const ko_qweight* w
 /* The M == 1 unit decomposition of K/MatMul.kt:494-512, exposed for tests:
  * out[0..5] = {target_units, rows_per_unit, row_units, column_units, block_bytes, blocks}. */
 void ko_row_units(const ko_qweight* w, int32_t* out6);
+
+/* ---- decoder pieces (kt_oracle_decoder.c) ---------------------------------------- */
+/* RoPE.invFreq (K/RoPE.kt:42-46) with RoPEScaling.scale (:18-30) when factor > 0. */
+void ko_rope_inv_freq(int32_t head_dim, float base, float factor, float low, float high, int32_t original_max,
+                      float* out);
+/* RMSNorm.forwardInto (K/RMSNorm.kt:71-90). */
+void ko_rmsnorm(const float* x, int32_t rows, int32_t dim, const float* weight, float eps, float* out);
+/* RoPE.applyRowsInPlace (K/RoPE.kt:139-164). */
+void ko_rope_rows(float* rows, int32_t tokens, int32_t width, int32_t head_dim, const float* inv_freq, int32_t start);
+/* Attention.attendCached/attendHead/dot (K/Attention.kt:277-349); scores: start+tokens floats. */
+void ko_attend(const float* q, int32_t tokens, int32_t start, const float* keys, const float* values, int32_t layer,
+               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t max_seq, float* context,
+               float* scores);
+/* gate = silu(gate) * up (K/SwiGLU.kt:19-25, K/Tensor.kt:223-237). */
+void ko_silu_mul(float* gate, const float* up, int32_t n);
+/* Transformer.argmaxOfLastToken (K/Transformer.kt:253-266). */
+int32_t ko_argmax(const float* logits, int32_t n);
 
 #ifdef __cplusplus
 }
