@@ -74,8 +74,7 @@ int32_t kt_set_device(int32_t device);
  *            kernel for two, where the layout allows), 1 = vector-ALU kernel for M == 1,
  *            2 = row-block MFMA kernel for M <= 2, 3 = wide-strip MFMA kernel for M == 1;
  * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic);
- * gemv_splits: workgroups along K per column tile (0 = automatic; at most 32 for the
- *              wide-strip kernel);
+ * gemv_splits: workgroups along K per column tile (0 = automatic);
  * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic);
  * gemv_reduce: how split sums meet (0 = automatic, 1 = a second kernel, 2 = inside the
  * kernel). Process-wide. */
@@ -92,6 +91,14 @@ int32_t kt_memset(void* dst, int32_t value, size_t bytes, void* stream);
 int32_t kt_stream_create(void** stream);
 int32_t kt_stream_destroy(void* stream);
 int32_t kt_stream_sync(void* stream);
+/* HIP graphs: kernels enqueued on `stream` between kt_graph_begin and kt_graph_end are
+ * recorded (not run) and instantiated into *graph, which kt_graph_launch replays on a
+ * stream. The replacement for a tracing compiler on the decode path: one decode step
+ * is recorded once and replayed per token. No counterpart in the reference. */
+int32_t kt_graph_begin(void* stream);
+int32_t kt_graph_end(void* stream, void** graph);
+int32_t kt_graph_launch(void* graph, void* stream);
+int32_t kt_graph_destroy(void* graph);
 
 /* ---- format helpers (pure host arithmetic, no device work) -------------------- */
 /* groups, storedColumns, bytesPerRow and sizeInBytes of K/QuantizedTensor.kt:47-49,97-98. */
@@ -159,6 +166,61 @@ int32_t kt_dequantize_rows(const kt_qweight* w, const int32_t* rows, int32_t cou
  * K/QuantizedTensor.kt:235-241). An index outside [0, columns) produces NaN. */
 int32_t kt_dequantize_columns(const kt_qweight* w, const int32_t* columns, int32_t count,
                               float* out, void* stream);
+
+/* ---- the rest of the decode/prefill step (kt_decoder.hip) ------------------------
+ * The pieces of Transformer.prefill/decode around the projections (K/Transformer.kt:
+ * 99-154, K/TransformerBlock.kt:204-220), device-resident. `position` is a device
+ * int32 holding the KV cache length (KVCache.length, K/KVCache.kt:12), read by the
+ * kernels and advanced with kt_position_add, so a decode step can be recorded in a HIP
+ * graph and replayed per token. The cache layout is KVCache's: keys and values of
+ * [layers x kv_heads x max_seq x head_dim] fp32 (K/KVCache.kt:9-27). The host checks
+ * capacity (the reference's "KV cache full" errors); the kernels never read or write
+ * outside the cache. */
+
+/* RoPE.invFreq with optional RoPEScaling (K/RoPE.kt:18-46), computed on the host into
+ * out[head_dim / 2]; factor <= 0 means no scaling. */
+int32_t kt_rope_inv_freq(int32_t head_dim, float base, float factor, float low, float high,
+                         int32_t original_max, float* out);
+/* RMSNorm.forwardInto (K/RMSNorm.kt:71-90): out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * weight,
+ * rows x dim (out may alias nothing but itself). */
+int32_t kt_rmsnorm(const float* x, int32_t rows, int32_t dim, const float* weight, float eps,
+                   float* out, void* stream);
+/* RoPE.applyRowsInPlace on q [tokens x num_heads*head_dim] and k [tokens x
+ * num_kv_heads*head_dim] at positions *position + t (K/RoPE.kt:139-164), then the
+ * cache writes of rotated k and of v for those positions (K/Attention.kt:254-270;
+ * decodeInto :220-233 is tokens = 1). inv_freq: device [head_dim / 2]. */
+int32_t kt_rope_kv(float* q, float* k, const float* v, int32_t tokens, int32_t num_heads,
+                   int32_t num_kv_heads, int32_t head_dim, const float* inv_freq,
+                   const int32_t* position, float* cache_k, float* cache_v, int32_t layer,
+                   int32_t max_seq, void* stream);
+/* Attention.attendCached (K/Attention.kt:277-349): for token t at position *position + t,
+ * softmax(q . k_j / sqrt(head_dim)) over cached positions j <= that position, of the
+ * kv head that serves its query head (GQA), times v, into context [tokens x
+ * num_heads*head_dim]. key_bound >= *position + tokens bounds the keys (it sizes the
+ * launch; a captured decode step passes max_seq). */
+int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound,
+                     const float* cache_k, const float* cache_v, int32_t layer, int32_t max_seq,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,
+                     void* stream);
+/* SwiGLU's gate (K/SwiGLU.kt:19-25; K/Tensor.kt:223-237): gate[i] = silu(gate[i]) * up[i]. */
+int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream);
+/* Transformer.argmaxOfLastToken (K/Transformer.kt:253-266) of logits[0..n) into the
+ * device int32 *index: the first index of the largest logit above -1e9, else 0. */
+int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream);
+/* KVCache.advance on the device copy of the length (K/KVCache.kt:29-35): *position += count. */
+int32_t kt_position_add(int32_t* position, int32_t count, void* stream);
+/* generated[*position] = *token when 0 <= *position < capacity: the device-side record of
+ * the greedy tokens of generate (K/Transformer.kt:224-231 yields them one by one), read
+ * by the host once at the end instead of after every step. */
+int32_t kt_record_token(const int32_t* token, const int32_t* position, int32_t* generated,
+                        int32_t capacity, void* stream);
+/* Tensor.addInPlace (K/Tensor.kt:201-221): x[i] = x[i] + y[i]; the residual adds of
+ * TransformerBlock.decodeInto/prefillInto (K/TransformerBlock.kt:207-219). */
+int32_t kt_add_inplace(float* x, const float* y, int64_t n, void* stream);
+/* Synthetic weights: out[i] = mean + stddev * N(0,1), element i a function of (seed, i)
+ * only (SplitMix64 and Box-Muller). No counterpart in the reference, which draws its
+ * initial weights from kotlin.random; used to build random-init models on the device. */
+int32_t kt_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float stddev, void* stream);
 
 /* ---- saveQuantized files (safetensors) -------------------------------------------
  * The reference stores quantized models as safetensors (SafeTensors.kt:12-249): an

@@ -4,8 +4,10 @@ weight-only quantization path.
 The product is ``libkotensor_hip.so`` (C ABI: ``include/kotensor_hip.h``). This
 package is a host-side mirror of the reference's API over that ABI:
 ``Quantization``, ``QuantizedTensor``, ``MatMul.multiply_quantized``,
-``DeviceTensor.matmul_dequant(_into)``, ``QuantizedLinear`` and the saveQuantized
-file format (``SafeTensorsFile``, ``save_quantized``, ``load_quantized``).
+``DeviceTensor.matmul_dequant(_into)``, ``QuantizedLinear``, the saveQuantized
+file format (``SafeTensorsFile``, ``save_quantized``, ``load_quantized``) and the
+device-resident decoder around the projections (``Transformer``, ``KVCache``,
+``InferenceBuffers``, ``RoPEScaling``).
 """
 from ._lib import IllegalArgumentException, IllegalStateException, LibraryMissingError, LIBRARY_PATH
 from .device import DeviceBuffer, Stream, synchronize, device_count
@@ -13,6 +15,7 @@ from .quantization import Quantization, QuantizedTensor
 from .matmul import MatMul, DeviceTensor
 from .linear import QuantizedLinear, projection, forward_into_group
 from .safetensors import SafeTensorsFile, save_entries, save_quantized, load_quantized
+from .transformer import Transformer, KVCache, InferenceBuffers, RoPEScaling
 
 __all__ = [
     "IllegalArgumentException",
@@ -34,4 +37,8 @@ __all__ = [
     "save_entries",
     "save_quantized",
     "load_quantized",
+    "Transformer",
+    "KVCache",
+    "InferenceBuffers",
+    "RoPEScaling",
 ]

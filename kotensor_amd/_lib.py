@@ -108,6 +108,20 @@ SIGNATURES = {
     "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],
     "kt_dequantize_rows": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
     "kt_dequantize_columns": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
+    "kt_rope_inv_freq": [_I, _F, _F, _F, _F, _I, _P],
+    "kt_rmsnorm": [_P, _I, _I, _P, _F, _P, _P],
+    "kt_rope_kv": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P],
+    "kt_attention": [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P],
+    "kt_silu_mul": [_P, _P, ctypes.c_int64, _P],
+    "kt_argmax": [_P, _I, _P, _P],
+    "kt_position_add": [_P, _I, _P],
+    "kt_record_token": [_P, _P, _P, _I, _P],
+    "kt_graph_begin": [_P],
+    "kt_graph_end": [_P, _P],
+    "kt_graph_launch": [_P, _P],
+    "kt_graph_destroy": [_P],
+    "kt_add_inplace": [_P, _P, ctypes.c_int64, _P],
+    "kt_fill_normal": [_P, ctypes.c_int64, ctypes.c_uint64, _F, _F, _P],
     "kt_st_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
     "kt_st_close": [_P],
     "kt_st_count": [_P, ctypes.POINTER(_I)],

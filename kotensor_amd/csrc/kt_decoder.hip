@@ -1,0 +1,557 @@
+// kt_decoder.hip -- the rest of the decode/prefill step around the quantized
+// projections, on the device: RMSNorm, RoPE with the KV-cache append, cached GQA
+// attention, the SwiGLU gate, the greedy argmax and the cache position.
+//
+// Reference semantics (Engine/kotensor/src/main/kotlin/, K/):
+//   RMSNorm.forwardInto          K/RMSNorm.kt:71-90
+//   RoPE.invFreq, RoPEScaling     K/RoPE.kt:18-46
+//   RoPE.applyRowsInPlace         K/RoPE.kt:139-164 (applyInPlace :117-137 is one row)
+//   Attention.prefillInto/decodeInto's cache writes  K/Attention.kt:220-233, 254-270
+//   Attention.attendCached/attendHead/dot            K/Attention.kt:277-349
+//   SwiGLU gate: siluInPlace, mulInPlace             K/SwiGLU.kt:19-25, K/Tensor.kt:223-237
+//   Transformer.argmaxOfLastToken                    K/Transformer.kt:253-266
+//   KVCache layout ((layer * kv_heads + head) * max_seq + position) * head_dim,
+//   K/KVCache.kt:25-27.
+//
+// The cache position is a device int32 (the cache length), read by the kernels and
+// advanced by kt_position_add, so a whole decode step can be recorded in a HIP graph
+// and replayed token after token.
+//
+// Numerics: the reference's transcendental functions are double-precision results
+// rounded to float; the RoPE angles use double cos/sin the same way, and the RoPE
+// rotation is computed without contraction, so q and k come out as the reference's.
+// RMSNorm, attention and the gate use the GPU's fp32 reductions and expf, which
+// differ from the reference's sequential sums by fp32 rounding only.
+#include <math.h>
+
+#include "kt_common.h"
+
+namespace kt {
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int KT = 64;        // keys per attention tile
+constexpr int MAX_NACC = 4;   // (head, dim) pairs per thread: heads per kv head x head_dim <= 1024
+constexpr int MAX_HD = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---- RMSNorm ---------------------------------------------------------------------
+// One workgroup per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * weight.
+__global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restrict__ x, int32_t dim,
+                                                          const float* __restrict__ w, float eps,
+                                                          float* __restrict__ out) {
+    __shared__ float part[THREADS / 64];
+    const float* row = x + static_cast<size_t>(blockIdx.x) * dim;
+    float* orow = out + static_cast<size_t>(blockIdx.x) * dim;
+    float s = 0.0f;
+    for (int32_t d = threadIdx.x; d < dim; d += THREADS) s = fmaf(row[d], row[d], s);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < THREADS / 64; ++i) total += part[i];
+    const float r = 1.0f / sqrtf(total / static_cast<float>(dim) + eps);
+    for (int32_t d = threadIdx.x; d < dim; d += THREADS) orow[d] = row[d] * r * w[d];
+}
+
+// ---- RoPE + cache append -----------------------------------------------------------
+// Thread (token t, unit u): u < num_heads * half rotates pair i of q head u / half;
+// the next num_kv_heads * half units rotate k and write k and v to the cache.
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(THREADS) rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                          const float* __restrict__ v, int32_t num_heads,
+                                                          int32_t num_kv_heads, int32_t head_dim,
+                                                          const float* __restrict__ inv_freq,
+                                                          const int32_t* __restrict__ position,
+                                                          float* __restrict__ cache_k, float* __restrict__ cache_v,
+                                                          int32_t layer, int32_t max_seq) {
+    const int32_t half = head_dim >> 1;
+    const int32_t t = blockIdx.y;
+    const int32_t u = blockIdx.x * THREADS + threadIdx.x;
+    const int32_t q_units = num_heads * half, units = q_units + num_kv_heads * half;
+    if (u >= units) return;
+    const int32_t pos = *position + t;
+    if (pos < 0 || pos >= max_seq) return;  // the host checks capacity; never write outside the cache
+    const bool is_q = u < q_units;
+    const int32_t h = (is_q ? u : u - q_units) / half;
+    const int32_t i = (is_q ? u : u - q_units) % half;
+    const float theta = static_cast<float>(pos) * inv_freq[i];
+    const float c = static_cast<float>(cos(static_cast<double>(theta)));
+    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    float* row = is_q ? q + static_cast<size_t>(t) * num_heads * head_dim
+                      : k + static_cast<size_t>(t) * num_kv_heads * head_dim;
+    const int32_t i1 = h * head_dim + i, i2 = i1 + half;
+    const float x1 = row[i1], x2 = row[i2];
+    const float y1 = x1 * c - x2 * s;
+    const float y2 = x1 * s + x2 * c;
+    row[i1] = y1;
+    row[i2] = y2;
+    if (!is_q) {
+        const size_t base = ((static_cast<size_t>(layer) * num_kv_heads + h) * max_seq + pos) * head_dim;
+        const float* vrow = v + static_cast<size_t>(t) * num_kv_heads * head_dim;
+        cache_k[base + i] = y1;
+        cache_k[base + i + half] = y2;
+        cache_v[base + i] = vrow[i1];
+        cache_v[base + i + half] = vrow[i2];
+    }
+}
+#pragma clang fp contract(on)
+
+// ---- cached attention ------------------------------------------------------------------
+struct AttnArgs {
+    const float* q;          // [tokens x num_heads * head_dim]
+    const int32_t* position;  // cache length before these tokens
+    const float* ck;
+    const float* cv;
+    float* context;          // [tokens x num_heads * head_dim]
+    float* partials;         // [tokens][num_heads][splits][head_dim + 2] when splits > 1
+    int32_t layer, max_seq, num_heads, num_kv_heads, head_dim, splits, span;
+    float scale;
+};
+
+// Workgroup (kv head g, key split s, token t): the G = num_heads / num_kv_heads query
+// heads of kv head g over keys [s * span, min((s + 1) * span, position + t + 1)), in
+// tiles of 64 keys with a running maximum and sum (scores, then exp(score - max),
+// then the weighted values). With one split the workgroup writes the context; with
+// several it writes (sum of weighted values, max, sum) for attn_combine_kernel.
+__global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
+    extern __shared__ float smem[];
+    const int32_t g = blockIdx.x, s = blockIdx.y, t = blockIdx.z;
+    const int32_t HD = a.head_dim, G = a.num_heads / a.num_kv_heads;
+    const int32_t dim = a.num_heads * HD;
+    const int32_t KP = HD + 1;  // padded key row: lanes reading consecutive rows hit distinct banks
+    float* qs = smem;                  // [G][HD]
+    float* ks = qs + G * HD;           // [KT][HD + 1]
+    float* sc = ks + KT * KP;          // [G][KT]
+    float* st = sc + G * KT;           // [G] x {m, l, alpha}
+    const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    const int32_t pos = *a.position + t;
+    const int32_t k_begin = s * a.span;
+    const int32_t k_end = min(min(k_begin + a.span, pos + 1), a.max_seq);  // never read outside the cache
+    const size_t base = (static_cast<size_t>(a.layer) * a.num_kv_heads + g) * a.max_seq;  // row of key 0
+
+    for (int32_t e = tid; e < G * HD; e += THREADS) qs[e] = a.q[static_cast<size_t>(t) * dim + g * G * HD + e];
+    for (int32_t i = tid; i < G; i += THREADS) {
+        st[3 * i] = -INFINITY;
+        st[3 * i + 1] = 0.0f;
+    }
+    const int32_t pairs = G * HD;
+    const int32_t nacc = (pairs + THREADS - 1) / THREADS;
+    float acc[MAX_NACC];
+#pragma unroll
+    for (int r = 0; r < MAX_NACC; ++r) acc[r] = 0.0f;
+    __syncthreads();
+
+    for (int32_t k0 = k_begin; k0 < k_end; k0 += KT) {
+        const int32_t n = min(KT, k_end - k0);
+        // key tile to LDS, coalesced rows
+        for (int32_t e = tid; e < n * HD; e += THREADS) {
+            const int32_t j = e / HD, d = e % HD;
+            ks[j * KP + d] = a.ck[(base + k0 + j) * HD + d];
+        }
+        __syncthreads();
+        // scores: pair (head i, key j)
+        for (int32_t e = tid; e < G * KT; e += THREADS) {
+            const int32_t i = e / KT, j = e % KT;
+            float score = -INFINITY;
+            if (j < n) {
+                const float* qi = qs + i * HD;
+                const float* kj = ks + j * KP;
+                float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+                for (int32_t d = 0; d < HD; d += 4) {
+                    s0 = fmaf(qi[d], kj[d], s0);
+                    s1 = fmaf(qi[d + 1], kj[d + 1], s1);
+                    s2 = fmaf(qi[d + 2], kj[d + 2], s2);
+                    s3 = fmaf(qi[d + 3], kj[d + 3], s3);
+                }
+                score = ((s0 + s1) + (s2 + s3)) * a.scale;
+            }
+            sc[i * KT + j] = score;
+        }
+        __syncthreads();
+        // running max and sum per head: one wave per head, a lane per key
+        for (int32_t i = wave; i < G; i += THREADS / 64) {
+            const float v = sc[i * KT + lane];
+            const float m_old = st[3 * i];
+            const float m_new = fmaxf(m_old, wave_max(v));
+            const float e = lane < n ? expf(v - m_new) : 0.0f;
+            sc[i * KT + lane] = e;
+            const float sum = wave_sum(e);
+            if (lane == 0) {
+                const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                st[3 * i] = m_new;
+                st[3 * i + 1] = st[3 * i + 1] * alpha + sum;
+                st[3 * i + 2] = alpha;
+            }
+        }
+        __syncthreads();
+        // weighted values: pair (head i, dim d)
+#pragma unroll
+        for (int r = 0; r < MAX_NACC; ++r) {
+            const int32_t e = tid + r * THREADS;
+            if (r < nacc && e < pairs) {
+                const int32_t i = e / HD, d = e % HD;
+                float x = acc[r] * st[3 * i + 2];
+                const float* vp = a.cv + (base + k0) * HD + d;
+                const float* ep = sc + i * KT;
+                for (int32_t j = 0; j < n; ++j) x = fmaf(ep[j], vp[static_cast<size_t>(j) * HD], x);
+                acc[r] = x;
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int r = 0; r < MAX_NACC; ++r) {
+        const int32_t e = tid + r * THREADS;
+        if (r < nacc && e < pairs) {
+            const int32_t i = e / HD, d = e % HD;
+            const int32_t head = g * G + i;
+            if (a.splits == 1) {
+                a.context[static_cast<size_t>(t) * dim + head * HD + d] = acc[r] * (1.0f / st[3 * i + 1]);
+            } else {
+                float* pp = a.partials + ((static_cast<size_t>(t) * a.num_heads + head) * a.splits + s) * (HD + 2);
+                pp[d] = acc[r];
+                if (d == 0) {
+                    pp[HD] = st[3 * i];
+                    pp[HD + 1] = st[3 * i + 1];
+                }
+            }
+        }
+    }
+}
+
+// Workgroup (token t, head h): merges the splits' (weighted values, max, sum).
+__global__ void __launch_bounds__(THREADS) attn_combine_kernel(AttnArgs a) {
+    const int32_t t = blockIdx.y, h = blockIdx.x, HD = a.head_dim;
+    const float* pp = a.partials + (static_cast<size_t>(t) * a.num_heads + h) * a.splits * (HD + 2);
+    float m = -INFINITY;
+    for (int32_t s = 0; s < a.splits; ++s) m = fmaxf(m, pp[s * (HD + 2) + HD]);
+    float l = 0.0f;
+    for (int32_t s = 0; s < a.splits; ++s) {
+        const float ms = pp[s * (HD + 2) + HD];
+        if (ms != -INFINITY) l += pp[s * (HD + 2) + HD + 1] * expf(ms - m);
+    }
+    const float inv = 1.0f / l;
+    for (int32_t d = threadIdx.x; d < HD; d += THREADS) {
+        float x = 0.0f;
+        for (int32_t s = 0; s < a.splits; ++s) {
+            const float ms = pp[s * (HD + 2) + HD];
+            if (ms != -INFINITY) x = fmaf(pp[s * (HD + 2) + d], expf(ms - m), x);
+        }
+        a.context[static_cast<size_t>(t) * a.num_heads * HD + h * HD + d] = x * inv;
+    }
+}
+
+// ---- SwiGLU gate -----------------------------------------------------------------------
+__global__ void __launch_bounds__(THREADS) silu_mul_kernel(float* __restrict__ gate, const float* __restrict__ up,
+                                                           int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (i >= n) return;
+    const float x = gate[i];
+    const float silu = x / (1.0f + static_cast<float>(exp(-static_cast<double>(x))));
+    gate[i] = silu * up[i];
+}
+
+// ---- argmax ----------------------------------------------------------------------------
+// Key of a candidate logit: larger value first, then smaller index. Logits not above
+// -1e9 (and NaNs) are not candidates; with none the key stays 0 and the index is 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, int32_t idx) {
+    if (!(v > -1e9f)) return 0;
+    uint32_t b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(0xFFFFFFFFu - static_cast<uint32_t>(idx));
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t w = (static_cast<uint64_t>(__shfl_xor(static_cast<uint32_t>(v >> 32), o, 64)) << 32) |
+                           __shfl_xor(static_cast<uint32_t>(v), o, 64);
+        v = max_u64(v, w);
+    }
+    return v;
+}
+
+// Each workgroup reduces a stride of the logits into partials[block]; the last one to
+// finish (counter) reduces the partials, writes the index and resets the counter.
+__global__ void __launch_bounds__(THREADS) argmax_kernel(const float* __restrict__ logits, int32_t n,
+                                                         int32_t* __restrict__ index, uint64_t* partials,
+                                                         uint32_t* counter) {
+    __shared__ uint64_t part[THREADS / 64];
+    __shared__ uint32_t last;
+    uint64_t best = 0;
+    for (int32_t i = blockIdx.x * THREADS + threadIdx.x; i < n; i += gridDim.x * THREADS)
+        best = max_u64(best, argmax_key(logits[i], i));
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = part[0];
+        for (int i = 1; i < THREADS / 64; ++i) b = max_u64(b, part[i]);
+        __hip_atomic_store(partials + blockIdx.x, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    uint64_t b = 0;
+    for (int32_t i = threadIdx.x; i < static_cast<int32_t>(gridDim.x); i += THREADS)
+        b = max_u64(b, __hip_atomic_load(partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    b = wave_max_u64(b);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < THREADS / 64; ++i) b = max_u64(b, part[i]);
+        b = max_u64(b, part[0]);
+        *index = b == 0 ? 0 : static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(b));
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ---- residual add and synthetic weights ---------------------------------------------
+__global__ void __launch_bounds__(THREADS) add_kernel(float* __restrict__ x, const float* __restrict__ y, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+// SplitMix64 of (seed, index): the same value for an element whatever the launch shape.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// Element i: Box-Muller on two 53-bit uniforms drawn from (seed, i).
+__global__ void __launch_bounds__(THREADS) fill_normal_kernel(float* __restrict__ out, int64_t n, uint64_t seed,
+                                                              float mean, float stddev) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t a = splitmix64(seed ^ splitmix64(2 * static_cast<uint64_t>(i)));
+    const uint64_t b = splitmix64(seed ^ splitmix64(2 * static_cast<uint64_t>(i) + 1));
+    const double u1 = (static_cast<double>(a >> 11) + 1.0) * 0x1.0p-53;  // (0, 1]
+    const double u2 = static_cast<double>(b >> 11) * 0x1.0p-53;          // [0, 1)
+    const double z = sqrt(-2.0 * log(u1)) * cos(2.0 * 3.141592653589793 * u2);
+    out[i] = static_cast<float>(static_cast<double>(mean) + static_cast<double>(stddev) * z);
+}
+
+__global__ void position_add_kernel(int32_t* position, int32_t count) {
+    if (threadIdx.x == 0) *position += count;
+}
+
+// generated[*position] = *token, when the position lies inside [0, capacity).
+__global__ void record_token_kernel(const int32_t* token, const int32_t* position, int32_t* generated, int32_t capacity) {
+    if (threadIdx.x == 0) {
+        const int32_t p = *position;
+        if (p >= 0 && p < capacity) generated[p] = *token;
+    }
+}
+
+constexpr int32_t ARGMAX_BLOCKS = 64;
+
+size_t attention_lds(int32_t G, int32_t HD) {
+    return sizeof(float) * (static_cast<size_t>(G) * HD + static_cast<size_t>(KT) * (HD + 1) +
+                            static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G));
+}
+
+}  // namespace
+}  // namespace kt
+
+using namespace kt;
+
+extern "C" {
+
+int32_t kt_rope_inv_freq(int32_t head_dim, float base, float factor, float low, float high, int32_t original_max,
+                         float* out) {
+    if (head_dim <= 0 || head_dim % 2 != 0) return fail(KT_ERR_ARGUMENT, "RoPE dimension must be even");
+    if (!out) return fail(KT_ERR_ARGUMENT, "out is NULL");
+    if (factor > 0.0f) {
+        if (original_max <= 0) return fail(KT_ERR_ARGUMENT, "Invalid RoPE scaling");
+        if (!(high > low)) return fail(KT_ERR_ARGUMENT, "highFrequencyFactor must exceed lowFrequencyFactor");
+    }
+    const double java_pi = 3.141592653589793;
+    for (int32_t i = 0; i < head_dim / 2; ++i) {
+        const float exponent = static_cast<float>(2 * i) / static_cast<float>(head_dim);
+        float f = 1.0f / static_cast<float>(pow(static_cast<double>(base), static_cast<double>(exponent)));
+        if (factor > 0.0f) {
+            const float low_wl = static_cast<float>(original_max) / low;
+            const float high_wl = static_cast<float>(original_max) / high;
+            const float wl = static_cast<float>(2.0 * java_pi / static_cast<double>(f));
+            if (wl < high_wl) {
+            } else if (wl > low_wl) {
+                f = f / factor;
+            } else {
+                const float smooth = (static_cast<float>(original_max) / wl - low) / (high - low);
+                f = (1.0f - smooth) * f / factor + smooth * f;
+            }
+        }
+        out[i] = f;
+    }
+    return KT_OK;
+}
+
+int32_t kt_rmsnorm(const float* x, int32_t rows, int32_t dim, const float* weight, float eps, float* out,
+                   void* stream) {
+    if (!x || !weight || !out) return fail(KT_ERR_ARGUMENT, "x, weight or out is NULL");
+    if (rows < 0 || dim <= 0) return fail(KT_ERR_SHAPE, "RMSNorm needs rows >= 0 and dimension > 0, got %d x %d", rows, dim);
+    if (rows == 0) return KT_OK;
+    rmsnorm_kernel<<<rows, THREADS, 0, static_cast<hipStream_t>(stream)>>>(x, dim, weight, eps, out);
+    KT_LAUNCHED("rmsnorm kernel");
+    return KT_OK;
+}
+
+int32_t kt_rope_kv(float* q, float* k, const float* v, int32_t tokens, int32_t num_heads, int32_t num_kv_heads,
+                   int32_t head_dim, const float* inv_freq, const int32_t* position, float* cache_k, float* cache_v,
+                   int32_t layer, int32_t max_seq, void* stream) {
+    if (!q || !k || !v || !inv_freq || !position || !cache_k || !cache_v)
+        return fail(KT_ERR_ARGUMENT, "a pointer argument is NULL");
+    if (head_dim <= 0 || head_dim % 2 != 0) return fail(KT_ERR_ARGUMENT, "RoPE dimension must be even");
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(KT_ERR_ARGUMENT, "numHeads %d must be a multiple of numKeyValueHeads %d", num_heads, num_kv_heads);
+    if (tokens < 0 || layer < 0 || max_seq <= 0) return fail(KT_ERR_ARGUMENT, "bad tokens, layer or maxSequenceLength");
+    if (tokens == 0) return KT_OK;
+    const int32_t units = (num_heads + num_kv_heads) * (head_dim / 2);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(units, THREADS)), static_cast<uint32_t>(tokens));
+    rope_kv_kernel<<<grid, THREADS, 0, static_cast<hipStream_t>(stream)>>>(q, k, v, num_heads, num_kv_heads, head_dim,
+                                                                         inv_freq, position, cache_k, cache_v, layer,
+                                                                         max_seq);
+    KT_LAUNCHED("rope/kv kernel");
+    return KT_OK;
+}
+
+int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound, const float* cache_k,
+                     const float* cache_v, int32_t layer, int32_t max_seq, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, float* context, void* stream) {
+    if (!q || !position || !cache_k || !cache_v || !context) return fail(KT_ERR_ARGUMENT, "a pointer argument is NULL");
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(KT_ERR_ARGUMENT, "numHeads %d must be a multiple of numKeyValueHeads %d", num_heads, num_kv_heads);
+    const int32_t G = num_heads / num_kv_heads;
+    if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > MAX_HD)
+        return fail(KT_ERR_ARGUMENT, "head dimension %d: a multiple of 4 up to %d", head_dim, MAX_HD);
+    if (G * head_dim > MAX_NACC * THREADS)
+        return fail(KT_ERR_ARGUMENT, "%d query heads per key/value head of %d dims exceed %d", G, head_dim,
+                    MAX_NACC * THREADS);
+    if (tokens < 0 || key_bound < tokens || key_bound > max_seq || layer < 0)
+        return fail(KT_ERR_ARGUMENT, "key bound %d must cover the %d tokens and fit maxSequenceLength %d", key_bound,
+                    tokens, max_seq);
+    if (tokens == 0) return KT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // Key splits: enough workgroups to fill the GPU when few tokens attend.
+    int32_t splits = 1;
+    const int32_t tiles = ceil_div(key_bound, KT);
+    const int64_t wgs = static_cast<int64_t>(tokens) * num_kv_heads;
+    if (wgs < 2 * cu_count()) {
+        splits = static_cast<int32_t>((2 * cu_count() + wgs - 1) / wgs);
+        if (splits > tiles) splits = tiles;
+        if (splits > 64) splits = 64;
+    }
+    AttnArgs a{};
+    a.q = q;
+    a.position = position;
+    a.ck = cache_k;
+    a.cv = cache_v;
+    a.context = context;
+    a.layer = layer;
+    a.max_seq = max_seq;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.head_dim = head_dim;
+    a.scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+    a.span = ceil_div(tiles, splits) * KT;
+    a.splits = ceil_div(key_bound, a.span);
+    if (a.splits > 1) {
+        void* ws = nullptr;
+        const size_t bytes = static_cast<size_t>(tokens) * num_heads * a.splits * (head_dim + 2) * sizeof(float);
+        const int32_t status = workspace(st, bytes, &ws);
+        if (status) return status;
+        a.partials = static_cast<float*>(ws);
+    }
+    const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(a.splits), static_cast<uint32_t>(tokens));
+    attention_kernel<<<grid, THREADS, attention_lds(G, head_dim), st>>>(a);
+    KT_LAUNCHED("attention kernel");
+    if (a.splits > 1) {
+        attn_combine_kernel<<<dim3(static_cast<uint32_t>(num_heads), static_cast<uint32_t>(tokens)), THREADS, 0, st>>>(a);
+        KT_LAUNCHED("attention combine kernel");
+    }
+    return KT_OK;
+}
+
+int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream) {
+    if (!gate || !up) return fail(KT_ERR_ARGUMENT, "gate or up is NULL");
+    if (n < 0) return fail(KT_ERR_SHAPE, "negative element count %lld", static_cast<long long>(n));
+    if (n == 0) return KT_OK;
+    const int64_t blocks = (n + THREADS - 1) / THREADS;
+    if (blocks > 0x7FFFFFFF) return fail(KT_ERR_SHAPE, "too many elements");
+    silu_mul_kernel<<<static_cast<uint32_t>(blocks), THREADS, 0, static_cast<hipStream_t>(stream)>>>(gate, up, n);
+    KT_LAUNCHED("silu*mul kernel");
+    return KT_OK;
+}
+
+int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream) {
+    if (!logits || !index) return fail(KT_ERR_ARGUMENT, "logits or index is NULL");
+    if (n <= 0) return fail(KT_ERR_SHAPE, "argmax needs at least one logit");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int32_t blocks = ceil_div(n, 4 * THREADS);
+    if (blocks > ARGMAX_BLOCKS) blocks = ARGMAX_BLOCKS;
+    void* ws = nullptr;
+    uint32_t* counters = nullptr;
+    const int32_t status = workspace_counters(st, ARGMAX_BLOCKS * sizeof(uint64_t), 1, &ws, &counters);
+    if (status) return status;
+    argmax_kernel<<<blocks, THREADS, 0, st>>>(logits, n, index, static_cast<uint64_t*>(ws), counters);
+    KT_LAUNCHED("argmax kernel");
+    return KT_OK;
+}
+
+int32_t kt_add_inplace(float* x, const float* y, int64_t n, void* stream) {
+    if (!x || !y) return fail(KT_ERR_ARGUMENT, "x or y is NULL");
+    if (n < 0) return fail(KT_ERR_SHAPE, "negative element count %lld", static_cast<long long>(n));
+    if (n == 0) return KT_OK;
+    const int64_t blocks = (n + THREADS - 1) / THREADS;
+    if (blocks > 0x7FFFFFFF) return fail(KT_ERR_SHAPE, "too many elements");
+    add_kernel<<<static_cast<uint32_t>(blocks), THREADS, 0, static_cast<hipStream_t>(stream)>>>(x, y, n);
+    KT_LAUNCHED("add kernel");
+    return KT_OK;
+}
+
+int32_t kt_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float stddev, void* stream) {
+    if (!out) return fail(KT_ERR_ARGUMENT, "out is NULL");
+    if (n < 0) return fail(KT_ERR_SHAPE, "negative element count %lld", static_cast<long long>(n));
+    if (n == 0) return KT_OK;
+    const int64_t blocks = (n + THREADS - 1) / THREADS;
+    if (blocks > 0x7FFFFFFF) return fail(KT_ERR_SHAPE, "too many elements");
+    fill_normal_kernel<<<static_cast<uint32_t>(blocks), THREADS, 0, static_cast<hipStream_t>(stream)>>>(out, n, seed,
+                                                                                                    mean, stddev);
+    KT_LAUNCHED("fill kernel");
+    return KT_OK;
+}
+
+int32_t kt_record_token(const int32_t* token, const int32_t* position, int32_t* generated, int32_t capacity,
+                        void* stream) {
+    if (!token || !position || !generated) return fail(KT_ERR_ARGUMENT, "token, position or generated is NULL");
+    if (capacity < 0) return fail(KT_ERR_ARGUMENT, "negative capacity");
+    record_token_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(token, position, generated, capacity);
+    KT_LAUNCHED("record kernel");
+    return KT_OK;
+}
+
+int32_t kt_position_add(int32_t* position, int32_t count, void* stream) {
+    if (!position) return fail(KT_ERR_ARGUMENT, "position is NULL");
+    position_add_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(position, count);
+    KT_LAUNCHED("position kernel");
+    return KT_OK;
+}
+
+}  // extern "C"

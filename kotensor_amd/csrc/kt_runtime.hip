@@ -262,6 +262,36 @@ int32_t kt_stream_sync(void* stream) {
     return KT_OK;
 }
 
+int32_t kt_graph_begin(void* stream) {
+    if (!stream) return fail(KT_ERR_ARGUMENT, "the null stream cannot be captured; create a stream");
+    KT_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+    return KT_OK;
+}
+
+int32_t kt_graph_end(void* stream, void** graph) {
+    if (!stream || !graph) return fail(KT_ERR_ARGUMENT, "stream or graph is NULL");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    KT_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (err != hipSuccess) return hip_fail(err, "hipGraphInstantiate");
+    *graph = exec;
+    return KT_OK;
+}
+
+int32_t kt_graph_launch(void* graph, void* stream) {
+    if (!graph) return fail(KT_ERR_ARGUMENT, "graph is NULL");
+    KT_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), static_cast<hipStream_t>(stream)));
+    return KT_OK;
+}
+
+int32_t kt_graph_destroy(void* graph) {
+    if (graph) KT_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
+    return KT_OK;
+}
+
 int32_t kt_qweight_layout(int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
                           int32_t has_zeros, int64_t* out4) {
     if (!out4) return fail(KT_ERR_ARGUMENT, "out is NULL");

@@ -69,6 +69,7 @@ class RefTransformer:
     quantized: dict  # name -> oracle.Quantized ("embedding" unless tied, blocks, "lmHead")
     norms: dict      # name -> fp32 [dimension] ("block.l.norm1", "block.l.norm2", "finalNorm")
     tied: bool = False
+    biases: dict = field(default_factory=dict)  # name -> fp32 [out]; QuantizedLinear.bias (QuantizedLinear.kt:16-25)
     inv_freq: np.ndarray = field(init=False)
 
     def __post_init__(self):
@@ -82,7 +83,11 @@ class RefTransformer:
 
     # -- pieces ----------------------------------------------------------------------
     def _project(self, x: np.ndarray, name: str) -> np.ndarray:
-        return oracle.multiply_quantized(x, self.quantized[name], x.shape[0], threads=16)
+        """QuantizedLinear.forwardInto: the product, then += bias."""
+        out = oracle.multiply_quantized(x, self.quantized[name], x.shape[0], threads=16)
+        if name in self.biases:
+            out = (out + self.biases[name][None, :]).astype(np.float32)
+        return out
 
     def embed(self, tokens) -> np.ndarray:
         if self.tied:
