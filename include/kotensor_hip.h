@@ -197,7 +197,7 @@ int32_t kt_rope_kv(float* q, float* k, const float* v, int32_t tokens, int32_t n
  * softmax(q . k_j / sqrt(head_dim)) over cached positions j <= that position, of the
  * kv head that serves its query head (GQA), times v, into context [tokens x
  * num_heads*head_dim]. key_bound >= *position + tokens bounds the keys (it sizes the
- * launch; a captured decode step passes max_seq). */
+ * launch; a captured decode step passes max_seq). q and the caches are 16-byte aligned. */
 int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound,
                      const float* cache_k, const float* cache_v, int32_t layer, int32_t max_seq,
                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,

@@ -46,23 +46,55 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---- RMSNorm ---------------------------------------------------------------------
-// One workgroup per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * weight.
+// One workgroup per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * weight. Rows of up
+// to 8192 floats (a multiple of 4) stay in registers: one load round trip per row.
+constexpr int NORM_F4 = 8;  // float4 per thread: dim <= 8192
+
 __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restrict__ x, int32_t dim,
                                                           const float* __restrict__ w, float eps,
-                                                          float* __restrict__ out) {
+                                                          float* __restrict__ out, int32_t aligned16) {
     __shared__ float part[THREADS / 64];
     const float* row = x + static_cast<size_t>(blockIdx.x) * dim;
     float* orow = out + static_cast<size_t>(blockIdx.x) * dim;
+    const int32_t tid = threadIdx.x;
+    const bool vec = aligned16 && (dim & 3) == 0 && dim <= NORM_F4 * 4 * THREADS;
+    float4 v[NORM_F4];
     float s = 0.0f;
-    for (int32_t d = threadIdx.x; d < dim; d += THREADS) s = fmaf(row[d], row[d], s);
+    if (vec) {
+        const int32_t n4 = dim >> 2;
+#pragma unroll
+        for (int i = 0; i < NORM_F4; ++i)  // in-bounds unconditional loads, masked after
+            v[i] = reinterpret_cast<const float4*>(row)[min(tid + i * THREADS, n4 - 1)];
+#pragma unroll
+        for (int i = 0; i < NORM_F4; ++i)
+            if (tid + i * THREADS >= n4) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < NORM_F4; ++i)
+            s = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, s))));
+    } else {
+        for (int32_t d = tid; d < dim; d += THREADS) s = fmaf(row[d], row[d], s);
+    }
     s = wave_sum(s);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
     float total = 0.0f;
 #pragma unroll
     for (int i = 0; i < THREADS / 64; ++i) total += part[i];
     const float r = 1.0f / sqrtf(total / static_cast<float>(dim) + eps);
-    for (int32_t d = threadIdx.x; d < dim; d += THREADS) orow[d] = row[d] * r * w[d];
+    if (vec) {
+        const int32_t n4 = dim >> 2;
+#pragma unroll
+        for (int i = 0; i < NORM_F4; ++i) {
+            const int32_t e = tid + i * THREADS;
+            if (e < n4) {
+                const float4 wv = reinterpret_cast<const float4*>(w)[e];
+                reinterpret_cast<float4*>(orow)[e] =
+                    make_float4(v[i].x * r * wv.x, v[i].y * r * wv.y, v[i].z * r * wv.z, v[i].w * r * wv.w);
+            }
+        }
+    } else {
+        for (int32_t d = tid; d < dim; d += THREADS) orow[d] = row[d] * r * w[d];
+    }
 }
 
 // ---- RoPE + cache append -----------------------------------------------------------
@@ -125,6 +157,21 @@ struct AttnArgs {
 // tiles of 64 keys with a running maximum and sum (scores, then exp(score - max),
 // then the weighted values). With one split the workgroup writes the context; with
 // several it writes (sum of weighted values, max, sum) for attn_combine_kernel.
+// Every global load of a tile is issued before the first is used (unrolled, predicated
+// float4 loads into registers, then LDS), so a tile costs one memory round trip.
+// TF4: float4 per thread for a full tile (4, 8, 16 for head_dim up to 64, 128, 256).
+// Unconditional loads of in-bounds addresses (indices past the tile repeat its last
+// float4; the stores are masked): no branch around a load, so all go out together.
+template <int TF4>
+__device__ __forceinline__ void load_tile(float4 (&r)[TF4], const float* src, int32_t n4) {
+#pragma unroll
+    for (int i = 0; i < TF4; ++i) {
+        const int32_t e = min(static_cast<int32_t>(threadIdx.x) + i * THREADS, n4 - 1);
+        r[i] = reinterpret_cast<const float4*>(src)[e];
+    }
+}
+
+template <int TF4>
 __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     extern __shared__ float smem[];
     const int32_t g = blockIdx.x, s = blockIdx.y, t = blockIdx.z;
@@ -133,7 +180,8 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     const int32_t KP = HD + 1;  // padded key row: lanes reading consecutive rows hit distinct banks
     float* qs = smem;                  // [G][HD]
     float* ks = qs + G * HD;           // [KT][HD + 1]
-    float* sc = ks + KT * KP;          // [G][KT]
+    float* vs = ks + KT * KP;          // [KT][HD]
+    float* sc = vs + KT * HD;          // [G][KT]
     float* st = sc + G * KT;           // [G] x {m, l, alpha}
     const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
@@ -142,24 +190,50 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     const int32_t k_end = min(min(k_begin + a.span, pos + 1), a.max_seq);  // never read outside the cache
     const size_t base = (static_cast<size_t>(a.layer) * a.num_kv_heads + g) * a.max_seq;  // row of key 0
 
-    for (int32_t e = tid; e < G * HD; e += THREADS) qs[e] = a.q[static_cast<size_t>(t) * dim + g * G * HD + e];
-    for (int32_t i = tid; i < G; i += THREADS) {
-        st[3 * i] = -INFINITY;
-        st[3 * i + 1] = 0.0f;
+    // q of the G heads (G * HD <= 1024 floats: at most one float4 per thread)
+    const int32_t q4 = G * HD / 4;
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < q4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(t) * dim + g * G * HD)[tid];
+    if (tid < G) {
+        st[3 * tid] = -INFINITY;
+        st[3 * tid + 1] = 0.0f;
     }
     const int32_t pairs = G * HD;
     const int32_t nacc = (pairs + THREADS - 1) / THREADS;
     float acc[MAX_NACC];
 #pragma unroll
     for (int r = 0; r < MAX_NACC; ++r) acc[r] = 0.0f;
-    __syncthreads();
 
+    // K and V tiles in registers together (one round trip) up to head_dim 128; wider
+    // heads load them one after the other to keep the registers in bounds.
+    constexpr bool TOGETHER = TF4 <= 8;
+    float4 kr[TF4], vr[TOGETHER ? TF4 : 1];
     for (int32_t k0 = k_begin; k0 < k_end; k0 += KT) {
         const int32_t n = min(KT, k_end - k0);
-        // key tile to LDS, coalesced rows
-        for (int32_t e = tid; e < n * HD; e += THREADS) {
-            const int32_t j = e / HD, d = e % HD;
-            ks[j * KP + d] = a.ck[(base + k0 + j) * HD + d];
+        const int32_t n4 = n * HD / 4;
+        load_tile<TF4>(kr, a.ck + (base + k0) * HD, n4);
+        if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k0) * HD, n4);
+        if (k0 == k_begin && tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
+#pragma unroll
+        for (int i = 0; i < TF4; ++i) {
+            const int32_t e = tid + i * THREADS;
+            if (e < n4) {
+                const int32_t j = (4 * e) / HD, d = (4 * e) % HD;
+                float* kd = ks + j * KP + d;
+                kd[0] = kr[i].x;
+                kd[1] = kr[i].y;
+                kd[2] = kr[i].z;
+                kd[3] = kr[i].w;
+                if constexpr (TOGETHER) reinterpret_cast<float4*>(vs)[e] = vr[i];
+            }
+        }
+        if constexpr (!TOGETHER) {
+            load_tile<TF4>(kr, a.cv + (base + k0) * HD, n4);
+#pragma unroll
+            for (int i = 0; i < TF4; ++i) {
+                const int32_t e = tid + i * THREADS;
+                if (e < n4) reinterpret_cast<float4*>(vs)[e] = kr[i];
+            }
         }
         __syncthreads();
         // scores: pair (head i, key j)
@@ -170,6 +244,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
                 const float* qi = qs + i * HD;
                 const float* kj = ks + j * KP;
                 float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll 4
                 for (int32_t d = 0; d < HD; d += 4) {
                     s0 = fmaf(qi[d], kj[d], s0);
                     s1 = fmaf(qi[d + 1], kj[d + 1], s1);
@@ -197,16 +272,17 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        // weighted values: pair (head i, dim d)
+        // weighted values: pair (head i, dim d), values from LDS
 #pragma unroll
         for (int r = 0; r < MAX_NACC; ++r) {
             const int32_t e = tid + r * THREADS;
             if (r < nacc && e < pairs) {
                 const int32_t i = e / HD, d = e % HD;
                 float x = acc[r] * st[3 * i + 2];
-                const float* vp = a.cv + (base + k0) * HD + d;
                 const float* ep = sc + i * KT;
-                for (int32_t j = 0; j < n; ++j) x = fmaf(ep[j], vp[static_cast<size_t>(j) * HD], x);
+                const float* vp = vs + d;
+#pragma unroll 8
+                for (int32_t j = 0; j < n; ++j) x = fmaf(ep[j], vp[j * HD], x);
                 acc[r] = x;
             }
         }
@@ -233,24 +309,31 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     }
 }
 
-// Workgroup (token t, head h): merges the splits' (weighted values, max, sum).
+constexpr int MAX_SPLITS = 64;
+
+// Workgroup (token t, head h): merges the splits' (weighted values, max, sum). The
+// splits' maxima and sums go through LDS first, so the loads are issued together.
 __global__ void __launch_bounds__(THREADS) attn_combine_kernel(AttnArgs a) {
-    const int32_t t = blockIdx.y, h = blockIdx.x, HD = a.head_dim;
-    const float* pp = a.partials + (static_cast<size_t>(t) * a.num_heads + h) * a.splits * (HD + 2);
-    float m = -INFINITY;
-    for (int32_t s = 0; s < a.splits; ++s) m = fmaxf(m, pp[s * (HD + 2) + HD]);
-    float l = 0.0f;
-    for (int32_t s = 0; s < a.splits; ++s) {
-        const float ms = pp[s * (HD + 2) + HD];
-        if (ms != -INFINITY) l += pp[s * (HD + 2) + HD + 1] * expf(ms - m);
+    __shared__ float ws[MAX_SPLITS];
+    __shared__ float total;
+    const int32_t t = blockIdx.y, h = blockIdx.x, HD = a.head_dim, S = a.splits;
+    const float* pp = a.partials + (static_cast<size_t>(t) * a.num_heads + h) * S * (HD + 2);
+    const int32_t tid = threadIdx.x;
+    if (tid < 64) {
+        const float ms = tid < S ? pp[tid * (HD + 2) + HD] : -INFINITY;
+        const float ls = tid < S ? pp[tid * (HD + 2) + HD + 1] : 0.0f;
+        const float m = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
+        const float l = wave_sum(w * ls);
+        if (tid < S) ws[tid] = w;
+        if (tid == 0) total = l;
     }
-    const float inv = 1.0f / l;
-    for (int32_t d = threadIdx.x; d < HD; d += THREADS) {
+    __syncthreads();
+    const float inv = 1.0f / total;
+    for (int32_t d = tid; d < HD; d += THREADS) {
         float x = 0.0f;
-        for (int32_t s = 0; s < a.splits; ++s) {
-            const float ms = pp[s * (HD + 2) + HD];
-            if (ms != -INFINITY) x = fmaf(pp[s * (HD + 2) + d], expf(ms - m), x);
-        }
+#pragma unroll 8
+        for (int32_t s = 0; s < S; ++s) x = fmaf(pp[s * (HD + 2) + d], ws[s], x);
         a.context[static_cast<size_t>(t) * a.num_heads * HD + h * HD + d] = x * inv;
     }
 }
@@ -364,7 +447,7 @@ constexpr int32_t ARGMAX_BLOCKS = 64;
 
 size_t attention_lds(int32_t G, int32_t HD) {
     return sizeof(float) * (static_cast<size_t>(G) * HD + static_cast<size_t>(KT) * (HD + 1) +
-                            static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G));
+                            static_cast<size_t>(KT) * HD + static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G));
 }
 
 }  // namespace
@@ -408,7 +491,8 @@ int32_t kt_rmsnorm(const float* x, int32_t rows, int32_t dim, const float* weigh
     if (!x || !weight || !out) return fail(KT_ERR_ARGUMENT, "x, weight or out is NULL");
     if (rows < 0 || dim <= 0) return fail(KT_ERR_SHAPE, "RMSNorm needs rows >= 0 and dimension > 0, got %d x %d", rows, dim);
     if (rows == 0) return KT_OK;
-    rmsnorm_kernel<<<rows, THREADS, 0, static_cast<hipStream_t>(stream)>>>(x, dim, weight, eps, out);
+    const int32_t al = aligned(x, 16) && aligned(weight, 16) && aligned(out, 16);
+    rmsnorm_kernel<<<rows, THREADS, 0, static_cast<hipStream_t>(stream)>>>(x, dim, weight, eps, out, al);
     KT_LAUNCHED("rmsnorm kernel");
     return KT_OK;
 }
@@ -447,6 +531,8 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
     if (tokens < 0 || key_bound < tokens || key_bound > max_seq || layer < 0)
         return fail(KT_ERR_ARGUMENT, "key bound %d must cover the %d tokens and fit maxSequenceLength %d", key_bound,
                     tokens, max_seq);
+    if (!aligned(q, 16) || !aligned(cache_k, 16) || !aligned(cache_v, 16))
+        return fail(KT_ERR_ARGUMENT, "attention: q and the caches must be 16-byte aligned");
     if (tokens == 0) return KT_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // Key splits: enough workgroups to fill the GPU when few tokens attend.
@@ -456,7 +542,7 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
     if (wgs < 2 * cu_count()) {
         splits = static_cast<int32_t>((2 * cu_count() + wgs - 1) / wgs);
         if (splits > tiles) splits = tiles;
-        if (splits > 64) splits = 64;
+        if (splits > MAX_SPLITS) splits = MAX_SPLITS;
     }
     AttnArgs a{};
     a.q = q;
@@ -480,7 +566,20 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
         a.partials = static_cast<float*>(ws);
     }
     const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(a.splits), static_cast<uint32_t>(tokens));
-    attention_kernel<<<grid, THREADS, attention_lds(G, head_dim), st>>>(a);
+    const size_t lds = attention_lds(G, head_dim);
+    if (lds > (64u << 10)) {  // beyond the default dynamic LDS limit (160 KB per CU on gfx950)
+        static bool raised = false;
+        if (!raised) {
+            KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<8>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10));
+            KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<16>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10));
+            raised = true;
+        }
+    }
+    if (head_dim <= 64) attention_kernel<4><<<grid, THREADS, lds, st>>>(a);
+    else if (head_dim <= 128) attention_kernel<8><<<grid, THREADS, lds, st>>>(a);
+    else attention_kernel<16><<<grid, THREADS, lds, st>>>(a);
     KT_LAUNCHED("attention kernel");
     if (a.splits > 1) {
         attn_combine_kernel<<<dim3(static_cast<uint32_t>(num_heads), static_cast<uint32_t>(tokens)), THREADS, 0, st>>>(a);
