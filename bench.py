@@ -25,7 +25,8 @@ The JSON line also carries:
                    Llama-3-8B FFN shape (4096->14336) and the INT8 group-32 prefill
                    GEMM at M = 512 on the 2048-wide layer's four projection shapes
                    (2048->2048, 2048->512, 2048->8192, 8192->2048) and their sum, each
-                   with its fraction of the MFMA peak.
+                   with its fraction of the MFMA peak; and the Llama-style 1B INT4
+                   decoder end to end (1024-token prefill, greedy decode steps).
 
 --only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
 calibration of the HBM byte counters) for rocprofv3 PMC runs.
@@ -175,6 +176,52 @@ def traffic_from_profiles():
         except (ValueError, OSError):
             return None
     return None
+
+
+def decoder_figures(torch, stream_obj) -> dict:
+    """The Llama-style 1B INT4 decoder (16 layers, d 2048, 32 q / 8 kv heads of 64,
+    SwiGLU 8192, vocab 32000, RMSNorm, RoPE theta 5e5; weights ~N(0, 0.02) quantized
+    g64 on the device): prefill of a 1024-token prompt (ids seed 2), then 127 greedy
+    decode steps replayed from one recorded HIP graph. HIP events on the launch stream;
+    the second of two runs is reported."""
+    import numpy as np
+    import kotensor_amd as kt
+    from kotensor_amd import _lib
+    ks = kt.Stream(handle=stream_obj.cuda_stream)
+    model = kt.Transformer(32000, 2048, 16, 32, 8192, 8, norm_eps=1e-5, rope_theta=500000.0,
+                           quantization=kt.Quantization.INT4, seed=1, stream=ks)
+    prompt = np.random.default_rng(2).integers(0, 32000, 1024).tolist()
+    steps = 127
+    # bytes a decode step streams: every projection and the head, not the embedding
+    # table (one row of it is gathered)
+    streamed = model.weight_bytes - model.weights["embedding"].size_in_bytes
+    out = {}
+    for _ in range(2):
+        cache, buffers = model.new_cache(1024 + steps + 1, ks), model.new_inference_buffers(1024 + steps + 1)
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record(stream_obj)
+        model.prefill(prompt, cache, buffers, ks)
+        e[1].record(stream_obj)
+        # the first greedy token and one eager step (which sizes the workspaces), then
+        # the recorded step replayed
+        _lib.call("kt_argmax", buffers.logits.ptr, model.vocabulary_size, buffers.tokens.ptr, ks.handle)
+        model.decode_step(cache, buffers, ks)
+        graph = model.capture_decode(cache, buffers, ks)
+        e[2].record(stream_obj)
+        graph.replay(steps - 1)
+        e[3].record(stream_obj)
+        torch.cuda.synchronize()
+        graph.destroy()
+        prefill_ms = e[0].elapsed_time(e[1])
+        decode_ms = e[2].elapsed_time(e[3]) / (steps - 1)
+        out = {"prefill_tokens": 1024, "prefill_ms": round(prefill_ms, 3),
+               "prefill_tok/s": round(1024 / (prefill_ms * 1e-3), 1),
+               "decode_ms_per_token": round(decode_ms, 4), "decode_tok/s": round(1e3 / decode_ms, 1),
+               "decode_weight_GB/s": round(streamed / (decode_ms * 1e-3) / 1e9, 1),
+               "decode_weight_bytes": streamed, "decode_steps_timed": steps - 1, "graph_replay": True}
+        del cache, buffers
+    return out
 
 
 def main() -> int:
@@ -333,6 +380,8 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         layer = tot_flops / (tot_ms * 1e-3) / 1e12
         extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
                                              "avg_us": round(tot_ms * 1e3, 3)}
+
+        extra["llama1b_int4_decoder"] = decoder_figures(torch, stream_obj)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {

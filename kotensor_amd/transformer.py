@@ -505,6 +505,60 @@ class Transformer:
         cache.length += 1
         return buffers
 
+    def greedy_decode(self, cache: KVCache, buffers: InferenceBuffers, steps: int, stream: Stream | None = None,
+                      use_graph: bool = True) -> list[int]:
+        """The greedy part of streamFrom (Transformer.kt:224-231) after a prefill: takes
+        the argmax of buffers.logits, then `steps` decode steps, each feeding the previous
+        greedy token (which never leaves the device) and taking the next argmax. Returns
+        the steps + 1 greedy tokens. With use_graph (on a created, non-null stream) one
+        decode step is recorded as a HIP graph and replayed."""
+        if cache.remaining < steps:
+            raise _lib.IllegalArgumentException(
+                f"KV cache full: {cache.length} + {steps} positions exceed maxSequenceLength {cache.max_sequence_length}")
+        if buffers.max_sequence_length < cache.length + steps + 1:
+            raise _lib.IllegalArgumentException(
+                f"InferenceBuffers sized for {buffers.max_sequence_length} positions, generation ends at "
+                f"{cache.length + steps + 1}")
+        st = _stream(stream)
+        first = cache.length
+        _lib.call("kt_argmax", buffers.logits.ptr, self.vocabulary_size, buffers.tokens.ptr, st)
+        _lib.call("kt_record_token", buffers.tokens.ptr, cache.position.ptr, buffers.generated.ptr,
+                  buffers.max_sequence_length, st)
+        if use_graph and steps > 1 and st:
+            self.decode_step(cache, buffers, stream)  # the first step also sizes the workspaces
+            graph = self.capture_decode(cache, buffers, stream)
+            try:
+                graph.replay(steps - 1)
+            finally:
+                (stream or default_stream()).synchronize()
+                graph.destroy()
+        else:
+            for _ in range(steps):
+                self.decode_step(cache, buffers, stream)
+        return buffers.generated.download(np.int32, count=steps + 1, stream=stream, offset=4 * first).tolist()
+
+    def decode_step(self, cache: KVCache, buffers: InferenceBuffers, stream: Stream | None = None) -> None:
+        """One greedy decode step on the device: the token in buffers.tokens (the last
+        argmax) in, its logits in buffers.logits, the next argmax in buffers.tokens and in
+        buffers.generated at its position."""
+        cache.check_room(1)
+        self._decode_step(cache, buffers, _stream(stream), argmax=True)
+        cache.length += 1
+
+    def capture_decode(self, cache: KVCache, buffers: InferenceBuffers, stream: Stream) -> "DecodeGraph":
+        """decode_step recorded once as a HIP graph on `stream` (a created stream; run one
+        decode_step first so the library's workspaces already have their sizes)."""
+        st = _stream(stream)
+        if not st:
+            raise _lib.IllegalArgumentException("the null stream cannot be captured; create a stream")
+        _lib.call("kt_graph_begin", st)
+        try:
+            self._decode_step(cache, buffers, st, argmax=True)
+        finally:
+            graph = ctypes.c_void_p()
+            _lib.call("kt_graph_end", st, ctypes.byref(graph))
+        return DecodeGraph(graph, cache, stream)
+
     def generate(self, prompt, max_tokens: int, stop_tokens=(), stream: Stream | None = None,
                  use_graph: bool = True) -> list[int]:
         """Greedy generate (Transformer.kt:167-233): prefill, then argmax and decode,
@@ -517,40 +571,15 @@ class Transformer:
             return list(prompt)
         own = stream is None and use_graph
         stream = Stream.create() if own else stream
-        st = _stream(stream)
         try:
             max_seq = len(prompt) + max_tokens
             cache = self.new_cache(max_seq, stream)
             buffers = self.new_inference_buffers(max_seq)
             self.prefill(prompt, cache, buffers, stream)
-            _lib.call("kt_argmax", buffers.logits.ptr, self.vocabulary_size, buffers.tokens.ptr, st)
-            _lib.call("kt_record_token", buffers.tokens.ptr, cache.position.ptr, buffers.generated.ptr, max_seq, st)
-            steps = max_tokens - 1
-            if use_graph and steps > 0:
-                self._decode_step(cache, buffers, st, argmax=True)  # the first step also sizes the workspaces
-                cache.length += 1
-                if steps > 1:
-                    _lib.call("kt_graph_begin", st)
-                    try:
-                        self._decode_step(cache, buffers, st, argmax=True)
-                    finally:
-                        graph = ctypes.c_void_p()
-                        _lib.call("kt_graph_end", st, ctypes.byref(graph))
-                    try:
-                        for _ in range(steps - 1):
-                            _lib.call("kt_graph_launch", graph, st)
-                            cache.length += 1
-                    finally:
-                        (stream or default_stream()).synchronize()
-                        _lib.call("kt_graph_destroy", graph)
-            else:
-                for _ in range(steps):
-                    self._decode_step(cache, buffers, st, argmax=True)
-                    cache.length += 1
-            out = buffers.generated.download(np.int32, count=max_seq, stream=stream)[len(prompt):max_seq]
+            out = self.greedy_decode(cache, buffers, max_tokens - 1, stream, use_graph)
             tokens = list(prompt)
             stops = set(int(s) for s in stop_tokens)
-            for t in out.tolist():
+            for t in out:
                 if t in stops:
                     break
                 tokens.append(int(t))
@@ -558,3 +587,34 @@ class Transformer:
         finally:
             if own:
                 stream.destroy()
+
+    @property
+    def weight_bytes(self) -> int:
+        """weightBytes (Transformer.kt:395-400): quantized tensors plus fp32 parameters."""
+        return sum(w.size_in_bytes for w in self.weights.values()) + sum(b.nbytes for b in self.parameters.values())
+
+
+class DecodeGraph:
+    """A recorded greedy decode step (Transformer.capture_decode): each replay decodes
+    one token at the cache's device position and advances it."""
+
+    def __init__(self, handle: ctypes.c_void_p, cache: KVCache, stream: Stream):
+        self._h, self.cache, self.stream = handle, cache, stream
+
+    def replay(self, steps: int = 1) -> None:
+        self.cache.check_room(steps)
+        for _ in range(steps):
+            _lib.call("kt_graph_launch", self._h, _stream(self.stream))
+            self.cache.length += 1
+
+    def destroy(self) -> None:
+        if self._h:
+            (self.stream or default_stream()).synchronize()  # no replay still in flight
+            _lib.call("kt_graph_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
