@@ -92,6 +92,12 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
 void set_gemv_wide_config(int32_t slices, int32_t waves);
 // Whether the automatic choice takes the wide-strip kernel for these weights.
 bool gemv_wide_preferred(const WeightView* ws, int32_t count);
+// The M == 1 latency kernel on 16-byte column strips over all of K (kt_gemv_strip.hip).
+bool gemv_strip_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+int32_t launch_gemv_strip(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                          int32_t count, int32_t accumulate, float alpha, hipStream_t st);
+// Whether the automatic choice takes the column-strip kernel for these weights.
+bool gemv_strip_preferred(const WeightView* ws, int32_t count);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
 // otherwise the generic kernel runs.

@@ -165,12 +165,13 @@ int32_t kt_set_device(int32_t device) {
     return KT_OK;
 }
 
-// 0: automatic, 1: vector-ALU kernel, 2: MFMA row-block kernel, 3: MFMA wide-strip kernel.
+// 0: automatic, 1: vector-ALU kernel, 2: MFMA row-block kernel, 3: MFMA wide-strip kernel,
+// 4: column-strip latency kernel.
 static int32_t g_gemv_kind = 0;
 
 int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits, int32_t gemv_waves,
                              int32_t gemv_reduce) {
-    if (gemv_kind < 0 || gemv_kind > 3) return fail(KT_ERR_ARGUMENT, "gemv_kind must be 0, 1, 2 or 3, got %d", gemv_kind);
+    if (gemv_kind < 0 || gemv_kind > 4) return fail(KT_ERR_ARGUMENT, "gemv_kind must be 0 to 4, got %d", gemv_kind);
     if (gemv_vec != 0 && gemv_vec != 4 && gemv_vec != 8)
         return fail(KT_ERR_ARGUMENT, "gemv_vec must be 0, 4 or 8, got %d", gemv_vec);
     if (gemv_splits < 0) return fail(KT_ERR_ARGUMENT, "gemv_splits must be >= 0, got %d", gemv_splits);
@@ -346,6 +347,8 @@ static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
     if (!a || !c) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const float* biases[1] = {bias};
+    if ((g_gemv_kind == 4 || (g_gemv_kind == 0 && gemv_strip_preferred(&v, 1))) && gemv_strip_supported(a, m, v, c))
+        return launch_gemv_strip(a, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 3 || (g_gemv_kind == 0 && gemv_wide_preferred(&v, 1))) && gemv_wide_supported(a, m, v, c))
         return launch_gemv_wide(a, &v, &c, biases, 1, accumulate, alpha, st);
     if (m <= 2 && gemv_mfma_supported(a, m, v, c)) return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
@@ -367,6 +370,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         bool fast = m == 1 && a != nullptr;
         bool mfma = m >= 1 && m <= 2 && a != nullptr;
         bool wide = (g_gemv_kind == 0 || g_gemv_kind == 3) && a != nullptr;
+        bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
             if (status) return status;
@@ -378,13 +382,17 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             fast = fast && gemv_supported(a, v, outputs[start + i]) && (!b || aligned(b, 16));
             mfma = mfma && gemv_mfma_supported(a, m, v, outputs[start + i]);
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
+            strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
         }
         if (m == 0) continue;
         if (!a) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input");
         hipStream_t st = static_cast<hipStream_t>(stream);
         int32_t status = KT_OK;
+        if (strip && g_gemv_kind == 0 && !gemv_strip_preferred(views, n)) strip = false;
         if (wide && g_gemv_kind == 0 && !gemv_wide_preferred(views, n)) wide = false;
-        if (wide) {
+        if (strip) {
+            status = launch_gemv_strip(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
+        } else if (wide) {
             status = launch_gemv_wide(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
         } else if (mfma) {
             status = launch_gemv_mfma(a, m, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,

@@ -72,7 +72,7 @@ def test_argument_errors_map_to_illegal_argument():
     assert lib.kt_qmatmul(fake, -1, ctypes.byref(w), fake, 0, ctypes.c_float(1.0), None) == _lib.KT_ERR_ARGUMENT
     assert "Negative row count" in _lib.last_error()
     assert lib.kt_qmatmul(fake, 0, ctypes.byref(w), fake, 0, ctypes.c_float(1.0), None) == _lib.KT_OK
-    assert lib.kt_set_kernel_config(4, 0, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_set_kernel_config(5, 0, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 5, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 0, 0, 3, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 0, 0, 0, 3) == _lib.KT_ERR_ARGUMENT

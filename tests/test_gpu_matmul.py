@@ -150,6 +150,7 @@ def test_gemv_work_splits_agree(kt, oracle_lib):
             configs += [(2, 0, waves, splits, reduce) for waves in (4, 8) for splits in (1, 2, 3, 5, q.groups)
                         for reduce in (1, 2)]
             configs += [(3, 0, waves, splits, 0) for waves in (0, 2, 4, 8) for splits in (0, 1, 2, 3, 5, k // 32)]
+            configs += [(4, 0, 0, 0, 0)]
             for kind, vec, waves, splits, reduce in configs:
                 banner("split", k, n, bits, kind, vec, waves, splits, reduce)
                 kt.MatMul.set_kernel_config(kind, vec, splits, waves, reduce)
