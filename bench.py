@@ -25,7 +25,9 @@ The JSON line also carries:
                    Llama-3-8B FFN shape (4096->14336) and the INT8 group-32 prefill
                    GEMM at M = 512 on the 2048-wide layer's four projection shapes
                    (2048->2048, 2048->512, 2048->8192, 8192->2048) and their sum, each
-                   with its fraction of the MFMA peak; and the Llama-style 1B INT4
+                   with its fraction of the MFMA peak and, for scale, the vendor library's
+                   plain bf16 GEMM (torch.matmul -> hipBLASLt, no dequantization) on the
+                   same shape timed the same way; and the Llama-style 1B INT4
                    decoder end to end (1024-token prefill, greedy decode steps).
 
 --only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
@@ -373,10 +375,23 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             tflops = flops / (ag * 1e-3) / 1e12
             tot_flops += flops
             tot_ms += ag
+            # the vendor library's plain bf16 GEMM of the same shape (no dequantization),
+            # timed the same way, for scale
+            wb = [torch.randn((k, n), generator=gen, device="cuda", dtype=torch.bfloat16)
+                  for _ in range(max(2, -(-2 * MALL_BYTES // (2 * k * n))))]
+            xb = xg.to(torch.bfloat16)
+            yb = torch.empty((512, n), device="cuda", dtype=torch.bfloat16)
+            for w in wb[:2]:  # eager calls first: the library sets up its handle outside capture
+                torch.matmul(xb, w, out=yb)
+            torch.cuda.synchronize()
+            ab = time_graph_launches(torch, stream_obj, lambda w: torch.matmul(xb, w, out=yb), wb, 32)
+            tb = flops / (ab * 1e-3) / 1e12
             extra[f"int8_g32_gemm_m512_{k}x{n}"] = {
                 "TFLOP/s": round(tflops, 1), "frac_mfma": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                "avg_us": round(ag * 1e3, 3), "copies": ng}
-            del cg, wg
+                "avg_us": round(ag * 1e3, 3), "copies": ng,
+                "hipblaslt_bf16_same_shape": {"TFLOP/s": round(tb, 1), "frac_mfma": round(tb / MFMA_PEAK_TFLOPS, 4),
+                                              "avg_us": round(ab * 1e3, 3)}}
+            del cg, wg, wb
         layer = tot_flops / (tot_ms * 1e-3) / 1e12
         extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
                                              "avg_us": round(tot_ms * 1e3, 3)}
