@@ -309,6 +309,193 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     }
 }
 
+// ---- prefill attention: blocked over queries, fp32 MFMA ---------------------------------
+// Workgroup (kv head g, block of QB = 128 / G consecutive tokens): the query rows
+// r = (token t0 + r / G, head g G + r % G), r < QB G, over keys 0 .. position + token,
+// 64 keys at a time; K and V tiles in LDS serve the four waves (32 rows each), so a key
+// row is read once per workgroup instead of once per token. Both products run on
+// v_mfma_f32_32x32x2_f32 (fp32 operands, fp32 sums; the reference's arithmetic up to
+// summation order):
+//   S^T = K Q^T: lane l ends with the scores of query row l % 32 against the 16 keys
+//     8 (e / 4) + 4 (l / 32) + e % 4 of each 32-key block (register e), so the running
+//     maximum, the exponentials and the rescaling of a row stay inside lanes l, l ^ 32;
+//   O^T += V^T P^T, taking the keys of each block in that same order: the B operand of
+//     step e is register e of the scores, as they lie.
+// Blocks go out longest first (the last tokens see the most keys).
+constexpr int PQ_ROWS = 128;  // query rows per workgroup
+constexpr int PKT = 64;       // keys per tile
+constexpr int PREFILL_MIN_TOKENS = 16;  // fewer tokens: the per-token kernel with key splits
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ void __launch_bounds__(THREADS) attention_prefill_kernel(AttnArgs a, int32_t tokens, int32_t qb_tokens,
+                                                                    int32_t nqb) {
+    extern __shared__ float smem[];
+    constexpr int KP = HD + 1;  // K row stride: 32 lanes on 32 rows hit distinct banks
+    constexpr int VP = HD + 8;  // V row stride: the two half-waves read rows 4 apart on other banks
+    constexpr int DB = HD / 32;
+    constexpr int QS = HD / 2;
+    constexpr int TF = PKT * HD / 4 / THREADS;  // float4 of a K (V) tile per thread
+    const int32_t g = blockIdx.x;
+    const int32_t qb = nqb - 1 - static_cast<int32_t>(blockIdx.y);
+    const int32_t G = a.num_heads / a.num_kv_heads;
+    const int32_t dim = a.num_heads * HD;
+    const int32_t t0 = qb * qb_tokens;
+    const int32_t t_end = min(t0 + qb_tokens, tokens);
+    const int32_t P0 = *a.position;
+    const int32_t n_keys = min(P0 + t_end, a.max_seq);  // never read outside the cache
+    const size_t base = (static_cast<size_t>(a.layer) * a.num_kv_heads + g) * a.max_seq;  // row of key 0
+    const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int32_t rl = lane & 31, h = lane >> 5;
+
+    const int32_t r = wave * 32 + rl;  // this lane's query row
+    const int32_t tl = r / G;
+    const int32_t tok = t0 + tl;
+    const bool row_ok = tl < qb_tokens && tok < t_end;
+    const int32_t head = g * G + r % G;
+    const int32_t p_r = row_ok ? min(P0 + tok, a.max_seq - 1) : -1;  // last key of the row
+
+    // the query rows through LDS into each lane's MFMA fragment: Q[r][2 s + h]
+    float qf[QS];
+    {
+        float* qs = smem;  // [PQ_ROWS][KP]
+        for (int32_t e = tid; e < PQ_ROWS * HD / 4; e += THREADS) {
+            const int32_t rr = e / (HD / 4), c4 = e % (HD / 4);
+            const int32_t tt = t0 + rr / G;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rr / G < qb_tokens && tt < t_end)
+                v = *reinterpret_cast<const float4*>(a.q + static_cast<size_t>(tt) * dim + (g * G + rr % G) * HD + 4 * c4);
+            float* d = qs + rr * KP + 4 * c4;
+            d[0] = v.x;
+            d[1] = v.y;
+            d[2] = v.z;
+            d[3] = v.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < QS; ++s) qf[s] = qs[r * KP + 2 * s + h];
+        __syncthreads();  // the area becomes the K and V tiles
+    }
+
+    float* ks = smem;             // [PKT][KP]
+    float* vs = smem + PKT * KP;  // [PKT][VP]
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[db][e] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    // a tile's K and V rows, all loads out before the first is used; rows past n_keys
+    // repeat the last key and are masked, and the tile after the last one repeats it
+    // (unconditional loads: no branch, and the arrays stay in registers)
+    v4f kr[TF], vr[TF];  // (native vectors: the HIP float4 struct keeps the arrays in scratch)
+#pragma unroll
+    for (int i = 0; i < TF; ++i) {
+        const int32_t e = tid + i * THREADS;
+        const int32_t j = e / (HD / 4), c4 = e % (HD / 4);
+        const size_t row = base + min(j, n_keys - 1);
+        kr[i] = *reinterpret_cast<const v4f*>(a.ck + row * HD + 4 * c4);
+        vr[i] = *reinterpret_cast<const v4f*>(a.cv + row * HD + 4 * c4);
+    }
+    for (int32_t k0 = 0; k0 < n_keys; k0 += PKT) {
+#pragma unroll
+        for (int i = 0; i < TF; ++i) {
+            const int32_t e = tid + i * THREADS;
+            const int32_t j = e / (HD / 4), c4 = e % (HD / 4);
+            float* kd = ks + j * KP + 4 * c4;
+            kd[0] = kr[i][0];
+            kd[1] = kr[i][1];
+            kd[2] = kr[i][2];
+            kd[3] = kr[i][3];
+            *reinterpret_cast<v4f*>(vs + j * VP + 4 * c4) = vr[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TF; ++i) {
+            const int32_t e = tid + i * THREADS;
+            const int32_t j = e / (HD / 4), c4 = e % (HD / 4);
+            const size_t row = base + min(k0 + PKT + j, n_keys - 1);
+            kr[i] = *reinterpret_cast<const v4f*>(a.ck + row * HD + 4 * c4);
+            vr[i] = *reinterpret_cast<const v4f*>(a.cv + row * HD + 4 * c4);
+        }
+
+        // S^T = K Q^T for the two 32-key blocks
+        f32x16 sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < QS; ++s)
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[(kb * 32 + rl) * KP + 2 * s + h], qf[s], sacc[kb], 0,
+                                                                0, 0);
+        }
+        // scale, causal mask, running max and sum of the row (lanes l and l ^ 32)
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int32_t j = k0 + kb * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                const float v = j <= p_r ? sacc[kb][e] * a.scale : -INFINITY;
+                sacc[kb][e] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m, tmax);
+        const bool none = m_new == -INFINITY;  // no key of the row yet (a padding row)
+        const float alpha = none || m == -INFINITY ? (none ? 1.0f : 0.0f) : expf(m - m_new);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = none ? 0.0f : expf(sacc[kb][e] - m_new);
+                sacc[kb][e] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 32);
+        l = l * alpha + psum;
+        m = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[db][e] *= alpha;
+        // O^T += V^T P^T, the keys of block kb in the order of the score registers
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float* vrow = vs + (kb * 32 + 8 * (e >> 2) + 4 * h + (e & 3)) * VP + rl;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[db * 32], sacc[kb][e], oacc[db], 0, 0, 0);
+            }
+        __syncthreads();  // the tiles are read before the next store
+    }
+
+    // O^T element (d, r) of block db: lane r + 32 ((d / 4) % 2), register (d / 8) * 4 + d % 4
+    if (row_ok) {
+        const float inv = 1.0f / l;
+        float* dst = a.context + static_cast<size_t>(tok) * dim + head * HD;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<float4*>(dst + db * 32 + 8 * c + 4 * h) =
+                    make_float4(oacc[db][4 * c] * inv, oacc[db][4 * c + 1] * inv, oacc[db][4 * c + 2] * inv,
+                                oacc[db][4 * c + 3] * inv);
+    }
+}
+
+size_t attention_prefill_lds(int32_t head_dim) {
+    const size_t q = static_cast<size_t>(PQ_ROWS) * (head_dim + 1);
+    const size_t kv = static_cast<size_t>(PKT) * (head_dim + 1) + static_cast<size_t>(PKT) * (head_dim + 8);
+    return (q > kv ? q : kv) * sizeof(float);
+}
+
 constexpr int MAX_SPLITS = 64;
 
 // Workgroup (token t, head h): merges the splits' (weighted values, max, sum). The
@@ -535,6 +722,39 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
         return fail(KT_ERR_ARGUMENT, "attention: q and the caches must be 16-byte aligned");
     if (tokens == 0) return KT_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (tokens >= PREFILL_MIN_TOKENS && (head_dim == 64 || head_dim == 128) && G <= PQ_ROWS) {
+        // many tokens: the query-blocked MFMA kernel
+        AttnArgs a{};
+        a.q = q;
+        a.position = position;
+        a.ck = cache_k;
+        a.cv = cache_v;
+        a.context = context;
+        a.layer = layer;
+        a.max_seq = max_seq;
+        a.num_heads = num_heads;
+        a.num_kv_heads = num_kv_heads;
+        a.head_dim = head_dim;
+        a.scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+        a.splits = 1;
+        const int32_t qb_tokens = PQ_ROWS / G;
+        const int32_t nqb = ceil_div(tokens, qb_tokens);
+        const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(nqb));
+        const size_t lds = attention_prefill_lds(head_dim);
+        if (head_dim == 64) {
+            attention_prefill_kernel<64><<<grid, THREADS, lds, st>>>(a, tokens, qb_tokens, nqb);
+        } else {
+            static bool raised = false;
+            if (!raised) {  // beyond the default dynamic LDS limit (160 KB per CU on gfx950)
+                KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_prefill_kernel<128>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10));
+                raised = true;
+            }
+            attention_prefill_kernel<128><<<grid, THREADS, lds, st>>>(a, tokens, qb_tokens, nqb);
+        }
+        KT_LAUNCHED("prefill attention kernel");
+        return KT_OK;
+    }
     // Key splits: enough workgroups to fill the GPU when few tokens attend.
     int32_t splits = 1;
     const int32_t tiles = ceil_div(key_bound, KT);
