@@ -205,6 +205,14 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
                      void* stream);
 /* SwiGLU's gate (K/SwiGLU.kt:19-25; K/Tensor.kt:223-237): gate[i] = silu(gate[i]) * up[i]. */
 int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream);
+/* SwiGLU.forwardInto's gate followed by the down projection (K/SwiGLU.kt:19-25 then
+ * QuantizedLinear.forwardInto, K/QuantizedLinear.kt:16-25):
+ * c = (accumulate ? c : 0) + alpha * (silu(gate) * up) . deq(W) (+ bias), gate and up
+ * [m x K]. For one row the M = 1 kernel computes the gate while it loads its input and
+ * gate is left unchanged; otherwise gate is overwritten with silu(gate) * up (exactly
+ * kt_silu_mul) and the product follows. Saves the gate launch of a decode step. */
+int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qweight* w, float* c,
+                          int32_t accumulate, float alpha, const float* bias, void* stream);
 /* Transformer.argmaxOfLastToken (K/Transformer.kt:253-266) of logits[0..n) into the
  * device int32 *index: the first index of the largest logit above -1e9, else 0. */
 int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream);

@@ -88,8 +88,13 @@ void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t
 // The M == 1 MFMA kernel on 512-byte row strips (kt_gemv_wide.hip).
 bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c);
 int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
-                         int32_t accumulate, float alpha, hipStream_t st);
+                         int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr);
 void set_gemv_wide_config(int32_t slices, int32_t waves);
+// The kernel choice of kt_set_kernel_config (0 automatic).
+int32_t gemv_kind();
+// kt_qmatmul with a bias (kt_qlinear_forward with accumulate and alpha).
+int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
+                const float* bias, void* stream);
 // Whether the automatic choice takes the wide-strip kernel for these weights.
 bool gemv_wide_preferred(const WeightView* ws, int32_t count);
 // The M == 1 latency kernel on 16-byte column strips over all of K (kt_gemv_strip.hip).

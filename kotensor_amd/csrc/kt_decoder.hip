@@ -819,6 +819,27 @@ int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream) {
     return KT_OK;
 }
 
+int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
+                          float alpha, const float* bias, void* stream) {
+    if (!gate || !up || !c) return fail(KT_ERR_ARGUMENT, "gate, up or the output is NULL");
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    if (m == 0) return KT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const float* biases[1] = {bias};
+    // one row: the wide GEMV computes the gate while it loads its input (and leaves the
+    // gate row as it was)
+    if (m == 1 && (gemv_kind() == 0 || gemv_kind() == 3) && gemv_wide_preferred(&v, 1) &&
+        gemv_wide_supported(gate, 1, v, c))
+        return launch_gemv_wide(gate, &v, &c, biases, 1, accumulate, alpha, st, up);
+    // otherwise the gate in place, then the product
+    status = kt_silu_mul(gate, up, static_cast<int64_t>(m) * v.K, stream);
+    if (status) return status;
+    return qmatmul(gate, m, w, c, accumulate, alpha, bias, stream);
+}
+
 int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream) {
     if (!logits || !index) return fail(KT_ERR_ARGUMENT, "logits or index is NULL");
     if (n <= 0) return fail(KT_ERR_SHAPE, "argmax needs at least one logit");

@@ -119,9 +119,13 @@ struct UnitScales {
     uint2 z[BITS == 4 ? 2 : 1];
 };
 
-template <int BITS, int NB, bool ZP, int WAVES>
+// SWIGLU: the input row is silu(x) * up (the SwiGLU gate, computed as silu_mul_kernel
+// does: x / (1 + exp(-x)) with exp in double rounded to float, times up), so the down
+// projection needs no separate gate launch.
+template <int BITS, int NB, bool ZP, int WAVES, bool SWIGLU>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
-    gemv_wide_kernel(const float* __restrict__ x, int32_t K, int32_t g, Jobs jobs, float alpha, int32_t accumulate) {
+    gemv_wide_kernel(const float* __restrict__ x, const float* __restrict__ up, int32_t K, int32_t g, Jobs jobs,
+                     float alpha, int32_t accumulate) {
     constexpr int THREADS = 64 * WAVES;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int SIDES = BITS == 4 ? 2 : 1;
@@ -174,13 +178,15 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         // ---- x: first batch of loads, before the weight loads --------------------------
         const int32_t sub = ln >> 5;  // two units per x instruction
         const int32_t kk = ln & 31;
-        float xv[XB];
+        float xv[XB], uv[XB];
         auto load_x = [&](int32_t k0) {
 #pragma unroll
             for (int b = 0; b < XB; ++b) {
                 int32_t k = k0 + 2 * b + sub;
                 k = k < my_units ? k : my_units - 1;
-                xv[b] = x[static_cast<size_t>(u_begin + wave + k * WAVES) * UNIT + kk];
+                const size_t i = static_cast<size_t>(u_begin + wave + k * WAVES) * UNIT + kk;
+                xv[b] = x[i];
+                if constexpr (SWIGLU) uv[b] = up[i];
             }
         };
         // Every loaded slot is processed (slots past my_units only skip their stores): a
@@ -189,6 +195,10 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
             for (int b = 0; b < XB; ++b) {
                 const int32_t k = k0 + 2 * b + sub;
+                if constexpr (SWIGLU) {
+                    const float gv = xv[b];
+                    xv[b] = gv / (1.0f + static_cast<float>(exp(-static_cast<double>(gv)))) * uv[b];
+                }
                 const float mx = half_reduce<true>(fabsf(xv[b]), ln);
                 int e = 0;
                 if (mx > 0.0f && mx <= 3.402823466e38f) {
@@ -404,24 +414,29 @@ constexpr size_t LDS_X_BYTES = 96 << 10;
 constexpr size_t X_UNIT_BYTES = 4 * UNIT * 2 + 16;
 
 template <int BITS, bool ZP, int WAVES>
-void launch_one(dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs, float alpha,
-                int32_t accumulate) {
-    gemv_wide_kernel<BITS, CPU_, ZP, WAVES><<<grid, dim3(64 * WAVES), lds, st>>>(a, K, g, jobs, alpha, accumulate);
+void launch_one(dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up, int32_t K, int32_t g,
+                const Jobs& jobs, float alpha, int32_t accumulate) {
+    if (up)
+        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, true><<<grid, dim3(64 * WAVES), lds, st>>>(a, up, K, g, jobs, alpha,
+                                                                                           accumulate);
+    else
+        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, false><<<grid, dim3(64 * WAVES), lds, st>>>(a, up, K, g, jobs, alpha,
+                                                                                            accumulate);
 }
 
 template <int BITS, bool ZP>
-void launch_waves(int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g, const Jobs& jobs,
-                  float alpha, int32_t accumulate) {
-    if (waves == 8) launch_one<BITS, ZP, 8>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
-    else if (waves == 4) launch_one<BITS, ZP, 4>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
-    else launch_one<BITS, ZP, 2>(grid, lds, st, a, K, g, jobs, alpha, accumulate);
+void launch_waves(int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up, int32_t K, int32_t g,
+                  const Jobs& jobs, float alpha, int32_t accumulate) {
+    if (waves == 8) launch_one<BITS, ZP, 8>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+    else if (waves == 4) launch_one<BITS, ZP, 4>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+    else launch_one<BITS, ZP, 2>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
 }
 
-void launch_kernel(int bits, bool zp, int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t K, int32_t g,
-                   const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (bits == 4) launch_waves<4, true>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
-    else if (zp) launch_waves<8, true>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
-    else launch_waves<8, false>(waves, grid, lds, st, a, K, g, jobs, alpha, accumulate);
+void launch_kernel(int bits, bool zp, int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up,
+                   int32_t K, int32_t g, const Jobs& jobs, float alpha, int32_t accumulate) {
+    if (bits == 4) launch_waves<4, true>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+    else if (zp) launch_waves<8, true>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+    else launch_waves<8, false>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
 }
 
 struct Plan {
@@ -479,7 +494,7 @@ bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const f
 }
 
 int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
-                         int32_t accumulate, float alpha, hipStream_t st) {
+                         int32_t accumulate, float alpha, hipStream_t st, const float* up) {
     const WeightView& w0 = ws[0];
     const int32_t units = w0.K / UNIT;
     bool zp = false;
@@ -538,7 +553,7 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
     }
     const size_t lds = lds_bytes(plan.ups, plan.waves, sides);
     const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
-    launch_kernel(w0.bits, zp, plan.waves, grid, lds, st, a, w0.K, w0.g, jobs, alpha, accumulate);
+    launch_kernel(w0.bits, zp, plan.waves, grid, lds, st, a, up, w0.K, w0.g, jobs, alpha, accumulate);
     KT_LAUNCHED("qmatmul: wide gemv kernel");
     return KT_OK;
 }

@@ -337,8 +337,8 @@ int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bi
     return KT_OK;
 }
 
-static int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
-                       float alpha, const float* bias, void* stream) {
+static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
+                            float alpha, const float* bias, void* stream) {
     WeightView v;
     int32_t status = view_weight(w, &v);
     if (status) return status;
@@ -411,12 +411,12 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
 
 int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
                    void* stream) {
-    return qmatmul(a, m, w, c, accumulate, alpha, nullptr, stream);
+    return qmatmul_impl(a, m, w, c, accumulate, alpha, nullptr, stream);
 }
 
 int32_t kt_qlinear_forward(const float* a, int32_t m, const kt_qweight* w, const float* bias, float* out,
                            void* stream) {
-    return qmatmul(a, m, w, out, 0, 1.0f, bias, stream);
+    return qmatmul_impl(a, m, w, out, 0, 1.0f, bias, stream);
 }
 
 int32_t kt_qmatmul_transposed(const float* dy, int32_t m, const kt_qweight* w, float* dx, int32_t accumulate,
@@ -452,3 +452,14 @@ int32_t kt_dequantize_columns(const kt_qweight* w, const int32_t* columns, int32
 }
 
 }  // extern "C"
+
+namespace kt {
+
+int32_t gemv_kind() { return g_gemv_kind; }
+
+int32_t qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
+                const float* bias, void* stream) {
+    return qmatmul_impl(a, m, w, c, accumulate, alpha, bias, stream);
+}
+
+}  // namespace kt

@@ -161,6 +161,50 @@ def test_silu_mul_and_add(kt, oracle_lib):
     np.testing.assert_array_equal(dx.download(np.float32), g + u)
 
 
+def test_swiglu_down_projection(kt, oracle_lib):
+    """kt_swiglu_qmatmul = SwiGLU's gate, then the down projection: one row through the
+    fused M = 1 kernel (gate left as it was), more rows through the gate in place and the
+    GEMM; with accumulate, alpha and a bias; against the oracle and, for one row, bit for
+    bit against kt_silu_mul followed by kt_qlinear of the same kernel."""
+    from kotensor_amd import _lib
+    from gpu_helpers import upload_quantized
+    rng = np.random.default_rng(14)
+    for (m, k, n, bits, g) in [(1, 8192, 2048, 4, 64), (1, 4864, 896, 4, 64), (1, 2048, 512, 8, 32), (3, 1024, 256, 4, 64)]:
+        banner("swiglu", m, k, n, bits, g)
+        w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+        st, q = oracle_lib.quantize(w, bits, g)
+        qt = upload_quantized(kt, q)
+        gate = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+        up = rng.standard_normal((m, k)).astype(np.float32)
+        c0 = rng.standard_normal((m, n)).astype(np.float32)
+        bias = rng.standard_normal(n).astype(np.float32)
+        fused = np.asarray(oracle_lib.silu_mul(gate.ravel(), up.ravel()), np.float32).reshape(m, k)
+        for use_bias in (False, True):
+            dg, du, dc, db = dev(kt, gate), dev(kt, up), dev(kt, c0), dev(kt, bias)
+            _lib.call("kt_swiglu_qmatmul", dg.ptr, du.ptr, m, ctypes.byref(qt.qweight), dc.ptr, 1, ctypes.c_float(0.5),
+                      db.ptr if use_bias else None, None)
+            got = dc.download(np.float32).reshape(m, n)
+            want = oracle_lib.multiply_quantized(fused, q, m, c=c0, accumulate=True, alpha=0.5, threads=16)
+            if use_bias:
+                want = (want + bias[None, :]).astype(np.float32)
+            assert normwise_rel(got, want) <= (1e-5 if m == 1 else 2e-3), (m, k, n, use_bias)
+            if m == 1:
+                assert np.array_equal(dg.download(np.float32).reshape(m, k), gate)  # left as it was
+                if not use_bias:
+                    # the unfused sequence through the same M = 1 kernel gives the same bits
+                    dg2, dc2 = dev(kt, gate), dev(kt, c0)
+                    _lib.call("kt_silu_mul", dg2.ptr, du.ptr, ctypes.c_int64(m * k), None)
+                    _lib.call("kt_set_kernel_config", 3, 0, 0, 0, 0)
+                    try:
+                        _lib.call("kt_qmatmul", dg2.ptr, m, ctypes.byref(qt.qweight), dc2.ptr, 1, ctypes.c_float(0.5),
+                                  None)
+                    finally:
+                        _lib.call("kt_set_kernel_config", 0, 0, 0, 0, 0)
+                    assert np.array_equal(got, dc2.download(np.float32).reshape(m, n))
+            else:
+                np.testing.assert_array_equal(dg.download(np.float32).reshape(m, k), fused)  # gate in place
+
+
 def test_argmax(kt, oracle_lib):
     from kotensor_amd import _lib
     rng = np.random.default_rng(5)
