@@ -205,6 +205,16 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
                      void* stream);
 /* SwiGLU's gate (K/SwiGLU.kt:19-25; K/Tensor.kt:223-237): gate[i] = silu(gate[i]) * up[i]. */
 int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream);
+/* RMSNorm.forward (K/RMSNorm.kt) of x [m x K] with weight, then the grouped projections of
+ * kt_qmatmul_group on the normalized rows: outputs[i] = (accumulate ? outputs[i] : 0)
+ * + alpha * RMSNorm(x) . deq(W_i) (+ biases[i]) (Attention's q/k/v, SwiGLU's gate/up, all
+ * weights with K rows). For one row and at most four weights the M = 1 kernel multiplies
+ * x * weight and scales the sums by 1 / sqrt(mean(x^2) + eps), the sum of squares reduced
+ * exactly as kt_rmsnorm reduces it (normed is not written); otherwise kt_rmsnorm writes
+ * normed [m x K] and kt_qmatmul_group follows. Saves the RMSNorm launch of a decode step. */
+int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
+                                 const kt_qweight* weights, int32_t count, float* const* outputs,
+                                 const float* const* biases, int32_t accumulate, float alpha, void* stream);
 /* SwiGLU.forwardInto's gate followed by the down projection (K/SwiGLU.kt:19-25 then
  * QuantizedLinear.forwardInto, K/QuantizedLinear.kt:16-25):
  * c = (accumulate ? c : 0) + alpha * (silu(gate) * up) . deq(W) (+ bias), gate and up

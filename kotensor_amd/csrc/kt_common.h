@@ -50,6 +50,35 @@ int32_t view_weight(const kt_qweight* w, WeightView* v);
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 __host__ __device__ inline int32_t ceil_div(int32_t a, int32_t b) { return (a + b - 1) / b; }
 
+// RMSNorm's reduction (K/RMSNorm.kt), shared by rmsnorm_kernel and the GEMV that takes
+// RMSNorm's input row, so both get the same scale r = 1 / sqrt(mean(x^2) + eps): thread
+// t < NORM_THREADS sums squares over the float4s t, t + 256, ... (zero past the row) in
+// this fmaf order, each 64-lane wave adds its lanes by xor butterfly, and the four wave
+// sums are added in wave order.
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_F4 = 8;  // float4 per thread: rows of up to 8192 floats
+typedef float norm_v4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float norm_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float norm_partial(const norm_v4 (&v)[NORM_F4], int32_t tid, int32_t n4) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NORM_F4; ++i) {
+        const norm_v4 u = tid + i * NORM_THREADS < n4 ? v[i] : norm_v4{0.0f, 0.0f, 0.0f, 0.0f};
+        s = fmaf(u[0], u[0], fmaf(u[1], u[1], fmaf(u[2], u[2], fmaf(u[3], u[3], s))));
+    }
+    return s;
+}
+__device__ __forceinline__ float norm_scale(const float (&wave_sums)[NORM_THREADS / 64], int32_t dim, float eps) {
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NORM_THREADS / 64; ++i) total += wave_sums[i];
+    return 1.0f / sqrtf(total / static_cast<float>(dim) + eps);
+}
+
 // Number of compute units of the current device (cached per device).
 int32_t cu_count();
 
@@ -88,7 +117,8 @@ void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t
 // The M == 1 MFMA kernel on 512-byte row strips (kt_gemv_wide.hip).
 bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const float* c);
 int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
-                         int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr);
+                         int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr,
+                         const float* norm_weight = nullptr, float eps = 0.0f);
 void set_gemv_wide_config(int32_t slices, int32_t waves);
 // The kernel choice of kt_set_kernel_config (0 automatic).
 int32_t gemv_kind();

@@ -46,9 +46,10 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---- RMSNorm ---------------------------------------------------------------------
-// One workgroup per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * weight. Rows of up
-// to 8192 floats (a multiple of 4) stay in registers: one load round trip per row.
-constexpr int NORM_F4 = 8;  // float4 per thread: dim <= 8192
+// One workgroup per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * weight, the sum of
+// squares as norm_partial / norm_wave_sum / norm_scale define it. Rows of up to 8192
+// floats (a multiple of 4) stay in registers: one load round trip per row.
+static_assert(THREADS == NORM_THREADS, "one thread per norm_partial slot");
 
 __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restrict__ x, int32_t dim,
                                                           const float* __restrict__ w, float eps,
@@ -58,29 +59,21 @@ __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restric
     float* orow = out + static_cast<size_t>(blockIdx.x) * dim;
     const int32_t tid = threadIdx.x;
     const bool vec = aligned16 && (dim & 3) == 0 && dim <= NORM_F4 * 4 * THREADS;
-    float4 v[NORM_F4];
+    norm_v4 v[NORM_F4];
     float s = 0.0f;
     if (vec) {
         const int32_t n4 = dim >> 2;
 #pragma unroll
-        for (int i = 0; i < NORM_F4; ++i)  // in-bounds unconditional loads, masked after
-            v[i] = reinterpret_cast<const float4*>(row)[min(tid + i * THREADS, n4 - 1)];
-#pragma unroll
-        for (int i = 0; i < NORM_F4; ++i)
-            if (tid + i * THREADS >= n4) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int i = 0; i < NORM_F4; ++i)
-            s = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, s))));
+        for (int i = 0; i < NORM_F4; ++i)  // in-bounds unconditional loads, masked in norm_partial
+            v[i] = reinterpret_cast<const norm_v4*>(row)[min(tid + i * THREADS, n4 - 1)];
+        s = norm_partial(v, tid, n4);
     } else {
         for (int32_t d = tid; d < dim; d += THREADS) s = fmaf(row[d], row[d], s);
     }
-    s = wave_sum(s);
+    s = norm_wave_sum(s);
     if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
-    float total = 0.0f;
-#pragma unroll
-    for (int i = 0; i < THREADS / 64; ++i) total += part[i];
-    const float r = 1.0f / sqrtf(total / static_cast<float>(dim) + eps);
+    const float r = norm_scale(part, dim, eps);
     if (vec) {
         const int32_t n4 = dim >> 2;
 #pragma unroll
@@ -89,7 +82,7 @@ __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restric
             if (e < n4) {
                 const float4 wv = reinterpret_cast<const float4*>(w)[e];
                 reinterpret_cast<float4*>(orow)[e] =
-                    make_float4(v[i].x * r * wv.x, v[i].y * r * wv.y, v[i].z * r * wv.z, v[i].w * r * wv.w);
+                    make_float4(v[i][0] * r * wv.x, v[i][1] * r * wv.y, v[i][2] * r * wv.z, v[i][3] * r * wv.w);
             }
         }
     } else {
@@ -817,6 +810,39 @@ int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream) {
     silu_mul_kernel<<<static_cast<uint32_t>(blocks), THREADS, 0, static_cast<hipStream_t>(stream)>>>(gate, up, n);
     KT_LAUNCHED("silu*mul kernel");
     return KT_OK;
+}
+
+int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
+                                 const kt_qweight* weights, int32_t count, float* const* outputs,
+                                 const float* const* biases, int32_t accumulate, float alpha, void* stream) {
+    if (!x || !norm_weight || !normed || !weights || !outputs)
+        return fail(KT_ERR_ARGUMENT, "x, the norm weight, normed, weights or outputs is NULL");
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    if (count <= 0) return fail(KT_ERR_ARGUMENT, "rmsnorm group needs at least one weight, got %d", count);
+    WeightView views[4];
+    int32_t status = view_weight(&weights[0], &views[0]);
+    if (status) return status;
+    const int32_t K = views[0].K;
+    if (m == 0) return KT_OK;
+    // one row, at most four weights the wide GEMV takes: RMSNorm inside the product
+    bool fused = m == 1 && count <= 4 && (gemv_kind() == 0 || gemv_kind() == 3) && aligned(x, 16) &&
+                 aligned(norm_weight, 4) && K % 4 == 0 && K <= NORM_F4 * 4 * NORM_THREADS;
+    for (int32_t i = 0; fused && i < count; ++i) {
+        if (i > 0) {
+            status = view_weight(&weights[i], &views[i]);
+            if (status) return status;
+        }
+        const WeightView& v = views[i];
+        fused = outputs[i] && v.K == K && v.bits == views[0].bits && v.g == views[0].g &&
+                (v.z != nullptr) == (views[0].z != nullptr) && gemv_wide_supported(x, 1, v, outputs[i]);
+    }
+    fused = fused && gemv_wide_preferred(views, count);
+    if (fused)
+        return launch_gemv_wide(x, views, outputs, biases, count, accumulate, alpha, static_cast<hipStream_t>(stream),
+                                nullptr, norm_weight, eps);
+    status = kt_rmsnorm(x, m, K, norm_weight, eps, normed, stream);
+    if (status) return status;
+    return kt_qmatmul_group(normed, m, weights, count, outputs, biases, accumulate, alpha, stream);
 }
 
 int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,

@@ -119,13 +119,22 @@ struct UnitScales {
     uint2 z[BITS == 4 ? 2 : 1];
 };
 
-// SWIGLU: the input row is silu(x) * up (the SwiGLU gate, computed as silu_mul_kernel
-// does: x / (1 + exp(-x)) with exp in double rounded to float, times up), so the down
-// projection needs no separate gate launch.
-template <int BITS, int NB, bool ZP, int WAVES, bool SWIGLU>
+// The input row, by XMODE:
+//   X_PLAIN  x;
+//   X_SWIGLU silu(x) * aux (the SwiGLU gate, computed as silu_mul_kernel does:
+//            x / (1 + exp(-x)) with exp in double rounded to float, times up), so the
+//            down projection needs no separate gate launch;
+//   X_NORM   RMSNorm(x) with weight aux: the product takes x * aux and the result is
+//            scaled by r = 1 / sqrt(mean(x^2) + eps), the sum of squares reduced as
+//            rmsnorm_kernel does (norm_partial etc.), so the q/k/v and gate/up
+//            projections need no separate RMSNorm launch. Every workgroup reads the
+//            whole row for the sum (at most 32 KB, from L2) while its weights stream.
+constexpr int X_PLAIN = 0, X_SWIGLU = 1, X_NORM = 2;
+
+template <int BITS, int NB, bool ZP, int WAVES, int XMODE>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
-    gemv_wide_kernel(const float* __restrict__ x, const float* __restrict__ up, int32_t K, int32_t g, Jobs jobs,
-                     float alpha, int32_t accumulate) {
+    gemv_wide_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t g,
+                     Jobs jobs, float alpha, int32_t accumulate) {
     constexpr int THREADS = 64 * WAVES;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int SIDES = BITS == 4 ? 2 : 1;
@@ -174,6 +183,18 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int a = 0; a < NACC; ++a) res[a] = 0.0f;
 
+    // X_NORM: the row for the sum of squares, loaded first (used after the first unit's
+    // loads are out); threads past NORM_THREADS load in-bounds copies and ignore them.
+    const int32_t n4 = K >> 2;
+    norm_v4 nv[NORM_F4];
+    float nsum = 0.0f;
+    if constexpr (XMODE == X_NORM) {
+#pragma unroll
+        for (int i = 0; i < NORM_F4; ++i)
+            nv[i] = reinterpret_cast<const norm_v4*>(x)[min(t + i * NORM_THREADS, n4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     if (my_units > 0) {
         // ---- x: first batch of loads, before the weight loads --------------------------
         const int32_t sub = ln >> 5;  // two units per x instruction
@@ -186,7 +207,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
                 k = k < my_units ? k : my_units - 1;
                 const size_t i = static_cast<size_t>(u_begin + wave + k * WAVES) * UNIT + kk;
                 xv[b] = x[i];
-                if constexpr (SWIGLU) uv[b] = up[i];
+                if constexpr (XMODE != X_PLAIN) uv[b] = aux[i];
             }
         };
         // Every loaded slot is processed (slots past my_units only skip their stores): a
@@ -195,9 +216,11 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
             for (int b = 0; b < XB; ++b) {
                 const int32_t k = k0 + 2 * b + sub;
-                if constexpr (SWIGLU) {
+                if constexpr (XMODE == X_SWIGLU) {
                     const float gv = xv[b];
                     xv[b] = gv / (1.0f + static_cast<float>(exp(-static_cast<double>(gv)))) * uv[b];
+                } else if constexpr (XMODE == X_NORM) {
+                    xv[b] *= uv[b];
                 }
                 const float mx = half_reduce<true>(fabsf(xv[b]), ln);
                 int e = 0;
@@ -245,6 +268,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 1; b < NB; ++b) load(buf[b], 0, b);
+        if constexpr (XMODE == X_NORM) nsum = t < NORM_THREADS ? norm_partial(nv, t, n4) : 0.0f;
 
         const int32_t scol = tile * TILE + kb * 128 + cl * 8;  // first column of the lane, low side
         const int32_t scol_c = active ? scol : 0;
@@ -343,6 +367,12 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     // ---- the workgroup's waves meet in LDS (reusing the x areas) ------------------------
     // red[wave][column] with column = side * 512 + (kb * 128 + cl * 8 + j) of the tile.
     float* red = reinterpret_cast<float*>(smem);
+    __shared__ float npart[NORM_THREADS / 64];
+    if constexpr (XMODE == X_NORM) {
+        if (my_units == 0) nsum = t < NORM_THREADS ? norm_partial(nv, t, n4) : 0.0f;
+        const float ws = norm_wave_sum(nsum);
+        if (t < NORM_THREADS && (t & 63) == 0) npart[t >> 6] = ws;
+    }
     __syncthreads();
 #pragma unroll
     for (int a = 0; a < NACC; ++a) {
@@ -392,12 +422,13 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
                              : 0.0f;
         if (t == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    const float al = XMODE == X_NORM ? alpha * norm_scale(npart, K, eps) : alpha;
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
         if (!live[i]) continue;
         float* dst = jb.out + colg[i];
         float o = accumulate ? *dst : 0.0f;
-        o = fmaf(alpha, sum[i], o);
+        o = fmaf(al, sum[i], o);
         if (jb.bias) o += jb.bias[colg[i]];
         *dst = o;
     }
@@ -413,30 +444,41 @@ Forced g_forced;
 constexpr size_t LDS_X_BYTES = 96 << 10;
 constexpr size_t X_UNIT_BYTES = 4 * UNIT * 2 + 16;
 
+struct XInput {
+    const float* x;
+    const float* aux;  // up (X_SWIGLU) or the RMSNorm weight (X_NORM)
+    float eps;
+    int mode;
+};
+
 template <int BITS, bool ZP, int WAVES>
-void launch_one(dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up, int32_t K, int32_t g,
-                const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (up)
-        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, true><<<grid, dim3(64 * WAVES), lds, st>>>(a, up, K, g, jobs, alpha,
-                                                                                           accumulate);
+void launch_one(dim3 grid, size_t lds, hipStream_t st, const XInput& in, int32_t K, int32_t g, const Jobs& jobs,
+                float alpha, int32_t accumulate) {
+    const dim3 block(64 * WAVES);
+    if (in.mode == X_SWIGLU)
+        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, X_SWIGLU><<<grid, block, lds, st>>>(in.x, in.aux, in.eps, K, g, jobs,
+                                                                                  alpha, accumulate);
+    else if (in.mode == X_NORM)
+        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, X_NORM><<<grid, block, lds, st>>>(in.x, in.aux, in.eps, K, g, jobs,
+                                                                                alpha, accumulate);
     else
-        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, false><<<grid, dim3(64 * WAVES), lds, st>>>(a, up, K, g, jobs, alpha,
-                                                                                            accumulate);
+        gemv_wide_kernel<BITS, CPU_, ZP, WAVES, X_PLAIN><<<grid, block, lds, st>>>(in.x, in.aux, in.eps, K, g, jobs,
+                                                                                 alpha, accumulate);
 }
 
 template <int BITS, bool ZP>
-void launch_waves(int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up, int32_t K, int32_t g,
+void launch_waves(int waves, dim3 grid, size_t lds, hipStream_t st, const XInput& in, int32_t K, int32_t g,
                   const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (waves == 8) launch_one<BITS, ZP, 8>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
-    else if (waves == 4) launch_one<BITS, ZP, 4>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
-    else launch_one<BITS, ZP, 2>(grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+    if (waves == 8) launch_one<BITS, ZP, 8>(grid, lds, st, in, K, g, jobs, alpha, accumulate);
+    else if (waves == 4) launch_one<BITS, ZP, 4>(grid, lds, st, in, K, g, jobs, alpha, accumulate);
+    else launch_one<BITS, ZP, 2>(grid, lds, st, in, K, g, jobs, alpha, accumulate);
 }
 
-void launch_kernel(int bits, bool zp, int waves, dim3 grid, size_t lds, hipStream_t st, const float* a, const float* up,
-                   int32_t K, int32_t g, const Jobs& jobs, float alpha, int32_t accumulate) {
-    if (bits == 4) launch_waves<4, true>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
-    else if (zp) launch_waves<8, true>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
-    else launch_waves<8, false>(waves, grid, lds, st, a, up, K, g, jobs, alpha, accumulate);
+void launch_kernel(int bits, bool zp, int waves, dim3 grid, size_t lds, hipStream_t st, const XInput& in, int32_t K,
+                   int32_t g, const Jobs& jobs, float alpha, int32_t accumulate) {
+    if (bits == 4) launch_waves<4, true>(waves, grid, lds, st, in, K, g, jobs, alpha, accumulate);
+    else if (zp) launch_waves<8, true>(waves, grid, lds, st, in, K, g, jobs, alpha, accumulate);
+    else launch_waves<8, false>(waves, grid, lds, st, in, K, g, jobs, alpha, accumulate);
 }
 
 struct Plan {
@@ -494,7 +536,8 @@ bool gemv_wide_supported(const float* a, int32_t m, const WeightView& w, const f
 }
 
 int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
-                         int32_t accumulate, float alpha, hipStream_t st, const float* up) {
+                         int32_t accumulate, float alpha, hipStream_t st, const float* up, const float* norm_weight,
+                         float eps) {
     const WeightView& w0 = ws[0];
     const int32_t units = w0.K / UNIT;
     bool zp = false;
@@ -553,7 +596,11 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
     }
     const size_t lds = lds_bytes(plan.ups, plan.waves, sides);
     const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
-    launch_kernel(w0.bits, zp, plan.waves, grid, lds, st, a, up, w0.K, w0.g, jobs, alpha, accumulate);
+    XInput in{a, up ? up : norm_weight, eps, up ? X_SWIGLU : norm_weight ? X_NORM : X_PLAIN};
+    if (up && norm_weight) return fail(KT_ERR_ARGUMENT, "wide gemv: one input transform at a time");
+    if (norm_weight && (w0.K % 4 != 0 || w0.K > NORM_F4 * 4 * NORM_THREADS || !aligned(a, 16)))
+        return fail(KT_ERR_ARGUMENT, "wide gemv: the RMSNorm input needs a 16-byte aligned row of <= 8192 floats");
+    launch_kernel(w0.bits, zp, plan.waves, grid, lds, st, in, w0.K, w0.g, jobs, alpha, accumulate);
     KT_LAUNCHED("qmatmul: wide gemv kernel");
     return KT_OK;
 }

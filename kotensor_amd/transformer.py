@@ -431,15 +431,13 @@ class Transformer:
         return None if self._zero_bias.get(name, True) else self.parameters[name + ".bias"].ptr
 
     def _layers(self, rows: _Rows, count: int, cache: KVCache, key_bound: int, st) -> None:
-        d, h = self.dimension, self.hidden_dimension
         for l in range(self.num_layers):
             p = f"block.{l}."
-            _lib.call("kt_rmsnorm", rows.x.ptr, count, d, self.parameters[p + "norm1.weight"].ptr,
-                      ctypes.c_float(self.norm_eps), rows.normed.ptr, st)
             names = [p + "attention.wQ", p + "attention.wK", p + "attention.wV"]
             n, ws, os_, bs = _group([self.weights[x] for x in names], [rows.q.ptr, rows.k.ptr, rows.v.ptr],
                                     [self._bias(x) for x in names])
-            _lib.call("kt_qmatmul_group", rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
+            _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm1.weight"].ptr,
+                      ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
             _lib.call("kt_rope_kv", rows.q.ptr, rows.k.ptr, rows.v.ptr, count, self.num_heads, self.num_key_value_heads,
                       self.head_dim, self.inv_freq.ptr, cache.position.ptr, cache.keys.ptr, cache.values.ptr, l,
                       cache.max_sequence_length, st)
@@ -447,12 +445,11 @@ class Transformer:
                       cache.values.ptr, l, cache.max_sequence_length, self.num_heads, self.num_key_value_heads,
                       self.head_dim, rows.context.ptr, st)
             self._residual_projection(p + "attention.wOut", rows.context, rows, count, st)
-            _lib.call("kt_rmsnorm", rows.x.ptr, count, d, self.parameters[p + "norm2.weight"].ptr,
-                      ctypes.c_float(self.norm_eps), rows.normed.ptr, st)
             names = [p + "ffn.wGate", p + "ffn.wUp"]
             n, ws, os_, bs = _group([self.weights[x] for x in names], [rows.gate.ptr, rows.up.ptr],
                                     [self._bias(x) for x in names])
-            _lib.call("kt_qmatmul_group", rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
+            _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm2.weight"].ptr,
+                      ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
             self._swiglu_down(p + "ffn.wDown", rows, count, st)
 
     def _head(self, x_row_ptr: int, buffers: InferenceBuffers, st) -> None:

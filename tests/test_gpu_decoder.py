@@ -205,6 +205,49 @@ def test_swiglu_down_projection(kt, oracle_lib):
                 np.testing.assert_array_equal(dg.download(np.float32).reshape(m, k), fused)  # gate in place
 
 
+def test_rmsnorm_grouped_projections(kt, oracle_lib):
+    """kt_rmsnorm_qmatmul_group = RMSNorm, then the grouped projections: one row through the
+    M = 1 kernel with the norm inside it (normed untouched), more rows through kt_rmsnorm
+    and the grouped product; with biases and accumulate; against the oracle's RMSNorm and
+    product, and for one row against kt_rmsnorm + kt_qmatmul_group of the same kernel
+    (the fused sum multiplies by r at the end, so agreement is to fp32 rounding)."""
+    from kotensor_amd import _lib
+    from gpu_helpers import upload_quantized
+    rng = np.random.default_rng(15)
+    for (m, k, ns, bits, g) in [(1, 2048, (2048, 512, 512), 4, 64), (1, 896, (896, 128, 128), 4, 64),
+                                (1, 2048, (8192, 8192), 8, 32), (1, 8192, (1024,), 4, 64), (4, 1024, (256, 64), 4, 64)]:
+        banner("rmsnorm group", m, k, ns, bits, g)
+        qs, qts = [], []
+        for n in ns:
+            w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+            st, q = oracle_lib.quantize(w, bits, g)
+            qs.append(q)
+            qts.append(upload_quantized(kt, q))
+        x = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+        nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        eps = 1e-5
+        normed_ref = oracle_lib.rmsnorm(x, nw, eps)
+        c0 = [rng.standard_normal((m, n)).astype(np.float32) for n in ns]
+        biases = [rng.standard_normal(n).astype(np.float32) for n in ns]
+        dx, dn, dnw = dev(kt, x), dev(kt, np.full((m, k), 7.0, np.float32)), dev(kt, nw)
+        douts = [dev(kt, c) for c in c0]
+        dbs = [dev(kt, b) for b in biases]
+        ws = (_lib.QWeight * len(ns))(*[qt.qweight for qt in qts])
+        outs = (ctypes.c_void_p * len(ns))(*[d.ptr for d in douts])
+        bs = (ctypes.c_void_p * len(ns))(*[d.ptr for d in dbs])
+        _lib.call("kt_rmsnorm_qmatmul_group", dx.ptr, dnw.ptr, ctypes.c_float(eps), dn.ptr, m, ws, len(ns),
+                  outs, bs, 1, ctypes.c_float(1.0), None)
+        for i, n in enumerate(ns):
+            got = douts[i].download(np.float32).reshape(m, n)
+            want = oracle_lib.multiply_quantized(normed_ref, qs[i], m, c=c0[i], accumulate=True, threads=16)
+            want = (want + biases[i][None, :]).astype(np.float32)
+            assert normwise_rel(got, want) <= (1e-5 if m == 1 else 2e-3), (m, k, n)
+        if m == 1:
+            assert np.all(dn.download(np.float32) == 7.0)  # normed untouched
+        else:
+            np.testing.assert_allclose(dn.download(np.float32).reshape(m, k), normed_ref, rtol=2e-6, atol=1e-7)
+
+
 def test_argmax(kt, oracle_lib):
     from kotensor_amd import _lib
     rng = np.random.default_rng(5)
