@@ -93,6 +93,9 @@ int32_t launch_gemv_group(const float* a, const WeightView* ws, float* const* cs
                           int32_t count, int32_t accumulate, float alpha, hipStream_t st);
 int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
                     float alpha, const float* bias, hipStream_t st);
+// Weights sharing a (K, bits, group size, zero points): one x preparation and one GEMM launch.
+int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float* const* cs, const float* const* biases,
+                          int32_t count, int32_t accumulate, float alpha, hipStream_t st);
 int32_t launch_generic(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate,
                        float alpha, const float* bias, hipStream_t st);
 int32_t launch_transposed(const float* dy, int32_t m, const WeightView& w, float* dx,

@@ -67,7 +67,40 @@ static_assert(LDS_HALFS >= 2 * 16384 && LDS_HALFS >= 2 * BM * (BN + 4), "LDS arr
 // outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at max).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int ROW_CHUNKS = 16;       // float4 chunks of a row each pre-pass thread keeps in registers
-constexpr int MAX_SCALE_BLOCKS = 256;  // pre-pass blocks over the scales (one maximum each)
+constexpr int MAX_SCALE_BLOCKS = 256;  // pre-pass blocks over one weight's scales (one maximum each)
+constexpr int MAX_GEMM_JOBS = 4;
+
+// One weight of a launch (kt_qmatmul_group's q/k/v or gate/up share a and K): its column
+// tiles are tile_begin .. tile_begin + tiles of the launch's tile row, its scale maxima
+// smax[smax_begin .. smax_begin + nsb).
+struct GemmJob {
+    const uint8_t* q;
+    const float* s;
+    const int8_t* z;
+    float* c;
+    float* partials;  // [splits][M][N] when K is split
+    const float* bias;
+    int64_t scale_quads;
+    int32_t N, bpr, tile_begin, smax_begin, nsb;
+};
+struct GemmJobs {
+    GemmJob job[MAX_GEMM_JOBS];
+    int32_t count;
+};
+__device__ __forceinline__ int32_t job_of_tile(const GemmJobs& jobs, int32_t tile_n) {
+    int32_t j = 0;
+#pragma unroll
+    for (int32_t i = 1; i < MAX_GEMM_JOBS; ++i)
+        if (i < jobs.count && tile_n >= jobs.job[i].tile_begin) j = i;
+    return j;
+}
+__device__ __forceinline__ int32_t job_of_scale_block(const GemmJobs& jobs, int32_t sb) {
+    int32_t j = 0;
+#pragma unroll
+    for (int32_t i = 1; i < MAX_GEMM_JOBS; ++i)
+        if (i < jobs.count && sb >= jobs.job[i].smax_begin) j = i;
+    return j;
+}
 
 // e such that max_abs * 2^-e lies in [2^(top-1), 2^top); 0 for zero or non-finite input.
 __device__ __forceinline__ int32_t scale_exponent(float max_abs, int32_t top) {
@@ -106,10 +139,10 @@ __device__ __forceinline__ f32x4 row_chunk(const float* row, int32_t c, int32_t 
 }
 
 // Blocks [0, Mp): row m of a as fp16 times 2^-er[m] (zeros for m >= M and k >= K).
-// Blocks [Mp, Mp + nsb): the largest |scale| over one slice of the G * N scales.
+// Blocks [Mp, Mp + sum of nsb): the largest |scale| over one slice of a job's G * N scales.
 __global__ void __launch_bounds__(256)
     gemm_prep(const float* __restrict__ a, int32_t M, int32_t K, int32_t Kp, int32_t vec_rows, int32_t Mp,
-              const float* __restrict__ s, int64_t scale_quads, int32_t nsb, _Float16* __restrict__ a16,
+              GemmJobs jobs, _Float16* __restrict__ a16,
               int32_t* __restrict__ er, float* __restrict__ smax) {
     __shared__ float red[4];
     const int32_t t = threadIdx.x;
@@ -156,8 +189,13 @@ __global__ void __launch_bounds__(256)
     }
     // Scales: G * N is a multiple of 4 and s is 16-byte aligned (checked by gemm_supported).
     const int32_t sb = b - Mp;
+    const GemmJob& jb = jobs.job[job_of_scale_block(jobs, sb)];
+    const float* s = jb.s;
+    const int64_t scale_quads = jb.scale_quads;
+    const int32_t nsb = jb.nsb;
     const int64_t per = (scale_quads + nsb - 1) / nsb;
-    const int64_t begin = per * sb;
+    const int32_t sl = sb - jb.smax_begin;
+    const int64_t begin = per * sl;
     const int64_t end = begin + per < scale_quads ? begin + per : scale_quads;
     float mx = 0.0f;
 #pragma unroll 8
@@ -243,11 +281,8 @@ __device__ __forceinline__ uint32_t load_bytes(const void* p) {
 template <int BITS, bool ZP, bool FAST>
 __global__ void __launch_bounds__(THREADS, 1)
     gemm_kernel(const _Float16* __restrict__ a16, int32_t Kp, const int32_t* __restrict__ er,
-                const float* __restrict__ smax, int32_t nsb, const uint8_t* __restrict__ q,
-                const float* __restrict__ s, const int8_t* __restrict__ z, int32_t M, int32_t K, int32_t N,
-                int32_t bpr, int32_t g, int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t steps_per_split,
-                float* __restrict__ c, float* __restrict__ partials, const float* __restrict__ bias, float alpha,
-                int32_t accumulate) {
+                const float* __restrict__ smax_all, GemmJobs jobs, int32_t M, int32_t K, int32_t g, int32_t tiles_m,
+                int32_t tiles_n, int32_t splits, int32_t steps_per_split, float alpha, int32_t accumulate) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[LDS_HALFS];
     __shared__ int32_t er_s[BM];
     __shared__ float red[THREADS / 64];
@@ -263,6 +298,16 @@ __global__ void __launch_bounds__(THREADS, 1)
     const int32_t per_n = tiles_m * splits;
     const int32_t tile_n = (j / per_n) * XCDS + pid % XCDS;
     if (tile_n >= tiles_n) return;
+    // the weight of this column tile
+    const GemmJob& jb = jobs.job[job_of_tile(jobs, tile_n)];
+    const uint8_t* __restrict__ q = jb.q;
+    const float* __restrict__ s = jb.s;
+    const int8_t* __restrict__ z = jb.z;
+    float* __restrict__ c = jb.c;
+    float* __restrict__ partials = jb.partials;
+    const float* __restrict__ bias = jb.bias;
+    const float* __restrict__ smax = smax_all + jb.smax_begin;
+    const int32_t N = jb.N, bpr = jb.bpr, nsb = jb.nsb;
     const int32_t rem = j % per_n;
     const int32_t tile_m = rem % tiles_m;
     const int32_t sp = rem / tiles_m;
@@ -276,7 +321,7 @@ __global__ void __launch_bounds__(THREADS, 1)
     const int32_t kh = __builtin_amdgcn_readfirstlane(wave >> 2);  // which half of each K step this wave multiplies
     const int32_t wm = (wave >> 1) & 1, wn = wave & 1;
     const int32_t m0 = tile_m * BM;
-    const int32_t b0 = tile_n * (BITS == 8 ? BN : BN / 2);  // first byte column of the tile
+    const int32_t b0 = (tile_n - jb.tile_begin) * (BITS == 8 ? BN : BN / 2);  // first byte column of the tile
 
     // Lane l of wave w takes byte group cq = l % 16 + 16 (l / 32) of rows rg * 4 .. rg * 4 + 3,
     // rg = 2 w + (l / 16) % 2. Its column j of the group goes to row 32 j + cq of the
@@ -590,11 +635,18 @@ bool gemm_supported(const float* a, int32_t m, const WeightView& w, const float*
     return aligned(w.q, 4) && aligned(w.s, 16) && (!w.z || aligned(w.z, 4)) && aligned(c, 16);
 }
 
-int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate, float alpha,
-                    const float* bias, hipStream_t st) {
+int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float* const* cs, const float* const* biases,
+                          int32_t count, int32_t accumulate, float alpha, hipStream_t st) {
+    if (count < 1 || count > MAX_GEMM_JOBS) return fail(KT_ERR_ARGUMENT, "gemm: 1 to %d weights, got %d", MAX_GEMM_JOBS, count);
+    const WeightView& w = ws[0];
+    for (int32_t i = 1; i < count; ++i)
+        if (ws[i].K != w.K || ws[i].bits != w.bits || ws[i].g != w.g || (ws[i].z != nullptr) != (w.z != nullptr))
+            return fail(KT_ERR_ARGUMENT, "gemm: grouped weights must share rows, bits, group size and zero points");
     const int32_t Mp = ceil_div(m, BM) * BM;
     const int32_t Kp = ceil_div(w.K, BK) * BK;
-    const int32_t tiles_n = ceil_div(w.bpr, w.bits == 8 ? BN : BN / 2);
+    const int32_t tile_bytes = w.bits == 8 ? BN : BN / 2;
+    int32_t tiles_n = 0;
+    for (int32_t i = 0; i < count; ++i) tiles_n += ceil_div(ws[i].bpr, tile_bytes);
     const int32_t tiles_m = Mp / BM;
     const int32_t k_steps = Kp / BK;
     // Split K when the tile grid leaves CUs idle, keeping at least 4 steps per slice.
@@ -608,35 +660,56 @@ int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, in
     const int32_t steps_per_split = ceil_div(k_steps, splits);
     splits = ceil_div(k_steps, steps_per_split);  // every slice has at least one step
 
-    const int64_t scale_quads = static_cast<int64_t>(w.G) * w.N / 4;
-    int64_t nsb64 = (scale_quads + 2047) / 2048;  // at least 8 quads per thread
-    if (nsb64 < 1) nsb64 = 1;
-    if (nsb64 > MAX_SCALE_BLOCKS) nsb64 = MAX_SCALE_BLOCKS;
-    const int32_t nsb = static_cast<int32_t>(nsb64);
+    GemmJobs jobs{};
+    jobs.count = count;
+    int32_t tile_begin = 0, nsb_total = 0;
+    size_t part_elems = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        GemmJob& jb = jobs.job[i];
+        jb.q = ws[i].q;
+        jb.s = ws[i].s;
+        jb.z = ws[i].z;
+        jb.c = cs[i];
+        jb.bias = biases ? biases[i] : nullptr;
+        jb.N = ws[i].N;
+        jb.bpr = ws[i].bpr;
+        jb.tile_begin = tile_begin;
+        tile_begin += ceil_div(ws[i].bpr, tile_bytes);
+        jb.scale_quads = static_cast<int64_t>(ws[i].G) * ws[i].N / 4;
+        int64_t nsb64 = (jb.scale_quads + 2047) / 2048;  // at least 8 quads per thread
+        if (nsb64 < 1) nsb64 = 1;
+        if (nsb64 > MAX_SCALE_BLOCKS) nsb64 = MAX_SCALE_BLOCKS;
+        jb.nsb = static_cast<int32_t>(nsb64);
+        jb.smax_begin = nsb_total;
+        nsb_total += jb.nsb;
+        if (splits > 1) part_elems += static_cast<size_t>(splits) * m * ws[i].N;
+    }
 
     auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t a16_bytes = round256(static_cast<size_t>(Mp) * Kp * sizeof(_Float16));
     const size_t er_bytes = round256(static_cast<size_t>(Mp) * 4);
-    const size_t smax_bytes = round256(static_cast<size_t>(nsb) * 4);
-    const size_t part_bytes = splits > 1 ? static_cast<size_t>(splits) * m * w.N * sizeof(float) : 0;
-    void* ws = nullptr;
-    int32_t status = workspace(st, a16_bytes + er_bytes + smax_bytes + part_bytes, &ws);
+    const size_t smax_bytes = round256(static_cast<size_t>(nsb_total) * 4);
+    const size_t part_bytes = part_elems * sizeof(float);
+    void* wsp = nullptr;
+    int32_t status = workspace(st, a16_bytes + er_bytes + smax_bytes + part_bytes, &wsp);
     if (status) return status;
-    char* base = static_cast<char*>(ws);
+    char* base = static_cast<char*>(wsp);
     _Float16* a16 = reinterpret_cast<_Float16*>(base);
     int32_t* er = reinterpret_cast<int32_t*>(base + a16_bytes);
     float* smax = reinterpret_cast<float*>(base + a16_bytes + er_bytes);
-    float* partials = splits > 1 ? reinterpret_cast<float*>(base + a16_bytes + er_bytes + smax_bytes) : nullptr;
+    float* part = reinterpret_cast<float*>(base + a16_bytes + er_bytes + smax_bytes);
+    for (int32_t i = 0; i < count && splits > 1; ++i) {
+        jobs.job[i].partials = part;
+        part += static_cast<size_t>(splits) * m * ws[i].N;
+    }
 
     const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
-    gemm_prep<<<Mp + nsb, 256, 0, st>>>(a, m, w.K, Kp, vec_rows, Mp, w.s, scale_quads, nsb, a16, er, smax);
+    gemm_prep<<<Mp + nsb_total, 256, 0, st>>>(a, m, w.K, Kp, vec_rows, Mp, jobs, a16, er, smax);
     KT_LAUNCHED("qmatmul: gemm prep");
     // Weight tiles dealt to the XCDs (padded to a multiple of 8), each with its row tiles
     // and K slices.
     const uint32_t blocks = static_cast<uint32_t>(ceil_div(tiles_n, XCDS) * XCDS * tiles_m * splits);
-#define KT_GEMM_ARGS                                                                                                 \
-    a16, Kp, er, smax, nsb, w.q, w.s, w.z, m, w.K, w.N, w.bpr, w.g, tiles_m, tiles_n, splits, steps_per_split, c, \
-        partials, bias, alpha, accumulate
+#define KT_GEMM_ARGS a16, Kp, er, smax, jobs, m, w.K, w.g, tiles_m, tiles_n, splits, steps_per_split, alpha, accumulate
     const bool fast = w.K % BK == 0 && (BK % w.g == 0 || w.g % BK == 0);
     if (w.bits == 4)
         fast ? gemm_kernel<4, true, true><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS)
@@ -649,13 +722,19 @@ int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, in
              : gemm_kernel<8, false, false><<<blocks, THREADS, 0, st>>>(KT_GEMM_ARGS);
 #undef KT_GEMM_ARGS
     KT_LAUNCHED("qmatmul: gemm kernel");
-    if (splits > 1) {
-        const size_t total = static_cast<size_t>(m) * w.N;
-        gemm_reduce<<<static_cast<uint32_t>((total + 255) / 256), 256, 0, st>>>(partials, splits, m, w.N, c, bias,
-                                                                             alpha, accumulate);
+    for (int32_t i = 0; i < count && splits > 1; ++i) {
+        const size_t total = static_cast<size_t>(m) * ws[i].N;
+        gemm_reduce<<<static_cast<uint32_t>((total + 255) / 256), 256, 0, st>>>(
+            jobs.job[i].partials, splits, m, ws[i].N, cs[i], biases ? biases[i] : nullptr, alpha, accumulate);
         KT_LAUNCHED("qmatmul: gemm reduce");
     }
     return KT_OK;
+}
+
+int32_t launch_gemm(const float* a, int32_t m, const WeightView& w, float* c, int32_t accumulate, float alpha,
+                    const float* bias, hipStream_t st) {
+    const float* biases[1] = {bias};
+    return launch_gemm_group(a, m, &w, &c, biases, 1, accumulate, alpha, st);
 }
 
 }  // namespace kt

@@ -371,6 +371,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         bool mfma = m >= 1 && m <= 2 && a != nullptr;
         bool wide = (g_gemv_kind == 0 || g_gemv_kind == 3) && a != nullptr;
         bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
+        bool gemm = m > 2 && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
             if (status) return status;
@@ -383,6 +384,8 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             mfma = mfma && gemv_mfma_supported(a, m, v, outputs[start + i]);
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
             strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
+            gemm = gemm && gemm_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 16)) &&
+                   (v.z != nullptr) == (views[0].z != nullptr);
         }
         if (m == 0) continue;
         if (!a) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input");
@@ -399,6 +402,9 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
                                       alpha, st);
         } else if (fast) {
             status = launch_gemv_group(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
+        } else if (gemm) {
+            status = launch_gemm_group(a, m, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,
+                                       alpha, st);
         } else {
             for (int32_t i = 0; i < n && status == KT_OK; ++i)
                 status = qmatmul(a, m, &weights[start + i], outputs[start + i], accumulate, alpha,

@@ -179,7 +179,7 @@ def test_quantized_linear_forward_with_bias(kt, oracle_lib):
         assert same_bits(layer.weight.qdata.view(np.uint8), q.qdata)
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 130])
 def test_grouped_projections(kt, oracle_lib, m):
     """kt_qmatmul_group: q/k/v and gate/up of one input in one call, with biases."""
     rng = np.random.default_rng(17)
