@@ -203,6 +203,17 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
                      const float* cache_k, const float* cache_v, int32_t layer, int32_t max_seq,
                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,
                      void* stream);
+/* kt_rope_kv followed by kt_attention (Attention.decodeInto/prefillInto,
+ * K/Attention.kt:207-275): RoPE on q and k at *position + t, k and v appended to the
+ * cache, then the cached attention into context. For one token (a decode step) RoPE and
+ * the append happen inside the attention launch: q and k are left as they were (the
+ * rotated q lives in LDS) and the cache row is written by the workgroup that reads it.
+ * For more tokens q and k are rotated in place, as kt_rope_kv does. Saves the RoPE
+ * launch of a decode step. */
+int32_t kt_rope_attention(float* q, float* k, const float* v, const float* inv_freq, int32_t tokens,
+                          const int32_t* position, int32_t key_bound, float* cache_k, float* cache_v,
+                          int32_t layer, int32_t max_seq, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_dim, float* context, void* stream);
 /* SwiGLU's gate (K/SwiGLU.kt:19-25; K/Tensor.kt:223-237): gate[i] = silu(gate[i]) * up[i]. */
 int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream);
 /* RMSNorm.forward (K/RMSNorm.kt) of x [m x K] with weight, then the grouped projections of

@@ -94,6 +94,16 @@ __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restric
 // Thread (token t, unit u): u < num_heads * half rotates pair i of q head u / half;
 // the next num_kv_heads * half units rotate k and write k and v to the cache.
 #pragma clang fp contract(off)
+// RoPE.applyInPlace's rotation of pair (x1, x2) = (row[i], row[i + half]) at pos:
+// theta = pos * invFreq[i] in fp32, cos and sin in double rounded to float, no
+// contraction (the whole region is compiled with fp contract off).
+__device__ __forceinline__ void rope_rotate(float x1, float x2, int32_t pos, float inv_freq_i, float& y1, float& y2) {
+    const float theta = static_cast<float>(pos) * inv_freq_i;
+    const float c = static_cast<float>(cos(static_cast<double>(theta)));
+    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    y1 = x1 * c - x2 * s;
+    y2 = x1 * s + x2 * c;
+}
 __global__ void __launch_bounds__(THREADS) rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
                                                           const float* __restrict__ v, int32_t num_heads,
                                                           int32_t num_kv_heads, int32_t head_dim,
@@ -111,15 +121,11 @@ __global__ void __launch_bounds__(THREADS) rope_kv_kernel(float* __restrict__ q,
     const bool is_q = u < q_units;
     const int32_t h = (is_q ? u : u - q_units) / half;
     const int32_t i = (is_q ? u : u - q_units) % half;
-    const float theta = static_cast<float>(pos) * inv_freq[i];
-    const float c = static_cast<float>(cos(static_cast<double>(theta)));
-    const float s = static_cast<float>(sin(static_cast<double>(theta)));
     float* row = is_q ? q + static_cast<size_t>(t) * num_heads * head_dim
                       : k + static_cast<size_t>(t) * num_kv_heads * head_dim;
     const int32_t i1 = h * head_dim + i, i2 = i1 + half;
-    const float x1 = row[i1], x2 = row[i2];
-    const float y1 = x1 * c - x2 * s;
-    const float y2 = x1 * s + x2 * c;
+    float y1, y2;
+    rope_rotate(row[i1], row[i2], pos, inv_freq[i], y1, y2);
     row[i1] = y1;
     row[i2] = y2;
     if (!is_q) {
@@ -143,6 +149,12 @@ struct AttnArgs {
     float* partials;         // [tokens][num_heads][splits][head_dim + 2] when splits > 1
     int32_t layer, max_seq, num_heads, num_kv_heads, head_dim, splits, span;
     float scale;
+    // one decode token with RoPE and the cache append inside: q, k_new, v_new are the
+    // projections before RoPE (rope_kv_kernel's inputs)
+    const float* k_new;
+    const float* v_new;
+    const float* inv_freq;
+    int32_t rope;
 };
 
 // Workgroup (kv head g, key split s, token t): the G = num_heads / num_kv_heads query
@@ -197,6 +209,39 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < MAX_NACC; ++r) acc[r] = 0.0f;
 
+    if (a.rope) {
+        // One decode token, RoPE inside: the G query heads are rotated in LDS, and the
+        // workgroup whose key range holds the new position rotates the new key, appends
+        // it and the value to the cache, and makes the writes visible to its own tile
+        // loads (the only reads of that row in this step).
+        if (tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
+        __syncthreads();
+        const int32_t half = HD >> 1;
+        for (int32_t e = tid; e < G * half; e += THREADS) {
+            const int32_t i = e % half, hh = e / half;
+            float y1, y2;
+            rope_rotate(qs[hh * HD + i], qs[hh * HD + i + half], pos, a.inv_freq[i], y1, y2);
+            qs[hh * HD + i] = y1;
+            qs[hh * HD + i + half] = y2;
+        }
+        if (pos >= k_begin && pos < k_end) {
+            float* ckw = const_cast<float*>(a.ck) + (base + pos) * HD;
+            float* cvw = const_cast<float*>(a.cv) + (base + pos) * HD;
+            const float* kn = a.k_new + static_cast<size_t>(g) * HD;
+            const float* vn = a.v_new + static_cast<size_t>(g) * HD;
+            for (int32_t i = tid; i < half; i += THREADS) {
+                float y1, y2;
+                rope_rotate(kn[i], kn[i + half], pos, a.inv_freq[i], y1, y2);
+                ckw[i] = y1;
+                ckw[i + half] = y2;
+                cvw[i] = vn[i];
+                cvw[i + half] = vn[i + half];
+            }
+            __threadfence();
+        }
+        __syncthreads();
+    }
+
     // K and V tiles in registers together (one round trip) up to head_dim 128; wider
     // heads load them one after the other to keep the registers in bounds.
     constexpr bool TOGETHER = TF4 <= 8;
@@ -206,7 +251,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         const int32_t n4 = n * HD / 4;
         load_tile<TF4>(kr, a.ck + (base + k0) * HD, n4);
         if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k0) * HD, n4);
-        if (k0 == k_begin && tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
+        if (!a.rope && k0 == k_begin && tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
 #pragma unroll
         for (int i = 0; i < TF4; ++i) {
             const int32_t e = tid + i * THREADS;
@@ -696,9 +741,10 @@ int32_t kt_rope_kv(float* q, float* k, const float* v, int32_t tokens, int32_t n
     return KT_OK;
 }
 
-int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound, const float* cache_k,
-                     const float* cache_v, int32_t layer, int32_t max_seq, int32_t num_heads, int32_t num_kv_heads,
-                     int32_t head_dim, float* context, void* stream) {
+static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound,
+                                const float* cache_k, const float* cache_v, int32_t layer, int32_t max_seq,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,
+                                const float* k_new, const float* v_new, const float* inv_freq, void* stream) {
     if (!q || !position || !cache_k || !cache_v || !context) return fail(KT_ERR_ARGUMENT, "a pointer argument is NULL");
     if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
         return fail(KT_ERR_ARGUMENT, "numHeads %d must be a multiple of numKeyValueHeads %d", num_heads, num_kv_heads);
@@ -715,7 +761,7 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
         return fail(KT_ERR_ARGUMENT, "attention: q and the caches must be 16-byte aligned");
     if (tokens == 0) return KT_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (tokens >= PREFILL_MIN_TOKENS && (head_dim == 64 || head_dim == 128) && G <= PQ_ROWS) {
+    if (!k_new && tokens >= PREFILL_MIN_TOKENS && (head_dim == 64 || head_dim == 128) && G <= PQ_ROWS) {
         // many tokens: the query-blocked MFMA kernel
         AttnArgs a{};
         a.q = q;
@@ -769,6 +815,10 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
     a.num_kv_heads = num_kv_heads;
     a.head_dim = head_dim;
     a.scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.inv_freq = inv_freq;
+    a.rope = k_new != nullptr ? 1 : 0;
     a.span = ceil_div(tiles, splits) * KT;
     a.splits = ceil_div(key_bound, a.span);
     if (a.splits > 1) {
@@ -799,6 +849,30 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
         KT_LAUNCHED("attention combine kernel");
     }
     return KT_OK;
+}
+
+int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound, const float* cache_k,
+                     const float* cache_v, int32_t layer, int32_t max_seq, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, float* context, void* stream) {
+    return attention_launch(q, tokens, position, key_bound, cache_k, cache_v, layer, max_seq, num_heads, num_kv_heads,
+                            head_dim, context, nullptr, nullptr, nullptr, stream);
+}
+
+int32_t kt_rope_attention(float* q, float* k, const float* v, const float* inv_freq, int32_t tokens,
+                          const int32_t* position, int32_t key_bound, float* cache_k, float* cache_v, int32_t layer,
+                          int32_t max_seq, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,
+                          void* stream) {
+    if (!q || !k || !v || !inv_freq || !position || !cache_k || !cache_v || !context)
+        return fail(KT_ERR_ARGUMENT, "a pointer argument is NULL");
+    if (head_dim <= 0 || head_dim % 2 != 0) return fail(KT_ERR_ARGUMENT, "RoPE dimension must be even");
+    if (tokens == 1)  // the decode step: RoPE and the cache append inside the attention kernel
+        return attention_launch(q, 1, position, key_bound, cache_k, cache_v, layer, max_seq, num_heads, num_kv_heads,
+                                head_dim, context, k, v, inv_freq, stream);
+    const int32_t status = kt_rope_kv(q, k, v, tokens, num_heads, num_kv_heads, head_dim, inv_freq, position, cache_k,
+                                      cache_v, layer, max_seq, stream);
+    if (status) return status;
+    return kt_attention(q, tokens, position, key_bound, cache_k, cache_v, layer, max_seq, num_heads, num_kv_heads,
+                        head_dim, context, stream);
 }
 
 int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream) {

@@ -438,12 +438,9 @@ class Transformer:
                                     [self._bias(x) for x in names])
             _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm1.weight"].ptr,
                       ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
-            _lib.call("kt_rope_kv", rows.q.ptr, rows.k.ptr, rows.v.ptr, count, self.num_heads, self.num_key_value_heads,
-                      self.head_dim, self.inv_freq.ptr, cache.position.ptr, cache.keys.ptr, cache.values.ptr, l,
-                      cache.max_sequence_length, st)
-            _lib.call("kt_attention", rows.q.ptr, count, cache.position.ptr, key_bound, cache.keys.ptr,
-                      cache.values.ptr, l, cache.max_sequence_length, self.num_heads, self.num_key_value_heads,
-                      self.head_dim, rows.context.ptr, st)
+            _lib.call("kt_rope_attention", rows.q.ptr, rows.k.ptr, rows.v.ptr, self.inv_freq.ptr, count,
+                      cache.position.ptr, key_bound, cache.keys.ptr, cache.values.ptr, l, cache.max_sequence_length,
+                      self.num_heads, self.num_key_value_heads, self.head_dim, rows.context.ptr, st)
             self._residual_projection(p + "attention.wOut", rows.context, rows, count, st)
             names = [p + "ffn.wGate", p + "ffn.wUp"]
             n, ws, os_, bs = _group([self.weights[x] for x in names], [rows.gate.ptr, rows.up.ptr],

@@ -146,6 +146,44 @@ def test_attention(kt, oracle_lib, heads, kvh, hd):
             np.testing.assert_allclose(got, want, rtol=0, atol=5e-6 * max(1.0, np.abs(want).max()))
 
 
+def test_rope_attention_fused_equals_unfused(kt, oracle_lib):
+    """kt_rope_attention: for one token RoPE and the cache append run inside the attention
+    launch and give the bits of kt_rope_kv + kt_attention (cache rows and context); for
+    more tokens it is that sequence. Key ranges split over several workgroups, the new
+    key in the last tile, a GQA group of 7, head_dim 64 and 128."""
+    from kotensor_amd import _lib
+    rng = np.random.default_rng(21)
+    for heads, kvh, hd, start, max_seq in [(32, 8, 64, 1100, 1200), (14, 2, 64, 0, 16), (8, 2, 128, 63, 200),
+                                          (32, 8, 64, 190, 191)]:
+        banner("rope attention", heads, kvh, hd, start, max_seq)
+        layers, layer = 2, 1
+        inv = oracle_lib.rope_inv_freq(hd, 10000.0, None).astype(np.float32)
+        keys = np.zeros((layers, kvh, max_seq, hd), np.float32)
+        values = np.zeros_like(keys)
+        keys[:, :, :start] = rng.standard_normal((layers, kvh, start, hd))
+        values[:, :, :start] = rng.standard_normal((layers, kvh, start, hd))
+        q = rng.standard_normal((1, heads * hd)).astype(np.float32)
+        k = rng.standard_normal((1, kvh * hd)).astype(np.float32)
+        v = rng.standard_normal((1, kvh * hd)).astype(np.float32)
+        outs = []
+        for fused in (True, False):
+            dq, dk, dv, dinv = dev(kt, q), dev(kt, k), dev(kt, v), dev(kt, inv)
+            dck, dcv = dev(kt, keys), dev(kt, values)
+            pos = dev(kt, np.array([start], np.int32))
+            ctx = kt.DeviceBuffer(q.nbytes)
+            if fused:
+                _lib.call("kt_rope_attention", dq.ptr, dk.ptr, dv.ptr, dinv.ptr, 1, pos.ptr, max_seq, dck.ptr, dcv.ptr,
+                          layer, max_seq, heads, kvh, hd, ctx.ptr, None)
+            else:
+                _lib.call("kt_rope_kv", dq.ptr, dk.ptr, dv.ptr, 1, heads, kvh, hd, dinv.ptr, pos.ptr, dck.ptr, dcv.ptr,
+                          layer, max_seq, None)
+                _lib.call("kt_attention", dq.ptr, 1, pos.ptr, max_seq, dck.ptr, dcv.ptr, layer, max_seq, heads, kvh, hd,
+                          ctx.ptr, None)
+            outs.append((ctx.download(np.float32), dck.download(np.float32), dcv.download(np.float32)))
+        for a_, b_ in zip(outs[0], outs[1]):
+            assert np.array_equal(a_, b_)
+
+
 def test_silu_mul_and_add(kt, oracle_lib):
     from kotensor_amd import _lib
     rng = np.random.default_rng(4)
