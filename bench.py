@@ -27,7 +27,8 @@ The JSON line also carries:
                    (2048->2048, 2048->512, 2048->8192, 8192->2048) and their sum, each
                    with its fraction of the MFMA peak and, for scale, the vendor library's
                    plain bf16 GEMM (torch.matmul -> hipBLASLt, no dequantization) on the
-                   same shape timed the same way; and the Llama-style 1B INT4
+                   same shape timed the same way; the M sweep (1, 16, 128, 512, 2048) of
+                   the INT8 2048 -> 8192 product; and the Llama-style 1B INT4
                    decoder end to end (1024-token prefill, greedy decode steps).
 
 --only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
@@ -395,6 +396,24 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         layer = tot_flops / (tot_ms * 1e-3) / 1e12
         extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
                                              "avg_us": round(tot_ms * 1e3, 3)}
+
+        # the M sweep of the INT8 g32 2048 -> 8192 product (M = 1, 16: the decode kernels;
+        # 128 and up: the GEMM): time per launch, TFLOP/s and GB/s of algorithmic bytes
+        wm = Weight(torch, kt_lib, 2048, 8192, 8, 32, seed=11, stream=stream)
+        nm = max(2, -(-2 * MALL_BYTES // wm.nbytes))
+        cm = [wm] + [wm.clone(kt_lib) for _ in range(nm - 1)]
+        sweep = {}
+        for mm in (1, 16, 128, 512, 2048):
+            xm = torch.randn((mm, 2048), generator=gen, device="cuda", dtype=torch.float32)
+            ym = torch.empty((mm, 8192), device="cuda", dtype=torch.float32)
+            for w in cm[:2]:
+                qmatmul(kt_lib, xm, mm, w, ym, stream)
+            am = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xm, mm, w, ym, stream), cm, 32)
+            flops = 2.0 * mm * 2048 * 8192
+            sweep[str(mm)] = {"avg_us": round(am * 1e3, 3), "TFLOP/s": round(flops / (am * 1e-3) / 1e12, 1),
+                              "GB/s": round(gemv_bytes(mm, 2048, 8192, 8, 32) / (am * 1e-3) / 1e9, 1)}
+        extra["int8_g32_m_sweep_2048x8192"] = sweep
+        del cm, wm
 
         extra["llama1b_int4_decoder"] = decoder_figures(torch, stream_obj)
 
