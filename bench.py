@@ -28,8 +28,12 @@ The JSON line also carries:
                    with its fraction of the MFMA peak and, for scale, the vendor library's
                    plain bf16 GEMM (torch.matmul -> hipBLASLt, no dequantization) on the
                    same shape timed the same way; the M sweep (1, 16, 128, 512, 2048) of
-                   the INT8 2048 -> 8192 product; and the Llama-style 1B INT4
+                   the INT8 2048 -> 8192 product; the Llama-3-8B projection shapes
+                   (4096->4096, 4096->1024, 4096->14336, 14336->4096), INT4 and INT8 g64
+                   at M = 1, 8, 64, 512; kt_quantize on 4096 x 14336 (per call,
+                   including its NaN-flag readback); and the Llama-style 1B INT4
                    decoder end to end (1024-token prefill, greedy decode steps).
+                   Every timed graph reads each of its weight copies (> 2x MALL).
 
 --only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
 calibration of the HBM byte counters) for rocprofv3 PMC runs.
@@ -119,6 +123,7 @@ def qmatmul_group(kt_lib, x, m, ws, ys, stream):
 def time_graph_launches(torch, stream_obj, fn, copies, launches, replays=3):
     """Average duration of one launch: `launches` back-to-back launches (rotating weight
     copies) captured in one graph, HIP events on the launch stream around the replays."""
+    launches = max(launches, len(copies))  # every copy is read in each replay
     gph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gph, stream=stream_obj):
         for i in range(launches):
@@ -414,6 +419,67 @@ def run(args, torch, kt_lib, stream_obj) -> int:
                               "GB/s": round(gemv_bytes(mm, 2048, 8192, 8, 32) / (am * 1e-3) / 1e9, 1)}
         extra["int8_g32_m_sweep_2048x8192"] = sweep
         del cm, wm
+
+        # Llama-3-8B projection shapes (q/o 4096 -> 4096, k/v 4096 -> 1024, gate/up
+        # 4096 -> 14336, down 14336 -> 4096), INT4 and INT8 at group 64, M = 1, 8, 64, 512
+        l8 = {}
+        for bits in (4, 8):
+            for (k, n) in [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]:
+                wl = Weight(torch, kt_lib, k, n, bits, 64, seed=13, stream=stream)
+                nl = max(2, -(-2 * MALL_BYTES // wl.nbytes))
+                cl = [wl] + [wl.clone(kt_lib) for _ in range(nl - 1)]
+                row = {}
+                for mm in (1, 8, 64, 512):
+                    xl = torch.randn((mm, k), generator=gen, device="cuda", dtype=torch.float32)
+                    yl = torch.empty((mm, n), device="cuda", dtype=torch.float32)
+                    for w in cl[:2]:
+                        qmatmul(kt_lib, xl, mm, w, yl, stream)
+                    al = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xl, mm, w, yl, stream), cl, 32)
+                    gbs = gemv_bytes(mm, k, n, bits, 64) / (al * 1e-3) / 1e9
+                    tfl = 2.0 * mm * k * n / (al * 1e-3) / 1e12
+                    row[str(mm)] = {"avg_us": round(al * 1e3, 3), "GB/s": round(gbs, 1),
+                                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "TFLOP/s": round(tfl, 1),
+                                    "frac_mfma": round(tfl / MFMA_PEAK_TFLOPS, 4)}
+                l8[f"int{bits}_g64_{k}x{n}"] = row
+                del cl, wl
+        extra["llama8b_projections_m_sweep"] = l8
+
+        # kt_quantize on the gate/up shape 4096 x 14336 at group 64 (reads the fp32 weight,
+        # writes the packed weight, scales and zeros), three distinct inputs (> 2x MALL);
+        # each call ends with the NaN flag's readback, so the figure is per call, event to
+        # event on the stream, not per kernel
+        qz = {}
+        kq, nq = 4096, 14336
+        srcs = [torch.randn((kq, nq), generator=gen, device="cuda", dtype=torch.float32) * 0.02 for _ in range(3)]
+        for bits in (4, 8):
+            groups, bpr = layout(kq, nq, bits, 64)
+            qq = torch.empty(kq * bpr, dtype=torch.uint8, device="cuda")
+            sq = torch.empty(groups * nq, dtype=torch.float32, device="cuda")
+            zq = torch.empty(groups * nq, dtype=torch.uint8, device="cuda") if bits == 4 else None
+
+            def quantize_once(src, bits=bits, qq=qq, sq=sq, zq=zq):
+                kt_lib.call("kt_quantize", src.data_ptr(), kq, nq, bits, 64, qq.data_ptr(), sq.data_ptr(),
+                            zq.data_ptr() if zq is not None else None, stream)
+
+            for src in srcs:
+                quantize_once(src)
+            torch.cuda.synchronize()
+            times = []
+            for i in range(12):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream_obj)
+                quantize_once(srcs[i % len(srcs)])
+                e1.record(stream_obj)
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+            tq = sorted(times)[len(times) // 2]
+            bq = 4 * kq * nq + kq * bpr + 4 * groups * nq + (groups * nq if bits == 4 else 0)
+            gq = bq / (tq * 1e-3) / 1e9
+            qz[f"int{bits}_g64_{kq}x{nq}"] = {"median_us_per_call": round(tq * 1e3, 3), "bytes": bq,
+                                              "GB/s": round(gq, 1), "frac_hbm": round(gq / HBM_PEAK_GBS, 4)}
+        extra["quantize_llama8b_gate_4096x14336"] = qz
+        del srcs
 
         extra["llama1b_int4_decoder"] = decoder_figures(torch, stream_obj)
 

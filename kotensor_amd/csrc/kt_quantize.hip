@@ -10,7 +10,8 @@
 //   * the group's rows are split over the workgroup's waves, RPW rows each, and
 //     stay in registers between the min/max pass and the rounding pass, so every
 //     input float is read from HBM exactly once (each wave row is 1 KB contiguous);
-//   * per-column min/max partials are combined across waves through LDS.
+//   * per-column min/max partials are combined across waves through LDS, and each
+//     column's scale, zero and inverse are computed once per workgroup.
 // Shapes the vector kernels cannot take (odd widths, misaligned pointers, group
 // sizes beyond 16 waves' rows) use a one-thread-per-column kernel that scans twice.
 //
@@ -28,16 +29,19 @@ namespace {
 
 // Math.round(float) contract: nearest integer, ties toward +inf, saturating at the
 // int range. NaN is what Float.roundToInt() rejects; it raises the error flag.
+// Branch-free: v_cvt_i32_f32 saturates out-of-range values (infinities included) to
+// INT32_MIN / INT32_MAX and turns NaN into 0, which is the contract for every input
+// whose floor is out of range; the +1 of a fraction >= 1/2 only occurs below 2^23.
+__device__ __forceinline__ int32_t cvt_sat(float f) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+    return r;
+}
 __device__ __forceinline__ int32_t java_round(float x, bool& nan_seen) {
-    if (x != x) {
-        nan_seen = true;
-        return 0;
-    }
-    if (x >= 2147483648.0f) return INT32_MAX;
-    if (x <= -2147483648.0f) return INT32_MIN;
-    float f = floorf(x);
-    float frac = x - f;  // exact whenever it can be close to one half
-    int32_t r = static_cast<int32_t>(f);
+    nan_seen |= x != x;
+    const float f = floorf(x);
+    const float frac = x - f;  // exact whenever it can be close to one half; NaN for +-inf
+    const int32_t r = cvt_sat(f);
     return frac >= 0.5f ? r + 1 : r;
 }
 
@@ -55,86 +59,100 @@ __device__ __forceinline__ float lane(const float4& v, int j) {
 
 __global__ void clear_flag(int32_t* flag) { *flag = 0; }
 
-// INT8, 4 columns per lane, RPW rows per wave, ceil(g / RPW) waves per workgroup.
+// The vector kernels: a workgroup owns one group and 64 column units, its waves split
+// the group's rows (RPW each) and keep them in registers. Per-lane partial extrema go
+// to LDS as [wave][component][lane] (lanes contiguous: no bank conflicts); then every
+// thread takes whole columns of the workgroup (consecutive threads, consecutive
+// columns: coalesced scale and zero stores), reduces the waves' partials, computes the
+// scale, zero and inverse once (the three correctly rounded divisions per column are
+// not repeated in every wave) and publishes inverse and zero as [component][lane] for
+// the rounding pass. Min and max are exact and order-free up to the sign of a zero,
+// which no output depends on; a NaN input makes the call fail whatever they hold.
+
+// INT8, 4 columns per lane (256 columns per workgroup), RPW rows per wave.
 template <int RPW>
 __global__ void __launch_bounds__(1024) quant8_vec(const float* __restrict__ data, int32_t K, int32_t N,
                                                    int32_t g, uint8_t* __restrict__ q, float* __restrict__ s,
                                                    int32_t* __restrict__ nan_flag) {
-    extern __shared__ float red[];  // [waves][64][4]
-    const int32_t ln = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const int32_t col_blocks = ceil_div(N >> 2, 64);
+    extern __shared__ float red[];  // [waves][4][64] max |x|, then [4][64] inverses
+    const int32_t t = threadIdx.x, ln = t & 63, wave = t >> 6, waves = blockDim.x >> 6;
+    const int32_t units = N >> 2;
+    const int32_t col_blocks = ceil_div(units, 64);
     const int32_t group = blockIdx.x / col_blocks;
-    const int32_t unit = (blockIdx.x % col_blocks) * 64 + ln;
-    const bool active = unit < (N >> 2);
+    const int32_t cb = blockIdx.x % col_blocks;
+    const int32_t unit = cb * 64 + ln;
+    const bool active = unit < units;
     const int32_t r0 = group * g;
     const int32_t r1 = min(r0 + g, K);
     const int32_t wr0 = r0 + wave * RPW;
-    const int32_t c0 = unit * 4;
+    const int32_t c0 = (active ? unit : 0) * 4;
     float4 v[RPW];
     float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
         const int32_t r = wr0 + i;
-        if (active && r < r1) {
+        if (r < r1) {  // wave-uniform
             v[i] = *reinterpret_cast<const float4*>(data + static_cast<size_t>(r) * N + c0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float a = fabsf(lane(v[i], j));
-                if (a > mx[j]) mx[j] = a;
-            }
+            for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], fabsf(lane(v[i], j)));
         }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[(wave * 64 + ln) * 4 + j] = mx[j];
+    for (int j = 0; j < 4; ++j) red[(wave * 4 + j) * 64 + ln] = mx[j];
     __syncthreads();
-    float scale[4], inverse[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float m = 0.0f;
-        for (int w = 0; w < waves; ++w) {
-            float a = red[(w * 64 + ln) * 4 + j];
-            if (a > m) m = a;
-        }
-        scale[j] = m > 0.0f ? m / 127.0f : 1.0f;
-        inverse[j] = 1.0f / scale[j];
-    }
-    if (!active) return;
-    if (wave == 0)
-        *reinterpret_cast<float4*>(s + static_cast<size_t>(group) * N + c0) =
-            make_float4(scale[0], scale[1], scale[2], scale[3]);
+    float* inv = red + waves * 4 * 64;  // [4][64]
     bool nan_seen = false;
+    for (int32_t c = t; c < 256; c += blockDim.x) {  // workgroup column c = 4 * lane + j
+        const int32_t cl = c >> 2, j = c & 3;
+        float m = 0.0f;
+        for (int w = 0; w < waves; ++w) m = fmaxf(m, red[(w * 4 + j) * 64 + cl]);
+        const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+        inv[j * 64 + cl] = 1.0f / scale;
+        if (cb * 64 + cl < units) s[static_cast<size_t>(group) * N + cb * 256 + c] = scale;
+    }
+    __syncthreads();
+    float inverse[4];
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int32_t r = wr0 + i;
-        if (r < r1) {
-            uint32_t packed = 0;
+    for (int j = 0; j < 4; ++j) inverse[j] = inv[j * 64 + ln];
+    if (active) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int32_t qv = clampi(java_round(lane(v[i], j) * inverse[j], nan_seen), -127, 127);
-                packed |= (static_cast<uint32_t>(qv) & 0xFFu) << (8 * j);
+        for (int i = 0; i < RPW; ++i) {
+            const int32_t r = wr0 + i;
+            if (r < r1) {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int32_t qv = clampi(java_round(lane(v[i], j) * inverse[j], nan_seen), -127, 127);
+                    packed |= (static_cast<uint32_t>(qv) & 0xFFu) << (8 * j);
+                }
+                *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(r) * N + c0) = packed;
             }
-            *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(r) * N + c0) = packed;
         }
     }
     if (nan_seen) *nan_flag = 1;
 }
 
-// INT4, 4 bytes (8 columns) per lane, RPW rows per wave.
+// INT4, 4 bytes (8 columns: 4 low-nibble, 4 high-nibble) per lane, 512 columns per
+// workgroup, RPW rows per wave.
 template <int RPW>
 __global__ void __launch_bounds__(1024) quant4_vec(const float* __restrict__ data, int32_t K, int32_t N,
                                                    int32_t g, uint8_t* __restrict__ q, float* __restrict__ s,
                                                    int8_t* __restrict__ z, int32_t* __restrict__ nan_flag) {
-    extern __shared__ float red[];  // [waves][64][16]: min lo, max lo, min hi, max hi (4 each)
-    const int32_t half = N >> 1;    // N % 8 == 0 here, so half == bytes per row
-    const int32_t ln = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const int32_t col_blocks = ceil_div(half >> 2, 64);
+    // [waves][16][64] partials (min lo, max lo, min hi, max hi, 4 each), then
+    // [8][64] inverses and [8][64] zeros (component side * 4 + j)
+    extern __shared__ float red[];
+    const int32_t half = N >> 1;  // N % 8 == 0 here, so half == bytes per row
+    const int32_t t = threadIdx.x, ln = t & 63, wave = t >> 6, waves = blockDim.x >> 6;
+    const int32_t units = half >> 2;
+    const int32_t col_blocks = ceil_div(units, 64);
     const int32_t group = blockIdx.x / col_blocks;
-    const int32_t unit = (blockIdx.x % col_blocks) * 64 + ln;
-    const bool active = unit < (half >> 2);
+    const int32_t cb = blockIdx.x % col_blocks;
+    const int32_t unit = cb * 64 + ln;
+    const bool active = unit < units;
     const int32_t r0 = group * g;
     const int32_t r1 = min(r0 + g, K);
     const int32_t wr0 = r0 + wave * RPW;
-    const int32_t b0 = unit * 4;
+    const int32_t b0 = (active ? unit : 0) * 4;
     float4 lo[RPW], hi[RPW];
     float mnl[4], mxl[4], mnh[4], mxh[4];
 #pragma unroll
@@ -147,86 +165,74 @@ __global__ void __launch_bounds__(1024) quant4_vec(const float* __restrict__ dat
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
         const int32_t r = wr0 + i;
-        if (active && r < r1) {
+        if (r < r1) {  // wave-uniform
             const float* row = data + static_cast<size_t>(r) * N;
             lo[i] = *reinterpret_cast<const float4*>(row + b0);
             hi[i] = *reinterpret_cast<const float4*>(row + half + b0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float a = lane(lo[i], j), b = lane(hi[i], j);
-                if (a < mnl[j]) mnl[j] = a;
-                if (a > mxl[j]) mxl[j] = a;
-                if (b < mnh[j]) mnh[j] = b;
-                if (b > mxh[j]) mxh[j] = b;
+                mnl[j] = fminf(mnl[j], lane(lo[i], j));
+                mxl[j] = fmaxf(mxl[j], lane(lo[i], j));
+                mnh[j] = fminf(mnh[j], lane(hi[i], j));
+                mxh[j] = fmaxf(mxh[j], lane(hi[i], j));
             }
         }
     }
-    float* mine = red + (wave * 64 + ln) * 16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        mine[j] = mnl[j];
-        mine[4 + j] = mxl[j];
-        mine[8 + j] = mnh[j];
-        mine[12 + j] = mxh[j];
+        red[(wave * 16 + j) * 64 + ln] = mnl[j];
+        red[(wave * 16 + 4 + j) * 64 + ln] = mxl[j];
+        red[(wave * 16 + 8 + j) * 64 + ln] = mnh[j];
+        red[(wave * 16 + 12 + j) * 64 + ln] = mxh[j];
     }
     __syncthreads();
-    // Min and max are exact and order-free up to the sign of a zero, which no
-    // output depends on.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    float* inv = red + waves * 16 * 64;  // [8][64]
+    int32_t* zer = reinterpret_cast<int32_t*>(inv + 8 * 64);  // [8][64]
+    bool nan_seen = false;
+    for (int32_t c = t; c < 512; c += blockDim.x) {  // side c / 256, byte 4 * lane + j
+        const int32_t side = c >> 8, cl = (c & 255) >> 2, j = c & 3;
+        float mn = FLT_MAX, mx = -FLT_MAX;
         for (int w = 0; w < waves; ++w) {
-            const float* other = red + (w * 64 + ln) * 16;
-            if (other[j] < mnl[j]) mnl[j] = other[j];
-            if (other[4 + j] > mxl[j]) mxl[j] = other[4 + j];
-            if (other[8 + j] < mnh[j]) mnh[j] = other[8 + j];
-            if (other[12 + j] > mxh[j]) mxh[j] = other[12 + j];
+            mn = fminf(mn, red[(w * 16 + side * 8 + j) * 64 + cl]);
+            mx = fmaxf(mx, red[(w * 16 + side * 8 + 4 + j) * 64 + cl]);
+        }
+        mn = mn > 0.0f ? 0.0f : mn;
+        mx = mx < 0.0f ? 0.0f : mx;
+        const float range = mx - mn;
+        const float scale = range > 0.0f ? range / 15.0f : 1.0f;
+        const int32_t zero = clampi(java_round(-mn / scale, nan_seen), 0, 15);
+        inv[(side * 4 + j) * 64 + cl] = 1.0f / scale;
+        zer[(side * 4 + j) * 64 + cl] = zero;
+        if (cb * 64 + cl < units) {
+            const size_t col = static_cast<size_t>(group) * N + (side ? half : 0) + cb * 256 + (c & 255);
+            s[col] = scale;
+            z[col] = static_cast<int8_t>(zero);
         }
     }
-    if (!active) return;
-    bool nan_seen = false;
-    float sl[4], sh[4], il[4], ih[4];
+    __syncthreads();
+    float il[4], ih[4];
     int32_t zl[4], zh[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        float mn = mnl[j] > 0.0f ? 0.0f : mnl[j];
-        float mx = mxl[j] < 0.0f ? 0.0f : mxl[j];
-        float range = mx - mn;
-        sl[j] = range > 0.0f ? range / 15.0f : 1.0f;
-        zl[j] = clampi(java_round(-mn / sl[j], nan_seen), 0, 15);
-        il[j] = 1.0f / sl[j];
-        mn = mnh[j] > 0.0f ? 0.0f : mnh[j];
-        mx = mxh[j] < 0.0f ? 0.0f : mxh[j];
-        range = mx - mn;
-        sh[j] = range > 0.0f ? range / 15.0f : 1.0f;
-        zh[j] = clampi(java_round(-mn / sh[j], nan_seen), 0, 15);
-        ih[j] = 1.0f / sh[j];
+        il[j] = inv[j * 64 + ln];
+        ih[j] = inv[(4 + j) * 64 + ln];
+        zl[j] = zer[j * 64 + ln];
+        zh[j] = zer[(4 + j) * 64 + ln];
     }
-    if (wave == 0) {
-        float* srow = s + static_cast<size_t>(group) * N;
-        *reinterpret_cast<float4*>(srow + b0) = make_float4(sl[0], sl[1], sl[2], sl[3]);
-        *reinterpret_cast<float4*>(srow + half + b0) = make_float4(sh[0], sh[1], sh[2], sh[3]);
-        int8_t* zrow = z + static_cast<size_t>(group) * N;
-        uint32_t zlp = 0, zhp = 0;
+    if (active) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            zlp |= static_cast<uint32_t>(zl[j]) << (8 * j);
-            zhp |= static_cast<uint32_t>(zh[j]) << (8 * j);
-        }
-        *reinterpret_cast<uint32_t*>(zrow + b0) = zlp;
-        *reinterpret_cast<uint32_t*>(zrow + half + b0) = zhp;
-    }
+        for (int i = 0; i < RPW; ++i) {
+            const int32_t r = wr0 + i;
+            if (r < r1) {
+                uint32_t packed = 0;
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int32_t r = wr0 + i;
-        if (r < r1) {
-            uint32_t packed = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int32_t ql = clampi(wrap_add(java_round(lane(lo[i], j) * il[j], nan_seen), zl[j]), 0, 15);
-                int32_t qh = clampi(wrap_add(java_round(lane(hi[i], j) * ih[j], nan_seen), zh[j]), 0, 15);
-                packed |= static_cast<uint32_t>(ql | (qh << 4)) << (8 * j);
+                for (int j = 0; j < 4; ++j) {
+                    const int32_t ql = clampi(wrap_add(java_round(lane(lo[i], j) * il[j], nan_seen), zl[j]), 0, 15);
+                    const int32_t qh = clampi(wrap_add(java_round(lane(hi[i], j) * ih[j], nan_seen), zh[j]), 0, 15);
+                    packed |= static_cast<uint32_t>(ql | (qh << 4)) << (8 * j);
+                }
+                *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(r) * half + b0) = packed;
             }
-            *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(r) * half + b0) = packed;
         }
     }
     if (nan_seen) *nan_flag = 1;
@@ -310,7 +316,7 @@ int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, i
         const int64_t blocks = static_cast<int64_t>(ceil_div(N / 4, 64)) * G;
         if (blocks > INT32_MAX) return fail(KT_ERR_SHAPE, "quantize: grid too large");
         const dim3 grid(static_cast<uint32_t>(blocks));
-        quant8_vec<RPW><<<grid, 64 * waves, waves * 64 * 4 * sizeof(float), st>>>(data, K, N, g, q, s, nan_flag);
+        quant8_vec<RPW><<<grid, 64 * waves, (waves + 1) * 4 * 64 * sizeof(float), st>>>(data, K, N, g, q, s, nan_flag);
         KT_LAUNCHED("quantize: int8 kernel");
         return KT_OK;
     }
@@ -320,7 +326,7 @@ int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, i
         const int64_t blocks = static_cast<int64_t>(ceil_div(N / 8, 64)) * G;
         if (blocks > INT32_MAX) return fail(KT_ERR_SHAPE, "quantize: grid too large");
         const dim3 grid(static_cast<uint32_t>(blocks));
-        quant4_vec<RPW><<<grid, 64 * waves, waves * 64 * 16 * sizeof(float), st>>>(data, K, N, g, q, s, z, nan_flag);
+        quant4_vec<RPW><<<grid, 64 * waves, (waves * 16 + 16) * 64 * sizeof(float), st>>>(data, K, N, g, q, s, z, nan_flag);
         KT_LAUNCHED("quantize: int4 kernel");
         return KT_OK;
     }

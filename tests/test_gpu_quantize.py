@@ -86,6 +86,26 @@ def test_adversarial_values_bit_exact(kt, oracle_lib, bits):
         _check(kt, oracle_lib, w, bits, g, f"adversarial_g{g}")
 
 
+def test_saturating_round_bit_exact(kt, oracle_lib):
+    """Groups of +-2^-149 values: the scale rounds to 0, the inverse is +inf, x * inverse
+    is +-inf and Math.round saturates to Int.MAX_VALUE / MIN_VALUE (INT4: the zero point
+    saturates too, and the wrapping add of the zero point decides the nibble)."""
+    rng = np.random.default_rng(11)
+    tiny = np.float32(1.4e-45)
+    for n in (64, 63):  # the vector kernels and the any-shape kernel
+        w = (rng.standard_normal((64, n)) * 0.02).astype(np.float32)
+        w[:, :24] = np.where(rng.random((64, 24)) < 0.5, -tiny, tiny).astype(np.float32)
+        w[:, 24:32] = -tiny
+        w[:, 32:40] = tiny  # INT4: min clamps to 0, so zero = round(0 / 0) is NaN: an error
+        for bits in (8, 4):
+            if bits == 4:
+                w[:, 32:40] = -tiny
+            for g in (64, 16):
+                q = _check(kt, oracle_lib, w, bits, g, f"saturate{n}")
+                assert q is not None
+                assert np.all(q.scales.reshape(-1, n)[:, :40] == 0.0)
+
+
 def test_nan_is_rejected_like_round_to_int(kt, oracle_lib):
     w = np.ones((64, 64), dtype=np.float32)
     w[5, 7] = np.nan
