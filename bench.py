@@ -35,8 +35,9 @@ The JSON line also carries:
                    decoder end to end (1024-token prefill, greedy decode steps).
                    Every timed graph reads each of its weight copies (> 2x MALL).
 
---only dominant | copy runs just the lm_head GEMV (or a 256 MB device copy, the
-calibration of the HBM byte counters) for rocprofv3 PMC runs.
+--only dominant | copy | quantize runs just the lm_head GEMV (or a 256 MB device copy,
+the calibration of the HBM byte counters, or kt_quantize INT4 g64 on 4096 x 14336) for
+rocprofv3 runs.
 """
 from __future__ import annotations
 
@@ -240,7 +241,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 8B GEMV and M=512 GEMM figures")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["dominant", "copy"], help="run one kernel for a rocprofv3 PMC run")
+    ap.add_argument("--only", choices=["dominant", "copy", "quantize"],
+                    help="run one kernel for a rocprofv3 run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -276,6 +278,23 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
                           "launches": args.steps}), flush=True)
+        return 0
+    if args.only == "quantize":
+        # kt_quantize INT4 g64 on 4096 x 14336, three distinct fp32 inputs in rotation
+        kq, nq = 4096, 14336
+        groups, bpr = layout(kq, nq, 4, 64)
+        srcs = [torch.randn((kq, nq), device="cuda", dtype=torch.float32) * 0.02 for _ in range(3)]
+        qq = torch.empty(kq * bpr, dtype=torch.uint8, device="cuda")
+        sq = torch.empty(groups * nq, dtype=torch.float32, device="cuda")
+        zq = torch.empty(groups * nq, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            kt_lib.call("kt_quantize", srcs[i % 3].data_ptr(), kq, nq, 4, 64, qq.data_ptr(), sq.data_ptr(),
+                        zq.data_ptr(), stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "quantize", "kernel": "quant4_vec 4096x14336 int4 g64",
+                          "algorithmic_bytes": 4 * kq * nq + kq * bpr + 5 * groups * nq, "launches": args.steps}),
+              flush=True)
         return 0
     w = Weight(torch, kt_lib, 896, 151936, 4, 64, seed=8, stream=stream)
     copies = [w] + [w.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // w.nbytes)) - 1)]
