@@ -41,12 +41,14 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int MAX_JOBS = 4;
 constexpr int CHUNK = 32;  // rows per MFMA k-step (4 lanes groups x 8 rows)
 constexpr int STRIP = 128; // bytes of a row per wave (16 lanes x 8 bytes)
 constexpr int NB = 4;      // chunks of weight loads in flight per wave
 constexpr int MAX_M = 2;   // x rows: three parts (and a zero row) of each take 4 A rows
+constexpr int MAX_M_ROWS = 16;  // row mode: one A row per x row
 constexpr int XB = 4;      // groups of x loaded per batch
 
 struct Job {
@@ -448,6 +450,254 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
 }
 
+// 3 <= M <= 16 x rows ("row mode"): the 16 A rows are the x rows themselves, one fp16
+// value each, scaled per (row, group) by a power of two so that the row's largest |x| in
+// the group lies in [2^14, 2^15). B is the exact fp16 integer q - zero (INT4 high
+// nibble: 16 (q - zero)), made as in the M <= 2 kernel and then reduced by the packed
+// fp16 difference with 1024 + zero (1152 + zero for INT8), which is exact; every product
+// is below 2^23 and exact in fp32, and the MFMA accumulates a group in fp32. Per group:
+// res += scale * 2^e(row) * D. The error is that of x rounded to fp16 (relative 2^-12 of
+// the row's group maximum), as in the prefill GEMM. Lane (cl, kb) keeps D rows
+// 4 kb .. 4 kb + 3 (x rows) of its own columns. An INT4 workgroup takes one nibble side
+// of its strip (eight accumulators): the two workgroups of a strip are numbered 8 apart,
+// so they run on one XCD and the second reads the strip's bytes from that XCD's L2.
+template <int BITS, int WAVES, int CPG, bool ZP>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+    gemv_rows_kernel(const float* __restrict__ x, int32_t M, int32_t K, Jobs jobs, int32_t wave_groups,
+                     float alpha, int32_t accumulate) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int g = CPG * CHUNK;
+    constexpr int NACC = 8;  // byte positions of the lane strip (one nibble side for INT4)
+    constexpr float OFF = BITS == 4 ? 1024.0f : 1152.0f;
+    static_assert(NB % CPG == 0, "a ring of NB chunks holds whole groups");
+
+    Job jb = jobs.job[blockIdx.y];
+    asm volatile("" ::"s"(jb.q), "s"(jb.s), "s"(jb.z), "s"(jb.out), "s"(jb.bias), "s"(jb.partials), "s"(jb.N),
+                 "s"(jb.bpr), "s"(jb.tiles), "s"(jb.slices), "s"(jb.groups_per_slice), "s"(x), "s"(M), "s"(K),
+                 "s"(wave_groups), "s"(alpha), "s"(accumulate));
+    const int32_t local = blockIdx.x;
+    const int32_t side = BITS == 4 ? (local >> 3) & 1 : 0;
+    const int32_t pair = BITS == 4 ? ((local >> 4) << 3) | (local & 7) : local;
+    if (pair >= jb.tiles * jb.slices) return;
+    const int32_t N = jb.N, bpr = jb.bpr, half = jb.bpr;
+    const int32_t tile = pair % jb.tiles;
+    const int32_t slice = pair / jb.tiles;
+    const int32_t G = K / g;
+    const int32_t g_begin = slice * jb.groups_per_slice;
+    const int32_t g_end = min(g_begin + jb.groups_per_slice, G);
+
+    const int32_t t = threadIdx.x;
+    const int32_t ln = t & 63;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int32_t cl = ln & 15, kb = ln >> 4;
+    const int32_t col_off = tile * STRIP + cl * 8;
+    const bool active = col_off < bpr;
+    const int32_t boff = active ? col_off : 0;  // lanes past the row end compute and discard
+
+    const int32_t my_groups = g_end - g_begin > wave ? (g_end - g_begin - wave + WAVES - 1) / WAVES : 0;
+    const int32_t my_chunks = my_groups * CPG;
+
+    // The wave's LDS area: x [wave_groups][16 rows][g] fp16, then [wave_groups][16] 2^e.
+    const int32_t xs_bytes = wave_groups * 16 * 2 * g;
+    const int32_t xw_bytes = xs_bytes + wave_groups * 16 * 4;
+    _Float16* xs = reinterpret_cast<_Float16*>(smem + wave * xw_bytes);
+    float* fw = reinterpret_cast<float*>(smem + wave * xw_bytes + xs_bytes);
+
+    int32_t col[NACC];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) col[a] = (side ? half : 0) + boff + a;
+    float res[NACC][4];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) res[a][r] = 0.0f;
+    const uint32_t mask = in_vgpr(side ? 0x00F000F0u : 0x000F000Fu);
+    const uint32_t flip = in_vgpr(0x00800080u), exp1024 = in_vgpr(0x64006400u);
+    const float zs = side ? 16.0f : 1.0f;       // the high nibble carries 16 q
+    const float ss = side ? 0.0625f : 1.0f;
+
+    if (my_groups > 0) {
+        // ---- x of this wave's groups: 16 rows (rows past M are zero) ------------------
+        constexpr int SEG = CPG >= 2 ? 64 : 32;      // lanes per group
+        constexpr int VPL = CPG >= 2 ? CPG / 2 : 1;  // x values per lane per group and row
+        constexpr int GPI = 64 / SEG;                // groups per wave instruction
+        const int32_t sub = SEG == 32 ? (ln >> 5) : 0;
+        const int32_t kk0 = ln & (SEG - 1);
+        float xv[16][VPL];
+        auto load_x = [&](int32_t k0) {
+            int32_t k = k0 + sub;
+            k = k < my_groups ? k : my_groups - 1;
+            const float* px = x + static_cast<size_t>(g_begin + wave + k * WAVES) * g + kk0;
+#pragma unroll
+            for (int m = 0; m < 16; ++m)
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) xv[m][v] = px[static_cast<size_t>(m < M ? m : 0) * K + 64 * v];
+        };
+        // Rows past M are neither prepared nor read (their A rows are zeroed at use).
+        auto prep_x = [&](int32_t k0) {
+            const int32_t k = k0 + sub;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                if (m >= M) break;  // M is wave-uniform
+                float mx = 0.0f;
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) mx = fmaxf(mx, fabsf(xv[m][v]));
+                mx = segment_reduce<SEG, true>(mx, ln);
+                int e = 0;
+                if (mx > 0.0f && mx <= 3.402823466e38f) {
+                    frexpf(mx, &e);
+                    e -= 15;
+                }
+                if (k < my_groups) {
+                    _Float16* dst = xs + (k * 16 + m) * g + kk0;
+#pragma unroll
+                    for (int v = 0; v < VPL; ++v) dst[64 * v] = static_cast<_Float16>(ldexpf(xv[m][v], -e));
+                    if (kk0 == 0) fw[k * 16 + m] = ldexpf(1.0f, e);
+                }
+            }
+        };
+        load_x(0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        uint32_t roff[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) roff[i] = static_cast<uint32_t>((8 * kb + i) * bpr + boff);
+        auto chunk_base = [&](int32_t c) {
+            const int32_t k = c / CPG, cc = c - k * CPG;
+            return jb.q + static_cast<size_t>((g_begin + wave + k * WAVES) * g + cc * CHUNK) * bpr;
+        };
+        auto load = [&](uint2* v, int32_t c) {
+            const uint8_t* base = chunk_base(c < my_chunks ? c : my_chunks - 1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint2*>(base + roff[i]);
+        };
+        uint2 buf[NB][8];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(buf[b], b);
+
+        auto load_scales = [&](int32_t k) {
+            GroupScales<NACC> sc;
+            const size_t gi = static_cast<size_t>(g_begin + wave + k * WAVES);
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                sc.s[a] = jb.s[gi * N + col[a]];
+                sc.z[a] = ZP ? static_cast<int32_t>(jb.z[gi * N + col[a]]) : 0;
+            }
+            return sc;
+        };
+        constexpr int SR = NB / CPG >= 2 ? 2 : 1;
+        GroupScales<NACC> scales[SR];
+#pragma unroll
+        for (int i = 0; i < SR; ++i) scales[i] = load_scales(i < my_groups ? i : my_groups - 1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        prep_x(0);
+        for (int32_t k0 = GPI; k0 < my_groups; k0 += GPI) {
+            load_x(k0);
+            prep_x(k0);
+        }
+
+        // ---- main loop --------------------------------------------------------------
+        f32x4 acc[NACC];
+        h2 zh[NACC];  // (OFF + zs * zero) in both halves, per column of the group
+        auto start_group = [&](const GroupScales<NACC>& gs) {
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                acc[a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                const _Float16 o = static_cast<_Float16>(OFF + zs * static_cast<float>(gs.z[a]));
+                zh[a] = h2{o, o};
+            }
+        };
+        auto compute = [&](const uint2* v, int32_t c) {
+            const int32_t k = c / CPG, cc = c - k * CPG;
+            const half8 xa = *reinterpret_cast<const half8*>(xs + (k * 16 + cl) * g + cc * CHUNK + 8 * kb);
+            const half8 a = cl < M ? xa : half8{};
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * w + jj;
+                    u32x4 bq;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t p =
+                            pair_bytes(w ? v[2 * i].y : v[2 * i].x, w ? v[2 * i + 1].y : v[2 * i + 1].x, jj);
+                        const uint32_t e = BITS == 8 ? (p ^ flip) + exp1024 : (p & mask) | exp1024;
+                        bq[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, e) - zh[j]);
+                    }
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(bq), acc[j], 0, 0, 0);
+                }
+            }
+        };
+        auto combine = [&](int32_t k, const GroupScales<NACC>& gs) {
+            const float4 f = *reinterpret_cast<const float4*>(fw + k * 16 + 4 * kb);
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) {
+                const float sc = gs.s[a] * ss;
+                res[a][0] = fmaf(sc * f.x, acc[a][0], res[a][0]);
+                res[a][1] = fmaf(sc * f.y, acc[a][1], res[a][1]);
+                res[a][2] = fmaf(sc * f.z, acc[a][2], res[a][2]);
+                res[a][3] = fmaf(sc * f.w, acc[a][3], res[a][3]);
+            }
+        };
+
+        start_group(scales[0]);
+        for (int32_t c0 = 0; c0 < my_chunks; c0 += NB) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int32_t c = c0 + b;
+                if (c < my_chunks) {
+                    compute(buf[b], c);
+                    if (b % CPG == CPG - 1) {
+                        const int32_t k = c / CPG;
+                        const int slot = (b / CPG) % SR;
+                        const int next = (slot + 1) % SR;
+                        combine(k, scales[slot]);
+                        scales[slot] = load_scales(k + SR < my_groups ? k + SR : my_groups - 1);
+                        if (k + 1 < my_groups) start_group(scales[next]);
+                    }
+                }
+                load(buf[b], c + NB);
+            }
+        }
+    }
+
+    // ---- waves of the workgroup meet in LDS (reusing the x areas), in wave order -------
+    float* red = reinterpret_cast<float*>(smem);  // [WAVES - 1][NACC][4][64 lanes]
+    __syncthreads();
+    if (wave > 0)
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(((wave - 1) * NACC + a) * 4 + r) * 64 + ln] = res[a][r];
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < WAVES; ++w)
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) res[a][r] += red[(((w - 1) * NACC + a) * 4 + r) * 64 + ln];
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int32_t row = 4 * kb + r;
+        if (row >= M) continue;
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) {
+            const int32_t n = col[a];
+            if (jb.partials) {
+                jb.partials[(static_cast<size_t>(slice) * M + row) * N + n] = res[a][r];
+            } else {
+                float* dst = jb.out + static_cast<size_t>(row) * N + n;
+                float o = accumulate ? *dst : 0.0f;
+                o = fmaf(alpha, res[a][r], o);
+                if (jb.bias) o += jb.bias[n];
+                *dst = o;
+            }
+        }
+    }
+}
+
 // Slice sums in slice order for jobs that were not reduced in the kernel.
 __global__ void __launch_bounds__(256) gemv_mfma_reduce(Jobs jobs, int32_t M, float alpha, int32_t accumulate) {
     const int32_t idx = blockIdx.x * 256 + threadIdx.x;
@@ -521,6 +771,33 @@ void launch_bits(int mp, int waves, int cpg, bool zp, dim3 grid, size_t lds, hip
     else launch_waves<BITS, 2>(waves, cpg, zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
 }
 
+template <int BITS, int WAVES, int CPG>
+void launch_rows_zp(bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M, int32_t K,
+                    const Jobs& jobs, int32_t wave_groups, float alpha, int32_t accumulate) {
+    if (BITS == 4 || zp)
+        gemv_rows_kernel<BITS, WAVES, CPG, true>
+            <<<grid, dim3(64 * WAVES), lds, st>>>(a, M, K, jobs, wave_groups, alpha, accumulate);
+    else
+        gemv_rows_kernel<BITS, WAVES, CPG, false>
+            <<<grid, dim3(64 * WAVES), lds, st>>>(a, M, K, jobs, wave_groups, alpha, accumulate);
+}
+
+template <int BITS>
+void launch_rows(int waves, int cpg, bool zp, dim3 grid, size_t lds, hipStream_t st, const float* a, int32_t M,
+                 int32_t K, const Jobs& jobs, int32_t wave_groups, float alpha, int32_t accumulate) {
+    // four waves: with eight the register budget of 2 waves per SIMD is exceeded
+    (void)waves;
+    if (cpg == 1) launch_rows_zp<BITS, 4, 1>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else if (cpg == 2) launch_rows_zp<BITS, 4, 2>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+    else launch_rows_zp<BITS, 4, 4>(zp, grid, lds, st, a, M, K, jobs, wave_groups, alpha, accumulate);
+}
+
+// LDS bytes of one quantization group of x per wave: M <= 2 keeps four fp16 parts per
+// value and row plus four floats per row; row mode keeps 16 fp16 rows plus 2^e per row.
+size_t x_group_bytes(int32_t m, int32_t g) {
+    return m > MAX_M ? static_cast<size_t>(16) * (2 * g + 4) : static_cast<size_t>(m) * (8 * g + 16);
+}
+
 }  // namespace
 
 void set_gemv_mfma_config(int32_t slices, int32_t waves, int32_t reduce, int32_t disable) {
@@ -534,7 +811,7 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
     (void)a;
     (void)c;
     if (g_forced.disable) return false;
-    if (m < 1 || m > MAX_M) return false;
+    if (m < 1 || m > MAX_M_ROWS) return false;
     if (w.g != 32 && w.g != 64 && w.g != 128) return false;  // whole 32-row chunks, up to 4 per group
     if (w.K % w.g != 0) return false;
     if (w.bpr % 8 != 0 || !aligned(w.q, 8)) return false;  // 8-byte lane strips
@@ -543,7 +820,7 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
     // lane row offsets within a chunk are 32-bit
     if (static_cast<int64_t>(CHUNK) * w.bpr >= (static_cast<int64_t>(1) << 31)) return false;
     // one x group of every row must fit a wave's LDS area
-    if (static_cast<size_t>(8) * m * (8 * w.g + 16) > LDS_X_BYTES) return false;
+    if (8 * x_group_bytes(m, w.g) > LDS_X_BYTES) return false;
     return true;
 }
 
@@ -557,17 +834,23 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
         for (int32_t i = 0; i < count; ++i)
             if (!ws[i].z) return fail(KT_ERR_ARGUMENT, "grouped weights must all have zero points or none");
 
+    // M > 2: row mode (gemv_rows_kernel); INT4 strips there take two workgroups (sides).
+    const bool rows = M > MAX_M;
+    const int32_t sides = rows && w0.bits == 4 ? 2 : 1;
     int64_t tiles_total = 0;
     for (int32_t i = 0; i < count; ++i) tiles_total += ceil_div(ws[i].bpr, STRIP);
     const int32_t target_waves = cu_count() * 8;
     // Waves per workgroup (each takes whole groups), then K-slices until the GPU is
     // covered; the x areas in LDS bound the groups of a slice.
-    int32_t waves = g_forced.waves ? g_forced.waves : 4;
-    int32_t slices = static_cast<int32_t>((target_waves + tiles_total * waves - 1) / (tiles_total * waves));
+    int32_t waves = g_forced.waves && !rows ? g_forced.waves : 4;
+    const int64_t wg_waves = tiles_total * sides * waves;
+    // row mode: as many K-slices as keep one round of workgroups (two per CU)
+    int32_t slices = rows ? static_cast<int32_t>(target_waves / wg_waves)
+                          : static_cast<int32_t>((target_waves + wg_waves - 1) / wg_waves);
     const int32_t max_slices = G / waves > 1 ? G / waves : 1;
     if (slices > max_slices) slices = max_slices;
     if (slices < 1) slices = 1;
-    const size_t per_group = static_cast<size_t>(M) * (8 * w0.g + 16);
+    const size_t per_group = x_group_bytes(M, w0.g);
     const int32_t cap_groups = static_cast<int32_t>(LDS_X_BYTES / (waves * per_group));  // per wave, >= 1
     const int32_t min_slices = ceil_div(G, cap_groups * waves);
     if (slices < min_slices) slices = min_slices;
@@ -588,9 +871,10 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
             ws_floats += static_cast<size_t>(slices) * M * ws[i].N;
             n_counters += ceil_div(ws[i].bpr, STRIP);
         }
-    bool inkernel = slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS;
+    bool inkernel = !rows && slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS;
     if (g_forced.reduce == 1) inkernel = false;
-    if (g_forced.reduce == 2 && slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS) inkernel = true;
+    if (g_forced.reduce == 2 && !rows && slices > 1 && slices <= MAX_INKERNEL_SLICES && n_counters <= MAX_COUNTERS)
+        inkernel = true;
     float* partials = nullptr;
     uint32_t* counters = nullptr;
     if (ws_floats) {
@@ -620,7 +904,9 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
         jb.counters = inkernel ? counters + coffset : nullptr;
         offset += static_cast<size_t>(slices) * M * ws[i].N;
         coffset += jb.tiles;
-        if (jb.tiles * slices > blocks) blocks = jb.tiles * slices;
+        // row mode INT4: workgroups b and b + 8 take the two sides of one (tile, slice)
+        const int32_t jb_blocks = sides == 2 ? ceil_div(jb.tiles * slices, 8) * 16 : jb.tiles * slices;
+        if (jb_blocks > blocks) blocks = jb_blocks;
         if (M * ws[i].N > widest) widest = M * ws[i].N;
     }
     // LDS: the waves' x areas; the cross-wave reduction reuses them.
@@ -629,12 +915,19 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     const int nacc = ncol / (4 / mp);
     const size_t xw = static_cast<size_t>(wave_groups) * per_group;
     const size_t lds_x = waves * xw;
-    const size_t lds_red = static_cast<size_t>(waves - 1) * nacc * 64 * sizeof(float);
+    // cross-wave sums: nacc values per lane, or (row mode) 8 columns x 4 rows
+    const size_t lds_red = static_cast<size_t>(waves - 1) * (rows ? 8 * 4 : nacc) * 64 * sizeof(float);
     const size_t lds = lds_x > lds_red ? lds_x : lds_red;
     const int cpg = w0.g / CHUNK;
     const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(count));
-    if (ws[0].bits == 4) launch_bits<4>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
-    else launch_bits<8>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+    if (rows) {
+        if (ws[0].bits == 4) launch_rows<4>(waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+        else launch_rows<8>(waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+    } else if (ws[0].bits == 4) {
+        launch_bits<4>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+    } else {
+        launch_bits<8>(mp, waves, cpg, zp, grid, lds, st, a, M, w0.K, jobs, wave_groups, alpha, accumulate);
+    }
     KT_LAUNCHED("qmatmul: mfma gemv kernel");
     if (slices > 1 && !inkernel) {
         gemv_mfma_reduce<<<ceil_div(widest, 256), 256, 0, st>>>(jobs, M, alpha, accumulate);

@@ -351,7 +351,7 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
         return launch_gemv_strip(a, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 3 || (g_gemv_kind == 0 && gemv_wide_preferred(&v, 1))) && gemv_wide_supported(a, m, v, c))
         return launch_gemv_wide(a, &v, &c, biases, 1, accumulate, alpha, st);
-    if (m <= 2 && gemv_mfma_supported(a, m, v, c)) return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
+    if (m <= 16 && gemv_mfma_supported(a, m, v, c)) return launch_gemv_mfma(a, m, &v, &c, biases, 1, accumulate, alpha, st);
     if (m == 1 && gemv_supported(a, v, c)) return launch_gemv(a, v, c, accumulate, alpha, bias, st);
     if (m > 1 && gemm_supported(a, m, v, c) && (!bias || aligned(bias, 16)))
         return launch_gemm(a, m, v, c, accumulate, alpha, bias, st);
@@ -368,7 +368,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
     for (int32_t start = 0; start < count; start += 4) {
         const int32_t n = count - start < 4 ? count - start : 4;
         bool fast = m == 1 && a != nullptr;
-        bool mfma = m >= 1 && m <= 2 && a != nullptr;
+        bool mfma = m >= 1 && m <= 16 && a != nullptr;
         bool wide = (g_gemv_kind == 0 || g_gemv_kind == 3) && a != nullptr;
         bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
         bool gemm = m > 2 && a != nullptr;

@@ -123,6 +123,23 @@ def test_llama8b_layers(kt, oracle_lib, k, n, bits):
         assert err <= TOL
 
 
+@pytest.mark.parametrize("m", [3, 4, 8, 9, 16])
+@pytest.mark.parametrize("bits,g", [(4, 64), (4, 32), (4, 128), (8, 64), (8, 32)])
+def test_row_mode_small_m(kt, oracle_lib, m, bits, g):
+    """3 <= M <= 16: one fp16 A row per x row, per-(row, group) powers of two; rows of
+    very different magnitude (and an all-zero row) keep the 2e-3 bound; accumulate and
+    alpha; strip counts that split into K-slices and the reduction kernel."""
+    rng = np.random.default_rng(100 * m + 10 * bits + g)
+    for k, n in [(512, 1024), (2048, 4096), (256, 272)]:
+        q = _weights(oracle_lib, k, n, bits, g, 3 + m, std=0.02)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x *= np.float32(10.0) ** rng.integers(-6, 6, size=(m, 1)).astype(np.float32)
+        x[m // 2] = 0.0
+        _compare(kt, oracle_lib, q, x, f"rows{k}x{n}")
+        c0 = rng.standard_normal((m, n)).astype(np.float32)
+        _compare(kt, oracle_lib, q, x, f"rows-acc{k}x{n}", c0=c0, accumulate=True, alpha=-0.5)
+
+
 def test_results_are_bit_reproducible(kt, oracle_lib):
     """Fixed-order reductions only: repeating a call gives the same bits."""
     rng = np.random.default_rng(3)
