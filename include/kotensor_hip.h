@@ -71,9 +71,10 @@ int32_t kt_set_device(int32_t device);
  * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they choose how the
  * small-M kernels split their work, never their result beyond fp32 rounding order.
  * gemv_kind: 0 = automatic (for one row the column-strip kernel up to a size and the
- *            wide-strip MFMA kernel above it, the row-block MFMA kernel for two, where the
- *            layout allows), 1 = vector-ALU kernel for M == 1, 2 = row-block MFMA kernel for
- *            M <= 2, 3 = wide-strip MFMA kernel for M == 1, 4 = column-strip kernel for M == 1;
+ *            wide-strip MFMA kernel above it, the row-block MFMA kernel for 2 to 16 rows,
+ *            where the layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA GEMV
+ *            for M > 1: those go to the GEMM), 2 = row-block MFMA kernel for M <= 16,
+ *            3 = wide-strip MFMA kernel for M == 1, 4 = column-strip kernel for M == 1;
  * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic);
  * gemv_splits: workgroups along K per column tile (0 = automatic);
  * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic);
