@@ -517,43 +517,50 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     const float ss = side ? 0.0625f : 1.0f;
 
     if (my_groups > 0) {
-        // ---- x of this wave's groups: 16 rows (rows past M are zero) ------------------
-        constexpr int SEG = CPG >= 2 ? 64 : 32;      // lanes per group
-        constexpr int VPL = CPG >= 2 ? CPG / 2 : 1;  // x values per lane per group and row
-        constexpr int GPI = 64 / SEG;                // groups per wave instruction
-        const int32_t sub = SEG == 32 ? (ln >> 5) : 0;
-        const int32_t kk0 = ln & (SEG - 1);
-        float xv[16][VPL];
-        auto load_x = [&](int32_t k0) {
-            int32_t k = k0 + sub;
+        // ---- x of this wave's groups ------------------------------------------------
+        // Lane (row xm = ln / 4, quarter xq = ln % 4) loads g / 4 consecutive values of its
+        // row's group: the row's group maximum is a quad maximum (two DPP steps), and the
+        // lane writes its fp16 values as 16-byte LDS stores. Lanes of rows past M load
+        // row 0 and store nothing: those A rows are zeroed at use.
+        constexpr int VQ = g / 4;   // values per lane: 8, 16 or 32
+        constexpr int F4 = VQ / 4;  // float4 loads per lane
+        const int32_t xm = ln >> 2, xq = ln & 3;
+        const int32_t xrow = xm < M ? xm : 0;
+        float4 xv[F4];
+        auto load_x = [&](int32_t k) {
             k = k < my_groups ? k : my_groups - 1;
-            const float* px = x + static_cast<size_t>(g_begin + wave + k * WAVES) * g + kk0;
+            const float4* px = reinterpret_cast<const float4*>(
+                x + static_cast<size_t>(xrow) * K + static_cast<size_t>(g_begin + wave + k * WAVES) * g + xq * VQ);
 #pragma unroll
-            for (int m = 0; m < 16; ++m)
-#pragma unroll
-                for (int v = 0; v < VPL; ++v) xv[m][v] = px[static_cast<size_t>(m < M ? m : 0) * K + 64 * v];
+            for (int f = 0; f < F4; ++f) xv[f] = px[f];
         };
-        // Rows past M are neither prepared nor read (their A rows are zeroed at use).
-        auto prep_x = [&](int32_t k0) {
-            const int32_t k = k0 + sub;
+        auto prep_x = [&](int32_t k) {
+            float mx = 0.0f;
 #pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                if (m >= M) break;  // M is wave-uniform
-                float mx = 0.0f;
+            for (int f = 0; f < F4; ++f)
+                mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[f].x), fabsf(xv[f].y))), fmaxf(fabsf(xv[f].z), fabsf(xv[f].w)));
+            mx = dpp_step<true>(mx, 0);  // quad [1,0,3,2]
+            mx = dpp_step<true>(mx, 1);  // quad [2,3,0,1]
+            int e = 0;
+            if (mx > 0.0f && mx <= 3.402823466e38f) {
+                frexpf(mx, &e);
+                e -= 15;
+            }
+            if (xm < M) {
+                _Float16* dst = xs + (k * 16 + xm) * g + xq * VQ;
 #pragma unroll
-                for (int v = 0; v < VPL; ++v) mx = fmaxf(mx, fabsf(xv[m][v]));
-                mx = segment_reduce<SEG, true>(mx, ln);
-                int e = 0;
-                if (mx > 0.0f && mx <= 3.402823466e38f) {
-                    frexpf(mx, &e);
-                    e -= 15;
+                for (int h = 0; h < VQ / 8; ++h) {
+                    half8 hv;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float4& q4 = xv[(8 * h + i) / 4];
+                        const int c = (8 * h + i) % 4;
+                        const float v = c == 0 ? q4.x : c == 1 ? q4.y : c == 2 ? q4.z : q4.w;
+                        hv[i] = static_cast<_Float16>(ldexpf(v, -e));
+                    }
+                    *reinterpret_cast<half8*>(dst + 8 * h) = hv;
                 }
-                if (k < my_groups) {
-                    _Float16* dst = xs + (k * 16 + m) * g + kk0;
-#pragma unroll
-                    for (int v = 0; v < VPL; ++v) dst[64 * v] = static_cast<_Float16>(ldexpf(xv[m][v], -e));
-                    if (kk0 == 0) fw[k * 16 + m] = ldexpf(1.0f, e);
-                }
+                if (xq == 0) fw[k * 16 + xm] = ldexpf(1.0f, e);
             }
         };
         load_x(0);
@@ -592,9 +599,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         __builtin_amdgcn_sched_barrier(0);
 
         prep_x(0);
-        for (int32_t k0 = GPI; k0 < my_groups; k0 += GPI) {
-            load_x(k0);
-            prep_x(k0);
+        for (int32_t k = 1; k < my_groups; ++k) {
+            load_x(k);
+            prep_x(k);
         }
 
         // ---- main loop --------------------------------------------------------------
@@ -821,6 +828,7 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
     if (static_cast<int64_t>(CHUNK) * w.bpr >= (static_cast<int64_t>(1) << 31)) return false;
     // one x group of every row must fit a wave's LDS area
     if (8 * x_group_bytes(m, w.g) > LDS_X_BYTES) return false;
+    if (m > MAX_M && !aligned(a, 16)) return false;  // row mode reads x as float4
     return true;
 }
 
