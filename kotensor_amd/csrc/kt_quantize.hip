@@ -321,12 +321,27 @@ int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, i
         return KT_OK;
     }
     if (bits == 4 && ptrs && N % 8 == 0 && g <= 16 * 8) {
-        constexpr int RPW = 8;
-        const int32_t waves = ceil_div(g, RPW);
         const int64_t blocks = static_cast<int64_t>(ceil_div(N / 8, 64)) * G;
         if (blocks > INT32_MAX) return fail(KT_ERR_SHAPE, "quantize: grid too large");
         const dim3 grid(static_cast<uint32_t>(blocks));
-        quant4_vec<RPW><<<grid, 64 * waves, (waves * 16 + 16) * 64 * sizeof(float), st>>>(data, K, N, g, q, s, z, nan_flag);
+        // four rows per wave up to g = 64 (more waves in flight per CU), eight beyond
+        if (g <= 16 * 4) {
+            const int32_t waves = ceil_div(g, 4);
+            const size_t lds = (waves * 16 + 16) * 64 * sizeof(float);  // 68 KB at 16 waves
+            if (lds > (64u << 10)) {  // beyond the default dynamic LDS limit (160 KB per CU on gfx950)
+                static bool raised = false;
+                if (!raised) {
+                    KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&quant4_vec<4>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10));
+                    raised = true;
+                }
+            }
+            quant4_vec<4><<<grid, 64 * waves, lds, st>>>(data, K, N, g, q, s, z, nan_flag);
+        } else {
+            const int32_t waves = ceil_div(g, 8);
+            quant4_vec<8><<<grid, 64 * waves, (waves * 16 + 16) * 64 * sizeof(float), st>>>(data, K, N, g, q, s, z,
+                                                                                          nan_flag);
+        }
         KT_LAUNCHED("quantize: int4 kernel");
         return KT_OK;
     }
