@@ -36,7 +36,7 @@ The JSON line also carries:
                    Every timed graph reads each of its weight copies (> 2x MALL).
 
 --only dominant | copy | quantize runs just the lm_head GEMV (or a 256 MB device copy,
-the calibration of the HBM byte counters, or kt_quantize INT4 g64 on 4096 x 14336) for
+the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64 on 4096 x 14336) for
 rocprofv3 runs.
 """
 from __future__ import annotations
@@ -280,21 +280,23 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
                           "launches": args.steps}), flush=True)
         return 0
     if args.only == "quantize":
-        # kt_quantize INT4 g64 on 4096 x 14336, three distinct fp32 inputs in rotation
+        # kt_quantize INT4 then INT8, g64, on 4096 x 14336, three distinct fp32 inputs in rotation
         kq, nq = 4096, 14336
-        groups, bpr = layout(kq, nq, 4, 64)
         srcs = [torch.randn((kq, nq), device="cuda", dtype=torch.float32) * 0.02 for _ in range(3)]
-        qq = torch.empty(kq * bpr, dtype=torch.uint8, device="cuda")
-        sq = torch.empty(groups * nq, dtype=torch.float32, device="cuda")
-        zq = torch.empty(groups * nq, dtype=torch.uint8, device="cuda")
-        torch.cuda.synchronize()
-        for i in range(args.steps):
-            kt_lib.call("kt_quantize", srcs[i % 3].data_ptr(), kq, nq, 4, 64, qq.data_ptr(), sq.data_ptr(),
-                        zq.data_ptr(), stream)
-        torch.cuda.synchronize()
-        print(json.dumps({"only": "quantize", "kernel": "quant4_vec 4096x14336 int4 g64",
-                          "algorithmic_bytes": 4 * kq * nq + kq * bpr + 5 * groups * nq, "launches": args.steps}),
-              flush=True)
+        done = {}
+        for bits in (4, 8):
+            groups, bpr = layout(kq, nq, bits, 64)
+            qq = torch.empty(kq * bpr, dtype=torch.uint8, device="cuda")
+            sq = torch.empty(groups * nq, dtype=torch.float32, device="cuda")
+            zq = torch.empty(groups * nq, dtype=torch.uint8, device="cuda") if bits == 4 else None
+            torch.cuda.synchronize()
+            for i in range(args.steps):
+                kt_lib.call("kt_quantize", srcs[i % 3].data_ptr(), kq, nq, bits, 64, qq.data_ptr(), sq.data_ptr(),
+                            zq.data_ptr() if zq is not None else None, stream)
+            torch.cuda.synchronize()
+            done[f"int{bits}"] = 4 * kq * nq + kq * bpr + (5 if bits == 4 else 4) * groups * nq
+        print(json.dumps({"only": "quantize", "kernel": "quant4_vec, quant8_vec 4096x14336 g64",
+                          "algorithmic_bytes": done, "launches_each": args.steps}), flush=True)
         return 0
     w = Weight(torch, kt_lib, 896, 151936, 4, 64, seed=8, stream=stream)
     copies = [w] + [w.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // w.nbytes)) - 1)]

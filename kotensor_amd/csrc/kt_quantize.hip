@@ -311,12 +311,17 @@ int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, i
     const int32_t bpr = bits == 4 ? (N + N % 2) / 2 : N;
     const bool ptrs = aligned(data, 16) && aligned(q, 4) && aligned(s, 16) && (!z || aligned(z, 4));
     if (bits == 8 && ptrs && N % 4 == 0 && g <= 16 * 16) {
-        constexpr int RPW = 16;
-        const int32_t waves = ceil_div(g, RPW);
         const int64_t blocks = static_cast<int64_t>(ceil_div(N / 4, 64)) * G;
         if (blocks > INT32_MAX) return fail(KT_ERR_SHAPE, "quantize: grid too large");
         const dim3 grid(static_cast<uint32_t>(blocks));
-        quant8_vec<RPW><<<grid, 64 * waves, (waves + 1) * 4 * 64 * sizeof(float), st>>>(data, K, N, g, q, s, nan_flag);
+        // eight rows per wave up to g = 128 (more waves in flight per CU), sixteen beyond
+        if (g <= 16 * 8) {
+            const int32_t waves = ceil_div(g, 8);
+            quant8_vec<8><<<grid, 64 * waves, (waves + 1) * 4 * 64 * sizeof(float), st>>>(data, K, N, g, q, s, nan_flag);
+        } else {
+            const int32_t waves = ceil_div(g, 16);
+            quant8_vec<16><<<grid, 64 * waves, (waves + 1) * 4 * 64 * sizeof(float), st>>>(data, K, N, g, q, s, nan_flag);
+        }
         KT_LAUNCHED("quantize: int8 kernel");
         return KT_OK;
     }
