@@ -852,11 +852,20 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     // covered; the x areas in LDS bound the groups of a slice.
     int32_t waves = g_forced.waves && !rows ? g_forced.waves : 4;
     const int64_t wg_waves = tiles_total * sides * waves;
-    // row mode: as many K-slices as keep one round of workgroups (two per CU)
-    int32_t slices = rows ? static_cast<int32_t>(target_waves / wg_waves)
-                          : static_cast<int32_t>((target_waves + wg_waves - 1) / wg_waves);
-    const int32_t max_slices = G / waves > 1 ? G / waves : 1;
-    if (slices > max_slices) slices = max_slices;
+    int32_t slices;
+    if (rows) {
+        // About one workgroup per CU, at least four K-slices, at most one group per slice
+        // (measured on MI355X: 4096 x 4096 INT4 11.9 us at 8 slices against 13.1 at 16,
+        // 896 x 4864 9.6 at 6 against 10.9 at 3; the 4096 x 14336 gate/up is best at 4).
+        slices = static_cast<int32_t>(cu_count() / (tiles_total * sides));
+        if (slices < 4) slices = 4;
+        if (slices > 16) slices = 16;  // the most measured; 4096 -> 1024 INT4 is best there
+        if (slices > G) slices = G;
+    } else {
+        slices = static_cast<int32_t>((target_waves + wg_waves - 1) / wg_waves);
+        const int32_t max_slices = G / waves > 1 ? G / waves : 1;
+        if (slices > max_slices) slices = max_slices;
+    }
     if (slices < 1) slices = 1;
     const size_t per_group = x_group_bytes(M, w0.g);
     const int32_t cap_groups = static_cast<int32_t>(LDS_X_BYTES / (waves * per_group));  // per wave, >= 1
@@ -866,7 +875,7 @@ int32_t launch_gemv_mfma(const float* a, int32_t M, const WeightView* ws, float*
     if (slices > G) slices = G;
     constexpr int32_t MAX_INKERNEL_SLICES = 8;
     // A few more slices than the in-kernel limit buy less than the reduction kernel costs.
-    if (!g_forced.slices && slices > MAX_INKERNEL_SLICES && slices < 2 * MAX_INKERNEL_SLICES &&
+    if (!rows && !g_forced.slices && slices > MAX_INKERNEL_SLICES && slices < 2 * MAX_INKERNEL_SLICES &&
         min_slices <= MAX_INKERNEL_SLICES)
         slices = MAX_INKERNEL_SLICES;
     // Every slice takes gps whole groups; the last may take fewer.
