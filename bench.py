@@ -35,9 +35,9 @@ The JSON line also carries:
                    decoder end to end (1024-token prefill, greedy decode steps).
                    Every timed graph reads each of its weight copies (> 2x MALL).
 
---only dominant | copy | quantize runs just the lm_head GEMV (or a 256 MB device copy,
-the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64 on 4096 x 14336) for
-rocprofv3 runs.
+--only dominant | copy | quantize | gemm runs just the lm_head GEMV (or a 256 MB device
+copy, the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64 on
+4096 x 14336, or the INT8 g32 M = 512 GEMM on 2048 -> 8192) for rocprofv3 runs.
 """
 from __future__ import annotations
 
@@ -241,7 +241,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 8B GEMV and M=512 GEMM figures")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["dominant", "copy", "quantize"],
+    ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm"],
                     help="run one kernel for a rocprofv3 run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -297,6 +297,19 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
             done[f"int{bits}"] = 4 * kq * nq + kq * bpr + (5 if bits == 4 else 4) * groups * nq
         print(json.dumps({"only": "quantize", "kernel": "quant4_vec, quant8_vec 4096x14336 g64",
                           "algorithmic_bytes": done, "launches_each": args.steps}), flush=True)
+        return 0
+    if args.only == "gemm":
+        # the INT8 g32 prefill GEMM at M = 512 on 2048 -> 8192, weight copies in rotation
+        wg = Weight(torch, kt_lib, 2048, 8192, 8, 32, seed=9, stream=stream)
+        cg = [wg] + [wg.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // wg.nbytes)) - 1)]
+        xg = torch.randn((512, 2048), device="cuda", dtype=torch.float32)
+        yg = torch.empty((512, 8192), device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            qmatmul(kt_lib, xg, 512, cg[i % len(cg)], yg, stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "gemm", "kernel": "gemm_kernel int8 g32 M=512 2048x8192",
+                          "flops": 2 * 512 * 2048 * 8192, "launches": args.steps}), flush=True)
         return 0
     w = Weight(torch, kt_lib, 896, 151936, 4, 64, seed=8, stream=stream)
     copies = [w] + [w.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // w.nbytes)) - 1)]
