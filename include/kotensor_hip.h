@@ -12,10 +12,11 @@
  *     The library keeps one internal workspace per (device, stream); calls that
  *     share a stream are ordered by it, calls on different streams never share one.
  *   - Return value: KT_OK (0) on success; a negative KT_ERR_* for an argument error
- *     (the reference raises IllegalArgumentException for the same cases); a positive
- *     value is a HIP runtime error code (the reference has no counterpart; a binding
- *     maps it to IllegalStateException). kt_last_error() returns the message of the
- *     last failure on the calling thread.
+ *     (the reference raises IllegalArgumentException for the same cases) except
+ *     KT_ERR_STATE; a positive value is a HIP runtime error code (the reference has no
+ *     counterpart). A binding maps KT_ERR_STATE and positive values to
+ *     IllegalStateException. kt_last_error() returns the message of the last failure
+ *     on the calling thread.
  *
  * Weight layout is the reference's, consumed without repacking:
  *   qdata  [rows x bytes_per_row], row-major. 8-bit: bytes_per_row = columns, each
@@ -47,6 +48,9 @@ extern "C" {
 #define KT_ERR_NAN (-3)        /* quantize met a value Float.roundToInt() rejects */
 #define KT_ERR_ZEROS (-4)      /* 4-bit tensor without zero points (K/QuantizedTensor.kt:69) */
 #define KT_ERR_RANGE (-5)      /* index out of range (row / column / token) */
+#define KT_ERR_STATE (-6)      /* not possible in the current state: a binding maps it to
+                                  IllegalStateException (e.g. a recorded call whose stream
+                                  has no workspace of the size it needs yet) */
 
 /* A quantized weight held in device memory. Mirrors the fields of
  * QuantizedTensor (K/QuantizedTensor.kt:27-49): rows = K (in), columns = N (out). */
@@ -96,7 +100,14 @@ int32_t kt_stream_sync(void* stream);
 /* HIP graphs: kernels enqueued on `stream` between kt_graph_begin and kt_graph_end are
  * recorded (not run) and instantiated into *graph, which kt_graph_launch replays on a
  * stream. The replacement for a tracing compiler on the decode path: one decode step
- * is recorded once and replayed per token. No counterpart in the reference. */
+ * is recorded once and replayed per token. No counterpart in the reference.
+ * Workspace rules: a recorded call uses the workspace of the stream it was recorded
+ * on, which must already be large enough (one eager call of the same shapes on that
+ * stream sizes it); otherwise the call returns KT_ERR_STATE and nothing is allocated
+ * or recorded for it. A workspace that a graph addresses is never freed before the
+ * process ends, even when a later call grows it or the stream is destroyed. Replays
+ * and eager calls that share a workspace must not run concurrently: replay a graph on
+ * the stream it was recorded on, or keep that stream idle during the replay. */
 int32_t kt_graph_begin(void* stream);
 int32_t kt_graph_end(void* stream, void** graph);
 int32_t kt_graph_launch(void* graph, void* stream);
@@ -160,7 +171,7 @@ int32_t kt_qmatmul_transposed(const float* dy, int32_t m, const kt_qweight* w, f
 /* dequantizeRow for each index in rows[0..count) (device int32 array), writing
  * out[i x N]; the row gather of QuantizedEmbedding.lookupInto/forward
  * (K/Embedding.kt:73-113 -> K/QuantizedTensor.kt:188-213). Indices outside
- * [0, rows) are not checked on the device; pass validated indices. */
+ * [0, rows) yield rows of NaN (kotensor_amd checks indices on the host first). */
 int32_t kt_dequantize_rows(const kt_qweight* w, const int32_t* rows, int32_t count, float* out,
                            void* stream);
 /* dequantizeColumn for each index in columns[0..count), writing out[i x K]; the

@@ -3,7 +3,7 @@
 This is the Python counterpart of the JDK Foreign Function & Memory downcalls a
 Kotlin host makes: every entry point takes plain pointers and sizes and returns an
 int32 status. A negative status raises :class:`IllegalArgumentException`, a
-positive (HIP runtime) status :class:`IllegalStateException`, mirroring the
+positive (HIP runtime) status or KT_ERR_STATE :class:`IllegalStateException`, mirroring the
 reference's ``require`` / ``check`` failures.
 
 The library is loaded from the package directory and never replaced by anything
@@ -48,6 +48,7 @@ KT_ERR_SHAPE = -2
 KT_ERR_NAN = -3
 KT_ERR_ZEROS = -4
 KT_ERR_RANGE = -5
+KT_ERR_STATE = -6
 
 
 class _QWeight(ctypes.Structure):
@@ -185,7 +186,7 @@ def check(status: int, what: str = "") -> None:
     if status == KT_OK:
         return
     message = last_error() or what
-    if status < 0:
+    if status < 0 and status != KT_ERR_STATE:
         raise IllegalArgumentException(message, status)
     raise IllegalStateException(message, status)
 

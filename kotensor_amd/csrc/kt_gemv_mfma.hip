@@ -48,7 +48,7 @@ constexpr int CHUNK = 32;  // rows per MFMA k-step (4 lanes groups x 8 rows)
 constexpr int STRIP = 128; // bytes of a row per wave (16 lanes x 8 bytes)
 constexpr int NB = 4;      // chunks of weight loads in flight per wave
 constexpr int MAX_M = 2;   // x rows: three parts (and a zero row) of each take 4 A rows
-constexpr int MAX_M_ROWS = 16;  // row mode: one A row per x row
+constexpr int MAX_M_ROWS = 16;  // row mode: one A row per x row (in each of two MFMAs)
 constexpr int XB = 4;      // groups of x loaded per batch
 
 struct Job {
@@ -450,14 +450,18 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
 }
 
-// 3 <= M <= 16 x rows ("row mode"): the 16 A rows are the x rows themselves, one fp16
-// value each, scaled per (row, group) by a power of two so that the row's largest |x| in
-// the group lies in [2^14, 2^15). B is the exact fp16 integer q - zero (INT4 high
-// nibble: 16 (q - zero)), made as in the M <= 2 kernel and then reduced by the packed
-// fp16 difference with 1024 + zero (1152 + zero for INT8), which is exact; every product
-// is below 2^23 and exact in fp32, and the MFMA accumulates a group in fp32. Per group:
-// res += scale * 2^e(row) * D. The error is that of x rounded to fp16 (relative 2^-12 of
-// the row's group maximum), as in the prefill GEMM. Lane (cl, kb) keeps D rows
+// 3 <= M <= 16 x rows ("row mode"): the 16 A rows are the x rows themselves, scaled per
+// (row, group) by a power of two so that the row's largest |x| in the group lies in
+// [2^14, 2^15), and each value is split into fp16 hi = fp16(x) and lo = fp16(x - hi);
+// two MFMAs (hi rows, then lo rows) share one accumulator. B is the exact fp16 integer
+// q - zero (INT4 high nibble: 16 (q - zero)), made as in the M <= 2 kernel and then
+// reduced by the packed fp16 difference with 1024 + zero (1152 + zero for INT8), which is
+// exact; every product is exact in fp32, and the MFMA accumulates a group in fp32. Per
+// group: res += scale * 2^e(row) * D. The error is that of x held to 22 significant bits
+// (relative 2^-22 of each value) plus fp32 accumulation, so a row's result does not
+// depend on the row count beyond fp32 rounding (the reference's rows do not: its tile
+// kernel gives every row the single-row result, QuantizationTest.kt:110-134); the kernel
+// is HBM-bound, so the second MFMA costs issue slots only. Lane (cl, kb) keeps D rows
 // 4 kb .. 4 kb + 3 (x rows) of its own columns. An INT4 workgroup takes one nibble side
 // of its strip (eight accumulators): the two workgroups of a strip are numbered 8 apart,
 // so they run on one XCD and the second reads the strip's bytes from that XCD's L2.
@@ -497,8 +501,8 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     const int32_t my_groups = g_end - g_begin > wave ? (g_end - g_begin - wave + WAVES - 1) / WAVES : 0;
     const int32_t my_chunks = my_groups * CPG;
 
-    // The wave's LDS area: x [wave_groups][16 rows][g] fp16, then [wave_groups][16] 2^e.
-    const int32_t xs_bytes = wave_groups * 16 * 2 * g;
+    // The wave's LDS area: x [wave_groups][hi, lo][16 rows][g] fp16, then [wave_groups][16] 2^e.
+    const int32_t xs_bytes = wave_groups * 2 * 16 * 2 * g;
     const int32_t xw_bytes = xs_bytes + wave_groups * 16 * 4;
     _Float16* xs = reinterpret_cast<_Float16*>(smem + wave * xw_bytes);
     float* fw = reinterpret_cast<float*>(smem + wave * xw_bytes + xs_bytes);
@@ -547,18 +551,22 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
                 e -= 15;
             }
             if (xm < M) {
-                _Float16* dst = xs + (k * 16 + xm) * g + xq * VQ;
+                // hi = fp16(x 2^-e), lo = fp16(x 2^-e - hi): 22 significant bits of every
+                // value, so a row's result does not depend on how many rows share the call
+                _Float16* dst = xs + (k * 32 + xm) * g + xq * VQ;
 #pragma unroll
                 for (int h = 0; h < VQ / 8; ++h) {
-                    half8 hv;
+                    half8 hv, lv;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const float4& q4 = xv[(8 * h + i) / 4];
                         const int c = (8 * h + i) % 4;
-                        const float v = c == 0 ? q4.x : c == 1 ? q4.y : c == 2 ? q4.z : q4.w;
-                        hv[i] = static_cast<_Float16>(ldexpf(v, -e));
+                        const float v = ldexpf(c == 0 ? q4.x : c == 1 ? q4.y : c == 2 ? q4.z : q4.w, -e);
+                        hv[i] = static_cast<_Float16>(v);
+                        lv[i] = static_cast<_Float16>(v - static_cast<float>(hv[i]));
                     }
                     *reinterpret_cast<half8*>(dst + 8 * h) = hv;
+                    *reinterpret_cast<half8*>(dst + 16 * g + 8 * h) = lv;
                 }
                 if (xq == 0) fw[k * 16 + xm] = ldexpf(1.0f, e);
             }
@@ -617,8 +625,11 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         };
         auto compute = [&](const uint2* v, int32_t c) {
             const int32_t k = c / CPG, cc = c - k * CPG;
-            const half8 xa = *reinterpret_cast<const half8*>(xs + (k * 16 + cl) * g + cc * CHUNK + 8 * kb);
+            const _Float16* pa = xs + (k * 32 + cl) * g + cc * CHUNK + 8 * kb;
+            const half8 xa = *reinterpret_cast<const half8*>(pa);
+            const half8 xl = *reinterpret_cast<const half8*>(pa + 16 * g);
             const half8 a = cl < M ? xa : half8{};
+            const half8 al = cl < M ? xl : half8{};
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
 #pragma unroll
@@ -633,6 +644,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
                         bq[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, e) - zh[j]);
                     }
                     acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(bq), acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, as_half8(bq), acc[j], 0, 0, 0);
                 }
             }
         };
@@ -800,9 +812,10 @@ void launch_rows(int waves, int cpg, bool zp, dim3 grid, size_t lds, hipStream_t
 }
 
 // LDS bytes of one quantization group of x per wave: M <= 2 keeps four fp16 parts per
-// value and row plus four floats per row; row mode keeps 16 fp16 rows plus 2^e per row.
+// value and row plus four floats per row; row mode keeps 16 rows of fp16 hi and lo parts
+// plus 2^e per row.
 size_t x_group_bytes(int32_t m, int32_t g) {
-    return m > MAX_M ? static_cast<size_t>(16) * (2 * g + 4) : static_cast<size_t>(m) * (8 * g + 16);
+    return m > MAX_M ? static_cast<size_t>(16) * (4 * g + 4) : static_cast<size_t>(m) * (8 * g + 16);
 }
 
 }  // namespace
@@ -826,8 +839,8 @@ bool gemv_mfma_supported(const float* a, int32_t m, const WeightView& w, const f
     if (w.bits == 4 && w.N % 16 != 0) return false;        // high-nibble columns start 8-aligned
     // lane row offsets within a chunk are 32-bit
     if (static_cast<int64_t>(CHUNK) * w.bpr >= (static_cast<int64_t>(1) << 31)) return false;
-    // one x group of every row must fit a wave's LDS area
-    if (8 * x_group_bytes(m, w.g) > LDS_X_BYTES) return false;
+    // one x group of every row must fit a wave's LDS area (row mode runs four waves)
+    if ((m > MAX_M ? 4 : 8) * x_group_bytes(m, w.g) > LDS_X_BYTES) return false;
     if (m > MAX_M && !aligned(a, 16)) return false;  // row mode reads x as float4
     return true;
 }

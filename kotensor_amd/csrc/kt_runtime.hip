@@ -7,6 +7,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "kt_common.h"
 
@@ -31,11 +32,17 @@ int32_t hip_fail(hipError_t err, const char* what) {
 namespace {
 struct Block {
     void* ptr = nullptr;
-    size_t bytes = 0;   // whole allocation
-    size_t zbytes = 0;  // the zeroed accumulator region after the counters
+    size_t bytes = 0;       // whole allocation
+    size_t zbytes = 0;      // the zeroed accumulator region after the counters
+    bool captured = false;  // handed to a kernel recorded into a graph
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Block> g_ws;
+// Blocks replaced or orphaned while a recorded graph may still address them. A graph
+// keeps the addresses it was recorded with, and graphs can outlive their stream, so
+// these stay allocated until the process ends (each is smaller than its successor, so
+// together they are bounded by a few times the largest workspace of the stream).
+std::vector<void*> g_retired;
 std::map<int, int32_t> g_cus;
 }  // namespace
 
@@ -47,17 +54,26 @@ constexpr size_t COUNTER_BYTES = 64 << 10;
 static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** out) {
     int device = 0;
     KT_HIP(hipGetDevice(&device));
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    KT_HIP(hipStreamIsCapturing(stream, &capture));
+    const bool capturing = capture != hipStreamCaptureStatusNone;
     Block& b = g_ws[std::make_pair(device, stream)];
     const size_t zcap = zbytes > b.zbytes ? zbytes + zbytes / 4 : b.zbytes;
     if (zbytes > b.zbytes || b.bytes < COUNTER_BYTES + zcap + bytes) {
+        // Growing needs an allocation and a zero fill, neither of which may be recorded:
+        // a graph gets the workspace an eager call of the same shapes has sized.
+        if (capturing)
+            return fail(KT_ERR_STATE,
+                        "the stream is capturing and its workspace is too small (needs %zu bytes, has %zu); "
+                        "run one eager call of the same shapes on this stream before recording",
+                        COUNTER_BYTES + zcap + bytes, b.bytes);
         const size_t need = COUNTER_BYTES + zcap + bytes;
         size_t want = need < (size_t(1) << 20) ? (size_t(1) << 20) : need + need / 4;
         if (b.ptr) {
             KT_HIP(hipStreamSynchronize(stream));
-            KT_HIP(hipFree(b.ptr));
-            b.ptr = nullptr;
-            b.bytes = 0;
-            b.zbytes = 0;
+            if (b.captured) g_retired.push_back(b.ptr);  // a graph may still address it
+            else KT_HIP(hipFree(b.ptr));
+            b = Block{};
         }
         KT_HIP(hipMalloc(&b.ptr, want));
         KT_HIP(hipMemsetAsync(b.ptr, 0, COUNTER_BYTES + zcap, stream));
@@ -65,6 +81,7 @@ static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** o
         b.bytes = want;
         b.zbytes = zcap;
     }
+    if (capturing) b.captured = true;
     *out = &b;
     return KT_OK;
 }
@@ -250,7 +267,9 @@ int32_t kt_stream_destroy(void* stream) {
         std::lock_guard<std::mutex> lock(g_ws_mutex);
         auto it = g_ws.find(std::make_pair(device, s));
         if (it != g_ws.end()) {
-            if (it->second.ptr) KT_HIP(hipFree(it->second.ptr));
+            // A graph recorded on this stream may be replayed on another one later.
+            if (it->second.ptr && it->second.captured) g_retired.push_back(it->second.ptr);
+            else if (it->second.ptr) KT_HIP(hipFree(it->second.ptr));
             g_ws.erase(it);
         }
     }

@@ -374,7 +374,9 @@ int32_t kt_st_open(const char* path, kt_st_file** file) {
             close_file(f);
             return fail(KT_ERR_ARGUMENT, "Tensor %s has no data_offsets", name.c_str());
         }
-        if (!(e.end >= e.start && e.start >= 0 && f->data_start + e.end <= static_cast<int64_t>(f->size))) {
+        // data_start <= size holds (checked above), so the right side cannot overflow; an
+        // end near INT64_MAX must not wrap into a small sum.
+        if (!(e.end >= e.start && e.start >= 0 && e.end <= static_cast<int64_t>(f->size) - f->data_start)) {
             const long long s = e.start, en = e.end, sz = static_cast<long long>(f->size);
             close_file(f);
             return fail(KT_ERR_ARGUMENT, "Tensor %s data range [%lld, %lld) exceeds file %lld", name.c_str(), s, en, sz);

@@ -558,11 +558,15 @@ class Transformer:
         if not st:
             raise _lib.IllegalArgumentException("the null stream cannot be captured; create a stream")
         _lib.call("kt_graph_begin", st)
+        graph = ctypes.c_void_p()
         try:
             self._decode_step(cache, buffers, st, argmax=True)
-        finally:
-            graph = ctypes.c_void_p()
-            _lib.call("kt_graph_end", st, ctypes.byref(graph))
+        except BaseException:
+            # end the capture so the stream is usable again, and drop the partial graph
+            if _lib.lib().kt_graph_end(st, ctypes.byref(graph)) == _lib.KT_OK and graph:
+                _lib.lib().kt_graph_destroy(graph)
+            raise
+        _lib.call("kt_graph_end", st, ctypes.byref(graph))
         return DecodeGraph(graph, cache, stream)
 
     def generate(self, prompt, max_tokens: int, stop_tokens=(), stream: Stream | None = None,

@@ -21,6 +21,13 @@ Embedding.kt:130-135). Pinning: the pieces are pinned in tests/test_oracle_decod
 the orchestration is checked there against the reference's own consistency properties
 (prefill across chunk boundaries equals one-token decoding; a continued prefill equals
 one long prefill; generate equals argmax of teacher-forced decoding).
+
+dense=True replaces the two costly pieces with brute force for models whose restated
+loops would take minutes (the 1B decoder over a 1024-token prompt): every projection is
+x . W with W the fully dequantized fp32 weight (value(r, c) of every element, the same
+numbers the reference's kernels multiply) through numpy's BLAS, and the cached attention
+is the same softmax over the same keys in float64. Each differs from the restated loops
+by summation order only; tests/test_oracle_decoder.py bounds the difference.
 """
 from __future__ import annotations
 
@@ -31,6 +38,27 @@ import numpy as np
 import oracle
 
 TILE_M = 32  # MatMul.TILE_M (MatMul.kt:16): the prefill chunk
+
+
+def attend_dense(q: np.ndarray, start: int, keys: np.ndarray, values: np.ndarray, layer: int, num_heads: int,
+                 num_kv_heads: int, head_dim: int, max_seq: int) -> np.ndarray:
+    """attendCached (Attention.kt:277-349) as oracle.attend computes it -- token t at
+    position start + t attends to cached positions 0..start + t of the kv head of its
+    query head, softmax of q . k / sqrt(head_dim), times v -- in float64 matrix form."""
+    tokens = q.shape[0]
+    group = num_heads // num_kv_heads
+    kv = keys.reshape(-1, num_kv_heads, max_seq, head_dim)[layer, :, :start + tokens].astype(np.float64)
+    vv = values.reshape(-1, num_kv_heads, max_seq, head_dim)[layer, :, :start + tokens].astype(np.float64)
+    qh = q.reshape(tokens, num_heads, head_dim).astype(np.float64)
+    scale = np.float64(np.float32(1.0) / np.float32(np.sqrt(np.float64(np.float32(head_dim)))))
+    visible = np.arange(start + tokens)[None, :] <= (start + np.arange(tokens))[:, None]
+    out = np.empty((tokens, num_heads, head_dim), dtype=np.float64)
+    for h in range(num_heads):
+        s = (qh[:, h] @ kv[h // group].T) * scale
+        s = np.where(visible, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ vv[h // group]
+    return out.reshape(tokens, num_heads * head_dim).astype(np.float32)
 
 
 @dataclass
@@ -70,7 +98,9 @@ class RefTransformer:
     norms: dict      # name -> fp32 [dimension] ("block.l.norm1", "block.l.norm2", "finalNorm")
     tied: bool = False
     biases: dict = field(default_factory=dict)  # name -> fp32 [out]; QuantizedLinear.bias (QuantizedLinear.kt:16-25)
+    dense: bool = False  # brute-force projections and attention (see the module docstring)
     inv_freq: np.ndarray = field(init=False)
+    _dense_weights: dict = field(init=False, default_factory=dict)
 
     def __post_init__(self):
         c = self.config
@@ -84,7 +114,13 @@ class RefTransformer:
     # -- pieces ----------------------------------------------------------------------
     def _project(self, x: np.ndarray, name: str) -> np.ndarray:
         """QuantizedLinear.forwardInto: the product, then += bias."""
-        out = oracle.multiply_quantized(x, self.quantized[name], x.shape[0], threads=16)
+        if self.dense:
+            w = self._dense_weights.get(name)
+            if w is None:
+                w = self._dense_weights[name] = self.quantized[name].dequantize()
+            out = np.matmul(x.astype(np.float32), w)
+        else:
+            out = oracle.multiply_quantized(x, self.quantized[name], x.shape[0], threads=16)
         if name in self.biases:
             out = (out + self.biases[name][None, :]).astype(np.float32)
         return out
@@ -114,7 +150,10 @@ class RefTransformer:
                 off = ((layer * kvh + h) * ms + start + t) * hd
                 cache.keys[off:off + hd] = k[t, h * hd:(h + 1) * hd]
                 cache.values[off:off + hd] = v[t, h * hd:(h + 1) * hd]
-        context = oracle.attend(q, start, cache.keys, cache.values, layer, c.num_heads, kvh, hd, ms)
+        if self.dense:
+            context = attend_dense(q, start, cache.keys, cache.values, layer, c.num_heads, kvh, hd, ms)
+        else:
+            context = oracle.attend(q, start, cache.keys, cache.values, layer, c.num_heads, kvh, hd, ms)
         x = (x + self._project(context, p + "attention.wOut")).astype(np.float32)
         normed = oracle.rmsnorm(x, self.norms[p + "norm2"], c.norm_eps)
         gate = self._project(normed, p + "ffn.wGate")

@@ -439,6 +439,60 @@ def test_generate_matches_teacher_forced_argmax_and_graph_replays_agree(kt, orac
         assert stopped == eager[:eager.index(stop, 45)]
 
 
+def test_recorded_decode_survives_a_workspace_that_grows(kt):
+    """A decode step recorded as a graph keeps working after a longer prefill on the same
+    stream has grown that stream's workspace (the graph still addresses the old block,
+    which the library keeps), and its tokens and logits equal eager decoding's. A
+    recording on a stream whose workspace was never sized raises IllegalStateException
+    and leaves the stream usable."""
+    model = kt.Transformer(2048, 512, 2, 8, 1536, 2, norm_eps=1e-5, rope_theta=10000.0,
+                           quantization=kt.Quantization.INT4, seed=5)
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, model.vocabulary_size, 5).tolist()
+    long_prompt = rng.integers(0, model.vocabulary_size, 2048).tolist()
+    steps = 6
+
+    banner("graph workspace: eager reference")
+    eager_stream = kt.Stream.create()
+    cache, buffers = model.new_cache(16, eager_stream), model.new_inference_buffers(16)
+    model.prefill(prompt, cache, buffers, eager_stream)
+    want = model.greedy_decode(cache, buffers, steps, eager_stream, use_graph=False)
+    want_logits = buffers.logits_numpy()
+    eager_stream.destroy()
+
+    banner("graph workspace: record, grow, replay")
+    stream = kt.Stream.create()
+    cache, buffers = model.new_cache(16, stream), model.new_inference_buffers(16)
+    model.prefill(prompt, cache, buffers, stream)
+    from kotensor_amd import _lib
+    first = cache.length
+    _lib.call("kt_argmax", buffers.logits.ptr, model.vocabulary_size, buffers.tokens.ptr, stream.handle)
+    _lib.call("kt_record_token", buffers.tokens.ptr, cache.position.ptr, buffers.generated.ptr,
+              buffers.max_sequence_length, stream.handle)
+    model.decode_step(cache, buffers, stream)  # sizes the decode step's workspace
+    graph = model.capture_decode(cache, buffers, stream)
+    big_cache, big_buffers = model.new_cache(2048, stream), model.new_inference_buffers(2048)
+    model.prefill(long_prompt, big_cache, big_buffers, stream)  # grows this stream's workspace
+    graph.replay(steps - 1)
+    stream.synchronize()
+    got = buffers.generated.download(np.int32, count=steps + 1, offset=4 * first).tolist()
+    graph.destroy()
+    assert got == want
+    assert np.array_equal(buffers.logits_numpy(), want_logits)
+
+    banner("graph workspace: cold stream")
+    cold = kt.Stream.create()
+    cache, buffers = model.new_cache(16), model.new_inference_buffers(16)
+    model.prefill(prompt, cache, buffers)  # on the null stream: the new stream stays cold
+    kt.synchronize()  # the null stream does not order work on a created (non-blocking) stream
+    with pytest.raises(kt.IllegalStateException, match="workspace"):
+        model.capture_decode(cache, buffers, cold)
+    model.decode_step(cache, buffers, cold)  # not left capturing
+    cold.synchronize()
+    stream.destroy()
+    cold.destroy()
+
+
 def test_save_and_load_quantized_model(kt, oracle_lib, tmp_path):
     model = small(kt, biases=True)
     path = tmp_path / "model.safetensors"
@@ -501,3 +555,52 @@ def test_llama_1b_shape_consistency(kt):
     banner("1b generate")
     a = model.generate(prompt[:64], 16)
     assert a == model.generate(prompt[:64], 16)
+
+
+@pytest.mark.timeout(600)
+def test_llama_1b_full_size_against_the_oracle(kt):
+    """The 1B INT4 decoder at its configured size (16 layers, 2048, 32/8 heads, SwiGLU
+    8192, vocab 32000, RMSNorm eps 1e-5, RoPE theta 5e5, weights ~N(0, 0.02) INT4 g64): the
+    logits of a 1024-token random-id prefill and of 8 teacher-forced decode steps after it
+    against the oracle's RefTransformer on the same quantized weights (dense mode: the
+    dequantized weights through BLAS and float64 attention, which the CPU tests hold to
+    the restated loops within 1e-5). Bound: the prefill GEMM's, normwise 1e-2 (every
+    prefill projection rounds x to fp16; the decode steps read the cache that prefill
+    wrote). The greedy tokens agree wherever the oracle's top two logits are apart."""
+    import time
+    model = kt.Transformer(32000, 2048, 16, 32, 8192, 8, norm_eps=1e-5, rope_theta=500000.0,
+                           quantization=kt.Quantization.INT4, seed=1)
+    rng = np.random.default_rng(24)
+    prompt = rng.integers(0, 32000, 1024).tolist()
+    steps = 8
+    banner("1b full: device prefill")
+    cache, buffers = model.new_cache(1024 + steps), model.new_inference_buffers(1024 + steps)
+    got = model.prefill(prompt, cache, buffers).logits_numpy()
+    t0 = time.time()
+    banner("1b full: weights to the host")
+    ref = to_oracle(kt, model)
+    ref.dense = True
+    banner(f"1b full: oracle prefill ({time.time() - t0:.1f} s so far)")
+    rc = ref.new_cache(1024 + steps)
+    want = ref.prefill(prompt, rc)
+    err = normwise_rel(got, want)
+    banner(f"1b full: prefill logits normwise {err:.2e} ({time.time() - t0:.1f} s)")
+    assert err <= tolerance(1024)
+    assert normwise_rel(cache.keys_numpy(), rc.keys) <= tolerance(1024)
+    for step in range(steps):
+        token = oracle_argmax_or_near_tie(want, got)
+        got = model.decode(token, cache, buffers).logits_numpy()
+        want = ref.decode(token, rc)
+        err = normwise_rel(got, want)
+        banner(f"1b full: decode step {step} token {token} normwise {err:.2e}")
+        assert err <= tolerance(1024)
+    assert cache.length == rc.length == 1024 + steps
+
+
+def oracle_argmax_or_near_tie(want: np.ndarray, got: np.ndarray) -> int:
+    """The oracle's greedy token; the device's argmax must be the same token unless the
+    oracle's logits hold a near-tie between the two."""
+    a, b = int(np.argmax(want)), int(np.argmax(got))
+    if a != b:
+        assert want[a] - want[b] <= 1e-2 * np.abs(want).max(), (a, b, want[a], want[b])
+    return a

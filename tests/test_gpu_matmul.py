@@ -92,18 +92,125 @@ def test_int8_gemv_2048(kt, oracle_lib, g):
 LLAMA1B = [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]
 
 
+def tile_rows(m: int, rng, every: int = 512) -> np.ndarray:
+    """Rows the oracle checks: all of them up to `every` rows, above that the first and
+    last row and one random row of every 128-row tile of the GEMM (so no tile, and no
+    position of the workgroup-to-tile mapping, goes unchecked)."""
+    if m <= every:
+        return np.arange(m)
+    tiles = np.arange(0, m, 128)
+    picks = [tiles, np.minimum(tiles + 127, m - 1), np.minimum(tiles + rng.integers(1, 127, tiles.size), m - 1)]
+    return np.unique(np.concatenate(picks))
+
+
 @pytest.mark.parametrize("k,n", LLAMA1B)
 @pytest.mark.parametrize("m", [1, 16, 128, 512, 2048])
 def test_int8_prefill_sweep(kt, oracle_lib, m, k, n):
-    """INT8 g64 on Llama-3.2-1B-like shapes; the oracle checks sampled row blocks."""
+    """INT8 g64 on Llama-3.2-1B-like shapes; every 128-row tile is checked."""
     rng = np.random.default_rng(m + k + n)
     x = rng.standard_normal((m, k), dtype=np.float32)
     q = _weights(oracle_lib, k, n, 8, 64, 1, std=0.02)
-    rows = np.arange(m) if m <= 16 else np.r_[0:8, m // 2:m // 2 + 8, m - 8:m]
-    _compare(kt, oracle_lib, q, x, "prefill", rows=rows)
+    _compare(kt, oracle_lib, q, x, "prefill", rows=tile_rows(m, rng))
+
+
+@pytest.mark.parametrize("k,n", LLAMA1B)
+@pytest.mark.parametrize("m", [17, 128, 512, 2048])
+def test_int8_g32_gemm_every_tile(kt, oracle_lib, m, k, n):
+    """INT8 g32 -- the configuration the prefill GEMM figures are measured on -- through
+    the GEMM (M >= 17): with g = 32 every 64-deep K step spans two groups. All rows up
+    to M = 512, rows from every 128-row tile at M = 2048."""
+    rng = np.random.default_rng(7 * m + k + n)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    q = _weights(oracle_lib, k, n, 8, 32, 1, std=0.02)
+    _compare(kt, oracle_lib, q, x, "gemm-g32", rows=tile_rows(m, rng))
+
+
+TWO_ROW_SHAPES = [(896, (896, 128, 128)), (896, (4864, 4864)), (4864, (896,)), (2048, (2048, 512, 512)),
+                  (2048, (8192, 8192)), (8192, (2048,)), (4096, (4096, 1024, 1024)), (4096, (14336, 14336)),
+                  (14336, (4096,))]
+
+
+@pytest.mark.parametrize("k,ns", TWO_ROW_SHAPES)
+@pytest.mark.parametrize("bits,g", [(4, 64), (8, 32)])
+def test_two_rows(kt, oracle_lib, k, ns, bits, g):
+    """M = 2 (the two-row kernel) on the Qwen2-0.5B, 1B and 8B projection shapes, each
+    weight alone and the weights of one input grouped. Its sums are exact in fp32 like
+    the one-row kernel's, so the bound is 1e-5."""
+    rng = np.random.default_rng(k + sum(ns) + bits + g)
+    x = rng.standard_normal((2, k), dtype=np.float32)
+    qs = [_weights(oracle_lib, k, n, bits, g, 40 + i, std=0.02) for i, n in enumerate(ns)]
+    qts = [upload_quantized(kt, q) for q in qs]
+    wants = [oracle_lib.multiply_quantized(x, q, 2, threads=16) for q in qs]
+    for q, qt, want in zip(qs, qts, wants):
+        banner("two-rows", k, q.columns, bits, g)
+        got = gpu_matmul(kt, x, qt, 2)
+        assert normwise_rel(got, want) <= 1e-5, normwise_rel(got, want)
+    banner("two-rows grouped", k, ns, bits, g)
+    outs = [kt.DeviceBuffer(2 * n * 4) for n in ns]
+    kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(x), qts, outs, 2)
+    kt.synchronize()
+    for o, want, n in zip(outs, wants, ns):
+        got = o.download(np.float32).reshape(2, n)
+        assert normwise_rel(got, want) <= 1e-5, normwise_rel(got, want)
+
+
+def test_batched_rows_equal_the_row_kernel(kt, oracle_lib):
+    """QuantizationTest.kt:110-134: a and W ~ U(-0.5, 0.5), INT4 g64; m copies of one row
+    give that row's one-row result within 1e-4 (absolute) for every m up to 16 -- the
+    reference's shape K = 300, N = 2100 (odd sizes: the generic kernels) and an aligned
+    2048 x 2048 that takes the two-row kernel (m = 2) and row mode (3..16, x split into
+    fp16 hi and lo parts). m >= 17 takes the prefill GEMM, whose operands are single fp16
+    values: there the bound is the normwise 2e-3 criterion (the largest difference is
+    printed)."""
+    rng = np.random.default_rng(4)
+    for k, n in ((300, 2100), (2048, 2048)):
+        a = (rng.random((1, k), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+        w = (rng.random((k, n), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+        st, q = oracle_lib.quantize(w, 4, 64)
+        assert st == 0
+        qt = upload_quantized(kt, q)
+        single = gpu_matmul(kt, a, qt, 1)
+        assert np.abs(single - oracle_lib.multiply_quantized(a, q, 1)).max() < 1e-4
+        for m in (2, 3, 5, 8, 9, 16, 17, 64):
+            banner("batched", k, n, m)
+            batched = gpu_matmul(kt, np.tile(a, (m, 1)), qt, m)
+            diff = float(np.abs(batched - single).max())
+            print(f"  max |batched - single| = {diff:.2e}", flush=True)
+            if m <= 16:
+                assert diff < 1e-4, (k, n, m, diff)
+            else:
+                assert normwise_rel(batched, np.tile(single, (m, 1))) <= TOL
 
 
 LLAMA8B = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_llama8b_lm_head(kt, oracle_lib, bits):
+    """The Llama-3-8B head 4096 -> 128256: quantized on the device bit for bit like the
+    oracle (INT4 and INT8, g64), then multiplied at M = 1, 8, 64 and 512 (rows of every
+    128-row tile checked; the oracle's M = 1 row-unit kernel for one row)."""
+    k, n = 4096, 128256
+    rng = np.random.default_rng(50 + bits)
+    banner("8b lm_head weights", bits)
+    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    qt = kt.QuantizedTensor.quantize(w, k, n, kt.Quantization(bits, 64))
+    st, q = oracle_lib.quantize(w, bits, 64)
+    assert st == 0
+    del w
+    assert same_bits(qt.qdata.view(np.uint8), q.qdata), "packed bytes differ"
+    assert same_bits(qt.scales, q.scales), "scales differ"
+    if bits == 4:
+        assert same_bits(qt.zeros.view(np.uint8), q.zeros.view(np.uint8)), "zeros differ"
+    for m in (1, 8, 64, 512):
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        banner("8b lm_head", bits, m)
+        got = gpu_matmul(kt, x, qt, m)
+        rows = np.arange(m) if m <= 8 else tile_rows(m, rng, every=0)
+        want = oracle_lib.multiply_quantized(x[rows], q, len(rows), threads=16)
+        err = normwise_rel(got[rows], want)
+        print(f"  normwise={err:.3e}", flush=True)
+        assert err <= (1e-5 if m <= 2 else TOL)
 
 
 @pytest.mark.parametrize("k,n", LLAMA8B)
@@ -116,7 +223,7 @@ def test_llama8b_layers(kt, oracle_lib, k, n, bits):
         x = rng.standard_normal((m, k), dtype=np.float32)
         banner("llama8b", k, n, bits, m)
         got = gpu_matmul(kt, x, qt, m)
-        rows = np.arange(m) if m <= 8 else np.r_[0:4, m - 4:m]
+        rows = np.arange(m) if m <= 8 else tile_rows(m, rng, every=64)
         want = oracle_lib.multiply_quantized(x[rows], q, len(rows), threads=16)
         err = normwise_rel(got[rows], want)
         print(f"  normwise={err:.3e}", flush=True)

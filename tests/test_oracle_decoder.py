@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
+from conftest import normwise_rel as normwise
 from oracle import decoder_ref
 
 
@@ -290,3 +291,39 @@ def test_decoder_against_an_fp64_forward():
         x = x + (gate / (1 + np.exp(-gate)) * (n2 @ deq[p + "ffn.wUp"])) @ deq[p + "ffn.wDown"]
     want = norm(x[-1:], model.norms["finalNorm"]) @ deq["lmHead"]
     np.testing.assert_allclose(logits, want[0], rtol=0, atol=2e-4 * np.abs(want).max())
+
+
+def test_dense_mode_agrees_with_the_restated_loops():
+    """RefTransformer(dense=True) -- BLAS products over the fully dequantized weights and
+    float64 attention -- gives the restated loops' prefill, cache and decode logits up to
+    summation order (normwise 1e-5), and attend_dense agrees with oracle.attend (causal,
+    GQA, a prefix already in the cache)."""
+    model, _ = small_model(4)
+    dense = decoder_ref.RefTransformer(model.config, model.quantized, model.norms, dense=True)
+    rng = np.random.default_rng(31)
+    prompt = rng.integers(0, model.config.vocabulary_size, 45).tolist()
+    c1, c2 = model.new_cache(49), dense.new_cache(49)
+    a, b = model.prefill(prompt, c1), dense.prefill(prompt, c2)
+    assert normwise(b, a) <= 1e-5 and normwise(c2.keys, c1.keys) <= 1e-5 and normwise(c2.values, c1.values) <= 1e-5
+    for t in rng.integers(0, model.config.vocabulary_size, 4).tolist():
+        assert normwise(dense.decode(t, c2), model.decode(t, c1)) <= 1e-5
+    heads, kvh, hd, ms, layers = 8, 2, 16, 40, 2
+    keys = rng.standard_normal(layers * kvh * ms * hd).astype(np.float32)
+    values = rng.standard_normal(layers * kvh * ms * hd).astype(np.float32)
+    for start, tokens in ((0, 7), (13, 5), (30, 1)):
+        q = rng.standard_normal((tokens, heads * hd)).astype(np.float32)
+        want = oracle.attend(q, start, keys, values, 1, heads, kvh, hd, ms)
+        got = decoder_ref.attend_dense(q, start, keys, values, 1, heads, kvh, hd, ms)
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_vectorised_dequantize_equals_the_row_accessor():
+    """oracle.Quantized.dequantize (numpy) is dequantize_row (C) bit for bit, INT8 with and
+    without a partial last group, INT4 with an odd column count."""
+    rng = np.random.default_rng(32)
+    for k, n, bits, g in ((100, 37, 4, 32), (70, 9, 4, 64), (65, 130, 8, 64), (33, 40, 8, 16)):
+        status, q = oracle.quantize((rng.standard_normal((k, n)) * 0.3).astype(np.float32), bits, g)
+        assert status == 0
+        full = q.dequantize()
+        for r in range(k):
+            assert np.array_equal(full[r].view(np.uint32), q.dequantize_row(r).view(np.uint32))

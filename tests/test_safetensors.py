@@ -107,6 +107,14 @@ def test_reader_rejects_malformed_files_like_the_reference(tmp_path):
         (_bad_file(tmp_path, "nooff.st", b'{"a":{"dtype":"F32","shape":[1]}}'), "Tensor a has no data_offsets"),
         (_bad_file(tmp_path, "range.st", b'{"a":{"dtype":"F32","shape":[4],"data_offsets":[0,16]}}', b"\0" * 8),
          "Tensor a data range [0, 16) exceeds file"),
+        # data_start + end would wrap past INT64_MAX into a small number: still rejected
+        (_bad_file(tmp_path, "wrap.st", b'{"a":{"dtype":"F32","shape":[1],'
+                   b'"data_offsets":[9223372036854775803,9223372036854775807]}}', b"\0" * 4),
+         "Tensor a data range [9223372036854775803, 9223372036854775807) exceeds file"),
+        (_bad_file(tmp_path, "neg.st", b'{"a":{"dtype":"F32","shape":[1],"data_offsets":[-4,0]}}', b"\0" * 4),
+         "Tensor a data range [-4, 0) exceeds file"),
+        (_bad_file(tmp_path, "huge.st", b'{"a":{"dtype":"F32","shape":[1],"data_offsets":[0,99999999999999999999]}}',
+                   b"\0" * 4), "Tensor a has no data_offsets"),
     ]
     for path, message in cases:
         with pytest.raises(IllegalArgumentException) as err:
