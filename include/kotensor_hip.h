@@ -143,6 +143,22 @@ int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bi
 int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c,
                    int32_t accumulate, float alpha, void* stream);
 
+/* kt_qmatmul that allocates nothing. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. Same arguments, kernels and results (bit for
+ * bit) as kt_qmatmul, but the kernels' scratch memory (split sums, counters, the
+ * prepared x of the prefill GEMM) is a fixed 64 MiB device array of the library, one
+ * per GPU, held until the process ends, instead of the per-stream workspace. A call
+ * whose scratch would exceed it returns KT_ERR_SHAPE before launching anything (one-row
+ * products need at most 8 bytes per output column, so N up to half a million fits; the
+ * prefill GEMM needs about 2 * M * K bytes). The first call
+ * on a device sets the array up and waits for that (KT_ERR_STATE if the stream is
+ * capturing then); later calls may be recorded into graphs. Every call on a GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (two streams, two threads, or
+ * a replay next to an eager call) race and must be serialized by the caller. */
+int32_t kt_qmatmul_noalloc(const float* a, int32_t m, const kt_qweight* w, float* c,
+                           int32_t accumulate, float alpha, void* stream);
+
 /* QuantizedLinear.forwardInto(input, out), K/QuantizedLinear.kt:22-25 (with
  * Tensor.matmulDequantInto K/Tensor.kt:180-188 and addInPlace K/Tensor.kt:201-221):
  *   out[m x N] = a . deq(W) + bias (bias fp32 [N] broadcast over rows, or NULL). */

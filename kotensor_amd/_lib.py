@@ -104,6 +104,7 @@ SIGNATURES = {
     "kt_qweight_check": [ctypes.POINTER(_QWeight)],
     "kt_quantize": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "kt_qmatmul": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],
+    "kt_qmatmul_noalloc": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],
     "kt_qlinear_forward": [_P, _I, ctypes.POINTER(_QWeight), _P, _P, _P],
     "kt_qmatmul_group": [_P, _I, ctypes.POINTER(_QWeight), _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _F, _P],
     "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],

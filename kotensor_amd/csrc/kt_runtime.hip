@@ -43,7 +43,18 @@ std::map<std::pair<int, hipStream_t>, Block> g_ws;
 // these stay allocated until the process ends (each is smaller than its successor, so
 // together they are bounded by a few times the largest workspace of the stream).
 std::vector<void*> g_retired;
-std::map<int, int32_t> g_cus;
+constexpr int MAX_DEVICES = 64;
+int32_t g_cus[MAX_DEVICES] = {};  // compute units per device, 0 until asked
+
+// A caller-provided workspace that replaces the per-stream one for the calls this
+// thread makes while it is set (kt_qmatmul_noalloc), laid out like a stream's:
+// counters, then zeroed fp64 accumulators, then the general area.
+struct FixedWorkspace {
+    char* ptr;
+    size_t bytes;       // whole area
+    size_t zero_bytes;  // the accumulator region after the counters
+};
+thread_local const FixedWorkspace* t_fixed = nullptr;
 }  // namespace
 
 // Each workspace starts with a COUNTER_BYTES region of uint32 counters and a region of
@@ -86,7 +97,29 @@ static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** o
     return KT_OK;
 }
 
+// The regions of the fixed workspace for a call that needs `doubles` accumulators and
+// `bytes` of general area; a call that needs more is an argument error.
+static int32_t fixed_regions(const FixedWorkspace& f, size_t doubles, size_t bytes, uint32_t** counters,
+                             double** accs, void** general) {
+    if (doubles * sizeof(double) > f.zero_bytes)
+        return fail(KT_ERR_SHAPE, "the call needs %zu bytes of zeroed accumulators; the fixed workspace has %zu",
+                    doubles * sizeof(double), f.zero_bytes);
+    const size_t head = COUNTER_BYTES + f.zero_bytes;
+    if (bytes > f.bytes - head)
+        return fail(KT_ERR_SHAPE, "the call needs %zu bytes of workspace; the fixed workspace has %zu", bytes,
+                    f.bytes - head);
+    *counters = reinterpret_cast<uint32_t*>(f.ptr);
+    *accs = reinterpret_cast<double*>(f.ptr + COUNTER_BYTES);
+    *general = f.ptr + head;
+    return KT_OK;
+}
+
 int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
+    if (t_fixed) {
+        uint32_t* c;
+        double* d;
+        return fixed_regions(*t_fixed, 0, bytes, &c, &d, out);
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block* b = nullptr;
     int32_t status = ensure(stream, 0, bytes, &b);
@@ -97,6 +130,10 @@ int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
 
 int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters) {
     if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    if (t_fixed) {
+        double* d;
+        return fixed_regions(*t_fixed, 0, bytes, counters, &d, general);
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block* b = nullptr;
     int32_t status = ensure(stream, 0, bytes, &b);
@@ -108,6 +145,10 @@ int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void*
 
 int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs) {
     if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    if (t_fixed) {
+        void* g;
+        return fixed_regions(*t_fixed, doubles, 0, counters, accs, &g);
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     Block* b = nullptr;
     int32_t status = ensure(stream, doubles * sizeof(double), 0, &b);
@@ -120,14 +161,62 @@ int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles,
 int32_t cu_count() {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return 256;
+    if (device < 0 || device >= MAX_DEVICES) return 256;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    auto it = g_cus.find(device);
-    if (it != g_cus.end()) return it->second;
+    if (g_cus[device] > 0) return g_cus[device];
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
         cus = 256;
     g_cus[device] = cus;
     return cus;
+}
+
+// ---- kt_qmatmul_noalloc's workspace -----------------------------------------------
+// A file-scope device array, one copy per device (each GPU holds its own until the
+// process ends). Host code never passes the array's name to a kernel: the name is a
+// host-side stand-in, so each device's address is taken once with hipGetSymbolAddress
+// and kept in g_scratch.
+constexpr size_t SCRATCH_BYTES = 64 << 20;      // counters, accumulators and general area
+constexpr size_t SCRATCH_ZERO_BYTES = 4 << 20;  // fp64 accumulators (half a million columns)
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+struct ScratchSlot {
+    char* ptr = nullptr;  // the device's address of `scratch`, once set up
+};
+ScratchSlot g_scratch[MAX_DEVICES];
+std::mutex g_scratch_mutex;
+
+__global__ void __launch_bounds__(256) clear_kernel(uint4* p, size_t n) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's scratch address. The first call on a device takes the address
+// and clears the counters and accumulators (kernels leave them at zero after that); it
+// runs the clear and waits for it, so it cannot be recorded into a graph.
+static int32_t scratch_address(hipStream_t st, char** out) {
+    int device = 0;
+    KT_HIP(hipGetDevice(&device));
+    if (device < 0 || device >= MAX_DEVICES) return fail(KT_ERR_ARGUMENT, "device %d out of range", device);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ScratchSlot& slot = g_scratch[device];
+    if (!slot.ptr) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        KT_HIP(hipStreamIsCapturing(st, &capture));
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(KT_ERR_STATE,
+                        "kt_qmatmul_noalloc sets up its device array on its first call on a device, which cannot be "
+                        "recorded; make one call outside a capture first");
+        void* p = nullptr;
+        KT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const size_t words = (COUNTER_BYTES + SCRATCH_ZERO_BYTES) / sizeof(uint4);
+        clear_kernel<<<256, 256, 0, st>>>(static_cast<uint4*>(p), words);
+        KT_LAUNCHED("kt_qmatmul_noalloc: clear");
+        KT_HIP(hipStreamSynchronize(st));
+        slot.ptr = static_cast<char*>(p);
+    }
+    *out = slot.ptr;
+    return KT_OK;
 }
 
 int32_t view_weight(const kt_qweight* w, WeightView* v) {
@@ -436,6 +525,19 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
 
 int32_t kt_qmatmul(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
                    void* stream) {
+    return qmatmul_impl(a, m, w, c, accumulate, alpha, nullptr, stream);
+}
+
+int32_t kt_qmatmul_noalloc(const float* a, int32_t m, const kt_qweight* w, float* c, int32_t accumulate, float alpha,
+                           void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char* base = nullptr;
+    if (int32_t status = scratch_address(st, &base)) return status;
+    const FixedWorkspace fixed{base, SCRATCH_BYTES, SCRATCH_ZERO_BYTES};
+    struct Scope {
+        explicit Scope(const FixedWorkspace* f) { t_fixed = f; }
+        ~Scope() { t_fixed = nullptr; }
+    } scope(&fixed);
     return qmatmul_impl(a, m, w, c, accumulate, alpha, nullptr, stream);
 }
 
