@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KT_ABI_VERSION 1
+#define KT_ABI_VERSION 2
 
 /* Status codes. */
 #define KT_OK 0
@@ -53,7 +53,9 @@ extern "C" {
                                   has no workspace of the size it needs yet) */
 
 /* A quantized weight held in device memory. Mirrors the fields of
- * QuantizedTensor (K/QuantizedTensor.kt:27-49): rows = K (in), columns = N (out). */
+ * QuantizedTensor (K/QuantizedTensor.kt:27-49): rows = K (in), columns = N (out).
+ * packed is optional (NULL or a copy written by kt_qweight_pack): a second, device-native
+ * arrangement of qdata that the one-row products read instead when it is present. */
 typedef struct kt_qweight {
     const void* qdata;
     const float* scales;
@@ -62,6 +64,7 @@ typedef struct kt_qweight {
     int32_t columns;
     int32_t bits;          /* 4 or 8 (Quantization.bits, K/QuantizedTensor.kt:10-17) */
     int32_t group_size;    /* > 0 (Quantization.groupSize) */
+    const void* packed;    /* NULL, or kt_qweight_packed_bytes bytes from kt_qweight_pack */
 } kt_qweight;
 
 /* ---- library / errors --------------------------------------------------------- */
@@ -74,13 +77,17 @@ int32_t kt_set_device(int32_t device);
 /* Kernel selection knobs, the counterpart of MatMul's runtime knobs
  * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they choose how the
  * small-M kernels split their work, never their result beyond fp32 rounding order.
- * gemv_kind: 0 = automatic (for one row the column-strip kernel up to a size and the
- *            wide-strip MFMA kernel above it, the row-block MFMA kernel for 2 to 16 rows,
- *            where the layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA GEMV
- *            for M > 1: those go to the GEMM), 2 = row-block MFMA kernel for M <= 16,
- *            3 = wide-strip MFMA kernel for M == 1, 4 = column-strip kernel for M == 1;
- * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic);
- * gemv_splits: workgroups along K per column tile (0 = automatic);
+ * gemv_kind: 0 = automatic (for one row the column-run kernel when the weight has a
+ *            packed copy, else the column-strip kernel up to a size and the wide-strip
+ *            MFMA kernel above it; the row-block MFMA kernel for 2 to 16 rows, where the
+ *            layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA GEMV for M > 1:
+ *            those go to the GEMM), 2 = row-block MFMA kernel for M <= 16, 3 = wide-strip
+ *            MFMA kernel for M == 1, 4 = column-strip kernel for M == 1, 5 = column-run
+ *            kernel for M == 1 (needs the packed copy);
+ * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic); for the
+ *            column-run kernel, the weights in flight per wave (4: 8 KB, 8: 16 KB);
+ * gemv_splits: workgroups along K per column tile (0 = automatic); for the column-run
+ *            kernel, the waves that split the K range of a column set (1, 2, 4 or 8);
  * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic);
  * gemv_reduce: how split sums meet (0 = automatic, 1 = a second kernel, 2 = inside the
  * kernel). Process-wide. */
@@ -120,6 +127,21 @@ int32_t kt_qweight_layout(int32_t rows, int32_t columns, int32_t bits, int32_t g
 /* Validates a weight the way the QuantizedTensor constructor does
  * (K/QuantizedTensor.kt:63-70). */
 int32_t kt_qweight_check(const kt_qweight* w);
+
+/* ---- the column-run copy (no counterpart in the reference) ---------------------
+ * The reference's layout keeps a row of the weight contiguous, which makes a one-row
+ * product at shapes like 4096 -> 14336 split its K range over workgroups and meet their
+ * sums through memory. The column-run copy keeps each column's K values contiguous in
+ * 16-column blocks (1 KB per 128 k for 4-bit, 2 KB for 8-bit), so the one-row kernel
+ * reads whole columns with no cross-workgroup sums. It is a device-side accelerator
+ * next to qdata, not a format: files, quantize, the accessors and products of more than
+ * one row keep using qdata. Write it once after qdata is final (and again if qdata
+ * changes), then set kt_qweight.packed. Size: ceil(columns / 16) * ceil(rows / 128)
+ * * (bits == 4 ? 1024 : 2048) bytes, 16-byte aligned. */
+int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int64_t* bytes);
+/* Writes the copy of w's qdata into `packed` (kt_qweight_packed_bytes bytes of device
+ * memory, 16-byte aligned); w->packed is ignored. Asynchronous. */
+int32_t kt_qweight_pack(const kt_qweight* w, void* packed, void* stream);
 
 /* ---- quantize + pack ---------------------------------------------------------- */
 /* QuantizedTensor.quantize(data, rows, columns, Quantization(bits, group_size)),

@@ -60,6 +60,7 @@ class _QWeight(ctypes.Structure):
         ("columns", ctypes.c_int32),
         ("bits", ctypes.c_int32),
         ("group_size", ctypes.c_int32),
+        ("packed", ctypes.c_void_p),
     ]
 
 
@@ -102,6 +103,8 @@ SIGNATURES = {
     "kt_stream_sync": [_P],
     "kt_qweight_layout": [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
     "kt_qweight_check": [ctypes.POINTER(_QWeight)],
+    "kt_qweight_packed_bytes": [_I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
+    "kt_qweight_pack": [ctypes.POINTER(_QWeight), _P, _P],
     "kt_quantize": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "kt_qmatmul": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],
     "kt_qmatmul_noalloc": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],

@@ -43,6 +43,7 @@ struct WeightView {
     const uint8_t* q;
     const float* s;
     const int8_t* z;  // nullptr when the weight has no zero points
+    const uint8_t* p;  // the column-run copy (kt_qweight_pack), or nullptr
     int32_t K, N, bits, g, G, bpr;
 };
 int32_t view_weight(const kt_qweight* w, WeightView* v);
@@ -136,6 +137,19 @@ int32_t launch_gemv_strip(const float* a, const WeightView* ws, float* const* cs
                           int32_t count, int32_t accumulate, float alpha, hipStream_t st);
 // Whether the automatic choice takes the column-strip kernel for these weights.
 bool gemv_strip_preferred(const WeightView* ws, int32_t count);
+
+// The one-row GEMV on the column-run copy (kt_gemv_packed.hip): bytes of the copy, the
+// kernel that writes it, support check, launch (up to four weights sharing the input;
+// up = SwiGLU's up row, norm_weight = RMSNorm's weight, as in launch_gemv_wide) and its
+// knobs (K-parts per column set, waves per workgroup, ring depth 4 or 8 = 8 or 16 KB per
+// wave; 0 = automatic).
+int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits);
+int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st);
+bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                           int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr,
+                           const float* norm_weight = nullptr, float eps = 0.0f);
+void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
 // otherwise the generic kernel runs.

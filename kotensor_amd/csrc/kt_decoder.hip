@@ -898,18 +898,26 @@ int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float
     if (status) return status;
     const int32_t K = views[0].K;
     if (m == 0) return KT_OK;
-    // one row, at most four weights the wide GEMV takes: RMSNorm inside the product
-    bool fused = m == 1 && count <= 4 && (gemv_kind() == 0 || gemv_kind() == 3) && aligned(x, 16) &&
-                 aligned(norm_weight, 4) && K % 4 == 0 && K <= NORM_F4 * 4 * NORM_THREADS;
-    for (int32_t i = 0; fused && i < count; ++i) {
+    // one row, at most four weights the column-run or wide GEMV takes: RMSNorm inside
+    // the product
+    bool fused = m == 1 && count <= 4 && aligned(x, 16) && aligned(norm_weight, 4) && K % 4 == 0 &&
+                 K <= NORM_F4 * 4 * NORM_THREADS;
+    bool packed = fused && (gemv_kind() == 0 || gemv_kind() == 5) && aligned(norm_weight, 16);
+    fused = fused && (gemv_kind() == 0 || gemv_kind() == 3);
+    for (int32_t i = 0; (fused || packed) && i < count; ++i) {
         if (i > 0) {
             status = view_weight(&weights[i], &views[i]);
             if (status) return status;
         }
         const WeightView& v = views[i];
-        fused = outputs[i] && v.K == K && v.bits == views[0].bits && v.g == views[0].g &&
-                (v.z != nullptr) == (views[0].z != nullptr) && gemv_wide_supported(x, 1, v, outputs[i]);
+        const bool same = outputs[i] && v.K == K && v.bits == views[0].bits && v.g == views[0].g &&
+                          (v.z != nullptr) == (views[0].z != nullptr);
+        packed = packed && same && gemv_packed_supported(x, 1, v, outputs[i]);
+        fused = fused && same && gemv_wide_supported(x, 1, v, outputs[i]);
     }
+    if (packed)
+        return launch_gemv_packed(x, views, outputs, biases, count, accumulate, alpha, static_cast<hipStream_t>(stream),
+                                  nullptr, norm_weight, eps);
     fused = fused && gemv_wide_preferred(views, count);
     if (fused)
         return launch_gemv_wide(x, views, outputs, biases, count, accumulate, alpha, static_cast<hipStream_t>(stream),
@@ -929,8 +937,10 @@ int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qwei
     if (m == 0) return KT_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const float* biases[1] = {bias};
-    // one row: the wide GEMV computes the gate while it loads its input (and leaves the
-    // gate row as it was)
+    // one row: the column-run or wide GEMV computes the gate while it loads its input
+    // (and leaves the gate row as it was)
+    if (m == 1 && (gemv_kind() == 0 || gemv_kind() == 5) && aligned(up, 16) && gemv_packed_supported(gate, 1, v, c))
+        return launch_gemv_packed(gate, &v, &c, biases, 1, accumulate, alpha, st, up);
     if (m == 1 && (gemv_kind() == 0 || gemv_kind() == 3) && gemv_wide_preferred(&v, 1) &&
         gemv_wide_supported(gate, 1, v, c))
         return launch_gemv_wide(gate, &v, &c, biases, 1, accumulate, alpha, st, up);

@@ -1,0 +1,592 @@
+// kt_gemv_packed.hip -- the one-row dequant-GEMV on a device-native copy of the packed
+// weights, and the kernel that writes that copy:
+//   c[1 x N] = (accumulate ? c : 0) + alpha * x[1 x K] . deq(W) (+ bias),
+// MatMul.multiplyQuantizedRow (Engine/kotensor/src/main/kotlin/MatMul.kt:494-536).
+//
+// Why a second layout. In the reference layout ([K x bytesPerRow], a row of the weight
+// is contiguous) a workgroup that owns a strip of columns must read all K rows of it,
+// and at shapes like 4096 -> 14336 there are too few strips to occupy 256 CUs: the K
+// range has to be split over workgroups whose partial sums then meet through memory,
+// several dependent round trips after the last load. In the column-run layout a column's
+// K values are contiguous, so a wave owns whole columns over all of K: no sums leave a
+// workgroup, every load instruction reads 1 KB of consecutive bytes, and the number of
+// workgroups is set by N alone. The copy is made once per weight (kt_qweight_pack) next
+// to the reference bytes, which stay the format of record (quantize, files, accessors
+// and the M > 1 kernels read them).
+//
+// Layout (a column set is 16 columns, a chunk 128 k; block = column set x chunk):
+//   blocks are ordered [column set][chunk]; INT4 blocks are 1 KB, INT8 blocks 2 KB;
+//   within a block, lane l = 16 kb + n of the reading wave owns the 16 bytes at
+//   16 l (INT8: and at 1024 + 16 l): column 16 set + n, the 32 k of run
+//   [128 chunk + 32 kb, + 32). INT8: byte b of the first 16 is k = run + b, of the
+//   second k = run + 16 + b. INT4: dword d = 2 m + h of the 16 bytes holds, in byte t,
+//   k = run + 16 m + 8 h + t in the low nibble and k = run + 16 m + 8 h + 4 + t in the
+//   high one, so that (d & 0x0F0F0F0F) and (d >> 4) & 0x0F0F0F0F are the int8 values
+//   of k = run + 16 m + 8 h + 0..3 and + 4..7. Padding (k >= K, columns >= N) is 0.
+//
+// Arithmetic (integer-exact products, then the reference's per-group combine):
+//   * x is cut into runs of 32 k. With E the binary exponent of the run's largest |x|
+//     (largest |x| < 2^E), X = (int)(x * 2^(30 - E)) holds x to 2^-30 of that maximum,
+//     and X = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 with signed byte digits (the bytes of
+//     ((X + 0x808080) ^ 0x808080)). The four digit rows of every run go to LDS;
+//   * v_mfma_i32_16x16x64_i8 with a block-diagonal A: lane group kb of B holds its own
+//     run's 16 k of 16 columns, A row 4 kb + p holds digit p of that run's x (rows of
+//     other lane groups' runs are 0), so one MFMA gives every lane group the four digit
+//     sums of its own run: D_p = sum d_p q, exact in int32 (two MFMAs per run);
+//   * per run: u = ((D_0 / 256 + D_1) / 256 + D_2) / 256 + D_3 in fp32, sum x q =
+//     u * 2^(E - 6), and y += scale * (sum x q - zero * sum x): the reference's
+//     combineGroup, scale * (acc - zero * rowSum) (MatMul.kt:804-828), applied per run;
+//   * the four lanes of a column (its four runs of a chunk) and the waves that split K
+//     meet by fixed-order sums inside the workgroup.
+// A column's result therefore depends only on x and that column's weights, never on
+// how the columns or the K range are divided among waves.
+#include "kt_common.h"
+
+namespace kt {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int SET = 16;      // columns per column set
+constexpr int CHUNK = 128;   // k per chunk
+constexpr int RUN = 32;      // k per lane run
+constexpr int MAX_JOBS = 4;
+constexpr int MAX_K = 16384;  // eight waves of at most 2048 k each
+constexpr int ZERO_BYTES = 32;
+
+__host__ __device__ constexpr int block_bytes(int bits) { return bits == 4 ? 1024 : 2048; }
+
+// The s_waitcnt immediate that waits until at most n vector memory operations are
+// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at
+// their maxima so they do not wait).
+__host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+struct PJob {
+    const uint8_t* packed;
+    const float* s;
+    const int8_t* z;
+    float* out;
+    const float* bias;
+    int32_t N, sets;
+};
+
+struct PJobs {
+    PJob job[MAX_JOBS];
+    int32_t count;
+};
+
+// Writes the column-run copy: one thread per output dword.
+__global__ void __launch_bounds__(256)
+    pack_kernel(const uint8_t* __restrict__ q, int32_t K, int32_t N, int32_t bits, int32_t bpr, int32_t chunks,
+                int64_t dwords, uint32_t* __restrict__ out) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < dwords;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int dw_per_block = block_bytes(bits) / 4;
+        const int64_t blk = i / dw_per_block;
+        const int within = static_cast<int>(i - blk * dw_per_block);
+        const int32_t set = static_cast<int32_t>(blk / chunks);
+        const int32_t chunk = static_cast<int32_t>(blk - static_cast<int64_t>(set) * chunks);
+        uint32_t v = 0;
+        if (bits == 4) {
+            const int lane = within >> 2, d = within & 3;
+            const int32_t col = set * SET + (lane & 15);
+            const int32_t k0 = chunk * CHUNK + (lane >> 4) * RUN + 16 * (d >> 1) + 8 * (d & 1);
+            if (col < N) {
+                const int32_t byte_col = col < bpr ? col : col - bpr;
+                const int shift = col < bpr ? 0 : 4;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int32_t kl = k0 + t, kh = k0 + 4 + t;
+                    const uint32_t lo = kl < K ? (q[static_cast<int64_t>(kl) * bpr + byte_col] >> shift) & 15u : 0u;
+                    const uint32_t hi = kh < K ? (q[static_cast<int64_t>(kh) * bpr + byte_col] >> shift) & 15u : 0u;
+                    v |= (lo | (hi << 4)) << (8 * t);
+                }
+            }
+        } else {
+            const int h = within >> 8, lane = (within >> 2) & 63, d = within & 3;
+            const int32_t col = set * SET + (lane & 15);
+            const int32_t k0 = chunk * CHUNK + (lane >> 4) * RUN + 16 * h + 4 * d;
+            if (col < N) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int32_t k = k0 + t;
+                    const uint32_t b = k < K ? q[static_cast<int64_t>(k) * bpr + col] : 0u;
+                    v |= b << (8 * t);
+                }
+            }
+        }
+        out[i] = v;
+    }
+}
+
+// Max over the 8 lanes of an aligned group (quad swaps, then the half-row mirror).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    return v;
+}
+// Sum over the same 8 lanes, in the same fixed pattern (lane 8 q's value is the one used).
+__device__ __forceinline__ float sum8(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    return v;
+}
+
+// The input row: X_PLAIN x; X_SWIGLU silu(x) * aux (the SwiGLU gate computed as
+// silu_mul_kernel does, x / (1 + exp(-x)) with exp in double rounded to float, times up);
+// X_NORM x * aux with the result scaled by r = 1 / sqrt(mean(x^2) + eps), RMSNorm with
+// weight aux (K/RMSNorm.kt:71-90), the sum of squares taken by the waves that split K
+// and added in K-part order (fp32 rounding apart from rmsnorm_kernel's order).
+constexpr int X_PLAIN = 0, X_SWIGLU = 1, X_NORM = 2;
+
+
+// Every wave works on its own: it copies its own columns' scales and zero points into
+// its own LDS area, loads x only for its own K range, turns it into digits there and
+// starts multiplying as soon as its first chunk of weights lands. No barrier comes
+// before the main loop (a workgroup-wide preparation would hold every wave until the
+// slowest wave's x and scales arrived, behind the first wave of weight loads of all
+// workgroups, and no refill would go out in that time). The waves of a workgroup meet
+// once, at the end, to add the K-parts of a column in fixed order.
+// One global_load_lds_dwordx4: lane l's 16 bytes at g land at LDS byte address lds + 16 l
+// (lds wave-uniform), with no registers in between. Inline assembly, so the compiler
+// does not count it among its loads: its own waits for later loads stay correct (they
+// count fewer loads than are outstanding, so they wait at least as long as needed), and
+// the kernel orders these copies itself by issuing them before any load it waits for
+// (loads complete in issue order). m0 is written here and used by nothing else.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory");
+}
+
+constexpr int MAX_WAVE_CHUNKS = 16;                      // a wave's K range: at most 2048
+constexpr int X_SLOTS = MAX_WAVE_CHUNKS * CHUNK / 256;  // float4s of x per lane
+
+// A wave's LDS area for waves of at most nmax chunks: digits [4][nmax * 128], 32 zero
+// bytes, run records [nmax * 4] x 8 bytes, scales [gw][16] fp32, zero points [gw][16].
+__host__ __device__ constexpr int32_t wave_digit_bytes(int32_t nmax) { return 4 * nmax * CHUNK; }
+__host__ __device__ constexpr int32_t wave_rec_offset(int32_t nmax) { return wave_digit_bytes(nmax) + ZERO_BYTES; }
+__host__ __device__ constexpr int32_t wave_scale_offset(int32_t nmax) {
+    return wave_rec_offset(nmax) + nmax * (CHUNK / RUN) * 8;
+}
+__host__ __device__ constexpr int32_t wave_bytes(int32_t nmax, int32_t gw) {
+    return wave_scale_offset(nmax) + gw * SET * 5 + ((16 - (gw * SET * 5) % 16) % 16);
+}
+// Groups a K range of nmax chunks can touch (one more when it starts inside a group).
+__host__ __device__ constexpr int32_t wave_groups(int32_t nmax, int32_t g) { return (nmax * CHUNK + g - 1) / g + 1; }
+
+template <int BITS, int W, int R, bool ZP, int XMODE>
+__global__ void __launch_bounds__(64 * W)
+    gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
+                       PJobs jobs, int32_t ks, int32_t nmax, float alpha, int32_t accumulate) {
+    constexpr int BB = block_bytes(BITS);
+    constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+    const PJob jb = jobs.job[blockIdx.y];
+    asm volatile("" ::"s"(jb.packed), "s"(jb.s), "s"(jb.z), "s"(jb.N), "s"(jb.sets), "s"(x), "s"(K), "s"(ks));
+    const int32_t cs = W / ks;  // column sets per workgroup
+    const int32_t set0 = blockIdx.x * cs;
+    if (set0 >= jb.sets) return;
+
+    const int32_t ln = threadIdx.x & 63;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t my_cs = wave % cs, kp = wave / cs;
+    const bool set_live = set0 + my_cs < jb.sets;
+    const int32_t set = set_live ? set0 + my_cs : jb.sets - 1;  // a dead wave computes a copy, never writes
+    const int32_t chunks = (K + CHUNK - 1) / CHUNK;
+    const int32_t G = (K + (RUN << gshift) - 1) / (RUN << gshift);  // quantization groups
+    const int32_t c_begin = kp * chunks / ks;
+    const int32_t n = (kp + 1) * chunks / ks - c_begin;  // chunks of this wave, 1 .. nmax
+    const int32_t k0 = c_begin * CHUNK;
+    const int32_t nl = ln & 15, kb = ln >> 4;
+    const int32_t col = set * SET + nl;
+    // groups of this wave's runs (the last chunk's padding runs take the last group)
+    const int32_t g_first = k0 >> (gshift + 5);
+    const int32_t gw = min((k0 + n * CHUNK - 1) >> (gshift + 5), G - 1) - g_first + 1;
+
+    // the wave's LDS area
+    const int32_t gwmax = wave_groups(nmax, RUN << gshift);
+    unsigned char* area = smem + wave * wave_bytes(nmax, gwmax);
+    int8_t* xd = reinterpret_cast<int8_t*>(area);
+    const int32_t ds = nmax * CHUNK;  // digit row stride
+    const int32_t zoff = wave_digit_bytes(nmax);
+    int2* rec = reinterpret_cast<int2*>(area + wave_rec_offset(nmax));
+    float* ssc = reinterpret_cast<float*>(area + wave_scale_offset(nmax));
+    uint8_t* szz = reinterpret_cast<uint8_t*>(ssc + gwmax * SET);
+
+    // ---- loads: scales and zero points straight into LDS, x into registers, then the
+    // first R chunks of weights. Loads complete in issue order, so the wait for x covers
+    // the LDS copies, and the wait for the first chunk covers x; x loads are unconditional
+    // (indices past the range clamped), so the waits for x never extend to the weights.
+    {
+        const uint32_t sc_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ssc));
+        const int32_t pieces = gw * 4;  // 16-byte pieces of the scale rows (16 floats each)
+#pragma unroll
+        for (int j = 0; j < (wave_groups(MAX_WAVE_CHUNKS, RUN) * 4 + 63) / 64; ++j) {
+            const int32_t p0 = 64 * j;
+            if (p0 < pieces) {
+                const int32_t p = min(p0 + ln, pieces - 1);
+                const float* src = jb.s + static_cast<int64_t>(g_first + (p >> 2)) * jb.N + set * SET + 4 * (p & 3);
+                if (p0 + ln < pieces) lds_dma16(src, sc_lds + 16 * p0);
+            }
+        }
+        if constexpr (ZP) {
+            const uint32_t z_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(szz));
+#pragma unroll
+            for (int j = 0; j < (wave_groups(MAX_WAVE_CHUNKS, RUN) + 63) / 64; ++j) {
+                const int32_t p0 = 64 * j;
+                if (p0 < gw) {
+                    const int32_t p = min(p0 + ln, gw - 1);
+                    if (p0 + ln < gw) lds_dma16(jb.z + static_cast<int64_t>(g_first + p) * jb.N + set * SET, z_lds + 16 * p0);
+                }
+            }
+        }
+    }
+    const int32_t n4 = K >> 2, q0 = k0 >> 2, nq = n * (CHUNK / 4);
+    float4 xv[X_SLOTS];
+    float4 uv[XMODE == X_PLAIN ? 1 : X_SLOTS];
+#pragma unroll
+    for (int j = 0; j < X_SLOTS; ++j) {
+        const int32_t i = min(q0 + min(ln + 64 * j, nq - 1), n4 - 1);
+        xv[j] = reinterpret_cast<const float4*>(x)[i];
+        if constexpr (XMODE != X_PLAIN) uv[j] = reinterpret_cast<const float4*>(aux)[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(jb.packed + (static_cast<int64_t>(set) * chunks + c_begin) * BB), 0, n * BB, 0x00020000);
+    u32x4 wb[R][NB];
+    auto issue = [&](int slot, int32_t cc) {
+        // chunks past this wave's range read as zeros without touching memory
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+            wb[slot][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        wr, cc * BB + h * 1024 + 16 * ln, 0, 0));
+    };
+#pragma unroll
+    for (int s = 0; s < R; ++s) issue(s, s);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x to digits and run records, in the wave's own area --------------------------
+    if (ln < ZERO_BYTES / 4) reinterpret_cast<uint32_t*>(area + zoff)[ln] = 0u;
+    float nsum = 0.0f;  // X_NORM: this wave's share of sum x^2
+#pragma unroll
+    for (int j = 0; j < X_SLOTS; ++j) {
+        const int32_t i = ln + 64 * j;  // float4 of the wave's range
+        // float4s past the range do nothing; the 8 lanes of a run are all in or all out
+        if (i >= nq) continue;
+        float v[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        const bool in_row = q0 + i < n4;
+        if constexpr (XMODE == X_SWIGLU) {
+            const float u[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + static_cast<float>(exp(-static_cast<double>(v[e])))) * u[e];
+        } else if constexpr (XMODE == X_NORM) {
+            const float u[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+            if (in_row) nsum = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], nsum))));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= u[e];
+        }
+        if (!in_row) v[0] = v[1] = v[2] = v[3] = 0.0f;
+        const float mx = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const bool finite = mx <= 3.402823466e38f;
+        int e = 0;
+        if (finite && mx > 0.0f) frexpf(mx, &e);
+        uint32_t dg[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int32_t X = finite ? static_cast<int32_t>(ldexpf(v[q], 30 - e)) : 0;
+            dg[q] = (static_cast<uint32_t>(X) + 0x808080u) ^ 0x808080u;
+        }
+        // 4 x 4 byte transpose: digit p of the four values into one dword
+        const uint32_t t01l = __builtin_amdgcn_perm(dg[1], dg[0], 0x05010400u);
+        const uint32_t t01h = __builtin_amdgcn_perm(dg[1], dg[0], 0x07030602u);
+        const uint32_t t23l = __builtin_amdgcn_perm(dg[3], dg[2], 0x05010400u);
+        const uint32_t t23h = __builtin_amdgcn_perm(dg[3], dg[2], 0x07030602u);
+        uint32_t* xw = reinterpret_cast<uint32_t*>(xd) + i;
+        xw[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+        xw[ds / 4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+        xw[2 * (ds / 4)] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+        xw[3 * (ds / 4)] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
+        const float sx = sum8((v[0] + v[1]) + (v[2] + v[3]));
+        if ((ln & 7) == 0) rec[i >> 3] = make_int2(e - 6, __float_as_int(finite ? sx : __builtin_nanf("")));
+    }
+
+    // ---- main loop: R chunks in flight ----------------------------------------------
+    // A: lane (row i = ln % 16, lane group kb) reads digit i % 4 of its own group's run
+    // when i / 4 == kb, the zero bytes otherwise.
+    const bool diag = (nl >> 2) == kb;
+    const int32_t a_base = diag ? (nl & 3) * ds + kb * RUN : zoff;
+    const int32_t a_step = diag ? CHUNK : 0;
+    const uint32_t mask = 0x0F0F0F0Fu;
+    float y = 0.0f;
+    auto process = [&](int s, int32_t cc) {
+        const int8_t* pa = xd + a_base + cc * a_step;
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(pa);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(pa + 16);
+        i32x4 b0, b1;
+        if constexpr (BITS == 4) {
+            const u32x4 d = wb[s][0];
+            b0 = i32x4{static_cast<int32_t>(d[0] & mask), static_cast<int32_t>((d[0] >> 4) & mask),
+                       static_cast<int32_t>(d[1] & mask), static_cast<int32_t>((d[1] >> 4) & mask)};
+            b1 = i32x4{static_cast<int32_t>(d[2] & mask), static_cast<int32_t>((d[2] >> 4) & mask),
+                       static_cast<int32_t>(d[3] & mask), static_cast<int32_t>((d[3] >> 4) & mask)};
+        } else {
+            b0 = __builtin_bit_cast(i32x4, wb[s][0]);
+            b1 = __builtin_bit_cast(i32x4, wb[s][1]);
+        }
+        i32x4 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+        const int32_t run = cc * (CHUNK / RUN) + kb;  // of the wave's range
+        const int2 rc = rec[run];
+        // a run past K (padding of the last chunk) takes the last group's scale; its
+        // digits are zero, so it adds nothing
+        const int32_t si = min(((k0 >> 5) + run) >> gshift, G - 1) - g_first;
+        const float scale = ssc[si * SET + nl];
+        const float zero = ZP ? static_cast<float>(static_cast<int8_t>(szz[si * SET + nl])) : 0.0f;
+        const float u = fmaf(fmaf(fmaf(static_cast<float>(acc[0]), 1.0f / 256.0f, static_cast<float>(acc[1])),
+                                  1.0f / 256.0f, static_cast<float>(acc[2])),
+                             1.0f / 256.0f, static_cast<float>(acc[3]));
+        const float v = fmaf(-zero, __int_as_float(rc.y), ldexpf(u, rc.x));
+        y = fmaf(scale, v, y);
+    };
+    // whole rounds that refill every slot, then a last round that only drains the ring
+    int32_t base = 0;
+    for (; base + R < n; base += R) {
+#pragma unroll
+        for (int s = 0; s < R; ++s) {
+            process(s, base + s);
+            issue(s, base + s + R);
+            __builtin_amdgcn_sched_barrier(0);  // keep each refill right behind its use
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < R; ++s)
+        if (base + s < n) process(s, base + s);
+
+    // ---- the column's four runs, then the waves that split K, in fixed order ----------
+    y += __shfl_xor(y, 16, 64);
+    y += __shfl_xor(y, 32, 64);
+    float* red = reinterpret_cast<float*>(smem + W * wave_bytes(nmax, gwmax));  // [W][16], then [W] x^2
+    if (ln < SET) red[wave * SET + ln] = y;
+    if constexpr (XMODE == X_NORM) {
+        const float w2 = norm_wave_sum(nsum);
+        if (ln == 0) red[W * SET + wave] = w2;
+    }
+    __syncthreads();
+    if (kp != 0 || ln >= SET || !set_live) return;
+    float sum = red[my_cs * SET + ln];
+    for (int32_t p = 1; p < ks; ++p) sum += red[(p * cs + my_cs) * SET + ln];
+    float al = alpha;
+    if constexpr (XMODE == X_NORM) {
+        float sq = red[W * SET + my_cs];
+        for (int32_t p = 1; p < ks; ++p) sq += red[W * SET + p * cs + my_cs];
+        al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
+    }
+    float* dst = jb.out + col;
+    float o = accumulate ? *dst : 0.0f;
+    o = fmaf(al, sum, o);
+    if (jb.bias) o += jb.bias[col];
+    *dst = o;
+}
+
+struct Forced {
+    int ks = 0;
+    int waves = 0;
+    int ring = 0;  // 1: 8 KB in flight per wave, 2: 16 KB, 0: automatic
+};
+Forced g_forced;
+
+template <int BITS, int W, bool ZP, int XMODE>
+void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+              int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate, int32_t nmax) {
+    // the ring: 8 KB of weights in flight per wave (16 KB when forced)
+    constexpr int RS = BITS == 4 ? 8 : 4;
+    if (g_forced.ring == 2)
+        gemv_packed_kernel<BITS, W, 2 * RS, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
+    else if (g_forced.ring == 1 || nmax > RS / 2)
+        gemv_packed_kernel<BITS, W, RS, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
+    else
+        gemv_packed_kernel<BITS, W, RS / 2, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
+}
+
+template <int BITS, bool ZP, int XMODE>
+void launch_w(int w, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+              int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate, int32_t nmax) {
+    if (w == 8) launch_r<BITS, 8, ZP, XMODE>(grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+    else launch_r<BITS, 4, ZP, XMODE>(grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+}
+
+template <int BITS, bool ZP>
+void launch_mode(int mode, int w, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
+                 int32_t K, int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate,
+                 int32_t nmax) {
+    if (mode == X_SWIGLU)
+        launch_w<BITS, ZP, X_SWIGLU>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+    else if (mode == X_NORM)
+        launch_w<BITS, ZP, X_NORM>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+    else
+        launch_w<BITS, ZP, X_PLAIN>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+}
+
+int32_t log2_exact(int32_t v) {
+    int32_t s = 0;
+    while ((1 << s) < v) ++s;
+    return (1 << s) == v ? s : -1;
+}
+
+}  // namespace
+
+int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits) {
+    const int64_t sets = ceil_div(columns, SET), chunks = ceil_div(rows, CHUNK);
+    return sets * chunks * block_bytes(bits);
+}
+
+int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st) {
+    const int32_t chunks = ceil_div(w.K, CHUNK);
+    const int64_t dwords = packed_bytes(w.K, w.N, w.bits) / 4;
+    int64_t blocks = (dwords + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    pack_kernel<<<static_cast<uint32_t>(blocks), 256, 0, st>>>(w.q, w.K, w.N, w.bits, w.bpr, chunks, dwords,
+                                                               static_cast<uint32_t*>(packed));
+    KT_LAUNCHED("qweight pack kernel");
+    return KT_OK;
+}
+
+void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring) {
+    g_forced.ks = ks == 1 || ks == 2 || ks == 4 || ks == 8 ? ks : 0;
+    g_forced.waves = waves == 4 || waves == 8 ? waves : 0;
+    g_forced.ring = ring == 4 ? 1 : ring == 8 ? 2 : 0;
+}
+
+namespace {
+
+// Largest LDS block the device gives a workgroup (cached per device).
+size_t lds_limit() {
+    static int32_t cached[64] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 64 << 10;
+    if (!cached[device]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess || v <= 0)
+            v = 64 << 10;
+        cached[device] = v;
+    }
+    return static_cast<size_t>(cached[device]);
+}
+
+struct PackedPlan {
+    int32_t waves = 0, ks = 0, nmax = 0;
+    size_t lds = 0;
+};
+
+// Waves per workgroup and K-parts per column set for a launch over weights with K rows,
+// groups of g, the smallest N min_n and sets_total column sets in all: the K range of a
+// column set is split over ks waves, the smallest power of two that keeps a wave's range
+// within 2048 (its x in registers) and gives about four waves per CU (at least two
+// chunks per wave); four waves per workgroup, eight when ks is 8. ks = 0 when nothing
+// fits (a workgroup's column sets must lie inside the weight, its waves' areas in LDS).
+PackedPlan plan_packed(int32_t K, int32_t g, int32_t min_n, int64_t sets_total) {
+    PackedPlan p;
+    const int32_t chunks = ceil_div(K, CHUNK);
+    int32_t ks = 1;
+    while (ks < 8 && ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) ks *= 2;
+    if (ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) return p;
+    if (g_forced.ks) {
+        if (g_forced.ks < ks) return p;
+        ks = g_forced.ks;
+    } else {
+        const int64_t target = 4LL * cu_count();
+        while (ks < 8 && 2 * ks <= chunks / 2 && sets_total * ks < target) ks *= 2;
+    }
+    if (ks > chunks) return p;
+    int32_t waves = g_forced.waves ? g_forced.waves : (ks > 4 ? 8 : 4);
+    if (ks > waves) return p;
+    if (waves / ks * SET > min_n) {  // fewer column sets per workgroup: split K further
+        while (ks < waves && waves / ks * SET > min_n && 2 * ks <= chunks) ks *= 2;
+        if (waves / ks * SET > min_n) return p;
+    }
+    const int32_t nmax = ceil_div(chunks, ks);
+    const size_t lds = static_cast<size_t>(waves) * wave_bytes(nmax, wave_groups(nmax, g)) +
+                       static_cast<size_t>(waves) * (SET + 1) * sizeof(float);
+    if (lds > lds_limit()) return p;
+    p.waves = waves;
+    p.ks = ks;
+    p.nmax = nmax;
+    p.lds = lds;
+    return p;
+}
+
+}  // namespace
+
+bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
+    (void)c;
+    if (m != 1 || !w.p) return false;
+    if (w.K % RUN != 0 || w.K > MAX_K) return false;             // whole runs; the digits fit LDS
+    if (w.g % RUN != 0 || log2_exact(w.g / RUN) < 0) return false;  // a run lies in one group
+    if (w.N % SET != 0) return false;                             // whole column sets
+    if (!aligned(w.p, 16) || !aligned(a, 16) || !aligned(w.s, 16) || (w.z && !aligned(w.z, 16))) return false;
+    // some workgroup shape fits (tiny K with few columns has none: K cannot be split
+    // below one chunk, and a workgroup's column sets must lie inside the weight)
+    return plan_packed(w.K, w.g, w.N, w.N / SET).ks != 0;
+}
+
+int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                           int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up,
+                           const float* norm_weight, float eps) {
+    const WeightView& w0 = ws[0];
+    bool zp = false;
+    for (int32_t i = 0; i < count; ++i) zp = zp || ws[i].z != nullptr;
+    if (zp)
+        for (int32_t i = 0; i < count; ++i)
+            if (!ws[i].z) return fail(KT_ERR_ARGUMENT, "grouped weights must all have zero points or none");
+    if (up && norm_weight) return fail(KT_ERR_ARGUMENT, "packed gemv: one input transform at a time");
+    const int mode = up ? X_SWIGLU : norm_weight ? X_NORM : X_PLAIN;
+    if (mode != X_PLAIN && !aligned(up ? up : norm_weight, 16))
+        return fail(KT_ERR_ARGUMENT, "packed gemv: the gate's up row or the RMSNorm weight must be 16-byte aligned");
+    int64_t sets_total = 0, sets_max = 0;
+    int32_t min_n = w0.N;
+    for (int32_t i = 0; i < count; ++i) {
+        const int64_t sets = ws[i].N / SET;
+        sets_total += sets;
+        if (sets > sets_max) sets_max = sets;
+        if (ws[i].N < min_n) min_n = ws[i].N;
+    }
+    const PackedPlan plan = plan_packed(w0.K, w0.g, min_n, sets_total);
+    if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed gemv: no workgroup shape fits K = %d, g = %d", w0.K, w0.g);
+    const int32_t per_wg = plan.waves / plan.ks;
+    const int32_t n_chunks = plan.nmax;
+
+    PJobs jobs{};
+    jobs.count = count;
+    for (int32_t i = 0; i < count; ++i) {
+        PJob& jb = jobs.job[i];
+        jb.packed = ws[i].p;
+        jb.s = ws[i].s;
+        jb.z = ws[i].z;
+        jb.out = cs[i];
+        jb.bias = biases ? biases[i] : nullptr;
+        jb.N = ws[i].N;
+        jb.sets = ws[i].N / SET;
+    }
+    const dim3 grid(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)), static_cast<uint32_t>(count));
+    const int32_t gshift = log2_exact(w0.g / RUN);
+    const float* aux = up ? up : norm_weight;
+    if (w0.bits == 4)
+        launch_mode<4, true>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
+                             accumulate, n_chunks);
+    else if (zp)
+        launch_mode<8, true>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
+                             accumulate, n_chunks);
+    else
+        launch_mode<8, false>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
+                              accumulate, n_chunks);
+    KT_LAUNCHED("qmatmul: packed gemv kernel");
+    return KT_OK;
+}
+
+}  // namespace kt

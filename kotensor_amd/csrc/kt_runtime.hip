@@ -230,6 +230,7 @@ int32_t view_weight(const kt_qweight* w, WeightView* v) {
     v->q = static_cast<const uint8_t*>(w->qdata);
     v->s = w->scales;
     v->z = reinterpret_cast<const int8_t*>(w->zeros);
+    v->p = static_cast<const uint8_t*>(w->packed);
     v->K = w->rows;
     v->N = w->columns;
     v->bits = w->bits;
@@ -272,12 +273,12 @@ int32_t kt_set_device(int32_t device) {
 }
 
 // 0: automatic, 1: vector-ALU kernel, 2: MFMA row-block kernel, 3: MFMA wide-strip kernel,
-// 4: column-strip latency kernel.
+// 4: column-strip latency kernel, 5: column-run kernel (packed copy).
 static int32_t g_gemv_kind = 0;
 
 int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits, int32_t gemv_waves,
                              int32_t gemv_reduce) {
-    if (gemv_kind < 0 || gemv_kind > 4) return fail(KT_ERR_ARGUMENT, "gemv_kind must be 0 to 4, got %d", gemv_kind);
+    if (gemv_kind < 0 || gemv_kind > 5) return fail(KT_ERR_ARGUMENT, "gemv_kind must be 0 to 5, got %d", gemv_kind);
     if (gemv_vec != 0 && gemv_vec != 4 && gemv_vec != 8)
         return fail(KT_ERR_ARGUMENT, "gemv_vec must be 0, 4 or 8, got %d", gemv_vec);
     if (gemv_splits < 0) return fail(KT_ERR_ARGUMENT, "gemv_splits must be >= 0, got %d", gemv_splits);
@@ -289,6 +290,7 @@ int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_s
     set_gemv_reduce_mode(gemv_reduce);
     set_gemv_mfma_config(gemv_splits, gemv_waves, gemv_reduce, gemv_kind == 1);
     set_gemv_wide_config(gemv_splits, gemv_waves);
+    set_gemv_packed_config(gemv_splits, gemv_waves, gemv_vec);
     g_gemv_kind = gemv_kind;
     return KT_OK;
 }
@@ -422,6 +424,23 @@ int32_t kt_qweight_check(const kt_qweight* w) {
     return view_weight(w, &v);
 }
 
+int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int64_t* bytes) {
+    if (!bytes) return fail(KT_ERR_ARGUMENT, "bytes is NULL");
+    if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
+    if (rows <= 0 || columns <= 0) return fail(KT_ERR_SHAPE, "QuantizedTensor needs a 2-D shape, got [%d, %d]", rows, columns);
+    *bytes = packed_bytes(rows, columns, bits);
+    return KT_OK;
+}
+
+int32_t kt_qweight_pack(const kt_qweight* w, void* packed, void* stream) {
+    WeightView v;
+    int32_t status = view_weight(w, &v);
+    if (status) return status;
+    if (!packed) return fail(KT_ERR_ARGUMENT, "packed is NULL");
+    if (!aligned(packed, 16)) return fail(KT_ERR_ARGUMENT, "packed must be 16-byte aligned");
+    return launch_pack(v, packed, static_cast<hipStream_t>(stream));
+}
+
 int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
                     void* qdata, float* scales, uint8_t* zeros, void* stream) {
     if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
@@ -455,6 +474,8 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
     if (!a || !c) return fail(KT_ERR_ARGUMENT, "matmul with a NULL input or output");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const float* biases[1] = {bias};
+    if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_packed_supported(a, m, v, c))
+        return launch_gemv_packed(a, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 4 || (g_gemv_kind == 0 && gemv_strip_preferred(&v, 1))) && gemv_strip_supported(a, m, v, c))
         return launch_gemv_strip(a, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 3 || (g_gemv_kind == 0 && gemv_wide_preferred(&v, 1))) && gemv_wide_supported(a, m, v, c))
@@ -479,6 +500,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         bool mfma = m >= 1 && m <= 16 && a != nullptr;
         bool wide = (g_gemv_kind == 0 || g_gemv_kind == 3) && a != nullptr;
         bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
+        bool packed = (g_gemv_kind == 0 || g_gemv_kind == 5) && a != nullptr;
         bool gemm = m > 2 && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
@@ -492,6 +514,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             mfma = mfma && gemv_mfma_supported(a, m, v, outputs[start + i]);
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
             strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
+            packed = packed && gemv_packed_supported(a, m, v, outputs[start + i]);
             gemm = gemm && gemm_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 16)) &&
                    (v.z != nullptr) == (views[0].z != nullptr);
         }
@@ -501,7 +524,10 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         int32_t status = KT_OK;
         if (strip && g_gemv_kind == 0 && !gemv_strip_preferred(views, n)) strip = false;
         if (wide && g_gemv_kind == 0 && !gemv_wide_preferred(views, n)) wide = false;
-        if (strip) {
+        if (packed) {
+            status = launch_gemv_packed(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,
+                                        alpha, st);
+        } else if (strip) {
             status = launch_gemv_strip(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
         } else if (wide) {
             status = launch_gemv_wide(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);

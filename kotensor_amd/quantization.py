@@ -68,8 +68,9 @@ class QuantizedTensor:
                                                          "entries", stream)
         if self.bits == 4 and not self.has_zero_points:
             raise _lib.IllegalArgumentException("4-bit tensors need zero points")
+        self._p = None
         self._struct = _lib.QWeight(self._q.ptr, self._s.ptr, self._z.ptr if self._z else None,
-                                    self.rows, self.columns, self.bits, self.group_size)
+                                    self.rows, self.columns, self.bits, self.group_size, None)
         _lib.call("kt_qweight_check", ctypes.byref(self._struct))
 
     @staticmethod
@@ -112,6 +113,33 @@ class QuantizedTensor:
     @property
     def zeros_buffer(self) -> DeviceBuffer | None:
         return self._z
+
+    @property
+    def packed_buffer(self) -> DeviceBuffer | None:
+        """The column-run copy of qdata written by :meth:`pack`, or None."""
+        return self._p
+
+    def pack(self, stream: Stream | None = None) -> "QuantizedTensor":
+        """Writes the device-native column-run copy of qdata (``kt_qweight_pack``) and
+        points the weight at it, so one-row products read it instead of qdata. qdata stays
+        the format of record (files, accessors, products of more rows). Costs
+        ``kt_qweight_packed_bytes`` more device memory (about the size of qdata); call it
+        again after qdata changes. Returns self."""
+        n = ctypes.c_int64()
+        _lib.call("kt_qweight_packed_bytes", self.rows, self.columns, self.bits, ctypes.byref(n))
+        if self._p is None or self._p.nbytes != n.value:
+            self._p = DeviceBuffer(n.value)
+        self._struct.packed = None
+        _lib.call("kt_qweight_pack", ctypes.byref(self._struct), self._p.ptr, (stream or default_stream()).handle)
+        self._struct.packed = self._p.ptr
+        return self
+
+    def unpack(self) -> None:
+        """Drops the column-run copy (one-row products read qdata again)."""
+        self._struct.packed = None
+        if self._p is not None:
+            self._p.free()
+            self._p = None
 
     # -- host copies (QuantizedTensor.kt:72-92) -----------------------------------
     @property
@@ -208,6 +236,7 @@ class QuantizedTensor:
         return QuantizedTensor(q, s, z, (rows, columns), quantization.bits, quantization.group_size)
 
     def free(self) -> None:
+        self.unpack()
         for b in (self._q, self._s, self._z):
             if b is not None:
                 b.free()

@@ -226,7 +226,7 @@ class Transformer:
                  hidden_dimension: int | None = None, num_key_value_heads: int | None = None,
                  norm_eps: float = 1e-6, rope_theta: float = 10000.0, rope_scaling: RoPEScaling | None = None,
                  quantization: Quantization | None = None, seed: int | None = 0, init_std: float = 0.02,
-                 stream: Stream | None = None):
+                 stream: Stream | None = None, packed: bool = True):
         hidden_dimension = 4 * dimension if hidden_dimension is None else hidden_dimension
         num_key_value_heads = num_heads if num_key_value_heads is None else num_key_value_heads
         if dimension % num_heads != 0:
@@ -260,6 +260,17 @@ class Transformer:
             self.set_parameter(f"block.{l}.norm2.weight", np.ones(dimension, np.float32), stream)
         self.set_parameter("finalNorm.weight", np.ones(dimension, np.float32), stream)
         self._graph = None
+        # column-run copies of the projections for the one-row (decode) products
+        self.packed = packed
+        if packed and seed is not None:
+            self.pack_weights(stream)
+
+    def pack_weights(self, stream: Stream | None = None) -> None:
+        """Writes the column-run copy of every projection weight (QuantizedTensor.pack), which
+        the decode step's one-row products read; prefill chunks read the reference layout."""
+        for name in self.projection_shapes():
+            self.weights[name].pack(stream)
+        self.packed = True
 
     # -- construction --------------------------------------------------------------------
     def projection_shapes(self) -> dict:
@@ -300,6 +311,8 @@ class Transformer:
         if (weight.rows, weight.columns) != want:
             raise _lib.IllegalArgumentException(
                 f"Quantized weight is {weight.rows} × {weight.columns}, layer is {want[0]} × {want[1]}")
+        if self.packed and name != "embedding":
+            weight.pack()
         self.weights[name] = weight
 
     def tie_embedding_to_head(self) -> "Transformer":
@@ -371,6 +384,8 @@ class Transformer:
             for name in list(model.weights):
                 k, n = (model.vocabulary_size, model.dimension) if name == "embedding" else model.projection_shapes()[name]
                 model.weights[name] = f.load_quantized(name, q, k, n, stream)
+            if model.packed:
+                model.pack_weights(stream)
             return model
 
     # -- caches and buffers -------------------------------------------------------------

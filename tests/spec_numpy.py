@@ -97,3 +97,30 @@ def decode(qdata, scales, zeros, K, N, bits, group_size) -> np.ndarray:
     else:
         z = np.asarray(zeros).view(np.int8).reshape(G, N)[gidx].astype(np.int32)
     return (s * (raw - z).astype(np.float32)).astype(np.float32)
+
+
+def pack_column_runs(qdata, K: int, N: int, bits: int) -> np.ndarray:
+    """The column-run copy of qdata (kt_qweight_pack), restated with numpy reshapes.
+
+    Blocks [column set of 16][chunk of 128 k]; in a block, lane l = 16 kb + n owns 16
+    bytes (INT8: two halves of 1 KB, lane bytes at h * 1024 + 16 l) for column 16 set + n
+    and k in [128 chunk + 32 kb, + 32). INT8 byte b of half h is k = run + 16 h + b;
+    INT4 byte 8 m + 4 hh + t holds k = run + 16 m + 8 hh + t (low nibble) and that k + 4
+    (high nibble). Values outside [K x N] are 0."""
+    bpr = (N + N % 2) // 2 if bits == 4 else N
+    q = np.asarray(qdata).view(np.uint8).reshape(K, bpr)
+    if bits == 8:
+        vals = q[:, :N]
+    else:
+        vals = np.empty((K, N), dtype=np.uint8)
+        vals[:, :bpr] = q[:, :bpr] & 0xF
+        vals[:, bpr:] = (q[:, :N - bpr] >> 4) & 0xF
+    sets, chunks = -(-N // 16), -(-K // 128)
+    V = np.zeros((chunks * 128, sets * 16), dtype=np.uint8)
+    V[:K, :N] = vals
+    if bits == 8:
+        R = V.reshape(chunks, 4, 2, 16, sets, 16)           # c, kb, h, b, set, n
+        return np.ascontiguousarray(R.transpose(4, 0, 2, 1, 5, 3)).reshape(-1)  # set, c, h, kb, n, b
+    R = V.reshape(chunks, 4, 2, 2, 2, 4, sets, 16)          # c, kb, m, hh, lohi, t, set, n
+    byte = R[:, :, :, :, 0] | (R[:, :, :, :, 1] << 4)       # c, kb, m, hh, t, set, n
+    return np.ascontiguousarray(byte.transpose(5, 0, 1, 6, 2, 3, 4)).reshape(-1)  # set, c, kb, n, m, hh, t

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.kt_abi_version() == 1
+    assert lib.kt_abi_version() == 2
     assert kotensor_amd.LIBRARY_PATH.name == "libkotensor_hip.so"
 
 
@@ -72,13 +72,23 @@ def test_argument_errors_map_to_illegal_argument():
     assert lib.kt_qmatmul(fake, -1, ctypes.byref(w), fake, 0, ctypes.c_float(1.0), None) == _lib.KT_ERR_ARGUMENT
     assert "Negative row count" in _lib.last_error()
     assert lib.kt_qmatmul(fake, 0, ctypes.byref(w), fake, 0, ctypes.c_float(1.0), None) == _lib.KT_OK
-    assert lib.kt_set_kernel_config(5, 0, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_set_kernel_config(6, 0, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 5, 0, 0, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 0, 0, 3, 0) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 0, 0, 0, 3) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_set_kernel_config(0, 0, 0, 0, 0) == _lib.KT_OK
     buf = ctypes.create_string_buffer(8)
     assert lib.kt_last_error(buf, 8) == 0 and len(buf.value) <= 7
+    # the column-run copy: size formula, and its checks before any device access
+    n = ctypes.c_int64()
+    assert lib.kt_qweight_packed_bytes(4096, 14336, 4, ctypes.byref(n)) == _lib.KT_OK
+    assert n.value == (14336 // 16) * (4096 // 128) * 1024
+    assert lib.kt_qweight_packed_bytes(300, 2100, 8, ctypes.byref(n)) == _lib.KT_OK
+    assert n.value == 132 * 3 * 2048  # ceil(2100 / 16) sets, ceil(300 / 128) chunks
+    assert lib.kt_qweight_packed_bytes(300, 2100, 5, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qweight_pack(ctypes.byref(w), None, None) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qweight_pack(ctypes.byref(w), ctypes.c_void_p(8), None) == _lib.KT_ERR_ARGUMENT
+    assert "16-byte aligned" in _lib.last_error()
 
 
 def test_product_does_not_reach_the_oracle():

@@ -167,3 +167,37 @@ def test_golden_fixtures_reproduce(oracle_lib):
         x = data[f"{name}.x"]
         assert np.array_equal(oracle_lib.multiply_quantized(x, q, 3), data[f"{name}.y3"]), name
         assert np.array_equal(oracle_lib.multiply_quantized(x[:1], q, 1), data[f"{name}.y1"]), name
+
+
+def test_column_run_spec_matches_its_definition():
+    """tests/spec_numpy.pack_column_runs (reshapes) against the layout's per-byte
+    definition, on ragged INT4/INT8 shapes with random bytes."""
+    from spec_numpy import pack_column_runs
+    rng = np.random.default_rng(0)
+    for K, N, bits in [(300, 2100, 4), (300, 2100, 8), (128, 16, 8), (200, 33, 4), (70, 9, 4)]:
+        bpr = (N + N % 2) // 2 if bits == 4 else N
+        q = rng.integers(0, 256, size=K * bpr, dtype=np.uint8)
+        Q = q.reshape(K, bpr)
+        if bits == 4 and N % 2:
+            Q[:, -1] &= 0x0F  # the pad nibble is 0
+
+        def val(k, c):
+            if k >= K or c >= N:
+                return 0
+            if bits == 8:
+                return int(Q[k, c])
+            return int(Q[k, c] & 15) if c < bpr else int(Q[k, c - bpr] >> 4)
+
+        P = pack_column_runs(q, K, N, bits)
+        sets, chunks, BB = -(-N // 16), -(-K // 128), 1024 if bits == 4 else 2048
+        assert P.size == sets * chunks * BB
+        for _ in range(2000):
+            s, c, lane = rng.integers(sets), rng.integers(chunks), rng.integers(64)
+            col, run = 16 * s + (lane & 15), 128 * c + 32 * (lane >> 4)
+            if bits == 8:
+                h, b = rng.integers(2), rng.integers(16)
+                assert P[(s * chunks + c) * BB + h * 1024 + 16 * lane + b] == val(run + 16 * h + b, col)
+            else:
+                d, t = rng.integers(4), rng.integers(4)
+                k = run + 16 * (d >> 1) + 8 * (d & 1) + t
+                assert P[(s * chunks + c) * BB + 16 * lane + 4 * d + t] == val(k, col) | (val(k + 4, col) << 4)
