@@ -85,10 +85,11 @@ int32_t kt_set_device(int32_t device);
  *            MFMA kernel for M == 1, 4 = column-strip kernel for M == 1, 5 = column-run
  *            kernel for M == 1 (needs the packed copy);
  * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic); for the
- *            column-run kernel, the weights in flight per wave (4: 8 KB, 8: 16 KB);
+ *            column-run kernel, the KB of weights in flight per wave (4 or 8);
  * gemv_splits: workgroups along K per column tile (0 = automatic); for the column-run
  *            kernel, the waves that split the K range of a column set (1, 2, 4 or 8);
- * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic);
+ * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic; the column-run kernel
+ *            always runs eight);
  * gemv_reduce: how split sums meet (0 = automatic, 1 = a second kernel, 2 = inside the
  * kernel). Process-wide. */
 int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits,

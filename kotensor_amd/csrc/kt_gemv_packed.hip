@@ -8,8 +8,8 @@
 // and at shapes like 4096 -> 14336 there are too few strips to occupy 256 CUs: the K
 // range has to be split over workgroups whose partial sums then meet through memory,
 // several dependent round trips after the last load. In the column-run layout a column's
-// K values are contiguous, so a wave owns whole columns over all of K: no sums leave a
-// workgroup, every load instruction reads 1 KB of consecutive bytes, and the number of
+// K values are contiguous, so a workgroup owns whole columns over all of K: no sums
+// leave it, every load instruction reads 1 KB of consecutive bytes, and the number of
 // workgroups is set by N alone. The copy is made once per weight (kt_qweight_pack) next
 // to the reference bytes, which stay the format of record (quantize, files, accessors
 // and the M > 1 kernels read them).
@@ -33,14 +33,17 @@
 //     run's 16 k of 16 columns, A row 4 kb + p holds digit p of that run's x (rows of
 //     other lane groups' runs are 0), so one MFMA gives every lane group the four digit
 //     sums of its own run: D_p = sum d_p q, exact in int32 (two MFMAs per run);
-//   * per run: u = ((D_0 / 256 + D_1) / 256 + D_2) / 256 + D_3 in fp32, sum x q =
-//     u * 2^(E - 6), and y += scale * (sum x q - zero * sum x): the reference's
-//     combineGroup, scale * (acc - zero * rowSum) (MatMul.kt:804-828), applied per run;
+//   * per run: u = (D_2 + 256 D_3) + (D_0 + 256 D_1) / 2^16 (digit pairs added in int32,
+//     then one fp32 fma), sum x q = u * 2^(E - 14), and y += scale * (sum x q - zero *
+//     sum x): the reference's combineGroup, scale * (acc - zero * rowSum)
+//     (MatMul.kt:804-828), applied per run;
 //   * the four lanes of a column (its four runs of a chunk) and the waves that split K
 //     meet by fixed-order sums inside the workgroup.
 // A column's result therefore depends only on x and that column's weights, never on
 // how the columns or the K range are divided among waves.
 #include "kt_common.h"
+#include <algorithm>
+#include <type_traits>
 
 namespace kt {
 namespace {
@@ -143,156 +146,141 @@ __device__ __forceinline__ float sum8(float v) {
 constexpr int X_PLAIN = 0, X_SWIGLU = 1, X_NORM = 2;
 
 
-// Every wave works on its own: it copies its own columns' scales and zero points into
-// its own LDS area, loads x only for its own K range, turns it into digits there and
-// starts multiplying as soon as its first chunk of weights lands. No barrier comes
-// before the main loop (a workgroup-wide preparation would hold every wave until the
-// slowest wave's x and scales arrived, behind the first wave of weight loads of all
-// workgroups, and no refill would go out in that time). The waves of a workgroup meet
-// once, at the end, to add the K-parts of a column in fixed order.
-// One global_load_lds_dwordx4: lane l's 16 bytes at g land at LDS byte address lds + 16 l
-// (lds wave-uniform), with no registers in between. Inline assembly, so the compiler
-// does not count it among its loads: its own waits for later loads stay correct (they
-// count fewer loads than are outstanding, so they wait at least as long as needed), and
-// the kernel orders these copies itself by issuing them before any load it waits for
-// (loads complete in issue order). m0 is written here and used by nothing else.
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory");
+// A workgroup of W = 8 waves owns W / ks column sets over all of K; each wave streams
+// one column set over one of the ks K-parts. The workgroup first turns all of x into
+// digits together (every wave a slice of K, the loads ahead of the weights), meets once
+// at a barrier, and from then on every wave streams its own chunks without waiting for
+// another; the K-parts of a column set add in fixed order in LDS at the end. (Digits made
+// by each wave for its own K-part alone, or units of one wave meeting through memory,
+// were measured slower: more x traffic ahead of the first weights, or a memory round trip
+// after the last.)
+// Calls f(std::integral_constant<int, I>) for I = B .. E - 1, so register arrays indexed by
+// I stay in registers.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
-constexpr int MAX_WAVE_CHUNKS = 16;                      // a wave's K range: at most 2048
-constexpr int X_SLOTS = MAX_WAVE_CHUNKS * CHUNK / 256;  // float4s of x per lane
+constexpr int W = 8;                  // waves per workgroup
+constexpr int MAX_WAVE_CHUNKS = 16;   // a wave's K range: at most 2048
+constexpr int X_SLOTS = MAX_K / (256 * W);  // float4s of x per thread
 
-// A wave's LDS area for waves of at most nmax chunks: digits [4][nmax * 128], 32 zero
-// bytes, run records [nmax * 4] x 8 bytes, scales [gw][16] fp32, zero points [gw][16].
-__host__ __device__ constexpr int32_t wave_digit_bytes(int32_t nmax) { return 4 * nmax * CHUNK; }
-__host__ __device__ constexpr int32_t wave_rec_offset(int32_t nmax) { return wave_digit_bytes(nmax) + ZERO_BYTES; }
-__host__ __device__ constexpr int32_t wave_scale_offset(int32_t nmax) {
-    return wave_rec_offset(nmax) + nmax * (CHUNK / RUN) * 8;
-}
-__host__ __device__ constexpr int32_t wave_bytes(int32_t nmax, int32_t gw) {
-    return wave_scale_offset(nmax) + gw * SET * 5 + ((16 - (gw * SET * 5) % 16) % 16);
-}
-// Groups a K range of nmax chunks can touch (one more when it starts inside a group).
-__host__ __device__ constexpr int32_t wave_groups(int32_t nmax, int32_t g) { return (nmax * CHUNK + g - 1) / g + 1; }
+// The workgroup's LDS: digit rows [4][kp] (kp = 128 chunks bytes), 32 zero bytes, run
+// records [4 chunks] x 8 bytes, then the meeting area: [W][16] sums and [W] sums of squares.
+__host__ __device__ constexpr int32_t lds_rec_offset(int32_t chunks) { return 4 * chunks * CHUNK + ZERO_BYTES; }
+__host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return lds_rec_offset(chunks) + chunks * (CHUNK / RUN) * 8; }
+__host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
 
-template <int BITS, int W, int R, bool ZP, int XMODE>
+template <int BITS, int R, bool ZP, int XMODE>
 __global__ void __launch_bounds__(64 * W)
     gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
-                       PJobs jobs, int32_t ks, int32_t nmax, float alpha, int32_t accumulate) {
+                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
+    // Everything below is shifts and masks of the arguments (K-parts and group sizes are
+    // powers of two), so the first loads go out one argument fetch after the start.
     const PJob jb = jobs.job[blockIdx.y];
-    asm volatile("" ::"s"(jb.packed), "s"(jb.s), "s"(jb.z), "s"(jb.N), "s"(jb.sets), "s"(x), "s"(K), "s"(ks));
-    const int32_t cs = W / ks;  // column sets per workgroup
-    const int32_t set0 = blockIdx.x * cs;
+    const int32_t tid = threadIdx.x, ln = tid & 63;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int32_t cslog = 3 - kslog;  // column sets per workgroup: 1 << cslog
+    const int32_t set0 = blockIdx.x << cslog;
     if (set0 >= jb.sets) return;
-
-    const int32_t ln = threadIdx.x & 63;
-    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int32_t my_cs = wave % cs, kp = wave / cs;
+    const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
     const bool set_live = set0 + my_cs < jb.sets;
     const int32_t set = set_live ? set0 + my_cs : jb.sets - 1;  // a dead wave computes a copy, never writes
-    const int32_t chunks = (K + CHUNK - 1) / CHUNK;
-    const int32_t G = (K + (RUN << gshift) - 1) / (RUN << gshift);  // quantization groups
-    const int32_t c_begin = kp * chunks / ks;
-    const int32_t n = (kp + 1) * chunks / ks - c_begin;  // chunks of this wave, 1 .. nmax
+    const int32_t chunks = (K + CHUNK - 1) >> 7;
+    const int32_t G = (K + (RUN << gshift) - 1) >> (gshift + 5);  // quantization groups
+    const int32_t c_begin = (kp * chunks) >> kslog;
+    const int32_t n = (((kp + 1) * chunks) >> kslog) - c_begin;  // chunks of this wave, 1 .. nmax
     const int32_t k0 = c_begin * CHUNK;
     const int32_t nl = ln & 15, kb = ln >> 4;
     const int32_t col = set * SET + nl;
-    // groups of this wave's runs (the last chunk's padding runs take the last group)
-    const int32_t g_first = k0 >> (gshift + 5);
-    const int32_t gw = min((k0 + n * CHUNK - 1) >> (gshift + 5), G - 1) - g_first + 1;
+    const int32_t kpad = chunks * CHUNK;  // digit row stride
 
-    // the wave's LDS area
-    const int32_t gwmax = wave_groups(nmax, RUN << gshift);
-    unsigned char* area = smem + wave * wave_bytes(nmax, gwmax);
-    int8_t* xd = reinterpret_cast<int8_t*>(area);
-    const int32_t ds = nmax * CHUNK;  // digit row stride
-    const int32_t zoff = wave_digit_bytes(nmax);
-    int2* rec = reinterpret_cast<int2*>(area + wave_rec_offset(nmax));
-    float* ssc = reinterpret_cast<float*>(area + wave_scale_offset(nmax));
-    uint8_t* szz = reinterpret_cast<uint8_t*>(ssc + gwmax * SET);
-
-    // ---- loads: scales and zero points straight into LDS, x into registers, then the
-    // first R chunks of weights. Loads complete in issue order, so the wait for x covers
-    // the LDS copies, and the wait for the first chunk covers x; x loads are unconditional
-    // (indices past the range clamped), so the waits for x never extend to the weights.
-    {
-        const uint32_t sc_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ssc));
-        const int32_t pieces = gw * 4;  // 16-byte pieces of the scale rows (16 floats each)
-#pragma unroll
-        for (int j = 0; j < (wave_groups(MAX_WAVE_CHUNKS, RUN) * 4 + 63) / 64; ++j) {
-            const int32_t p0 = 64 * j;
-            if (p0 < pieces) {
-                const int32_t p = min(p0 + ln, pieces - 1);
-                const float* src = jb.s + static_cast<int64_t>(g_first + (p >> 2)) * jb.N + set * SET + 4 * (p & 3);
-                if (p0 + ln < pieces) lds_dma16(src, sc_lds + 16 * p0);
-            }
-        }
-        if constexpr (ZP) {
-            const uint32_t z_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(szz));
-#pragma unroll
-            for (int j = 0; j < (wave_groups(MAX_WAVE_CHUNKS, RUN) + 63) / 64; ++j) {
-                const int32_t p0 = 64 * j;
-                if (p0 < gw) {
-                    const int32_t p = min(p0 + ln, gw - 1);
-                    if (p0 + ln < gw) lds_dma16(jb.z + static_cast<int64_t>(g_first + p) * jb.N + set * SET, z_lds + 16 * p0);
-                }
-            }
-        }
-    }
-    const int32_t n4 = K >> 2, q0 = k0 >> 2, nq = n * (CHUNK / 4);
+    // ---- loads, in the order they complete: this thread's share of x (buffer loads:
+    // slots past the row read zeros without memory traffic), then the first R chunks of
+    // weights with their scales and zero points.
+    const int32_t n4 = K >> 2, kp4 = kpad >> 2;
+    const int32_t used = (kp4 + 64 * W - 1) / (64 * W);  // slots that reach into the digit rows
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, K * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ur =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(XMODE == X_PLAIN ? x : aux), 0, K * 4, 0x00020000);
     float4 xv[X_SLOTS];
     float4 uv[XMODE == X_PLAIN ? 1 : X_SLOTS];
-#pragma unroll
-    for (int j = 0; j < X_SLOTS; ++j) {
-        const int32_t i = min(q0 + min(ln + 64 * j, nq - 1), n4 - 1);
-        xv[j] = reinterpret_cast<const float4*>(x)[i];
-        if constexpr (XMODE != X_PLAIN) uv[j] = reinterpret_cast<const float4*>(aux)[i];
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, X_SLOTS>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j < used) {
+            xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (tid + 64 * W * j) * 16, 0, 0));
+            if constexpr (XMODE != X_PLAIN)
+                uv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, (tid + 64 * W * j) * 16, 0, 0));
+        } else {
+            xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (XMODE != X_PLAIN) uv[j] = xv[j];
+        }
+    });
+
+    int8_t* xd = reinterpret_cast<int8_t*>(smem);
+    const int32_t zoff = 4 * kpad;
+    int2* rec = reinterpret_cast<int2*>(smem + lds_rec_offset(chunks));
+
+    // the wave's blocks are contiguous; chunks past its range read as zeros without
+    // touching memory
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(jb.packed + (static_cast<int64_t>(set) * chunks + c_begin) * BB), 0, n * BB, 0x00020000);
+    // a chunk's scale and zero point for this lane's run and column travel with its
+    // weights (a run past K, padding of the last chunk, takes the last group's: its digits
+    // are zero, so it adds nothing)
+    const __amdgpu_buffer_rsrc_t sr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(jb.s), 0, G * jb.N * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(ZP ? jb.z : reinterpret_cast<const int8_t*>(jb.s)), 0, G * jb.N, 0x00020000);
+    const int32_t run_base = (k0 >> 5) + kb;  // this lane's run in chunk 0 of its range
     u32x4 wb[R][NB];
+    float sc[R];
+    int32_t zz[ZP ? R : 1];
     auto issue = [&](int slot, int32_t cc) {
-        // chunks past this wave's range read as zeros without touching memory
 #pragma unroll
         for (int h = 0; h < NB; ++h)
             wb[slot][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                         wr, cc * BB + h * 1024 + 16 * ln, 0, 0));
+        const int32_t at = min((run_base + cc * (CHUNK / RUN)) >> gshift, G - 1) * jb.N + col;
+        sc[slot] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, at * 4, 0, 0));
+        if constexpr (ZP) zz[slot] = static_cast<int8_t>(__builtin_amdgcn_raw_buffer_load_b8(zr, at, 0, 0));
     };
 #pragma unroll
     for (int s = 0; s < R; ++s) issue(s, s);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- x to digits and run records, in the wave's own area --------------------------
-    if (ln < ZERO_BYTES / 4) reinterpret_cast<uint32_t*>(area + zoff)[ln] = 0u;
-    float nsum = 0.0f;  // X_NORM: this wave's share of sum x^2
-#pragma unroll
-    for (int j = 0; j < X_SLOTS; ++j) {
-        const int32_t i = ln + 64 * j;  // float4 of the wave's range
-        // float4s past the range do nothing; the 8 lanes of a run are all in or all out
-        if (i >= nq) continue;
+    // ---- x to digits and run records, the whole row by the whole workgroup --------------
+    // (float4 slot j of thread t is float4 t + 64 W j of the row; a run's 8 float4s are 8
+    // lanes of one wave). Float4s past the row give zero digits.
+    if (tid < ZERO_BYTES / 4) reinterpret_cast<uint32_t*>(smem + zoff)[tid] = 0u;
+    float nsum = 0.0f;  // X_NORM: this thread's share of sum x^2
+    static_for<0, X_SLOTS>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int32_t i = tid + 64 * W * j;
+        if (j >= used) return;
         float v[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-        const bool in_row = q0 + i < n4;
+        const bool in_row = i < n4;
         if constexpr (XMODE == X_SWIGLU) {
             const float u[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + static_cast<float>(exp(-static_cast<double>(v[e])))) * u[e];
         } else if constexpr (XMODE == X_NORM) {
             const float u[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
-            if (in_row) nsum = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], nsum))));
+            nsum = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], nsum))));
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] *= u[e];
         }
         if (!in_row) v[0] = v[1] = v[2] = v[3] = 0.0f;
         const float mx = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
         const bool finite = mx <= 3.402823466e38f;
-        int e = 0;
-        if (finite && mx > 0.0f) frexpf(mx, &e);
+        const int e = finite && mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) : 0;
         uint32_t dg[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -304,20 +292,28 @@ __global__ void __launch_bounds__(64 * W)
         const uint32_t t01h = __builtin_amdgcn_perm(dg[1], dg[0], 0x07030602u);
         const uint32_t t23l = __builtin_amdgcn_perm(dg[3], dg[2], 0x05010400u);
         const uint32_t t23h = __builtin_amdgcn_perm(dg[3], dg[2], 0x07030602u);
-        uint32_t* xw = reinterpret_cast<uint32_t*>(xd) + i;
-        xw[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
-        xw[ds / 4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
-        xw[2 * (ds / 4)] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
-        xw[3 * (ds / 4)] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
         const float sx = sum8((v[0] + v[1]) + (v[2] + v[3]));
-        if ((ln & 7) == 0) rec[i >> 3] = make_int2(e - 6, __float_as_int(finite ? sx : __builtin_nanf("")));
+        if (i < kp4) {
+            uint32_t* xw = reinterpret_cast<uint32_t*>(xd) + i;
+            xw[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+            xw[kp4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+            xw[2 * kp4] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+            xw[3 * kp4] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
+            if ((ln & 7) == 0) rec[i >> 3] = make_int2(e - 14, __float_as_int(finite ? sx : __builtin_nanf("")));
+        }
+    });
+    float* red = reinterpret_cast<float*>(smem + lds_red_offset(chunks));  // [W][16], then [W] x^2
+    if constexpr (XMODE == X_NORM) {
+        const float w2 = norm_wave_sum(nsum);
+        if (ln == 0) red[W * SET + wave] = w2;
     }
+    __syncthreads();
 
     // ---- main loop: R chunks in flight ----------------------------------------------
     // A: lane (row i = ln % 16, lane group kb) reads digit i % 4 of its own group's run
     // when i / 4 == kb, the zero bytes otherwise.
     const bool diag = (nl >> 2) == kb;
-    const int32_t a_base = diag ? (nl & 3) * ds + kb * RUN : zoff;
+    const int32_t a_base = diag ? (nl & 3) * kpad + k0 + kb * RUN : zoff;
     const int32_t a_step = diag ? CHUNK : 0;
     const uint32_t mask = 0x0F0F0F0Fu;
     float y = 0.0f;
@@ -338,50 +334,42 @@ __global__ void __launch_bounds__(64 * W)
         }
         i32x4 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
-        const int32_t run = cc * (CHUNK / RUN) + kb;  // of the wave's range
-        const int2 rc = rec[run];
-        // a run past K (padding of the last chunk) takes the last group's scale; its
-        // digits are zero, so it adds nothing
-        const int32_t si = min(((k0 >> 5) + run) >> gshift, G - 1) - g_first;
-        const float scale = ssc[si * SET + nl];
-        const float zero = ZP ? static_cast<float>(static_cast<int8_t>(szz[si * SET + nl])) : 0.0f;
-        const float u = fmaf(fmaf(fmaf(static_cast<float>(acc[0]), 1.0f / 256.0f, static_cast<float>(acc[1])),
-                                  1.0f / 256.0f, static_cast<float>(acc[2])),
-                             1.0f / 256.0f, static_cast<float>(acc[3]));
+        const int2 rc = rec[run_base + cc * (CHUNK / RUN)];
+        const float scale = sc[s];
+        const float zero = ZP ? static_cast<float>(zz[s]) : 0.0f;
+        // digit pairs in integer (exact: |D_p| < 2^16 for INT4, so D_0 + 256 D_1 < 2^24;
+        // INT8 sums round once in the conversion), then one fma: u = D_23 + D_01 / 2^16
+        // with D_23 = D_2 + 256 D_3, D_01 = D_0 + 256 D_1; the run record holds E - 14
+        const int32_t d01 = acc[0] + (acc[1] << 8), d23 = acc[2] + (acc[3] << 8);
+        const float u = fmaf(static_cast<float>(d01), 1.0f / 65536.0f, static_cast<float>(d23));
         const float v = fmaf(-zero, __int_as_float(rc.y), ldexpf(u, rc.x));
         y = fmaf(scale, v, y);
     };
-    // whole rounds that refill every slot, then a last round that only drains the ring
-    int32_t base = 0;
-    for (; base + R < n; base += R) {
-#pragma unroll
-        for (int s = 0; s < R; ++s) {
-            process(s, base + s);
-            issue(s, base + s + R);
+    // Unrolled over the largest range so that the ring sits in registers; the wave leaves
+    // at its own chunk count. Refills past the range read zeros without memory traffic
+    // and are never used.
+    static_for<0, MAX_WAVE_CHUNKS>([&](auto ci) {
+        constexpr int c = decltype(ci)::value;
+        if (c < n) {
+            process(c % R, c);
+            if constexpr (c + R < MAX_WAVE_CHUNKS) issue(c % R, c + R);
             __builtin_amdgcn_sched_barrier(0);  // keep each refill right behind its use
         }
-    }
-#pragma unroll
-    for (int s = 0; s < R; ++s)
-        if (base + s < n) process(s, base + s);
+    });
 
-    // ---- the column's four runs, then the waves that split K, in fixed order ----------
+    // ---- the column's four runs, then the K-parts of the column set, in fixed order ----
     y += __shfl_xor(y, 16, 64);
     y += __shfl_xor(y, 32, 64);
-    float* red = reinterpret_cast<float*>(smem + W * wave_bytes(nmax, gwmax));  // [W][16], then [W] x^2
     if (ln < SET) red[wave * SET + ln] = y;
-    if constexpr (XMODE == X_NORM) {
-        const float w2 = norm_wave_sum(nsum);
-        if (ln == 0) red[W * SET + wave] = w2;
-    }
     __syncthreads();
     if (kp != 0 || ln >= SET || !set_live) return;
+    const int32_t ks = 1 << kslog, cs = 1 << cslog;
     float sum = red[my_cs * SET + ln];
     for (int32_t p = 1; p < ks; ++p) sum += red[(p * cs + my_cs) * SET + ln];
     float al = alpha;
     if constexpr (XMODE == X_NORM) {
-        float sq = red[W * SET + my_cs];
-        for (int32_t p = 1; p < ks; ++p) sq += red[W * SET + p * cs + my_cs];
+        float sq = red[W * SET];
+        for (int32_t w = 1; w < W; ++w) sq += red[W * SET + w];
         al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
     }
     float* dst = jb.out + col;
@@ -393,44 +381,36 @@ __global__ void __launch_bounds__(64 * W)
 
 struct Forced {
     int ks = 0;
-    int waves = 0;
-    int ring = 0;  // 1: 8 KB in flight per wave, 2: 16 KB, 0: automatic
+    int ring = 0;  // 1: 4 KB of weights in flight per wave, 2: 8 KB, 0: automatic
 };
 Forced g_forced;
 
-template <int BITS, int W, bool ZP, int XMODE>
-void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
-              int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate, int32_t nmax) {
-    // the ring: 8 KB of weights in flight per wave (16 KB when forced)
-    constexpr int RS = BITS == 4 ? 8 : 4;
-    if (g_forced.ring == 2)
-        gemv_packed_kernel<BITS, W, 2 * RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
-    else if (g_forced.ring == 1 || nmax > RS / 2)
-        gemv_packed_kernel<BITS, W, RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
-    else
-        gemv_packed_kernel<BITS, W, RS / 2, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, ks, nmax, alpha, accumulate);
-}
-
 template <int BITS, bool ZP, int XMODE>
-void launch_w(int w, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
-              int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate, int32_t nmax) {
-    if (w == 8) launch_r<BITS, 8, ZP, XMODE>(grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
-    else launch_r<BITS, 4, ZP, XMODE>(grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+    // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
+    constexpr int RS = BITS == 4 ? 4 : 2;
+    if (g_forced.ring == 2)
+        gemv_packed_kernel<BITS, 2 * RS, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+    else if (g_forced.ring == 1 || nmax > RS / 2)
+        gemv_packed_kernel<BITS, RS, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+    else
+        gemv_packed_kernel<BITS, RS / 2, ZP, XMODE>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
 }
 
 template <int BITS, bool ZP>
-void launch_mode(int mode, int w, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
-                 int32_t K, int32_t gshift, const PJobs& jobs, int32_t ks, float alpha, int32_t accumulate,
+void launch_mode(int mode, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
+                 int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate,
                  int32_t nmax) {
     if (mode == X_SWIGLU)
-        launch_w<BITS, ZP, X_SWIGLU>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_SWIGLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
     else if (mode == X_NORM)
-        launch_w<BITS, ZP, X_NORM>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_NORM>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
     else
-        launch_w<BITS, ZP, X_PLAIN>(w, grid, lds, st, x, aux, eps, K, gshift, jobs, ks, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_PLAIN>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
 }
 
 int32_t log2_exact(int32_t v) {
@@ -459,7 +439,7 @@ int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st) {
 
 void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring) {
     g_forced.ks = ks == 1 || ks == 2 || ks == 4 || ks == 8 ? ks : 0;
-    g_forced.waves = waves == 4 || waves == 8 ? waves : 0;
+    (void)waves;  // eight per workgroup
     g_forced.ring = ring == 4 ? 1 : ring == 8 ? 2 : 0;
 }
 
@@ -480,41 +460,32 @@ size_t lds_limit() {
 }
 
 struct PackedPlan {
-    int32_t waves = 0, ks = 0, nmax = 0;
+    int32_t ks = 0, nmax = 0;
     size_t lds = 0;
 };
 
-// Waves per workgroup and K-parts per column set for a launch over weights with K rows,
-// groups of g, the smallest N min_n and sets_total column sets in all: the K range of a
-// column set is split over ks waves, the smallest power of two that keeps a wave's range
-// within 2048 (its x in registers) and gives about four waves per CU (at least two
-// chunks per wave); four waves per workgroup, eight when ks is 8. ks = 0 when nothing
-// fits (a workgroup's column sets must lie inside the weight, its waves' areas in LDS).
-PackedPlan plan_packed(int32_t K, int32_t g, int32_t min_n, int64_t sets_total) {
+// K-parts per column set for a launch over weights with K rows, groups of g and
+// sets_total column sets in all: the smallest power of two that keeps a wave's range
+// within 2048 k, doubled while the workgroups (8 / ks column sets each) number fewer than
+// 4/5 of the CUs and every part keeps at least two chunks (measured: at 4096 -> 14336,
+// 224 workgroups of 16-chunk waves beat 448 of 8-chunk ones; at 2048 -> 8192, 256 of
+// 4-chunk waves beat 128 of 8-chunk ones). ks = 0 when nothing fits.
+PackedPlan plan_packed(int32_t K, int32_t g, int64_t sets_total) {
     PackedPlan p;
     const int32_t chunks = ceil_div(K, CHUNK);
     int32_t ks = 1;
-    while (ks < 8 && ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) ks *= 2;
+    while (ks < W && ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) ks *= 2;
     if (ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) return p;
     if (g_forced.ks) {
-        if (g_forced.ks < ks) return p;
+        if (g_forced.ks < ks || g_forced.ks > chunks) return p;
         ks = g_forced.ks;
     } else {
-        const int64_t target = 4LL * cu_count();
-        while (ks < 8 && 2 * ks <= chunks / 2 && sets_total * ks < target) ks *= 2;
-    }
-    if (ks > chunks) return p;
-    int32_t waves = g_forced.waves ? g_forced.waves : (ks > 4 ? 8 : 4);
-    if (ks > waves) return p;
-    if (waves / ks * SET > min_n) {  // fewer column sets per workgroup: split K further
-        while (ks < waves && waves / ks * SET > min_n && 2 * ks <= chunks) ks *= 2;
-        if (waves / ks * SET > min_n) return p;
+        while (ks < W && 2 * ks <= chunks && 5 * ((sets_total * ks + W - 1) / W) < 4 * cu_count()) ks *= 2;
     }
     const int32_t nmax = ceil_div(chunks, ks);
-    const size_t lds = static_cast<size_t>(waves) * wave_bytes(nmax, wave_groups(nmax, g)) +
-                       static_cast<size_t>(waves) * (SET + 1) * sizeof(float);
+    (void)g;
+    const size_t lds = static_cast<size_t>(lds_bytes(chunks));
     if (lds > lds_limit()) return p;
-    p.waves = waves;
     p.ks = ks;
     p.nmax = nmax;
     p.lds = lds;
@@ -530,9 +501,7 @@ bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const
     if (w.g % RUN != 0 || log2_exact(w.g / RUN) < 0) return false;  // a run lies in one group
     if (w.N % SET != 0) return false;                             // whole column sets
     if (!aligned(w.p, 16) || !aligned(a, 16) || !aligned(w.s, 16) || (w.z && !aligned(w.z, 16))) return false;
-    // some workgroup shape fits (tiny K with few columns has none: K cannot be split
-    // below one chunk, and a workgroup's column sets must lie inside the weight)
-    return plan_packed(w.K, w.g, w.N, w.N / SET).ks != 0;
+    return plan_packed(w.K, w.g, w.N / SET).ks != 0;
 }
 
 int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
@@ -549,18 +518,13 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
     if (mode != X_PLAIN && !aligned(up ? up : norm_weight, 16))
         return fail(KT_ERR_ARGUMENT, "packed gemv: the gate's up row or the RMSNorm weight must be 16-byte aligned");
     int64_t sets_total = 0, sets_max = 0;
-    int32_t min_n = w0.N;
     for (int32_t i = 0; i < count; ++i) {
-        const int64_t sets = ws[i].N / SET;
-        sets_total += sets;
-        if (sets > sets_max) sets_max = sets;
-        if (ws[i].N < min_n) min_n = ws[i].N;
+        sets_total += ws[i].N / SET;
+        sets_max = std::max<int64_t>(sets_max, ws[i].N / SET);
     }
-    const PackedPlan plan = plan_packed(w0.K, w0.g, min_n, sets_total);
-    if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed gemv: no workgroup shape fits K = %d, g = %d", w0.K, w0.g);
-    const int32_t per_wg = plan.waves / plan.ks;
-    const int32_t n_chunks = plan.nmax;
-
+    const PackedPlan plan = plan_packed(w0.K, w0.g, sets_total);
+    if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed gemv: no work split fits K = %d, g = %d", w0.K, w0.g);
+    const int32_t kslog = log2_exact(plan.ks);
     PJobs jobs{};
     jobs.count = count;
     for (int32_t i = 0; i < count; ++i) {
@@ -573,18 +537,19 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
         jb.N = ws[i].N;
         jb.sets = ws[i].N / SET;
     }
+    const int32_t per_wg = W / plan.ks;  // column sets per workgroup
     const dim3 grid(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)), static_cast<uint32_t>(count));
     const int32_t gshift = log2_exact(w0.g / RUN);
     const float* aux = up ? up : norm_weight;
     if (w0.bits == 4)
-        launch_mode<4, true>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
-                             accumulate, n_chunks);
+        launch_mode<4, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
+                             plan.nmax);
     else if (zp)
-        launch_mode<8, true>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
-                             accumulate, n_chunks);
+        launch_mode<8, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
+                             plan.nmax);
     else
-        launch_mode<8, false>(mode, plan.waves, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, plan.ks, alpha,
-                              accumulate, n_chunks);
+        launch_mode<8, false>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
+                              plan.nmax);
     KT_LAUNCHED("qmatmul: packed gemv kernel");
     return KT_OK;
 }

@@ -82,23 +82,24 @@ def test_packed_group_sizes_and_ragged_shapes(kt, oracle_lib):
 
 
 def test_packed_work_splits_agree(kt, oracle_lib):
-    """Every split of a column set's K range over 1, 2, 4 or 8 waves, with 4 or 8 waves
-    per workgroup, gives the oracle's result; the splits differ by fp32 rounding only."""
+    """Every split of a column set's K range over 1, 2, 4 or 8 waves, with 4 or 8 KB of
+    weights in flight per wave, gives the oracle's result; the splits differ by fp32
+    rounding only."""
     rng = np.random.default_rng(6)
     try:
-        for k, n, bits in [(4096, 14336, 4), (896, 4864, 4), (2048, 2048, 8), (8192, 2048, 4)]:
+        for k, n, bits in [(4096, 14336, 4), (896, 4864, 4), (2048, 2048, 8), (8192, 2048, 4), (16384, 1024, 8)]:
             q = _weights(oracle_lib, k, n, bits, 64, 8)
             qt = _packed(kt, q)
             x = rng.standard_normal((1, k), dtype=np.float32)
             want = oracle_lib.multiply_quantized(x, q, 1, threads=16)
-            for waves in (4, 8):
+            for ring in (4, 8):
                 for ks in (1, 2, 4, 8):
-                    if ks > waves or (waves == 4 and k > 4096):
+                    if -(-k // 128) > 16 * ks:  # a wave's range holds at most 16 chunks
                         continue
-                    banner("packed-split", k, n, bits, waves, ks)
-                    kt.MatMul.set_kernel_config(5, 0, ks, waves, 0)
+                    banner("packed-split", k, n, bits, ring, ks)
+                    kt.MatMul.set_kernel_config(5, ring, ks, 0, 0)
                     got = gpu_matmul(kt, x, qt, 1)
-                    assert normwise_rel(got, want) <= TOL, (waves, ks)
+                    assert normwise_rel(got, want) <= TOL, (ring, ks)
     finally:
         kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
