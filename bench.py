@@ -1,43 +1,42 @@
 #!/usr/bin/env python3
 """Benchmark of the dequant-GEMV hot path on one MI355X.
 
-Workload (one "step"): the INT4 (g64) M = 1 projections of a Qwen2-0.5B-shaped
-decoder layer plus its lm_head -- q/o 896->896, k/v 896->128, gate/up 896->4864,
-down 4864->896, lm_head 896->151936 -- with x ~ N(0,1) fp32 and W ~ N(0, 0.02)
-quantized on the device by kt_quantize (the reference layout: qdata [K x N/2],
-fp32 scales and u8 zeros [K/64 x N]). Inputs are resident in HBM before timing.
-q/k/v (one input) and gate/up (one input) each go out as one grouped launch
-(kt_qmatmul_group), o, down and lm_head as one launch each. Each step uses a
-different copy of the weight set so that the timed loop streams more than twice
-the 256 MB Infinity Cache; a step's launches are captured in a HIP graph (one graph
-per weight copy) and replayed.
+Workload (one "step"): the INT4 group-64 one-row product y = x . deq(W) on the
+Llama-3-8B gate/up projection shape, K = 4096 -> N = 14336, with x ~ N(0,1) fp32 and
+W ~ N(0, 0.02) quantized on the device by kt_quantize (the reference layout: qdata
+[K x N/2], fp32 scales and u8 zeros [K/64 x N]) plus the column-run copy that the
+one-row kernel streams (kt_qweight_pack). Inputs are resident in HBM before timing.
+The weight is cloned until one pass over the copies streams more than twice the 256 MB
+Infinity Cache; `--steps` launches rotating over the copies are recorded in one HIP
+graph and replayed once between synchronizations (HIP events on the launch stream),
+after `--warmup` launches recorded and replayed the same way.
 
 value = algorithmic bytes of a step / measured step time (GB/s). Algorithmic bytes
-per GEMV = K*bytesPerRow + 4*groups*N + groups*N (zeros) + 4*K (x) + 4*N (y).
+per product = K*bytesPerRow + 4*groups*N + groups*N (zeros) + 4*K (x) + 4*N (y).
 
 The JSON line also carries:
-  roofline      -- the dominant kernel (the lm_head GEMV): back-to-back launches in a
-                   graph on the launch stream, HIP events around the timed replays,
-                   against 8 TB/s; traffic from rocprofv3 PMC runs (profiles/);
+  roofline      -- the headline kernel itself against 8 TB/s; traffic (HBM bytes per
+                   launch) from rocprofv3 PMC runs recorded under profiles/;
   cpu_baseline  -- the oracle (C restatement of MatMul.multiplyQuantized, M == 1
-                   unit schedule, work-stealing threads) on the same workload;
-  extra         -- the two targets of the workload family: INT4 GEMV on the
-                   Llama-3-8B FFN shape (4096->14336) and the INT8 group-32 prefill
-                   GEMM at M = 512 on the 2048-wide layer's four projection shapes
-                   (2048->2048, 2048->512, 2048->8192, 8192->2048) and their sum, each
-                   with its fraction of the MFMA peak and, for scale, the vendor library's
-                   plain bf16 GEMM (torch.matmul -> hipBLASLt, no dequantization) on the
-                   same shape timed the same way; the M sweep (1, 16, 128, 512, 2048) of
-                   the INT8 2048 -> 8192 product; the Llama-3-8B projection shapes
-                   (4096->4096, 4096->1024, 4096->14336, 14336->4096), INT4 and INT8 g64
-                   at M = 1, 8, 64, 512; kt_quantize on 4096 x 14336 (per call,
-                   including its NaN-flag readback); and the Llama-style 1B INT4
-                   decoder end to end (1024-token prefill, greedy decode steps).
-                   Every timed graph reads each of its weight copies (> 2x MALL).
+                   unit schedule, work-stealing threads) on the same product on this
+                   host: faithful and FMA-contracted builds, all threads and one, the
+                   median of 5 samples after 3 warm-up calls;
+  extra         -- the rest of the workload family: C2, the Qwen2-0.5B layer step
+                   (grouped launches) and each projection alone at g64 and g32; C1, the
+                   INT8 2048 x 2048 GEMV at g64 and g32; C5's g32 rows at M = 1; the
+                   INT8 group-32 prefill GEMM at M = 512 on the 2048-wide layer's four
+                   shapes and their sum, each beside the vendor library's plain bf16
+                   GEMM (torch.matmul -> hipBLASLt, no dequantization) timed the same
+                   way; the M sweep (1, 16, 128, 512, 2048) of the INT8 2048 -> 8192
+                   product; the Llama-3-8B projection shapes (4096->4096, 4096->1024,
+                   4096->14336, 14336->4096), INT4 and INT8 g64 at M = 1, 8, 64, 512;
+                   kt_quantize on 4096 x 14336; and the Llama-style 1B INT4 decoder end
+                   to end (1024-token prefill, greedy decode steps). Every timed graph
+                   reads each of its weight copies (> 2x MALL).
 
---only dominant | copy | quantize | gemm runs just the lm_head GEMV (or a 256 MB device
-copy, the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64 on
-4096 x 14336, or the INT8 g32 M = 512 GEMM on 2048 -> 8192) for rocprofv3 runs.
+--only dominant | copy | quantize | gemm runs just the headline product (or a 256 MB
+device copy, the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64
+on 4096 x 14336, or the INT8 g32 M = 512 GEMM on 2048 -> 8192) for rocprofv3 runs.
 """
 from __future__ import annotations
 
@@ -57,6 +56,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 MALL_BYTES = 256 << 20
 
+# the headline: K, N, bits, group size of the Llama-3-8B gate/up projection
+HEADLINE = (4096, 14336, 4, 64)
 QWEN = [("q", 896, 896), ("k", 896, 128), ("v", 896, 128), ("o", 896, 896), ("gate", 896, 4864),
         ("up", 896, 4864), ("down", 4864, 896), ("lm_head", 896, 151936)]
 
@@ -87,13 +88,24 @@ class Weight:
         kt_lib.call("kt_quantize", w.data_ptr(), k, n, bits, g, self.q.data_ptr(), self.s.data_ptr(),
                     self.z.data_ptr() if self.z is not None else None, stream)
         del w
+        self.p = None
         self.struct = None
         self._bind(kt_lib)
 
     def _bind(self, kt_lib):
         self.struct = kt_lib.QWeight(self.q.data_ptr(), self.s.data_ptr(),
                                      self.z.data_ptr() if self.z is not None else None,
-                                     self.k, self.n, self.bits, self.g)
+                                     self.k, self.n, self.bits, self.g,
+                                     self.p.data_ptr() if self.p is not None else None)
+
+    def pack(self, torch, kt_lib, stream):
+        """Adds the column-run copy (kt_qweight_pack) that the one-row kernel streams."""
+        nbytes = ctypes.c_int64()
+        kt_lib.call("kt_qweight_packed_bytes", self.k, self.n, self.bits, ctypes.byref(nbytes))
+        self.p = torch.empty(nbytes.value, dtype=torch.uint8, device="cuda")
+        self._bind(kt_lib)
+        kt_lib.call("kt_qweight_pack", ctypes.byref(self.struct), self.p.data_ptr(), stream)
+        return self
 
     def clone(self, kt_lib):
         c = object.__new__(Weight)
@@ -101,6 +113,7 @@ class Weight:
         c.q = self.q.clone()
         c.s = self.s.clone()
         c.z = self.z.clone() if self.z is not None else None
+        c.p = self.p.clone() if self.p is not None else None
         c._bind(kt_lib)
         return c
 
@@ -141,44 +154,86 @@ def time_graph_launches(torch, stream_obj, fn, copies, launches, replays=3):
     return t0.elapsed_time(t1) / (replays * launches)
 
 
+def host_threads() -> int:
+    """The cores this process may use: its affinity set, capped by OMP_NUM_THREADS when the
+    host sets it (the share of a multi-GPU host's cores that belongs to one GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float = 10.0):
-    """The oracle's M == 1 kernel on the same Qwen set, on this host's cores."""
+    """The oracle's M == 1 product (C restatement of MatMul.multiplyQuantized, the M == 1
+    unit schedule on work-stealing threads) on the headline workload, on this host.
+    Four modes: faithful (-ffp-contract=off, the reference's rounding) and fast (FMA
+    contraction, AVX2), each on all of the host's threads and on one; each mode is 3
+    warm-up calls, then 5 samples of repeated calls, and the median sample is reported."""
     import numpy as np
 
     import oracle
 
     oracle.build()
-    threads = max(1, min(16, os.cpu_count() or 1))
+    k, n, bits, g = HEADLINE
     rng = np.random.default_rng(1)
-    weights = []
-    for _, k, n in QWEN:
-        w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-        st, q = oracle.quantize(w, 4, 64)
-        weights.append((k, n, q))
-    xs = {k: np.random.default_rng(0).standard_normal((1, k), dtype=np.float32) for k in (896, 4864)}
-    step_bytes = sum(gemv_bytes(1, k, n, 4, 64) for _, k, n in QWEN)
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        for k, n, q in weights:
-            oracle.multiply_quantized(xs[k], q, 1, threads=threads)
-        steps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
+    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    _, q = oracle.quantize(w, bits, g)
+    del w
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    nbytes = gemv_bytes(1, k, n, bits, g)
+    threads = host_threads()
+    per_sample = seconds / 20.0
+
+    def measure(t, fast):
+        for _ in range(3):
+            oracle.multiply_quantized(x, q, 1, threads=t, fast=fast)
+        t0 = time.perf_counter()
+        oracle.multiply_quantized(x, q, 1, threads=t, fast=fast)
+        reps = max(1, int(per_sample / max(time.perf_counter() - t0, 1e-6)))
+        samples = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                oracle.multiply_quantized(x, q, 1, threads=t, fast=fast)
+            samples.append((time.perf_counter() - t0) / reps)
+        sec = sorted(samples)[2]
+        return {"GB/s": round(nbytes / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 3), "calls_per_sample": reps}
+
+    faithful = measure(threads, False)
     return {
-        "value": round(step_bytes * steps / elapsed / 1e9, 3),
+        "value": faithful["GB/s"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{steps} passes of the 8 Qwen2-0.5B INT4 g64 M=1 projections ({elapsed:.1f} s), "
-                  "C restatement of MatMul.multiplyQuantized's M=1 unit schedule, -O3 -ffp-contract=off",
+        "sample": f"INT4 g64 M=1 4096x14336 ({nbytes} algorithmic bytes per call), C restatement of "
+                  f"MatMul.multiplyQuantized's M=1 unit schedule built -O3 -ffp-contract=off, {threads} threads, "
+                  "median of 5 samples after 3 warm-up calls",
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
+        "modes": {
+            f"faithful_{threads}t": faithful,
+            "faithful_1t": measure(1, False),
+            f"fast_{threads}t": measure(threads, True),
+            "fast_1t": measure(1, True),
+        },
     }
 
 
 def traffic_from_profiles():
-    """HBM bytes per lm_head launch measured with rocprofv3 --pmc (profiles/), if recorded."""
-    path = ROOT / "profiles" / "traffic_gemv_int4_lm_head.json"
+    """HBM bytes per launch of the headline kernel measured with rocprofv3 --pmc
+    (profiles/), if recorded."""
+    path = ROOT / "profiles" / "traffic_gemv_packed_int4_4096x14336.json"
     if path.exists():
         try:
             return json.loads(path.read_text()).get("bytes_per_launch")
@@ -311,42 +366,96 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
         print(json.dumps({"only": "gemm", "kernel": "gemm_kernel int8 g32 M=512 2048x8192",
                           "flops": 2 * 512 * 2048 * 8192, "launches": args.steps}), flush=True)
         return 0
-    w = Weight(torch, kt_lib, 896, 151936, 4, 64, seed=8, stream=stream)
-    copies = [w] + [w.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // w.nbytes)) - 1)]
-    x = torch.randn((1, 896), device="cuda", dtype=torch.float32)
-    y = torch.empty((1, 151936), device="cuda", dtype=torch.float32)
+    k, n, bits, g = HEADLINE
+    copies = weight_copies(torch, kt_lib, k, n, bits, g, 8, stream, packed=True)
+    x = torch.randn((1, k), device="cuda", dtype=torch.float32)
+    y = torch.empty((1, n), device="cuda", dtype=torch.float32)
     torch.cuda.synchronize()
     for i in range(args.steps):
         qmatmul(kt_lib, x, 1, copies[i % len(copies)], y, stream)
     torch.cuda.synchronize()
-    print(json.dumps({"only": "dominant", "kernel": "lm_head 896x151936 int4 g64 M=1",
-                      "algorithmic_bytes": gemv_bytes(1, 896, 151936, 4, 64), "launches": args.steps}), flush=True)
+    print(json.dumps({"only": "dominant", "kernel": "gemv_packed_kernel INT4 g64 M=1 4096x14336",
+                      "algorithmic_bytes": gemv_bytes(1, k, n, bits, g), "launches": args.steps}), flush=True)
     return 0
 
 
-def run(args, torch, kt_lib, stream_obj) -> int:
-    stream = ctypes.c_void_p(stream_obj.cuda_stream)
-    bits, g = 4, 64
+def progress(what):
+    """One line on stderr per finished section (stdout carries only the JSON line)."""
+    print(f"[bench] {what}", file=sys.stderr, flush=True)
 
-    # ---- weights: one quantized set, cloned until the rotation exceeds 2x the MALL
-    base = [Weight(torch, kt_lib, k, n, bits, g, seed=1 + i, stream=stream) for i, (_, k, n) in enumerate(QWEN)]
+
+def weight_copies(torch, kt_lib, k, n, bits, g, seed, stream, packed):
+    """A quantized weight and enough clones that one pass over them streams more than
+    twice the MALL; packed adds each one's column-run copy (what M == 1 reads)."""
+    w = Weight(torch, kt_lib, k, n, bits, g, seed, stream)
+    if packed:
+        w.pack(torch, kt_lib, stream)
+    count = max(2, -(-2 * MALL_BYTES // w.nbytes))
+    out = [w] + [w.clone(kt_lib) for _ in range(count - 1)]
+    torch.cuda.synchronize()
+    return out
+
+
+def time_exact_steps(torch, stream_obj, fn, copies, steps, warmup):
+    """Exactly `steps` launches (rotating the weight copies), recorded in one graph and
+    replayed once between synchronizations, HIP events on the launch stream around the
+    replay; `warmup` launches replayed the same way before. Returns ms per launch."""
+    warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(warm, stream=stream_obj):
+        for i in range(max(1, warmup)):
+            fn(copies[i % len(copies)])
+    timed = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(timed, stream=stream_obj):
+        for i in range(steps):
+            fn(copies[i % len(copies)])
+    warm.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream_obj)
+    timed.replay()
+    t1.record(stream_obj)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def gemv_row(torch, kt_lib, stream_obj, k, n, bits, g, seed, launches=64):
+    """Average launch time of the one-row product on the packed copy, back to back."""
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    cs = weight_copies(torch, kt_lib, k, n, bits, g, seed, stream, packed=True)
+    x = torch.randn((1, k), device="cuda", dtype=torch.float32)
+    y = torch.empty((1, n), device="cuda", dtype=torch.float32)
+    for w in cs[:2]:
+        qmatmul(kt_lib, x, 1, w, y, stream)
+    ms = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, x, 1, w, y, stream), cs, launches)
+    nbytes = gemv_bytes(1, k, n, bits, g)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del cs
+    return {"avg_us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes}
+
+
+def qwen_step(torch, kt_lib, stream_obj, bits, g, steps):
+    """One Qwen2-0.5B layer's projections and the head at M = 1 on packed weights: q/k/v
+    and gate/up as one grouped launch each, o, down and the head one launch each; one
+    graph per weight copy, replayed. Returns (ms per step, bytes per step, copies)."""
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    base = [Weight(torch, kt_lib, k, n, bits, g, seed=1 + i, stream=stream).pack(torch, kt_lib, stream)
+            for i, (_, k, n) in enumerate(QWEN)]
     set_bytes = sum(w.nbytes for w in base)
     copies = max(2, -(-2 * MALL_BYTES // set_bytes))
     sets = [base] + [[w.clone(kt_lib) for w in base] for _ in range(copies - 1)]
-    gen = torch.Generator(device="cuda").manual_seed(0)
-    xs = {k: torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32) for k in (896, 4864)}
+    xs = {k: torch.randn((1, k), device="cuda", dtype=torch.float32) for k in (896, 4864)}
     ys = [torch.empty((1, n), device="cuda", dtype=torch.float32) for _, _, n in QWEN]
     torch.cuda.synchronize()
 
     def step(ws):
-        # q, k, v share x; gate, up share x: one grouped launch each
         qmatmul_group(kt_lib, xs[896], 1, ws[0:3], ys[0:3], stream)
         qmatmul(kt_lib, xs[896], 1, ws[3], ys[3], stream)
         qmatmul_group(kt_lib, xs[896], 1, ws[4:6], ys[4:6], stream)
         qmatmul(kt_lib, xs[4864], 1, ws[6], ys[6], stream)
         qmatmul(kt_lib, xs[896], 1, ws[7], ys[7], stream)
 
-    # eager warm-up (allocates the library's per-stream workspace before capture)
     for r in range(copies):
         step(sets[r])
     torch.cuda.synchronize()
@@ -356,49 +465,69 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         with torch.cuda.graph(gph, stream=stream_obj):
             step(sets[r])
         graphs.append(gph)
-    torch.cuda.synchronize()
-    for i in range(args.warmup):
+    for i in range(4 * copies):
         graphs[i % copies].replay()
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record(stream_obj)
-    for i in range(args.steps):
+    for i in range(steps):
         graphs[i % copies].replay()
     t1.record(stream_obj)
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
-    step_bytes = sum(gemv_bytes(1, k, n, bits, g) for _, k, n in QWEN)
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del graphs, sets, base
+    return t0.elapsed_time(t1) / steps, sum(gemv_bytes(1, k, n, bits, g) for _, k, n in QWEN), copies
 
-    # ---- dominant kernel: the lm_head GEMV, back-to-back launches on the launch stream
-    head = [s[-1] for s in sets]
-    head_y = ys[-1]
-    head_bytes = gemv_bytes(1, 896, 151936, bits, g)
-    avg_ms = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xs[896], 1, w, head_y, stream), head, 60)
-    achieved = head_bytes / (avg_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "gemv_wide_kernel<4,4,true> (lm_head 896x151936 int4 g64 M=1)",
-                "algorithmic_bytes": head_bytes, "avg_us": round(avg_ms * 1e3, 3)}
+
+def run(args, torch, kt_lib, stream_obj) -> int:
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+
+    # ---- the headline: INT4 g64 one-row product on the Llama-3-8B gate/up shape, packed
+    k, n, bits, g = HEADLINE
+    head = weight_copies(torch, kt_lib, k, n, bits, g, 7, stream, packed=True)
+    x = torch.randn((1, k), generator=gen, device="cuda", dtype=torch.float32)
+    y = torch.empty((1, n), device="cuda", dtype=torch.float32)
+    for w in head:
+        qmatmul(kt_lib, x, 1, w, y, stream)
+    torch.cuda.synchronize()
+    ms_per_step = time_exact_steps(torch, stream_obj, lambda w: qmatmul(kt_lib, x, 1, w, y, stream), head,
+                                   args.steps, args.warmup)
+    step_bytes = gemv_bytes(1, k, n, bits, g)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                "kernel": "gemv_packed_kernel<4,4,true,0> (INT4 g64 M=1 4096x14336, packed copy)",
+                "algorithmic_bytes": step_bytes, "avg_us": round(ms_per_step * 1e3, 3)}
+    copies_head = len(head)
+    del head
+    progress(f"headline {ms_per_step * 1e3:.3f} us/step, {value:.1f} GB/s")
 
     extra = {}
     if not args.no_extra:
-        # INT4 GEMV on the Llama-3-8B FFN shape, 16 copies (> 2x MALL)
-        w8 = Weight(torch, kt_lib, 4096, 14336, 4, 64, seed=7, stream=stream)
-        n8 = max(2, -(-2 * MALL_BYTES // w8.nbytes))
-        c8 = [w8] + [w8.clone(kt_lib) for _ in range(n8 - 1)]
-        x8 = torch.randn((1, 4096), generator=gen, device="cuda", dtype=torch.float32)
-        y8 = torch.empty((1, 14336), device="cuda", dtype=torch.float32)
-        for w in c8:
-            qmatmul(kt_lib, x8, 1, w, y8, stream)
-        a8 = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, x8, 1, w, y8, stream), c8, 64)
-        b8 = gemv_bytes(1, 4096, 14336, 4, 64)
-        extra["int4_gemv_llama8b_ffn_4096x14336"] = {
-            "GB/s": round(b8 / (a8 * 1e-3) / 1e9, 1), "frac_hbm": round(b8 / (a8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "avg_us": round(a8 * 1e3, 3), "bytes": b8, "copies": n8}
-        del c8, w8
+        # C2: the Qwen2-0.5B layer step (grouped launches) and each projection alone,
+        # group 64 (primary) and 32 (secondary)
+        c2 = {}
+        for gg in (64, 32):
+            ms, b, cp = qwen_step(torch, kt_lib, stream_obj, 4, gg, 200)
+            gbs = b / (ms * 1e-3) / 1e9
+            row = {"step": {"ms": round(ms, 5), "bytes": b, "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                            "launches": 5, "weight_copies": cp}}
+            for name, kk, nn in [("q_o", 896, 896), ("k_v", 896, 128), ("gate_up", 896, 4864), ("down", 4864, 896),
+                                 ("lm_head", 896, 151936)]:
+                row[f"{name}_{kk}x{nn}"] = gemv_row(torch, kt_lib, stream_obj, kk, nn, 4, gg, 3)
+            c2[f"g{gg}"] = row
+        extra["c2_qwen2_0.5b_int4_m1"] = c2
+        progress("C2 rows")
+
+        # C1: INT8 GEMV 2048 x 2048 (group 64 and 32); per launch, back to back
+        extra["c1_int8_gemv_2048x2048"] = {f"g{gg}": gemv_row(torch, kt_lib, stream_obj, 2048, 2048, 8, gg, 5, 128)
+                                          for gg in (64, 32)}
+
+        # C5 at M = 1, group 32 secondaries: gate/up and the head, INT4 and INT8
+        progress("C1 rows")
+        extra["c5_m1_g32"] = {f"int{bb}_{kk}x{nn}": gemv_row(torch, kt_lib, stream_obj, kk, nn, bb, 32, 17)
+                              for bb in (4, 8) for kk, nn in [(4096, 14336), (4096, 128256)]}
         # INT8 prefill GEMM at M = 512, group 32, on the four projection shapes of a
         # 2048-wide layer; "layer" is their flops over their summed time (one of each).
         tot_flops = tot_ms = 0.0
@@ -433,6 +562,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
                                               "avg_us": round(ab * 1e3, 3)}}
             del cg, wg, wb
         layer = tot_flops / (tot_ms * 1e-3) / 1e12
+        progress("C3 M=512 GEMM rows")
         extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
                                              "avg_us": round(tot_ms * 1e3, 3)}
 
@@ -452,6 +582,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             sweep[str(mm)] = {"avg_us": round(am * 1e3, 3), "TFLOP/s": round(flops / (am * 1e-3) / 1e12, 1),
                               "GB/s": round(gemv_bytes(mm, 2048, 8192, 8, 32) / (am * 1e-3) / 1e9, 1)}
         extra["int8_g32_m_sweep_2048x8192"] = sweep
+        progress("C3 M sweep")
         del cm, wm
 
         # Llama-3-8B projection shapes (q/o 4096 -> 4096, k/v 4096 -> 1024, gate/up
@@ -459,7 +590,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         l8 = {}
         for bits in (4, 8):
             for (k, n) in [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]:
-                wl = Weight(torch, kt_lib, k, n, bits, 64, seed=13, stream=stream)
+                wl = Weight(torch, kt_lib, k, n, bits, 64, seed=13, stream=stream).pack(torch, kt_lib, stream)
                 nl = max(2, -(-2 * MALL_BYTES // wl.nbytes))
                 cl = [wl] + [wl.clone(kt_lib) for _ in range(nl - 1)]
                 row = {}
@@ -477,6 +608,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
                 l8[f"int{bits}_g64_{k}x{n}"] = row
                 del cl, wl
         extra["llama8b_projections_m_sweep"] = l8
+        progress("C5 M sweep")
 
         # kt_quantize on the gate/up shape 4096 x 14336 at group 64 (reads the fp32 weight,
         # writes the packed weight, scales and zeros), three distinct inputs (> 2x MALL);
@@ -513,9 +645,11 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             qz[f"int{bits}_g64_{kq}x{nq}"] = {"median_us_per_call": round(tq * 1e3, 3), "bytes": bq,
                                               "GB/s": round(gq, 1), "frac_hbm": round(gq / HBM_PEAK_GBS, 4)}
         extra["quantize_llama8b_gate_4096x14336"] = qz
+        progress("quantize")
         del srcs
 
         extra["llama1b_int4_decoder"] = decoder_figures(torch, stream_obj)
+        progress("C4 decoder")
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
@@ -531,10 +665,12 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: x ~ N(0,1) fp32, W ~ N(0,0.02) fp32 quantized on device (seeded)",
-        "config": {"workload": "qwen2-0.5b int4 g64 M=1 projection GEMVs (q,k,v,o,gate,up,down,lm_head)",
-                   "launches_per_step": 5,
-                   "weights": "uint4 + fp32 scales + u8 zeros, reference layout", "group_size": g, "m": 1,
-                   "step_bytes": step_bytes, "weight_copies": copies, "graph_replay": True},
+        "config": {"workload": "llama-3-8b gate/up projection 4096x14336, INT4 g64, M=1 (one dequant-GEMV "
+                               "launch per step)",
+                   "launches_per_step": 1,
+                   "weights": "uint4 + fp32 scales + u8 zeros (reference layout) with the column-run copy the "
+                              "one-row kernel streams", "group_size": g, "m": 1,
+                   "step_bytes": step_bytes, "weight_copies": copies_head, "graph_replay": True},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,

@@ -17,6 +17,8 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "_build" / "libkt_oracle.so"
+# The same source built with FMA contraction and AVX2: a CPU baseline, never a checker.
+FAST_LIBRARY_PATH = HERE / "_build" / "libkt_oracle_fast.so"
 
 KO_OK = 0
 KO_ERR_ARG = -1
@@ -81,6 +83,22 @@ def lib():
         L.ko_argmax.argtypes = [P, I]
         _lib = L
     return _lib
+
+
+_fast = None
+
+
+def fast_lib():
+    """The contracted (FMA, AVX2) build, for the CPU baseline's "fast" figure only."""
+    global _fast
+    if _fast is None:
+        if not FAST_LIBRARY_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(FAST_LIBRARY_PATH))
+        L.ko_multiply_quantized.argtypes = [ctypes.c_void_p, ctypes.POINTER(QW), ctypes.c_void_p, ctypes.c_int32,
+                                            ctypes.c_int32, ctypes.c_float, ctypes.c_int32]
+        _fast = L
+    return _fast
 
 
 def _p(a: np.ndarray | None):
@@ -173,14 +191,15 @@ def quantize(data: np.ndarray, bits: int, group_size: int) -> tuple[int, Quantiz
 
 
 def multiply_quantized(a: np.ndarray, w: Quantized, m: int, c: np.ndarray | None = None, accumulate: bool = False,
-                       alpha: float = 1.0, threads: int = 1) -> np.ndarray:
-    """MatMul.multiplyQuantized (MatMul.kt:460-486), returning c ``[m x N]``."""
+                       alpha: float = 1.0, threads: int = 1, fast: bool = False) -> np.ndarray:
+    """MatMul.multiplyQuantized (MatMul.kt:460-486), returning c ``[m x N]``; fast=True
+    runs the contracted build (CPU baseline timing only: its sums round differently)."""
     a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
     if c is None:
         c = np.zeros(m * w.columns, dtype=np.float32)
     c = np.ascontiguousarray(c, dtype=np.float32).reshape(-1).copy()
-    st = lib().ko_multiply_quantized(_p(a), ctypes.byref(w.qw), _p(c), m, int(accumulate), ctypes.c_float(alpha),
-                                     threads)
+    st = (fast_lib() if fast else lib()).ko_multiply_quantized(_p(a), ctypes.byref(w.qw), _p(c), m, int(accumulate),
+                                                               ctypes.c_float(alpha), threads)
     if st != KO_OK:
         raise ValueError(f"oracle multiply_quantized status {st}")
     return c.reshape(m, w.columns)
