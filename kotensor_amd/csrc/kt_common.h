@@ -85,8 +85,9 @@ int32_t cu_count();
 
 // Launch entry points implemented by the kernel translation units. All take
 // validated arguments. bias may be nullptr; partial results never leave the stream.
+// A NaN input stores epoch into *nan_slot (device address of pinned host memory).
 int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, int32_t g,
-                        uint8_t* q, float* s, int8_t* z, int32_t* nan_flag, hipStream_t st);
+                        uint8_t* q, float* s, int8_t* z, int32_t* nan_slot, int32_t epoch, hipStream_t st);
 int32_t launch_gemv(const float* a, const WeightView& w, float* c, int32_t accumulate, float alpha,
                     const float* bias, hipStream_t st);
 // One launch for up to four weights that share the input row (same K, bits, group size).

@@ -57,7 +57,16 @@ __device__ __forceinline__ float lane(const float4& v, int j) {
     return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
 
-__global__ void clear_flag(int32_t* flag) { *flag = 0; }
+// A NaN input marks the call: the kernel stores the call's epoch into its slot of a
+// pinned host array (system scope, so the host reads it after the stream syncs). Slots
+// are never cleared; an older call's mark holds another epoch.
+struct NanFlag {
+    int32_t* slot;
+    int32_t epoch;
+};
+__device__ __forceinline__ void mark_nan(const NanFlag& f) {
+    __hip_atomic_store(f.slot, f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 // The vector kernels: a workgroup owns one group and 64 column units, its waves split
 // the group's rows (RPW each) and keep them in registers. Per-lane partial extrema go
@@ -73,7 +82,7 @@ __global__ void clear_flag(int32_t* flag) { *flag = 0; }
 template <int RPW>
 __global__ void __launch_bounds__(1024) quant8_vec(const float* __restrict__ data, int32_t K, int32_t N,
                                                    int32_t g, uint8_t* __restrict__ q, float* __restrict__ s,
-                                                   int32_t* __restrict__ nan_flag) {
+                                                   NanFlag nan_flag) {
     extern __shared__ float red[];  // [waves][4][64] max |x|, then [4][64] inverses
     const int32_t t = threadIdx.x, ln = t & 63, wave = t >> 6, waves = blockDim.x >> 6;
     const int32_t units = N >> 2;
@@ -129,7 +138,7 @@ __global__ void __launch_bounds__(1024) quant8_vec(const float* __restrict__ dat
             }
         }
     }
-    if (nan_seen) *nan_flag = 1;
+    if (nan_seen) mark_nan(nan_flag);
 }
 
 // INT4, 4 bytes (8 columns: 4 low-nibble, 4 high-nibble) per lane, 512 columns per
@@ -137,7 +146,7 @@ __global__ void __launch_bounds__(1024) quant8_vec(const float* __restrict__ dat
 template <int RPW>
 __global__ void __launch_bounds__(1024) quant4_vec(const float* __restrict__ data, int32_t K, int32_t N,
                                                    int32_t g, uint8_t* __restrict__ q, float* __restrict__ s,
-                                                   int8_t* __restrict__ z, int32_t* __restrict__ nan_flag) {
+                                                   int8_t* __restrict__ z, NanFlag nan_flag) {
     // [waves][16][64] partials (min lo, max lo, min hi, max hi, 4 each), then
     // [8][64] inverses and [8][64] zeros (component side * 4 + j)
     extern __shared__ float red[];
@@ -235,7 +244,7 @@ __global__ void __launch_bounds__(1024) quant4_vec(const float* __restrict__ dat
             }
         }
     }
-    if (nan_seen) *nan_flag = 1;
+    if (nan_seen) mark_nan(nan_flag);
 }
 
 // Any shape: one thread per (group, column) for INT8 or per (group, byte) for INT4,
@@ -243,7 +252,7 @@ __global__ void __launch_bounds__(1024) quant4_vec(const float* __restrict__ dat
 __global__ void __launch_bounds__(256) quant_generic(const float* __restrict__ data, int32_t K, int32_t N,
                                                     int32_t bits, int32_t g, int32_t bpr,
                                                     uint8_t* __restrict__ q, float* __restrict__ s,
-                                                    int8_t* __restrict__ z, int32_t* __restrict__ nan_flag) {
+                                                    int8_t* __restrict__ z, NanFlag nan_flag) {
     const int32_t units = bits == 8 ? N : bpr;
     const int32_t col_blocks = ceil_div(units, static_cast<int32_t>(blockDim.x));
     const int32_t group = blockIdx.x / col_blocks;
@@ -298,15 +307,14 @@ __global__ void __launch_bounds__(256) quant_generic(const float* __restrict__ d
             q[static_cast<size_t>(r) * half + unit] = static_cast<uint8_t>(ql | (qh << 4));
         }
     }
-    if (nan_seen) *nan_flag = 1;
+    if (nan_seen) mark_nan(nan_flag);
 }
 
 }  // namespace
 
 int32_t launch_quantize(const float* data, int32_t K, int32_t N, int32_t bits, int32_t g, uint8_t* q, float* s,
-                        int8_t* z, int32_t* nan_flag, hipStream_t st) {
-    clear_flag<<<1, 1, 0, st>>>(nan_flag);
-    KT_LAUNCHED("quantize: clear flag");
+                        int8_t* z, int32_t* nan_slot, int32_t epoch, hipStream_t st) {
+    const NanFlag nan_flag{nan_slot, epoch};
     const int32_t G = ceil_div(K, g);
     const int32_t bpr = bits == 4 ? (N + N % 2) / 2 : N;
     const bool ptrs = aligned(data, 16) && aligned(q, 4) && aligned(s, 16) && (!z || aligned(z, 4));

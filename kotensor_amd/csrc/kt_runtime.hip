@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -441,6 +442,8 @@ int32_t kt_qweight_pack(const kt_qweight* w, void* packed, void* stream) {
     return launch_pack(v, packed, static_cast<hipStream_t>(stream));
 }
 
+constexpr uint32_t NAN_SLOTS = 1024;  // quantize calls that may be in flight at once
+
 int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bits, int32_t group_size,
                     void* qdata, float* scales, uint8_t* zeros, void* stream) {
     if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
@@ -450,17 +453,38 @@ int32_t kt_quantize(const float* data, int32_t rows, int32_t columns, int32_t bi
     if (bits == 4 && !zeros) return fail(KT_ERR_ZEROS, "4-bit tensors need zero points");
     if (bits == 8 && zeros) return fail(KT_ERR_ARGUMENT, "8-bit quantize writes no zero points; pass NULL");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    void* ws = nullptr;
-    int32_t status = workspace(st, 256, &ws);
+    // The NaN report (the reference throws from inside quantize): a pinned host array of
+    // NAN_SLOTS flags, one per call in flight, never cleared. Each call takes the next
+    // epoch (nonzero) and its slot; the kernel stores the epoch there when it meets a NaN,
+    // and the call reads the slot once the stream has synchronized. No clearing launch and
+    // no copy: the call costs the kernel and the synchronization.
+    static std::once_flag once;
+    static int32_t* host_slots = nullptr;
+    static int32_t* dev_slots = nullptr;
+    static hipError_t init_err = hipSuccess;
+    std::call_once(once, [] {
+        void* h = nullptr;
+        init_err = hipHostMalloc(&h, NAN_SLOTS * sizeof(int32_t), hipHostMallocPortable | hipHostMallocMapped);
+        if (init_err != hipSuccess) return;
+        memset(h, 0, NAN_SLOTS * sizeof(int32_t));
+        void* d = nullptr;
+        init_err = hipHostGetDevicePointer(&d, h, 0);
+        if (init_err != hipSuccess) return;
+        host_slots = static_cast<int32_t*>(h);
+        dev_slots = static_cast<int32_t*>(d);
+    });
+    if (init_err != hipSuccess) return hip_fail(init_err, "quantize: pinned NaN flags");
+    static std::atomic<uint32_t> epochs{0};
+    uint32_t e = 0;
+    while (e == 0) e = (epochs.fetch_add(1) + 1) & 0x7FFFFFFFu;
+    const int32_t epoch = static_cast<int32_t>(e);
+    int32_t* slot = dev_slots + (e % NAN_SLOTS);
+    int32_t status = launch_quantize(data, rows, columns, bits, group_size, static_cast<uint8_t*>(qdata), scales,
+                                     reinterpret_cast<int8_t*>(zeros), slot, epoch, st);
     if (status) return status;
-    int32_t* flag = static_cast<int32_t*>(ws);
-    status = launch_quantize(data, rows, columns, bits, group_size, static_cast<uint8_t*>(qdata), scales,
-                             reinterpret_cast<int8_t*>(zeros), flag, st);
-    if (status) return status;
-    int32_t host_flag = 0;
-    KT_HIP(hipMemcpyAsync(&host_flag, flag, sizeof(int32_t), hipMemcpyDeviceToHost, st));
     KT_HIP(hipStreamSynchronize(st));
-    if (host_flag) return fail(KT_ERR_NAN, "Cannot round NaN value.");
+    if (__atomic_load_n(host_slots + (e % NAN_SLOTS), __ATOMIC_ACQUIRE) == epoch)
+        return fail(KT_ERR_NAN, "Cannot round NaN value.");
     return KT_OK;
 }
 

@@ -119,6 +119,25 @@ def test_nan_is_rejected_like_round_to_int(kt, oracle_lib):
         _check(kt, oracle_lib, ok, bits, 64, "after_nan")
 
 
+def test_nan_report_belongs_to_its_call(kt, oracle_lib):
+    """The NaN marks are never cleared: each call checks only its own. NaN calls in a row
+    all fail, clean calls between and after them all pass, on every kernel path (the
+    vector kernels and the generic one)."""
+    rng = np.random.default_rng(12)
+    for bits, (k, n) in [(4, (64, 64)), (8, (64, 64)), (4, (96, 33)), (8, (70, 9))]:
+        banner("nan-sequence", bits, k, n)
+        clean = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+        bad = clean.copy()
+        bad[k // 2, n // 3] = np.nan
+        for pattern in ("bbcbccb", "cbbbc"):
+            for c in pattern:
+                if c == "b":
+                    with pytest.raises(kt.IllegalArgumentException):
+                        gpu_quantize(kt, bad, bits, 32)
+                else:
+                    _check(kt, oracle_lib, clean, bits, 32, "between_nan")
+
+
 @pytest.mark.parametrize("shape", [(2048, 2048), (896, 4864), (4864, 896), (2048, 8192), (4096, 14336),
                                    (14336, 4096), (896, 151936)])
 @pytest.mark.parametrize("bits", [4, 8])
