@@ -206,6 +206,21 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
 int32_t kt_qmatmul_transposed(const float* dy, int32_t m, const kt_qweight* w, float* dx,
                               int32_t accumulate, void* stream);
 
+/* fusedCrossEntropyLoss(hidden, head, targets, ignoreIndex) with a QuantizedLinear head,
+ * K/Loss.kt:114-219: the loss and the gradients its backward closure adds for an upstream
+ * gradient of 1. hidden [rows x K] device; head: K -> N with bias [N] (device, NULL =
+ * zeros); targets [rows] HOST int32, each ignore_index or in [0, N) (read before the call
+ * returns). *loss (device float) = mean over the other rows of max + ln(sum exp(l - max))
+ * - l[target], l = hidden . deq(W) + bias. hidden_grad [rows x K] and bias_grad [N]
+ * (device, each may be NULL) receive d loss / d hidden and d loss / d bias, added to
+ * what they hold when accumulate != 0 (ignored rows get 0). Rows go through in chunks of
+ * 2^22 / N logits as in the reference; scratch for one chunk is allocated on the stream
+ * (hipMallocAsync) and freed after it. Asynchronous. KT_ERR_ARGUMENT for no rows or a
+ * target out of range ("target t out of bounds N"). */
+int32_t kt_fused_cross_entropy(const float* hidden, int32_t rows, const kt_qweight* head, const float* bias,
+                               const int32_t* targets, int32_t ignore_index, float* loss, float* hidden_grad,
+                               float* bias_grad, int32_t accumulate, void* stream);
+
 /* ---- dequant accessors ---------------------------------------------------------- */
 /* dequantizeRow for each index in rows[0..count) (device int32 array), writing
  * out[i x N]; the row gather of QuantizedEmbedding.lookupInto/forward

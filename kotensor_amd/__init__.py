@@ -7,7 +7,8 @@ package is a host-side mirror of the reference's API over that ABI:
 ``DeviceTensor.matmul_dequant(_into)``, ``QuantizedLinear``, the saveQuantized
 file format (``SafeTensorsFile``, ``save_quantized``, ``load_quantized``) and the
 device-resident decoder around the projections (``Transformer``, ``KVCache``,
-``InferenceBuffers``, ``RoPEScaling``).
+``InferenceBuffers``, ``RoPEScaling``) and the fused projection + cross-entropy with a
+quantized head (``fused_cross_entropy_loss``).
 """
 from ._lib import IllegalArgumentException, IllegalStateException, LibraryMissingError, LIBRARY_PATH
 from .device import DeviceBuffer, Stream, synchronize, device_count
@@ -16,6 +17,7 @@ from .matmul import MatMul, DeviceTensor
 from .linear import QuantizedLinear, projection, forward_into_group
 from .safetensors import SafeTensorsFile, save_entries, save_quantized, load_quantized
 from .transformer import Transformer, KVCache, InferenceBuffers, RoPEScaling
+from .loss import fused_cross_entropy_loss, FusedLoss, IGNORE_INDEX
 
 __all__ = [
     "IllegalArgumentException",
@@ -41,4 +43,7 @@ __all__ = [
     "KVCache",
     "InferenceBuffers",
     "RoPEScaling",
+    "fused_cross_entropy_loss",
+    "FusedLoss",
+    "IGNORE_INDEX",
 ]

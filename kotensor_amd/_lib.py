@@ -111,6 +111,7 @@ SIGNATURES = {
     "kt_qlinear_forward": [_P, _I, ctypes.POINTER(_QWeight), _P, _P, _P],
     "kt_qmatmul_group": [_P, _I, ctypes.POINTER(_QWeight), _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _F, _P],
     "kt_qmatmul_transposed": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _P],
+    "kt_fused_cross_entropy": [_P, _I, ctypes.POINTER(_QWeight), _P, _P, _I, _P, _P, _P, _I, _P],
     "kt_dequantize_rows": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
     "kt_dequantize_columns": [ctypes.POINTER(_QWeight), _P, _I, _P, _P],
     "kt_rope_inv_freq": [_I, _F, _F, _F, _F, _I, _P],

@@ -81,6 +81,7 @@ def lib():
         L.ko_silu_mul.argtypes = [P, P, I]
         L.ko_silu_mul.restype = None
         L.ko_argmax.argtypes = [P, I]
+        L.ko_fused_cross_entropy.argtypes = [P, I, ctypes.POINTER(QW), P, P, I, P, P, P, I]
         _lib = L
     return _lib
 
@@ -203,6 +204,25 @@ def multiply_quantized(a: np.ndarray, w: Quantized, m: int, c: np.ndarray | None
     if st != KO_OK:
         raise ValueError(f"oracle multiply_quantized status {st}")
     return c.reshape(m, w.columns)
+
+
+def fused_cross_entropy(hidden: np.ndarray, w: Quantized, targets, bias: np.ndarray | None = None,
+                        ignore_index: int = -100, grads: bool = True, threads: int = 1):
+    """fusedCrossEntropyLoss with a quantized head (Loss.kt:114-219): returns (loss,
+    hidden_grad [rows x K], bias_grad [N]) for an upstream gradient of 1, the gradients
+    None when grads is False. Raises ValueError where the reference's require fails."""
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32).reshape(-1)
+    t = np.ascontiguousarray(np.asarray(targets, dtype=np.int32).reshape(-1))
+    rows = t.size
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+    loss = np.zeros(1, dtype=np.float32)
+    hg = np.zeros(rows * w.rows, dtype=np.float32) if grads else None
+    bg = np.zeros(w.columns, dtype=np.float32) if grads else None
+    st = lib().ko_fused_cross_entropy(_p(hidden), rows, ctypes.byref(w.qw), _p(b), _p(t), ignore_index, _p(loss),
+                                      _p(hg), _p(bg), threads)
+    if st != KO_OK:
+        raise ValueError(f"oracle fused_cross_entropy status {st}")
+    return float(loss[0]), (None if hg is None else hg.reshape(rows, w.rows)), bg
 
 
 def multiply_by_quantized_transposed(dy: np.ndarray, w: Quantized, m: int, dx: np.ndarray | None = None,

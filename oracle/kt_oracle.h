@@ -118,6 +118,17 @@ void ko_silu_mul(float* gate, const float* up, int32_t n);
 /* Transformer.argmaxOfLastToken (K/Transformer.kt:253-266). */
 int32_t ko_argmax(const float* logits, int32_t n);
 
+/* ---- the fused loss (kt_oracle_loss.c) -------------------------------------------- */
+/* fusedCrossEntropyLoss(hidden, QuantizedLinear(w, bias), targets, ignoreIndex),
+ * K/Loss.kt:114-219: *loss = mean over the rows whose target is not ignore_index of
+ * max + ln(sum exp(l - max)) - l[target], logits l = hidden . deq(w) + bias (bias may be
+ * NULL: zeros). hidden_grad [rows x K] and bias_grad [N] (each may be NULL) receive, added
+ * to what they hold, the gradients the backward closure adds for an upstream gradient of
+ * 1 (ignored rows get nothing). KO_ERR_ARG for no rows or a target outside [0, N). */
+int32_t ko_fused_cross_entropy(const float* hidden, int32_t rows, const ko_qweight* w, const float* bias,
+                               const int32_t* targets, int32_t ignore_index, float* loss, float* hidden_grad,
+                               float* bias_grad, int32_t threads);
+
 #ifdef __cplusplus
 }
 #endif
