@@ -31,6 +31,7 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int KT = 64;        // keys per attention tile
+constexpr int MAX_SPLITS = 64;  // key splits of one (token, kv head); the merge holds one weight per lane
 constexpr int MAX_NACC = 4;   // (head, dim) pairs per thread: heads per kv head x head_dim <= 1024
 constexpr int MAX_HD = 256;
 
@@ -155,24 +156,30 @@ struct AttnArgs {
     const float* v_new;
     const float* inv_freq;
     int32_t rope;
+    // several splits: one counter per (token, kv head), zero on entry and on exit; the
+    // split that takes it to splits - 1 merges all splits (no second kernel)
+    uint32_t* counters;
 };
 
 // Workgroup (kv head g, key split s, token t): the G = num_heads / num_kv_heads query
 // heads of kv head g over keys [s * span, min((s + 1) * span, position + t + 1)), in
 // tiles of 64 keys with a running maximum and sum (scores, then exp(score - max),
 // then the weighted values). With one split the workgroup writes the context; with
-// several it writes (sum of weighted values, max, sum) for attn_combine_kernel.
+// several the last split to finish merges every split's (sum of weighted values, max,
+// sum) and writes the context.
 // Every global load of a tile is issued before the first is used (unrolled, predicated
 // float4 loads into registers, then LDS), so a tile costs one memory round trip.
 // TF4: float4 per thread for a full tile (4, 8, 16 for head_dim up to 64, 128, 256).
 // Unconditional loads of in-bounds addresses (indices past the tile repeat its last
 // float4; the stores are masked): no branch around a load, so all go out together.
+// (native 4-vectors: the registers of a tile stay registers across the loop)
+typedef float f4 __attribute__((ext_vector_type(4)));
 template <int TF4>
-__device__ __forceinline__ void load_tile(float4 (&r)[TF4], const float* src, int32_t n4) {
+__device__ __forceinline__ void load_tile(f4 (&r)[TF4], const float* src, int32_t n4) {
 #pragma unroll
     for (int i = 0; i < TF4; ++i) {
         const int32_t e = min(static_cast<int32_t>(threadIdx.x) + i * THREADS, n4 - 1);
-        r[i] = reinterpret_cast<const float4*>(src)[e];
+        r[i] = reinterpret_cast<const f4*>(src)[e];
     }
 }
 
@@ -188,17 +195,31 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     float* vs = ks + KT * KP;          // [KT][HD]
     float* sc = vs + KT * HD;          // [G][KT]
     float* st = sc + G * KT;           // [G] x {m, l, alpha}
+    float* kn_s = st + 3 * G;          // [HD] the new key after RoPE (the workgroup holding it), then one word
     const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     const int32_t pos = *a.position + t;
     const int32_t k_begin = s * a.span;
     const int32_t k_end = min(min(k_begin + a.span, pos + 1), a.max_seq);  // never read outside the cache
     const size_t base = (static_cast<size_t>(a.layer) * a.num_kv_heads + g) * a.max_seq;  // row of key 0
+    // With RoPE inside, the workgroup whose key range holds the new position appends the
+    // rotated key and the value to the cache for later steps and uses them from LDS in
+    // its own tile (its tile load may see the row before or after the append; the LDS copy
+    // replaces it), so no fence or second read of the row is needed.
+    const bool holder = a.rope && pos >= k_begin && pos < k_end;
 
     // q of the G heads (G * HD <= 1024 floats: at most one float4 per thread)
     const int32_t q4 = G * HD / 4;
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < q4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(t) * dim + g * G * HD)[tid];
+    // the first tile's keys and values go out with q, before the RoPE work
+    constexpr bool TOGETHER = TF4 <= 8;
+    f4 kr[TF4], vr[TOGETHER ? TF4 : 1];
+    if (k_begin < k_end) {
+        const int32_t n4 = min(KT, k_end - k_begin) * HD / 4;
+        load_tile<TF4>(kr, a.ck + (base + k_begin) * HD, n4);
+        if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k_begin) * HD, n4);
+    }
     if (tid < G) {
         st[3 * tid] = -INFINITY;
         st[3 * tid + 1] = 0.0f;
@@ -210,10 +231,8 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     for (int r = 0; r < MAX_NACC; ++r) acc[r] = 0.0f;
 
     if (a.rope) {
-        // One decode token, RoPE inside: the G query heads are rotated in LDS, and the
-        // workgroup whose key range holds the new position rotates the new key, appends
-        // it and the value to the cache, and makes the writes visible to its own tile
-        // loads (the only reads of that row in this step).
+        // one decode token: the G query heads are rotated in LDS; the holder rotates the
+        // new key into LDS and appends it and the value to the cache
         if (tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
         __syncthreads();
         const int32_t half = HD >> 1;
@@ -224,7 +243,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             qs[hh * HD + i] = y1;
             qs[hh * HD + i + half] = y2;
         }
-        if (pos >= k_begin && pos < k_end) {
+        if (holder) {
             float* ckw = const_cast<float*>(a.ck) + (base + pos) * HD;
             float* cvw = const_cast<float*>(a.cv) + (base + pos) * HD;
             const float* kn = a.k_new + static_cast<size_t>(g) * HD;
@@ -232,25 +251,26 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             for (int32_t i = tid; i < half; i += THREADS) {
                 float y1, y2;
                 rope_rotate(kn[i], kn[i + half], pos, a.inv_freq[i], y1, y2);
+                kn_s[i] = y1;
+                kn_s[i + half] = y2;
                 ckw[i] = y1;
                 ckw[i + half] = y2;
                 cvw[i] = vn[i];
                 cvw[i + half] = vn[i + half];
             }
-            __threadfence();
         }
         __syncthreads();
     }
 
     // K and V tiles in registers together (one round trip) up to head_dim 128; wider
     // heads load them one after the other to keep the registers in bounds.
-    constexpr bool TOGETHER = TF4 <= 8;
-    float4 kr[TF4], vr[TOGETHER ? TF4 : 1];
     for (int32_t k0 = k_begin; k0 < k_end; k0 += KT) {
         const int32_t n = min(KT, k_end - k0);
         const int32_t n4 = n * HD / 4;
-        load_tile<TF4>(kr, a.ck + (base + k0) * HD, n4);
-        if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k0) * HD, n4);
+        if (k0 != k_begin) {
+            load_tile<TF4>(kr, a.ck + (base + k0) * HD, n4);
+            if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k0) * HD, n4);
+        }
         if (!a.rope && k0 == k_begin && tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
 #pragma unroll
         for (int i = 0; i < TF4; ++i) {
@@ -262,7 +282,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
                 kd[1] = kr[i].y;
                 kd[2] = kr[i].z;
                 kd[3] = kr[i].w;
-                if constexpr (TOGETHER) reinterpret_cast<float4*>(vs)[e] = vr[i];
+                if constexpr (TOGETHER) reinterpret_cast<f4*>(vs)[e] = vr[i];
             }
         }
         if constexpr (!TOGETHER) {
@@ -270,7 +290,18 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < TF4; ++i) {
                 const int32_t e = tid + i * THREADS;
-                if (e < n4) reinterpret_cast<float4*>(vs)[e] = kr[i];
+                if (e < n4) reinterpret_cast<f4*>(vs)[e] = kr[i];
+            }
+        }
+        if (holder && pos >= k0 && pos < k0 + n) {
+            // the new row from LDS and the projection, whatever the tile load saw (each
+            // thread replaces elements it did not write, so the tile writes come first)
+            __syncthreads();
+            const int32_t j = pos - k0;
+            const float* vn = a.v_new + static_cast<size_t>(g) * HD;
+            for (int32_t d = tid; d < HD; d += THREADS) {
+                ks[j * KP + d] = kn_s[d];
+                vs[j * HD + d] = vn[d];
             }
         }
         __syncthreads();
@@ -327,24 +358,70 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         __syncthreads();
     }
 
+    if (a.splits == 1) {
+#pragma unroll
+        for (int r = 0; r < MAX_NACC; ++r) {
+            const int32_t e = tid + r * THREADS;
+            if (r < nacc && e < pairs) {
+                const int32_t i = e / HD, d = e % HD;
+                a.context[static_cast<size_t>(t) * dim + (g * G + i) * HD + d] = acc[r] * (1.0f / st[3 * i + 1]);
+            }
+        }
+        return;
+    }
+    // Several splits: every split stores (sum of weighted values, max, sum) per head with
+    // write-through (system-scope) stores and waits for them; the workgroup that then
+    // takes the (token, kv head) counter to splits - 1 is the last one: it reads every
+    // split's values back past the caches and merges them in split order, as
+    // attn_combine_kernel does, then returns the counter to zero. No fence and no waiting
+    // on other workgroups; the merge order, and so the result, does not depend on timing.
+    const size_t pbase = (static_cast<size_t>(t) * a.num_heads + g * G) * a.splits;  // (head g G, split 0)
 #pragma unroll
     for (int r = 0; r < MAX_NACC; ++r) {
         const int32_t e = tid + r * THREADS;
         if (r < nacc && e < pairs) {
             const int32_t i = e / HD, d = e % HD;
-            const int32_t head = g * G + i;
-            if (a.splits == 1) {
-                a.context[static_cast<size_t>(t) * dim + head * HD + d] = acc[r] * (1.0f / st[3 * i + 1]);
-            } else {
-                float* pp = a.partials + ((static_cast<size_t>(t) * a.num_heads + head) * a.splits + s) * (HD + 2);
-                pp[d] = acc[r];
-                if (d == 0) {
-                    pp[HD] = st[3 * i];
-                    pp[HD + 1] = st[3 * i + 1];
-                }
+            float* pp = a.partials + (pbase + static_cast<size_t>(i) * a.splits + s) * (HD + 2);
+            __hip_atomic_store(pp + d, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (d == 0) {
+                __hip_atomic_store(pp + HD, st[3 * i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(pp + HD + 1, st[3 * i + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // every thread's stores are complete before the count
+    uint32_t* counter = a.counters + static_cast<size_t>(t) * a.num_kv_heads + g;
+    uint32_t* last_s = reinterpret_cast<uint32_t*>(kn_s + HD);  // in the dynamic LDS: no static LDS
+    if (tid == 0) *last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*last_s != static_cast<uint32_t>(a.splits - 1)) return;
+    const int32_t S = a.splits;
+    float* ws = sc;  // [G][S] weights (S <= MAX_SPLITS <= KT)
+    for (int32_t i = wave; i < G; i += THREADS / 64) {
+        const float* pp = a.partials + (pbase + static_cast<size_t>(i) * S) * (HD + 2);
+        const float ms = lane < S ? __hip_atomic_load(pp + lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                                  : -INFINITY;
+        const float ls = lane < S ? __hip_atomic_load(pp + lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_SYSTEM)
+                                  : 0.0f;
+        const float m = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
+        const float l = wave_sum(w * ls);
+        if (lane < S) ws[i * KT + lane] = w;
+        if (lane == 0) st[3 * i + 1] = l;
+    }
+    __syncthreads();
+    for (int32_t e = tid; e < pairs; e += THREADS) {
+        const int32_t i = e / HD, d = e % HD;
+        const float* pp = a.partials + (pbase + static_cast<size_t>(i) * S) * (HD + 2);
+        float x = 0.0f;
+        for (int32_t sp = 0; sp < S; ++sp)
+            x = fmaf(__hip_atomic_load(pp + sp * (HD + 2) + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM),
+                     ws[i * KT + sp], x);
+        a.context[static_cast<size_t>(t) * dim + (g * G + i) * HD + d] = x * (1.0f / st[3 * i + 1]);
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- prefill attention: blocked over queries, fp32 MFMA ---------------------------------
@@ -534,35 +611,6 @@ size_t attention_prefill_lds(int32_t head_dim) {
     return (q > kv ? q : kv) * sizeof(float);
 }
 
-constexpr int MAX_SPLITS = 64;
-
-// Workgroup (token t, head h): merges the splits' (weighted values, max, sum). The
-// splits' maxima and sums go through LDS first, so the loads are issued together.
-__global__ void __launch_bounds__(THREADS) attn_combine_kernel(AttnArgs a) {
-    __shared__ float ws[MAX_SPLITS];
-    __shared__ float total;
-    const int32_t t = blockIdx.y, h = blockIdx.x, HD = a.head_dim, S = a.splits;
-    const float* pp = a.partials + (static_cast<size_t>(t) * a.num_heads + h) * S * (HD + 2);
-    const int32_t tid = threadIdx.x;
-    if (tid < 64) {
-        const float ms = tid < S ? pp[tid * (HD + 2) + HD] : -INFINITY;
-        const float ls = tid < S ? pp[tid * (HD + 2) + HD + 1] : 0.0f;
-        const float m = wave_max(ms);
-        const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
-        const float l = wave_sum(w * ls);
-        if (tid < S) ws[tid] = w;
-        if (tid == 0) total = l;
-    }
-    __syncthreads();
-    const float inv = 1.0f / total;
-    for (int32_t d = tid; d < HD; d += THREADS) {
-        float x = 0.0f;
-#pragma unroll 8
-        for (int32_t s = 0; s < S; ++s) x = fmaf(pp[s * (HD + 2) + d], ws[s], x);
-        a.context[static_cast<size_t>(t) * a.num_heads * HD + h * HD + d] = x * inv;
-    }
-}
-
 // ---- SwiGLU gate -----------------------------------------------------------------------
 __global__ void __launch_bounds__(THREADS) silu_mul_kernel(float* __restrict__ gate, const float* __restrict__ up,
                                                            int64_t n) {
@@ -672,7 +720,8 @@ constexpr int32_t ARGMAX_BLOCKS = 64;
 
 size_t attention_lds(int32_t G, int32_t HD) {
     return sizeof(float) * (static_cast<size_t>(G) * HD + static_cast<size_t>(KT) * (HD + 1) +
-                            static_cast<size_t>(KT) * HD + static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G));
+                            static_cast<size_t>(KT) * HD + static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G) +
+                            static_cast<size_t>(HD) + 1);
 }
 
 }  // namespace
@@ -821,10 +870,11 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     a.rope = k_new != nullptr ? 1 : 0;
     a.span = ceil_div(tiles, splits) * KT;
     a.splits = ceil_div(key_bound, a.span);
-    if (a.splits > 1) {
+    if (a.splits > 1) {  // tokens * num_kv_heads < 2 * CUs counters
         void* ws = nullptr;
         const size_t bytes = static_cast<size_t>(tokens) * num_heads * a.splits * (head_dim + 2) * sizeof(float);
-        const int32_t status = workspace(st, bytes, &ws);
+        const int32_t status =
+            workspace_counters(st, bytes, static_cast<size_t>(tokens) * num_kv_heads, &ws, &a.counters);
         if (status) return status;
         a.partials = static_cast<float*>(ws);
     }
@@ -844,10 +894,6 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     else if (head_dim <= 128) attention_kernel<8><<<grid, THREADS, lds, st>>>(a);
     else attention_kernel<16><<<grid, THREADS, lds, st>>>(a);
     KT_LAUNCHED("attention kernel");
-    if (a.splits > 1) {
-        attn_combine_kernel<<<dim3(static_cast<uint32_t>(num_heads), static_cast<uint32_t>(tokens)), THREADS, 0, st>>>(a);
-        KT_LAUNCHED("attention combine kernel");
-    }
     return KT_OK;
 }
 
