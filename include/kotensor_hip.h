@@ -55,7 +55,8 @@ extern "C" {
 /* A quantized weight held in device memory. Mirrors the fields of
  * QuantizedTensor (K/QuantizedTensor.kt:27-49): rows = K (in), columns = N (out).
  * packed is optional (NULL or a copy written by kt_qweight_pack): a second, device-native
- * arrangement of qdata that the one-row products read instead when it is present. */
+ * arrangement of qdata that the one-row products read instead when it is present, and
+ * the prefill GEMM too when group_size is a multiple of 32. */
 typedef struct kt_qweight {
     const void* qdata;
     const float* scales;
@@ -134,10 +135,11 @@ int32_t kt_qweight_check(const kt_qweight* w);
  * product at shapes like 4096 -> 14336 split its K range over workgroups and meet their
  * sums through memory. The column-run copy keeps each column's K values contiguous in
  * 16-column blocks (1 KB per 128 k for 4-bit, 2 KB for 8-bit), so the one-row kernel
- * reads whole columns with no cross-workgroup sums. It is a device-side accelerator
- * next to qdata, not a format: files, quantize, the accessors and products of more than
- * one row keep using qdata. Write it once after qdata is final (and again if qdata
- * changes), then set kt_qweight.packed. Size: ceil(columns / 16) * ceil(rows / 128)
+ * reads whole columns with no cross-workgroup sums; the prefill GEMM (three or more
+ * rows, group_size % 32 == 0) reads each lane's MFMA operand bytes from it as 16 or 8
+ * contiguous bytes. It is a device-side accelerator next to qdata, not a format: files,
+ * quantize and the accessors keep using qdata. Write it once after qdata is final (and
+ * again if qdata changes), then set kt_qweight.packed. Size: ceil(columns / 16) * ceil(rows / 128)
  * * (bits == 4 ? 1024 : 2048) bytes, 16-byte aligned. */
 int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int64_t* bytes);
 /* Writes the copy of w's qdata into `packed` (kt_qweight_packed_bytes bytes of device

@@ -75,6 +75,7 @@ constexpr int MAX_GEMM_JOBS = 4;
 // smax[smax_begin .. smax_begin + nsb).
 struct GemmJob {
     const uint8_t* q;
+    const uint8_t* p;  // the column-run copy (gemm_packed_kernel)
     const float* s;
     const int8_t* z;
     float* c;
@@ -138,6 +139,28 @@ __device__ __forceinline__ f32x4 row_chunk(const float* row, int32_t c, int32_t 
     return v;
 }
 
+// The largest |scale| over slice sb of the launch's scale slices, into smax[sb] (256
+// threads). G * N is a multiple of 4 and s is 16-byte aligned (checked by the launchers).
+__device__ __forceinline__ void scale_slice_max(const GemmJobs& jobs, int32_t sb, float* red, float* __restrict__ smax) {
+    const int32_t t = threadIdx.x;
+    const GemmJob& jb = jobs.job[job_of_scale_block(jobs, sb)];
+    const float* s = jb.s;
+    const int64_t scale_quads = jb.scale_quads;
+    const int32_t nsb = jb.nsb;
+    const int64_t per = (scale_quads + nsb - 1) / nsb;
+    const int32_t sl = sb - jb.smax_begin;
+    const int64_t begin = per * sl;
+    const int64_t end = begin + per < scale_quads ? begin + per : scale_quads;
+    float mx = 0.0f;
+#pragma unroll 8
+    for (int64_t i = begin + t; i < end; i += 256) {
+        const f32x4 u = reinterpret_cast<const f32x4*>(s)[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3]))));
+    }
+    mx = block_max<4>(mx, red);
+    if (t == 0) smax[sb] = mx;
+}
+
 // Blocks [0, Mp): row m of a as fp16 times 2^-er[m] (zeros for m >= M and k >= K).
 // Blocks [Mp, Mp + sum of nsb): the largest |scale| over one slice of a job's G * N scales.
 __global__ void __launch_bounds__(256)
@@ -187,24 +210,7 @@ __global__ void __launch_bounds__(256)
         if (t == 0) er[m] = e;
         return;
     }
-    // Scales: G * N is a multiple of 4 and s is 16-byte aligned (checked by gemm_supported).
-    const int32_t sb = b - Mp;
-    const GemmJob& jb = jobs.job[job_of_scale_block(jobs, sb)];
-    const float* s = jb.s;
-    const int64_t scale_quads = jb.scale_quads;
-    const int32_t nsb = jb.nsb;
-    const int64_t per = (scale_quads + nsb - 1) / nsb;
-    const int32_t sl = sb - jb.smax_begin;
-    const int64_t begin = per * sl;
-    const int64_t end = begin + per < scale_quads ? begin + per : scale_quads;
-    float mx = 0.0f;
-#pragma unroll 8
-    for (int64_t i = begin + t; i < end; i += 256) {
-        const f32x4 u = reinterpret_cast<const f32x4*>(s)[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3]))));
-    }
-    mx = block_max<4>(mx, red);
-    if (t == 0) smax[sb] = mx;
+    scale_slice_max(jobs, b - Mp, red, smax);
 }
 
 // Work split of the 512 threads per K step: the weight tile is 64 rows x 32 lanes of
@@ -625,6 +631,403 @@ __global__ void __launch_bounds__(256)
     c[idx] = bias ? o + bias[idx % N] : o;
 }
 
+
+// ---- prefill GEMM on the column-run copy ------------------------------------------------
+// With the weight's column-run copy (kt_qweight_pack) and g a multiple of 32, each of the
+// four waves of a workgroup computes the whole 128 x 128 output tile over its own quarter
+// of K: slabs of 32 k, wave w taking slabs w, w + 4, ... of the workgroup's range. A wave
+// shares no operand with another, so the K loop has no LDS traffic and no barrier: every
+// operand goes from memory straight into registers in the MFMA layout (16-byte lanes for
+// a, 16 or 8 contiguous bytes of one column for the weights), PDEPTH slabs ahead, and the
+// 128 x 128 fp32 sums (16 blocks of v_mfma_f32_32x32x16_f16) sit in the accumulation
+// registers. The four waves' sums meet once, through LDS, at the end, added in wave order.
+//
+// MFMA k order. In slab s, lane l (row or column l % 32, hl = l / 32) supplies elements
+// e = 0..7 of sub-product i = 0, 1 at k =
+//   INT8: 32 s + 16 hl + 8 i + e      (column-run bytes 8 i + e of piece hl of run s),
+//   INT4: 64 (s / 2) + 32 hl + 16 (s % 2) + 8 i + e   (dword 2 (s % 2) + i of the lane's
+//         16 bytes of run 2 (s / 2) + hl: low nibbles e = 0..3, high nibbles e = 4..7),
+// so a lane's weight bytes are contiguous in the copy. The fp16 copy of a is written in
+// the same order by gemm_prep_tiled: per (row tile, slab) 8 KiB, piece (row block rb,
+// sub i) of 1 KiB holding lane l's 16 bytes at 16 l. With g % 32 == 0 a lane's 16 or 32 k
+// of a column lie in one scale group.
+// Dequantization and scaling are those of gemm_kernel (same fp16 values of the weights and
+// of a, the same powers of two); only the order of the fp32 sums differs.
+constexpr int PT = 128;                  // tile rows and columns
+constexpr int PTHREADS = 256;
+constexpr int PDEPTH = 3;                // slabs a wave holds or has in flight
+constexpr int PSLAB = PT * 32 * 2;       // bytes of fp16 a per (row tile, slab)
+constexpr int MPITCH = PT + 4;           // floats per row of the epilogue's meet
+constexpr size_t PLDS = 4 * 64 * MPITCH * sizeof(float);  // the meet: four waves x 64 rows, 132 KiB
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Rows of a in the tiled fp16 order above, one wave per row (blocks [0, Mp / 4)), then the
+// scale slices as gemm_prep. S = slabs (K rounded up to 128, over 32).
+template <int BITS>
+__global__ void __launch_bounds__(256)
+    gemm_prep_tiled(const float* __restrict__ a, int32_t M, int32_t K, int32_t S, int32_t vec_rows, int32_t Mp,
+                    GemmJobs jobs, _Float16* __restrict__ a16t, int32_t* __restrict__ er, float* __restrict__ smax) {
+    __shared__ float red[4];
+    const int32_t b = blockIdx.x;
+    if (b >= Mp / 4) {
+        scale_slice_max(jobs, b - Mp / 4, red, smax);
+        return;
+    }
+    const int32_t m = b * 4 + (threadIdx.x >> 6);
+    const int32_t ln = threadIdx.x & 63;
+    const int32_t tm = m / PT, r = m % PT, rb = r / 32, rl = r % 32;
+    // the piece holding k = 32 sp + 8 o8 .. + 8 of this row
+    auto piece = [&](int32_t sp, int32_t o8) -> u32x4* {
+        const int32_t q = o8 >> 1, i = o8 & 1;
+        const int32_t slab = BITS == 8 ? sp : 2 * (sp >> 1) + q;
+        const int32_t hl = BITS == 8 ? q : (sp & 1);
+        return reinterpret_cast<u32x4*>(a16t) + ((static_cast<size_t>(tm) * S + slab) * 8 + rb * 2 + i) * 64 + rl + 32 * hl;
+    };
+    if (m >= M) {
+        for (int32_t sp = ln; sp < S; sp += 64)
+#pragma unroll
+            for (int o8 = 0; o8 < 4; ++o8) *piece(sp, o8) = u32x4{0u, 0u, 0u, 0u};
+        if (ln == 0) er[m] = 0;
+        return;
+    }
+    const float* row = a + static_cast<size_t>(m) * K;
+    const bool vec = vec_rows != 0;
+    auto absmax = [](const f32x4& v) { return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))); };
+    auto put = [&](int32_t sp, int o8, const f32x4& v0, const f32x4& v1, int32_t e) {
+        *piece(sp, o8) = u32x4{pack_half2(ldexpf(v0[0], -e), ldexpf(v0[1], -e)),
+                               pack_half2(ldexpf(v0[2], -e), ldexpf(v0[3], -e)),
+                               pack_half2(ldexpf(v1[0], -e), ldexpf(v1[1], -e)),
+                               pack_half2(ldexpf(v1[2], -e), ldexpf(v1[3], -e))};
+    };
+    float mx = 0.0f;
+    if (S <= 2 * 64) {
+        // K <= 4096: the lane's (at most two) spans stay in registers, the row is read once
+        f32x4 v[2][8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const int32_t sp = ln + 64 * h;
+                v[h][c] = sp < S ? row_chunk(row, sp * 8 + c, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                mx = fmaxf(mx, absmax(v[h][c]));
+            }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const int32_t e = scale_exponent(mx, 15);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            if (ln + 64 * h < S)
+#pragma unroll
+                for (int o8 = 0; o8 < 4; ++o8) put(ln + 64 * h, o8, v[h][2 * o8], v[h][2 * o8 + 1], e);
+        if (ln == 0) er[m] = e;
+        return;
+    }
+    for (int32_t sp = ln; sp < S; sp += 64) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) mx = fmaxf(mx, absmax(row_chunk(row, sp * 8 + c, K, vec)));
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const int32_t e = scale_exponent(mx, 15);
+    for (int32_t sp = ln; sp < S; sp += 64) {
+#pragma unroll
+        for (int o8 = 0; o8 < 4; ++o8)
+            put(sp, o8, row_chunk(row, sp * 8 + 2 * o8, K, vec), row_chunk(row, sp * 8 + 2 * o8 + 1, K, vec), e);
+    }
+    if (ln == 0) er[m] = e;
+}
+
+// One slab of a wave: a pieces (2 rb + i), the weight bytes of its four column blocks, and
+// their scales and zero points.
+template <int BITS>
+struct PSlab {
+    u32x4 a[8];
+    typename std::conditional<BITS == 8, u32x4, u32x2>::type w[4];
+    float s[4];
+    uint32_t z[4];  // the dword holding the column's zero byte
+};
+
+// v_perm_b32 selectors: bytes (0, 1) or (2, 3) of a word into the low bytes of its halves.
+constexpr uint32_t SEL01 = 0x0c010c00u, SEL23 = 0x0c030c02u;
+
+template <int BITS, bool ZP>
+__global__ void __launch_bounds__(PTHREADS, 1)
+    gemm_packed_kernel(const _Float16* __restrict__ a16t, const int32_t* __restrict__ er,
+                       const float* __restrict__ smax_all, GemmJobs jobs, int32_t M, int32_t K, int32_t S, int32_t g,
+                       int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t slabs_per_split, float alpha,
+                       int32_t accumulate) {
+    extern __shared__ f32x4 meet[];  // the epilogue's meet, PLDS bytes
+    __shared__ int32_t er_s[PT];
+    __shared__ float red[4];
+
+    // Block -> (tile_n, tile_m, slice) as gemm_kernel: the workgroups of one weight tile on one XCD.
+    const int32_t pid = blockIdx.x;
+    const int32_t jx = pid / XCDS;
+    const int32_t per_n = tiles_m * splits;
+    const int32_t tile_n = (jx / per_n) * XCDS + pid % XCDS;
+    if (tile_n >= tiles_n) return;
+    const GemmJob& jb = jobs.job[job_of_tile(jobs, tile_n)];
+    const int32_t N = jb.N, nsb = jb.nsb;
+    const int32_t sets = (N + 15) / 16, chunks = S / 4, G = (K + g - 1) / g;
+    const int32_t rem = jx % per_n;
+    const int32_t tile_m = rem % tiles_m;
+    const int32_t sp = rem / tiles_m;
+    const int32_t col0 = (tile_n - jb.tile_begin) * PT;
+    const int32_t m0 = tile_m * PT;
+    const int32_t t = threadIdx.x, ln = t & 63, hl = ln >> 5;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int32_t s_begin = sp * slabs_per_split;
+    const int32_t n_mine = (min(S, s_begin + slabs_per_split) - s_begin) / 4;  // >= 1: the host keeps slices whole
+
+    const float smx = t < nsb ? smax_all[jb.smax_begin + t] : 0.0f;  // nsb <= 256
+    const int32_t erv = t < PT && m0 + t < M ? er[m0 + t] : 0;
+
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a16t) + static_cast<size_t>(tile_m) * S * (PSLAB / 2), 0, S * PSLAB, 0x00020000);
+    const uint32_t wbytes = static_cast<uint32_t>(sets) * chunks * (BITS == 8 ? 2048u : 1024u);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(jb.p), 0, wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(jb.s), 0, static_cast<uint32_t>(G) * N * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(ZP ? jb.z : nullptr), 0, ZP ? static_cast<uint32_t>(G) * N : 0u, 0x00020000);
+
+    // Lane offsets fixed for the whole loop.
+    uint32_t w_off[4], z_shift[4];
+    int32_t col_c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int32_t col = col0 + 32 * j + (ln & 31);
+        const int32_t set = min(col >> 4, sets - 1);  // past the last column: any valid bytes, outputs dropped
+        w_off[j] = static_cast<uint32_t>(set) * chunks * (BITS == 8 ? 2048u : 1024u) +
+                   (BITS == 8 ? hl * 1024u : hl * 256u) + (ln & 15) * 16u;
+        col_c[j] = min(col, N - 1);
+        z_shift[j] = 8u * (col_c[j] & 3);
+    }
+    auto load = [&](PSlab<BITS>& d, int32_t x) {
+        const int32_t s = s_begin + wave + 4 * min(x, n_mine - 1);
+#pragma unroll
+        for (int pc = 0; pc < 8; ++pc)
+            d.a[pc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, (pc * 64 + ln) * 16, s * PSLAB, 0));
+        const int32_t wso = BITS == 8 ? (s >> 2) * 2048 + (s & 3) * 256 : (s >> 2) * 1024 + ((s >> 1) & 1) * 512 + (s & 1) * 8;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (BITS == 8)
+                d.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, w_off[j], wso, 0));
+            else
+                d.w[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, w_off[j], wso, 0));
+        }
+        const int32_t kg = BITS == 8 ? 32 * s : 64 * (s >> 1) + 32 * hl;  // first k of the lane's run
+        const int32_t grp = min(kg / g, G - 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t at = static_cast<uint32_t>(grp) * N + col_c[j];
+            d.s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, at * 4, 0, 0));
+            // the dword holding the zero byte (N % 4 == 0: it lies inside the array); a byte
+            // load's extension would be placed ahead of the loop and wait for every load
+            if constexpr (ZP) d.z[j] = __builtin_amdgcn_raw_buffer_load_b32(zr, at & ~3u, 0, 0);
+        }
+    };
+
+    PSlab<BITS> sl[PDEPTH];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d + 1 < PDEPTH; ++d) {
+        load(sl[d], d);  // in slab order: the loop's waits count on it
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t < PT) er_s[t] = erv;
+    const int32_t ew = scale_exponent(block_max<PTHREADS / 64>(smx, red), 7);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float16v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // Dequantizes sub-product i of one slab's weights (the fp16 values gemm_kernel's
+    // store_piece makes): column block j's operand into b[j]. Sub-product 0 also turns the
+    // slab's scales and zero points into their fp16 forms, kept in s and z for sub-product 1.
+    auto dequant = [&](PSlab<BITS>& d, int i, half8 (&b)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (BITS == 8) {
+                if (i == 0) {
+                    const float sc = ldexpf(d.s[j], -ew);
+                    const half2v scv = {static_cast<_Float16>(sc), static_cast<_Float16>(sc)};
+                    uint32_t off = 0xE480E480u;  // -1152
+                    if constexpr (ZP) {
+                        const uint32_t zz = ((d.z[j] >> z_shift[j]) & 0xFFu) * 0x00010001u;
+                        off = (zz ^ 0x00800080u) + 0xE400E400u;
+                    }
+                    d.s[j] = __builtin_bit_cast(float, scv);
+                    d.z[j] = off;
+                }
+                const half2v scv = __builtin_bit_cast(half2v, d.s[j]);
+                const half2v ofv = as_h2(d.z[j]);
+                uint32_t h[4];
+#pragma unroll
+                for (int dw = 0; dw < 2; ++dw) {
+                    const uint32_t wv = d.w[j][2 * i + dw];
+                    const uint32_t p0 = (__builtin_amdgcn_perm(0u, wv, SEL01) ^ 0x00800080u) + 0x64006400u;
+                    const uint32_t p1 = (__builtin_amdgcn_perm(0u, wv, SEL23) ^ 0x00800080u) + 0x64006400u;
+                    h[2 * dw] = __builtin_bit_cast(uint32_t, (as_h2(p0) + ofv) * scv);
+                    h[2 * dw + 1] = __builtin_bit_cast(uint32_t, (as_h2(p1) + ofv) * scv);
+                }
+                b[j] = __builtin_bit_cast(half8, u32x4{h[0], h[1], h[2], h[3]});
+            } else {
+                if (i == 0) {
+                    const float sc = ldexpf(d.s[j], -ew);
+                    const float sh = ldexpf(d.s[j], -ew - 4);  // high nibbles enter as 1024 + 16 q
+                    const half2v lh = {static_cast<_Float16>(sc), static_cast<_Float16>(sh)};
+                    d.s[j] = __builtin_bit_cast(float, lh);
+                    d.z[j] = ((d.z[j] >> z_shift[j]) & 0xFFu) * 0x00010001u;
+                }
+                const half2v lh = __builtin_bit_cast(half2v, d.s[j]);
+                const half2v scl = {lh[0], lh[0]}, sch = {lh[1], lh[1]};
+                const uint32_t zz = d.z[j];
+                const uint32_t mlo = in_vgpr(0x000F000Fu), mhi = in_vgpr(0x00F000F0u), e1024 = in_vgpr(0x64006400u);
+                const half2v ofl = as_h2(zz | 0xE400E400u), ofh = as_h2((zz << 4) | 0xE400E400u);
+                const uint32_t wv = d.w[j][i];
+                const uint32_t p01 = __builtin_amdgcn_perm(0u, wv, SEL01), p23 = __builtin_amdgcn_perm(0u, wv, SEL23);
+                const uint32_t h0 = __builtin_bit_cast(uint32_t, (as_h2((p01 & mlo) | e1024) + ofl) * scl);
+                const uint32_t h1 = __builtin_bit_cast(uint32_t, (as_h2((p23 & mlo) | e1024) + ofl) * scl);
+                const uint32_t h2 = __builtin_bit_cast(uint32_t, (as_h2((p01 & mhi) | e1024) + ofh) * sch);
+                const uint32_t h3 = __builtin_bit_cast(uint32_t, (as_h2((p23 & mhi) | e1024) + ofh) * sch);
+                b[j] = __builtin_bit_cast(half8, u32x4{h0, h1, h2, h3});
+            }
+        }
+    };
+    // The 16 products of sub-product i of one slab.
+    auto multiply = [&](const PSlab<BITS>& d, int i, const half8 (&b)[4]) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const half8 av = __builtin_bit_cast(half8, d.a[rb * 2 + i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[j], acc[rb][j], 0, 0, 0);
+        }
+    };
+    // Software pipeline. Step u multiplies slab set u: its first sub-product's MFMAs run while
+    // the second sub-product is dequantized and the loads that refill the set freed by the
+    // step before are issued; its second sub-product's MFMAs run while the next set's first
+    // sub-product is dequantized. One MFMA, then a few vector ALU and memory instructions, in
+    // turn (sched_group_barrier), so the matrix unit is not left idle while operands are
+    // prepared and the loads go out spread over the step.
+    half8 b0[4], b1[4];
+    constexpr int NLOADS = 8 + 4 + 4 + (ZP ? 4 : 0);  // vector memory instructions per slab
+    auto step = [&](PSlab<BITS>& d, PSlab<BITS>& nx, PSlab<BITS>& refill, int32_t refill_x) {
+        multiply(d, 0, b0);
+        dequant(d, 1, b1);
+        load(refill, refill_x);  // past the end: the last slab again, never used
+#pragma unroll
+        for (int k = 0; k < NLOADS - 16; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // vector ALU
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // loads
+        }
+#pragma unroll
+        for (int k = NLOADS - 16; k < 16; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(d, 1, b1);
+        dequant(nx, 0, b0);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Sets 0 .. PDEPTH - 2 are loaded here; step u loads set (u + PDEPTH - 1) % PDEPTH (the
+    // one step u - 1 finished) with slab x + u + PDEPTH - 1.
+    dequant(sl[0], 0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t x = 0;
+    for (; x + PDEPTH <= n_mine; x += PDEPTH) {
+#pragma unroll
+        for (int u = 0; u < PDEPTH; ++u)
+            step(sl[u], sl[(u + 1) % PDEPTH], sl[(u + PDEPTH - 1) % PDEPTH], x + u + PDEPTH - 1);
+    }
+    // the last slabs; the dequantization after the last one reads a loaded set and is not used
+#pragma unroll
+    for (int u = 0; u < PDEPTH; ++u)
+        if (x + u < n_mine) step(sl[u], sl[(u + 1) % PDEPTH], sl[(u + PDEPTH - 1) % PDEPTH], x + u + PDEPTH - 1);
+
+    // The waves' sums meet in LDS, a half of the tile (64 rows) at a time: each wave writes
+    // its sums row-major (element (r, c) of a 32 x 32 block is in lane c + 32 ((r / 4) % 2),
+    // register (r / 8) * 4 + r % 4), then each thread adds four consecutive columns of a row
+    // over the waves in wave order and stores them with one 16-byte store. Any loads of old
+    // outputs and biases are all issued before the first store (on gfx9 a wait for a load
+    // also waits for every earlier store), and the copy without them has no load at all.
+    // Buffer operations on the tile's rows: an element outside [M x N] (N % 4 == 0, so a
+    // quad is inside or outside whole) gets an offset past the buffer, where loads read 0
+    // and stores are dropped.
+    float* out = jb.partials ? jb.partials + static_cast<size_t>(sp) * M * N : jb.c;
+    const bool add = !jb.partials && accumulate;
+    const float* bs = jb.partials ? nullptr : jb.bias;
+    const float al = jb.partials ? 1.0f : alpha;
+    const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+        out + static_cast<size_t>(m0) * N, 0, static_cast<uint32_t>(min(M - m0, PT)) * N * 4, 0x00020000);
+    float* mt = reinterpret_cast<float*>(meet);  // [wave][64 rows][MPITCH]
+    const int32_t c4 = t & 31, rsub = t >> 5;      // this thread's column quad and row within 8
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        __syncthreads();  // er_s written; the previous half's meet read
+#pragma unroll
+        for (int rl = 0; rl < 2; ++rl)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int32_t r = rl * 32 + (e >> 2) * 8 + (ln >> 5) * 4 + (e & 3);
+                    mt[(wave * 64 + r) * MPITCH + j * 32 + (ln & 31)] = acc[half * 2 + rl][j][e];
+                }
+        __syncthreads();
+        // item it: row it * 8 + rsub of the half, columns 4 c4 .. 4 c4 + 3
+        auto offset = [&](int it) -> uint32_t {
+            const int32_t rt = half * 64 + it * 8 + rsub;  // tile row
+            return m0 + rt < M && col0 + 4 * c4 < N ? static_cast<uint32_t>(rt * N + col0 + 4 * c4) * 4u : 0x80000000u;
+        };
+        auto total = [&](int it) -> f32x4 {
+            const int32_t r = it * 8 + rsub;
+            const int32_t idx = r * MPITCH + 4 * c4;
+            f32x4 v = *reinterpret_cast<const f32x4*>(mt + idx);
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(mt + w * 64 * MPITCH + idx);
+            return v * ldexpf(1.0f, er_s[half * 64 + r] + ew);
+        };
+        auto store = [&](auto loads) {
+            constexpr bool LOADS = decltype(loads)::value;
+            f32x4 old[8];
+            f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (LOADS) {
+                if (bs) bv = *reinterpret_cast<const f32x4*>(bs + min(col0 + 4 * c4, N - 4));
+#pragma unroll
+                for (int it = 0; it < 8; ++it)
+                    old[it] = add ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(orr, offset(it), 0, 0))
+                                  : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const f32x4 sm = total(it);
+                f32x4 v;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = LOADS ? fmaf(al, sm[c], old[it][c]) + bv[c] : al * sm[c];
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orr, offset(it), 0, 0);
+            }
+        };
+        if (add || bs) store(std::true_type{});
+        else store(std::false_type{});
+    }
+}
 }  // namespace
 
 bool gemm_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
@@ -635,6 +1038,121 @@ bool gemm_supported(const float* a, int32_t m, const WeightView& w, const float*
     return aligned(w.q, 4) && aligned(w.s, 16) && (!w.z || aligned(w.z, 4)) && aligned(c, 16);
 }
 
+// The job table of a launch: column tiles of `tile_cols` columns (value columns for the
+// column-run kernel, byte columns for gemm_kernel), scale slices for the maxima.
+static void fill_jobs(GemmJobs& jobs, const WeightView* ws, float* const* cs, const float* const* biases, int32_t count,
+                      int32_t tile_cols, bool value_columns, int32_t splits, int32_t m, int32_t* nsb_total,
+                      size_t* part_elems) {
+    jobs = GemmJobs{};
+    jobs.count = count;
+    int32_t tile_begin = 0;
+    *nsb_total = 0;
+    *part_elems = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        GemmJob& jb = jobs.job[i];
+        jb.q = ws[i].q;
+        jb.p = ws[i].p;
+        jb.s = ws[i].s;
+        jb.z = ws[i].z;
+        jb.c = cs[i];
+        jb.bias = biases ? biases[i] : nullptr;
+        jb.N = ws[i].N;
+        jb.bpr = ws[i].bpr;
+        jb.tile_begin = tile_begin;
+        tile_begin += ceil_div(value_columns ? ws[i].N : ws[i].bpr, tile_cols);
+        jb.scale_quads = static_cast<int64_t>(ws[i].G) * ws[i].N / 4;
+        int64_t nsb64 = (jb.scale_quads + 2047) / 2048;  // at least 8 quads per thread
+        if (nsb64 < 1) nsb64 = 1;
+        if (nsb64 > MAX_SCALE_BLOCKS) nsb64 = MAX_SCALE_BLOCKS;
+        jb.nsb = static_cast<int32_t>(nsb64);
+        jb.smax_begin = *nsb_total;
+        *nsb_total += jb.nsb;
+        if (splits > 1) *part_elems += static_cast<size_t>(splits) * m * ws[i].N;
+    }
+}
+
+// The column-run kernel: every weight of the group has its copy, g % 32 == 0, and INT4
+// weights have zero points (as every INT4 quantization does).
+static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
+    for (int32_t i = 0; i < count; ++i)
+        if (!ws[i].p || ws[i].g % 32 != 0 || (ws[i].bits == 4 && !ws[i].z)) return false;
+    return true;
+}
+
+static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                  const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                  hipStream_t st) {
+    const WeightView& w = ws[0];
+    const int32_t Mp = ceil_div(m, PT) * PT;
+    const int32_t chunks = ceil_div(w.K, 128);
+    const int32_t S = chunks * 4;
+    int32_t tiles_n = 0;
+    for (int32_t i = 0; i < count; ++i) tiles_n += ceil_div(ws[i].N, PT);
+    const int32_t tiles_m = Mp / PT;
+    // Split K (in whole 128-k chunks, at least two per slice) when the tiles leave CUs idle.
+    int32_t splits = 1;
+    const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+    const int32_t cus = cu_count();
+    if (tiles < cus) splits = static_cast<int32_t>((cus + tiles - 1) / tiles);
+    const int32_t cap = chunks / 2 > 1 ? chunks / 2 : 1;
+    if (splits > cap) splits = cap;
+    if (splits > MAX_SPLITS) splits = MAX_SPLITS;
+    const int32_t chunks_per_split = ceil_div(chunks, splits);
+    splits = ceil_div(chunks, chunks_per_split);
+
+    GemmJobs jobs;
+    int32_t nsb_total = 0;
+    size_t part_elems = 0;
+    fill_jobs(jobs, ws, cs, biases, count, PT, true, splits, m, &nsb_total, &part_elems);
+    auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t a16_bytes = round256(static_cast<size_t>(Mp) * S * 64);
+    const size_t er_bytes = round256(static_cast<size_t>(Mp) * 4);
+    const size_t smax_bytes = round256(static_cast<size_t>(nsb_total) * 4);
+    void* wsp = nullptr;
+    int32_t status = workspace(st, a16_bytes + er_bytes + smax_bytes + part_elems * sizeof(float), &wsp);
+    if (status) return status;
+    char* base = static_cast<char*>(wsp);
+    _Float16* a16t = reinterpret_cast<_Float16*>(base);
+    int32_t* er = reinterpret_cast<int32_t*>(base + a16_bytes);
+    float* smax = reinterpret_cast<float*>(base + a16_bytes + er_bytes);
+    float* part = reinterpret_cast<float*>(base + a16_bytes + er_bytes + smax_bytes);
+    for (int32_t i = 0; i < count && splits > 1; ++i) {
+        jobs.job[i].partials = part;
+        part += static_cast<size_t>(splits) * m * ws[i].N;
+    }
+    const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
+    const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4 + nsb_total);
+    if (w.bits == 4)
+        gemm_prep_tiled<4><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+    else
+        gemm_prep_tiled<8><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+    KT_LAUNCHED("qmatmul: tiled gemm prep");
+    static bool raised = false;
+    if (!raised) {  // the epilogue's 128 KiB meet is beyond the default dynamic LDS limit
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<4, true>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, true>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, false>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
+        raised = true;
+    }
+    const uint32_t blocks = static_cast<uint32_t>(ceil_div(tiles_n, XCDS) * XCDS * tiles_m * splits);
+#define KT_GEMM_ARGS a16t, er, smax, jobs, m, w.K, S, w.g, tiles_m, tiles_n, splits, chunks_per_split * 4, alpha, accumulate
+    if (w.bits == 4) gemm_packed_kernel<4, true><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
+    else if (w.z) gemm_packed_kernel<8, true><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
+    else gemm_packed_kernel<8, false><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
+#undef KT_GEMM_ARGS
+    KT_LAUNCHED("qmatmul: packed gemm kernel");
+    for (int32_t i = 0; i < count && splits > 1; ++i) {
+        const size_t total = static_cast<size_t>(m) * ws[i].N;
+        gemm_reduce<<<static_cast<uint32_t>((total + 255) / 256), 256, 0, st>>>(
+            jobs.job[i].partials, splits, m, ws[i].N, cs[i], biases ? biases[i] : nullptr, alpha, accumulate);
+        KT_LAUNCHED("qmatmul: gemm reduce");
+    }
+    return KT_OK;
+}
+
 int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float* const* cs, const float* const* biases,
                           int32_t count, int32_t accumulate, float alpha, hipStream_t st) {
     if (count < 1 || count > MAX_GEMM_JOBS) return fail(KT_ERR_ARGUMENT, "gemm: 1 to %d weights, got %d", MAX_GEMM_JOBS, count);
@@ -642,6 +1160,7 @@ int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float
     for (int32_t i = 1; i < count; ++i)
         if (ws[i].K != w.K || ws[i].bits != w.bits || ws[i].g != w.g || (ws[i].z != nullptr) != (w.z != nullptr))
             return fail(KT_ERR_ARGUMENT, "gemm: grouped weights must share rows, bits, group size and zero points");
+    if (gemm_packed_usable(ws, count)) return launch_gemm_packed(a, m, ws, cs, biases, count, accumulate, alpha, st);
     const int32_t Mp = ceil_div(m, BM) * BM;
     const int32_t Kp = ceil_div(w.K, BK) * BK;
     const int32_t tile_bytes = w.bits == 8 ? BN : BN / 2;
@@ -660,30 +1179,10 @@ int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float
     const int32_t steps_per_split = ceil_div(k_steps, splits);
     splits = ceil_div(k_steps, steps_per_split);  // every slice has at least one step
 
-    GemmJobs jobs{};
-    jobs.count = count;
-    int32_t tile_begin = 0, nsb_total = 0;
+    GemmJobs jobs;
+    int32_t nsb_total = 0;
     size_t part_elems = 0;
-    for (int32_t i = 0; i < count; ++i) {
-        GemmJob& jb = jobs.job[i];
-        jb.q = ws[i].q;
-        jb.s = ws[i].s;
-        jb.z = ws[i].z;
-        jb.c = cs[i];
-        jb.bias = biases ? biases[i] : nullptr;
-        jb.N = ws[i].N;
-        jb.bpr = ws[i].bpr;
-        jb.tile_begin = tile_begin;
-        tile_begin += ceil_div(ws[i].bpr, tile_bytes);
-        jb.scale_quads = static_cast<int64_t>(ws[i].G) * ws[i].N / 4;
-        int64_t nsb64 = (jb.scale_quads + 2047) / 2048;  // at least 8 quads per thread
-        if (nsb64 < 1) nsb64 = 1;
-        if (nsb64 > MAX_SCALE_BLOCKS) nsb64 = MAX_SCALE_BLOCKS;
-        jb.nsb = static_cast<int32_t>(nsb64);
-        jb.smax_begin = nsb_total;
-        nsb_total += jb.nsb;
-        if (splits > 1) part_elems += static_cast<size_t>(splits) * m * ws[i].N;
-    }
+    fill_jobs(jobs, ws, cs, biases, count, tile_bytes, false, splits, m, &nsb_total, &part_elems);
 
     auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t a16_bytes = round256(static_cast<size_t>(Mp) * Kp * sizeof(_Float16));

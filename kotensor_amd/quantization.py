@@ -121,8 +121,9 @@ class QuantizedTensor:
 
     def pack(self, stream: Stream | None = None) -> "QuantizedTensor":
         """Writes the device-native column-run copy of qdata (``kt_qweight_pack``) and
-        points the weight at it, so one-row products read it instead of qdata. qdata stays
-        the format of record (files, accessors, products of more rows). Costs
+        points the weight at it, so one-row products (and, for group sizes that are
+        multiples of 32, the prefill GEMM) read it instead of qdata. qdata stays the format
+        of record (files, accessors, the other kernels). Costs
         ``kt_qweight_packed_bytes`` more device memory (about the size of qdata); call it
         again after qdata changes. Returns self."""
         n = ctypes.c_int64()
@@ -135,7 +136,7 @@ class QuantizedTensor:
         return self
 
     def unpack(self) -> None:
-        """Drops the column-run copy (one-row products read qdata again)."""
+        """Drops the column-run copy (every product reads qdata again)."""
         self._struct.packed = None
         if self._p is not None:
             self._p.free()

@@ -267,7 +267,8 @@ class Transformer:
 
     def pack_weights(self, stream: Stream | None = None) -> None:
         """Writes the column-run copy of every projection weight (QuantizedTensor.pack), which
-        the decode step's one-row products read; prefill chunks read the reference layout."""
+        the decode step's one-row products read, and the prefill GEMM too when the group
+        size is a multiple of 32."""
         for name in self.projection_shapes():
             self.weights[name].pack(stream)
         self.packed = True
