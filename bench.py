@@ -117,6 +117,15 @@ class Weight:
         c._bind(kt_lib)
         return c
 
+    def without_copy(self, kt_lib):
+        """The same weight (shared tensors) without its column-run copy: the kernels for
+        the reference layout."""
+        c = object.__new__(Weight)
+        c.k, c.n, c.bits, c.g = self.k, self.n, self.bits, self.g
+        c.q, c.s, c.z, c.p = self.q, self.s, self.z, None
+        c._bind(kt_lib)
+        return c
+
     @property
     def nbytes(self):
         return self.q.numel() + 4 * self.s.numel() + (self.z.numel() if self.z is not None else 0)
@@ -296,6 +305,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 8B GEMV and M=512 GEMM figures")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--plain", action="store_true",
+                    help="with --only gemm: weights without the column-run copy (the reference-layout GEMM)")
     ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm"],
                     help="run one kernel for a rocprofv3 run")
     args = ap.parse_args()
@@ -354,16 +365,20 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
                           "algorithmic_bytes": done, "launches_each": args.steps}), flush=True)
         return 0
     if args.only == "gemm":
-        # the INT8 g32 prefill GEMM at M = 512 on 2048 -> 8192, weight copies in rotation
+        # the INT8 g32 prefill GEMM at M = 512 on 2048 -> 8192 (column-run copy), weight
+        # copies in rotation
         wg = Weight(torch, kt_lib, 2048, 8192, 8, 32, seed=9, stream=stream)
-        cg = [wg] + [wg.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // wg.nbytes)) - 1)]
+        if not args.plain:
+            wg.pack(torch, kt_lib, stream)
+        cg = [wg] + [wg.clone(kt_lib) for _ in range(max(1, -(-2 * MALL_BYTES // (2 * wg.nbytes))) - 1)]
         xg = torch.randn((512, 2048), device="cuda", dtype=torch.float32)
         yg = torch.empty((512, 8192), device="cuda", dtype=torch.float32)
         torch.cuda.synchronize()
         for i in range(args.steps):
             qmatmul(kt_lib, xg, 512, cg[i % len(cg)], yg, stream)
         torch.cuda.synchronize()
-        print(json.dumps({"only": "gemm", "kernel": "gemm_kernel int8 g32 M=512 2048x8192",
+        kernel = "gemm_kernel" if args.plain else "gemm_packed_kernel"
+        print(json.dumps({"only": "gemm", "kernel": f"{kernel} int8 g32 M=512 2048x8192",
                           "flops": 2 * 512 * 2048 * 8192, "launches": args.steps}), flush=True)
         return 0
     k, n, bits, g = HEADLINE
@@ -529,17 +544,21 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         extra["c5_m1_g32"] = {f"int{bb}_{kk}x{nn}": gemv_row(torch, kt_lib, stream_obj, kk, nn, bb, 32, 17)
                               for bb in (4, 8) for kk, nn in [(4096, 14336), (4096, 128256)]}
         # INT8 prefill GEMM at M = 512, group 32, on the four projection shapes of a
-        # 2048-wide layer; "layer" is their flops over their summed time (one of each).
+        # 2048-wide layer, weights with their column-run copy (the column-run GEMM);
+        # "layer" is their flops over their summed time (one of each). The same weights
+        # without the copy (the reference-layout GEMM) are timed beside them.
         tot_flops = tot_ms = 0.0
         for (k, n) in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
-            wg = Weight(torch, kt_lib, k, n, 8, 32, seed=9, stream=stream)
-            ng = max(2, -(-2 * MALL_BYTES // wg.nbytes))
+            wg = Weight(torch, kt_lib, k, n, 8, 32, seed=9, stream=stream).pack(torch, kt_lib, stream)
+            ng = max(2, -(-2 * MALL_BYTES // (2 * wg.nbytes)))
             cg = [wg] + [wg.clone(kt_lib) for _ in range(ng - 1)]
             xg = torch.randn((512, k), generator=gen, device="cuda", dtype=torch.float32)
             yg = torch.empty((512, n), device="cuda", dtype=torch.float32)
             for w in cg:
                 qmatmul(kt_lib, xg, 512, w, yg, stream)
             ag = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 32)
+            plain = [w.without_copy(kt_lib) for w in cg]
+            ap = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), plain, 32)
             flops = 2.0 * 512 * k * n
             tflops = flops / (ag * 1e-3) / 1e12
             tot_flops += flops
@@ -555,21 +574,25 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             torch.cuda.synchronize()
             ab = time_graph_launches(torch, stream_obj, lambda w: torch.matmul(xb, w, out=yb), wb, 32)
             tb = flops / (ab * 1e-3) / 1e12
+            tpl = flops / (ap * 1e-3) / 1e12
             extra[f"int8_g32_gemm_m512_{k}x{n}"] = {
                 "TFLOP/s": round(tflops, 1), "frac_mfma": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                "avg_us": round(ag * 1e3, 3), "copies": ng,
+                "avg_us": round(ag * 1e3, 3), "copies": ng, "kernel": "column-run GEMM (packed copy)",
+                "reference_layout_gemm": {"TFLOP/s": round(tpl, 1), "frac_mfma": round(tpl / MFMA_PEAK_TFLOPS, 4),
+                                          "avg_us": round(ap * 1e3, 3)},
                 "hipblaslt_bf16_same_shape": {"TFLOP/s": round(tb, 1), "frac_mfma": round(tb / MFMA_PEAK_TFLOPS, 4),
                                               "avg_us": round(ab * 1e3, 3)}}
-            del cg, wg, wb
+            del cg, wg, wb, plain
         layer = tot_flops / (tot_ms * 1e-3) / 1e12
         progress("C3 M=512 GEMM rows")
         extra["int8_g32_gemm_m512_layer"] = {"TFLOP/s": round(layer, 1), "frac_mfma": round(layer / MFMA_PEAK_TFLOPS, 4),
                                              "avg_us": round(tot_ms * 1e3, 3)}
 
         # the M sweep of the INT8 g32 2048 -> 8192 product (M = 1, 16: the decode kernels;
-        # 128 and up: the GEMM): time per launch, TFLOP/s and GB/s of algorithmic bytes
-        wm = Weight(torch, kt_lib, 2048, 8192, 8, 32, seed=11, stream=stream)
-        nm = max(2, -(-2 * MALL_BYTES // wm.nbytes))
+        # 128 and up: the GEMM), weights with their column-run copy: time per launch,
+        # TFLOP/s and GB/s of algorithmic bytes
+        wm = Weight(torch, kt_lib, 2048, 8192, 8, 32, seed=11, stream=stream).pack(torch, kt_lib, stream)
+        nm = max(2, -(-2 * MALL_BYTES // (2 * wm.nbytes)))
         cm = [wm] + [wm.clone(kt_lib) for _ in range(nm - 1)]
         sweep = {}
         for mm in (1, 16, 128, 512, 2048):
