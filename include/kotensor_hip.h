@@ -294,6 +294,18 @@ int32_t kt_silu_mul(float* gate, const float* up, int64_t n, void* stream);
 int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
                                  const kt_qweight* weights, int32_t count, float* const* outputs,
                                  const float* const* biases, int32_t accumulate, float alpha, void* stream);
+/* SwiGLU's gate and up projections and its gate in one call (K/SwiGLU.kt:19-25; with
+ * RMSNorm.forward of x first when norm_weight is not NULL, as the decoder block's norm2,
+ * K/RMSNorm.kt): up = RMSNorm(x) . deq(w_up) (+ bias_up) and
+ * gate = silu(RMSNorm(x) . deq(w_gate) (+ bias_gate)) * up, silu(g) = g / (1 + exp(-g))
+ * exactly as kt_silu_mul computes it; gate and up are [m x N]. For one row on weights with
+ * column-run copies one launch: each workgroup multiplies the same columns of both weights
+ * and computes the gate in its epilogue (normed is not written); otherwise
+ * kt_rmsnorm_qmatmul_group (or kt_qmatmul_group) then kt_silu_mul. The down projection is
+ * then a plain product of gate. Saves a decode step's separate gate work. */
+int32_t kt_rmsnorm_swiglu_gate(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
+                               const kt_qweight* w_gate, const kt_qweight* w_up, const float* bias_gate,
+                               const float* bias_up, float* gate, float* up, void* stream);
 /* SwiGLU.forwardInto's gate followed by the down projection (K/SwiGLU.kt:19-25 then
  * QuantizedLinear.forwardInto, K/QuantizedLinear.kt:16-25):
  * c = (accumulate ? c : 0) + alpha * (silu(gate) * up) . deq(W) (+ bias), gate and up

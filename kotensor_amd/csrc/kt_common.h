@@ -147,9 +147,12 @@ bool gemv_strip_preferred(const WeightView* ws, int32_t count);
 int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits);
 int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st);
 bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+// glu: ws[0], ws[1] are SwiGLU's gate and up weights; cs[0] receives silu(gate) * up and
+// cs[1] up (no accumulate); needs gemv_packed_pair_supported.
 int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
                            int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr,
-                           const float* norm_weight = nullptr, float eps = 0.0f);
+                           const float* norm_weight = nullptr, float eps = 0.0f, bool glu = false);
+bool gemv_packed_pair_supported(const float* a, const WeightView* ws, float* const* cs);
 void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);

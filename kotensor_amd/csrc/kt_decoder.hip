@@ -973,6 +973,33 @@ int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float
     return kt_qmatmul_group(normed, m, weights, count, outputs, biases, accumulate, alpha, stream);
 }
 
+int32_t kt_rmsnorm_swiglu_gate(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
+                               const kt_qweight* w_gate, const kt_qweight* w_up, const float* bias_gate,
+                               const float* bias_up, float* gate, float* up, void* stream) {
+    if (!x || !w_gate || !w_up || !gate || !up) return fail(KT_ERR_ARGUMENT, "x, a weight, gate or up is NULL");
+    if (norm_weight && !normed) return fail(KT_ERR_ARGUMENT, "normed is NULL");
+    if (m < 0) return fail(KT_ERR_ARGUMENT, "Negative row count %d", m);
+    WeightView views[2];
+    int32_t status = view_weight(w_gate, &views[0]);
+    if (status) return status;
+    if ((status = view_weight(w_up, &views[1]))) return status;
+    if (views[0].K != views[1].K || views[0].N != views[1].N)
+        return fail(KT_ERR_SHAPE, "gate and up weights must have the same shape");
+    if (m == 0) return KT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    float* outs[2] = {gate, up};
+    const float* biases[2] = {bias_gate, bias_up};
+    // one row on column-run copies: one launch, the gate computed in the product's epilogue
+    if (m == 1 && (gemv_kind() == 0 || gemv_kind() == 5) && (!norm_weight || aligned(norm_weight, 16)) &&
+        (!norm_weight || views[0].K <= NORM_F4 * 4 * NORM_THREADS) && gemv_packed_pair_supported(x, views, outs))
+        return launch_gemv_packed(x, views, outs, biases, 2, 0, 1.0f, st, nullptr, norm_weight, eps, true);
+    kt_qweight ws[2] = {*w_gate, *w_up};
+    status = norm_weight ? kt_rmsnorm_qmatmul_group(x, norm_weight, eps, normed, m, ws, 2, outs, biases, 0, 1.0f, stream)
+                         : kt_qmatmul_group(x, m, ws, 2, outs, biases, 0, 1.0f, stream);
+    if (status) return status;
+    return kt_silu_mul(gate, up, static_cast<int64_t>(m) * views[0].N, stream);
+}
+
 int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
                           float alpha, const float* bias, void* stream) {
     if (!gate || !up || !c) return fail(KT_ERR_ARGUMENT, "gate, up or the output is NULL");

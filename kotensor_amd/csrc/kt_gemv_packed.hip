@@ -174,25 +174,30 @@ __host__ __device__ constexpr int32_t lds_rec_offset(int32_t chunks) { return 4 
 __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return lds_rec_offset(chunks) + chunks * (CHUNK / RUN) * 8; }
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
 
+// glu: jobs 0 and 1 are SwiGLU's gate and up weights (same N); a workgroup's column sets
+// are pairs (gate set s, up set s), and the gate wave's epilogue writes
+// silu(gate) * up to job 0's output (silu_mul_kernel's expression) and up to job 1's.
 template <int BITS, int R, bool ZP, int XMODE>
 __global__ void __launch_bounds__(64 * W)
     gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
-                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate) {
+                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate, int32_t glu) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // Everything below is shifts and masks of the arguments (K-parts and group sizes are
     // powers of two), so the first loads go out one argument fetch after the start.
-    const PJob jb = jobs.job[blockIdx.y];
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t cslog = 3 - kslog;  // column sets per workgroup: 1 << cslog
-    const int32_t set0 = blockIdx.x << cslog;
-    if (set0 >= jb.sets) return;
     const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
-    const bool set_live = set0 + my_cs < jb.sets;
-    const int32_t set = set_live ? set0 + my_cs : jb.sets - 1;  // a dead wave computes a copy, never writes
+    // glu: set slot my_cs holds weight my_cs % 2, column set my_cs / 2 of the pair range
+    const PJob jb = jobs.job[glu ? (my_cs & 1) : blockIdx.y];
+    const int32_t set0 = glu ? blockIdx.x << (cslog - 1) : blockIdx.x << cslog;
+    if (set0 >= jb.sets) return;
+    const int32_t my_set = set0 + (glu ? my_cs >> 1 : my_cs);
+    const bool set_live = my_set < jb.sets;
+    const int32_t set = set_live ? my_set : jb.sets - 1;  // a dead wave computes a copy, never writes
     const int32_t chunks = (K + CHUNK - 1) >> 7;
     const int32_t G = (K + (RUN << gshift) - 1) >> (gshift + 5);  // quantization groups
     const int32_t c_begin = (kp * chunks) >> kslog;
@@ -372,6 +377,20 @@ __global__ void __launch_bounds__(64 * W)
         for (int32_t w = 1; w < W; ++w) sq += red[W * SET + w];
         al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
     }
+    if (glu) {
+        // the gate wave of the pair: its partner (slot my_cs + 1) holds up's sums
+        if (my_cs & 1) return;
+        float usum = red[(my_cs + 1) * SET + ln];
+        for (int32_t p = 1; p < ks; ++p) usum += red[(p * cs + my_cs + 1) * SET + ln];
+        float g = fmaf(al, sum, 0.0f);
+        if (jb.bias) g += jb.bias[col];
+        const PJob& ju = jobs.job[1];
+        float u = fmaf(al, usum, 0.0f);
+        if (ju.bias) u += ju.bias[col];
+        ju.out[col] = u;
+        jb.out[col] = g / (1.0f + static_cast<float>(exp(-static_cast<double>(g)))) * u;
+        return;
+    }
     float* dst = jb.out + col;
     float o = accumulate ? *dst : 0.0f;
     o = fmaf(al, sum, o);
@@ -387,30 +406,31 @@ Forced g_forced;
 
 template <int BITS, bool ZP, int XMODE>
 void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
-              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax,
+              int32_t glu) {
     // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
     constexpr int RS = BITS == 4 ? 4 : 2;
     if (g_forced.ring == 2)
         gemv_packed_kernel<BITS, 2 * RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
     else if (g_forced.ring == 1 || nmax > RS / 2)
         gemv_packed_kernel<BITS, RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
     else
         gemv_packed_kernel<BITS, RS / 2, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
 }
 
 template <int BITS, bool ZP>
 void launch_mode(int mode, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
                  int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate,
-                 int32_t nmax) {
+                 int32_t nmax, int32_t glu) {
     if (mode == X_SWIGLU)
-        launch_r<BITS, ZP, X_SWIGLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_SWIGLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
     else if (mode == X_NORM)
-        launch_r<BITS, ZP, X_NORM>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_NORM>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
     else
-        launch_r<BITS, ZP, X_PLAIN>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
+        launch_r<BITS, ZP, X_PLAIN>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
 }
 
 int32_t log2_exact(int32_t v) {
@@ -504,9 +524,18 @@ bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const
     return plan_packed(w.K, w.g, w.N / SET).ks != 0;
 }
 
+bool gemv_packed_pair_supported(const float* a, const WeightView* ws, float* const* cs) {
+    if (!gemv_packed_supported(a, 1, ws[0], cs[0]) || !gemv_packed_supported(a, 1, ws[1], cs[1])) return false;
+    if (ws[0].N != ws[1].N || ws[0].K != ws[1].K || ws[0].bits != ws[1].bits || ws[0].g != ws[1].g ||
+        (ws[0].z != nullptr) != (ws[1].z != nullptr))
+        return false;
+    const PackedPlan plan = plan_packed(ws[0].K, ws[0].g, 2 * (ws[0].N / SET));
+    return plan.ks != 0 && plan.ks <= W / 2;  // two column sets per workgroup at least
+}
+
 int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
                            int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up,
-                           const float* norm_weight, float eps) {
+                           const float* norm_weight, float eps, bool glu) {
     const WeightView& w0 = ws[0];
     bool zp = false;
     for (int32_t i = 0; i < count; ++i) zp = zp || ws[i].z != nullptr;
@@ -524,6 +553,8 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
     }
     const PackedPlan plan = plan_packed(w0.K, w0.g, sets_total);
     if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed gemv: no work split fits K = %d, g = %d", w0.K, w0.g);
+    if (glu && (count != 2 || ws[0].N != ws[1].N || plan.ks > W / 2 || accumulate || up))
+        return fail(KT_ERR_ARGUMENT, "packed gemv: the paired gate/up form needs two weights of one shape");
     const int32_t kslog = log2_exact(plan.ks);
     PJobs jobs{};
     jobs.count = count;
@@ -537,19 +568,20 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
         jb.N = ws[i].N;
         jb.sets = ws[i].N / SET;
     }
-    const int32_t per_wg = W / plan.ks;  // column sets per workgroup
-    const dim3 grid(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)), static_cast<uint32_t>(count));
+    const int32_t per_wg = glu ? W / plan.ks / 2 : W / plan.ks;  // column sets (of each weight, glu) per workgroup
+    const dim3 grid(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)),
+                    static_cast<uint32_t>(glu ? 1 : count));
     const int32_t gshift = log2_exact(w0.g / RUN);
     const float* aux = up ? up : norm_weight;
     if (w0.bits == 4)
         launch_mode<4, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                             plan.nmax);
+                             plan.nmax, glu ? 1 : 0);
     else if (zp)
         launch_mode<8, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                             plan.nmax);
+                             plan.nmax, glu ? 1 : 0);
     else
         launch_mode<8, false>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                              plan.nmax);
+                              plan.nmax, glu ? 1 : 0);
     KT_LAUNCHED("qmatmul: packed gemv kernel");
     return KT_OK;
 }

@@ -430,19 +430,6 @@ class Transformer:
                       rows.attention_out.ptr, st)
             _lib.call("kt_add_inplace", rows.x.ptr, rows.attention_out.ptr, ctypes.c_int64(count * self.dimension), st)
 
-    def _swiglu_down(self, name: str, rows: _Rows, count: int, st) -> None:
-        """x += (silu(gate) * up) · deq(W) + bias: SwiGLU.forwardInto's gate and down
-        projection in one call (one launch for a decode row; the gate is computed in
-        place first for more rows), the residual as in _residual_projection."""
-        w = self.weights[name]
-        if self._zero_bias.get(name, True):
-            _lib.call("kt_swiglu_qmatmul", rows.gate.ptr, rows.up.ptr, count, ctypes.byref(w.qweight), rows.x.ptr, 1,
-                      ctypes.c_float(1.0), None, st)
-        else:
-            _lib.call("kt_swiglu_qmatmul", rows.gate.ptr, rows.up.ptr, count, ctypes.byref(w.qweight),
-                      rows.attention_out.ptr, 0, ctypes.c_float(1.0), self.parameters[name + ".bias"].ptr, st)
-            _lib.call("kt_add_inplace", rows.x.ptr, rows.attention_out.ptr, ctypes.c_int64(count * self.dimension), st)
-
     def _bias(self, name: str):
         return None if self._zero_bias.get(name, True) else self.parameters[name + ".bias"].ptr
 
@@ -458,12 +445,13 @@ class Transformer:
                       cache.position.ptr, key_bound, cache.keys.ptr, cache.values.ptr, l, cache.max_sequence_length,
                       self.num_heads, self.num_key_value_heads, self.head_dim, rows.context.ptr, st)
             self._residual_projection(p + "attention.wOut", rows.context, rows, count, st)
-            names = [p + "ffn.wGate", p + "ffn.wUp"]
-            n, ws, os_, bs = _group([self.weights[x] for x in names], [rows.gate.ptr, rows.up.ptr],
-                                    [self._bias(x) for x in names])
-            _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm2.weight"].ptr,
-                      ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
-            self._swiglu_down(p + "ffn.wDown", rows, count, st)
+            # norm2, gate and up, and the gate silu(gate) * up in one call; then the down
+            # projection of the gate row with the residual
+            _lib.call("kt_rmsnorm_swiglu_gate", rows.x.ptr, self.parameters[p + "norm2.weight"].ptr,
+                      ctypes.c_float(self.norm_eps), rows.normed.ptr, count,
+                      ctypes.byref(self.weights[p + "ffn.wGate"].qweight), ctypes.byref(self.weights[p + "ffn.wUp"].qweight),
+                      self._bias(p + "ffn.wGate"), self._bias(p + "ffn.wUp"), rows.gate.ptr, rows.up.ptr, st)
+            self._residual_projection(p + "ffn.wDown", rows.gate, rows, count, st)
 
     def _head(self, x_row_ptr: int, buffers: InferenceBuffers, st) -> None:
         """finalNorm and lmHead of one row into buffers.logits."""

@@ -199,3 +199,71 @@ def test_packed_fused_decoder_steps(kt, oracle_lib):
         assert same_bits(dg.download(np.float32).reshape(1, -1), gate)  # the gate row is left as it was
         want = oracle_lib.multiply_quantized(oracle_lib.silu_mul(gate, up), down, 1)
         assert normwise_rel(out.download(np.float32).reshape(1, -1), want) <= TOL
+
+
+def test_packed_swiglu_gate_pairs(kt, oracle_lib):
+    """kt_rmsnorm_swiglu_gate: one launch for a row on column-run copies (each workgroup
+    multiplies the same columns of gate and up and computes silu(gate) * up in its
+    epilogue). Against the unfused calls (kt_rmsnorm_qmatmul_group, then kt_silu_mul): the
+    same bits, since the column sums split K the same way and the gate is the same
+    expression; against the oracle (RMSNorm, products, silu_mul) to the one-row bound.
+    With and without RMSNorm and biases; three rows and weights without the copy take the
+    unfused sequence."""
+    from kotensor_amd import _lib
+    rng = np.random.default_rng(40)
+    for k, n, bits, g in [(2048, 8192, 4, 64), (896, 4864, 4, 64), (2048, 8192, 8, 32), (4096, 14336, 4, 64)]:
+        qg, qu = _weights(oracle_lib, k, n, bits, g, 41), _weights(oracle_lib, k, n, bits, g, 42)
+        tg, tu = _packed(kt, qg), _packed(kt, qu)
+        nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        bg, bu = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+        dnw, dbg, dbu = (kt.DeviceBuffer.from_numpy(v) for v in (nw, bg, bu))
+        for m in (1, 3):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            dx = kt.DeviceBuffer.from_numpy(x)
+            normed = kt.DeviceBuffer(m * k * 4)
+            for use_norm, use_bias in ((True, False), (True, True), (False, False)):
+                banner("swiglu-gate", k, n, bits, g, m, use_norm, use_bias)
+                gate, up = kt.DeviceBuffer(m * n * 4), kt.DeviceBuffer(m * n * 4)
+                _lib.call("kt_rmsnorm_swiglu_gate", dx.ptr, dnw.ptr if use_norm else None, ctypes.c_float(1e-5),
+                          normed.ptr, m, ctypes.byref(tg.qweight), ctypes.byref(tu.qweight),
+                          dbg.ptr if use_bias else None, dbu.ptr if use_bias else None, gate.ptr, up.ptr, None)
+                # the unfused calls
+                g2, u2 = kt.DeviceBuffer(m * n * 4), kt.DeviceBuffer(m * n * 4)
+                ws = (_lib.QWeight * 2)(tg.qweight, tu.qweight)
+                os_ = (ctypes.c_void_p * 2)(g2.ptr, u2.ptr)
+                bs = (ctypes.c_void_p * 2)(dbg.ptr, dbu.ptr) if use_bias else None
+                if use_norm:
+                    _lib.call("kt_rmsnorm_qmatmul_group", dx.ptr, dnw.ptr, ctypes.c_float(1e-5), normed.ptr, m, ws, 2, os_,
+                              bs, 0, ctypes.c_float(1.0), None)
+                else:
+                    _lib.call("kt_qmatmul_group", dx.ptr, m, ws, 2, os_, bs, 0, ctypes.c_float(1.0), None)
+                _lib.call("kt_silu_mul", g2.ptr, u2.ptr, ctypes.c_int64(m * n), None)
+                kt.synchronize()
+                got_g, got_u = gate.download(np.float32).reshape(m, n), up.download(np.float32).reshape(m, n)
+                assert same_bits(got_u, u2.download(np.float32).reshape(m, n))
+                assert same_bits(got_g, g2.download(np.float32).reshape(m, n))
+                xn = oracle_lib.rmsnorm(x, nw, 1e-5) if use_norm else x
+                want_u = oracle_lib.multiply_quantized(xn, qu, m) + (bu if use_bias else 0)
+                want_g = oracle_lib.multiply_quantized(xn, qg, m) + (bg if use_bias else 0)
+                assert normwise_rel(got_u, want_u) <= TOL
+                assert normwise_rel(got_g, oracle_lib.silu_mul(want_g.astype(np.float32), want_u.astype(np.float32))) <= 1e-4
+    # a weight without the copy: the unfused sequence, same results
+    k, n = 896, 4864
+    qg, qu = _weights(oracle_lib, k, n, 4, 64, 43), _weights(oracle_lib, k, n, 4, 64, 44)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    dx = kt.DeviceBuffer.from_numpy(x)
+    outs = []
+    for pack in (True, False):
+        tg = _packed(kt, qg) if pack else upload_quantized(kt, qg)
+        tu = _packed(kt, qu)
+        gate, up = kt.DeviceBuffer(n * 4), kt.DeviceBuffer(n * 4)
+        _lib.call("kt_rmsnorm_swiglu_gate", dx.ptr, None, ctypes.c_float(1e-5), None, 1, ctypes.byref(tg.qweight),
+                  ctypes.byref(tu.qweight), None, None, gate.ptr, up.ptr, None)
+        kt.synchronize()
+        outs.append(gate.download(np.float32))
+    assert normwise_rel(outs[0], outs[1]) <= 1e-5
+    with pytest.raises(kt.IllegalArgumentException):
+        small = _packed(kt, _weights(oracle_lib, k, 128, 4, 64, 45))
+        _lib.call("kt_rmsnorm_swiglu_gate", dx.ptr, None, ctypes.c_float(1e-5), None, 1, ctypes.byref(small.qweight),
+                  ctypes.byref(_packed(kt, qu).qweight), None, None, kt.DeviceBuffer(n * 4).ptr,
+                  kt.DeviceBuffer(n * 4).ptr, None)
