@@ -198,28 +198,29 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     float* kn_s = st + 3 * G;          // [HD] the new key after RoPE (the workgroup holding it), then one word
     const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    const int32_t pos = *a.position + t;
     const int32_t k_begin = s * a.span;
-    const int32_t k_end = min(min(k_begin + a.span, pos + 1), a.max_seq);  // never read outside the cache
     const size_t base = (static_cast<size_t>(a.layer) * a.num_kv_heads + g) * a.max_seq;  // row of key 0
+    // q of the G heads (G * HD <= 1024 floats: at most one float4 per thread)
+    const int32_t q4 = G * HD / 4;
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < q4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(t) * dim + g * G * HD)[tid];
+    // The first tile's keys and values go out with q and the position, before anything
+    // waits: a whole tile from k_begin (rows of the cache, k_begin < max_seq), so the
+    // addresses do not wait for the position; rows past the key range are never used.
+    constexpr bool TOGETHER = TF4 <= 8;
+    f4 kr[TF4], vr[TOGETHER ? TF4 : 1];
+    {
+        const int32_t n4 = min(KT, a.max_seq - k_begin) * HD / 4;
+        load_tile<TF4>(kr, a.ck + (base + k_begin) * HD, n4);
+        if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k_begin) * HD, n4);
+    }
+    const int32_t pos = *a.position + t;
+    const int32_t k_end = min(min(k_begin + a.span, pos + 1), a.max_seq);  // never read outside the cache
     // With RoPE inside, the workgroup whose key range holds the new position appends the
     // rotated key and the value to the cache for later steps and uses them from LDS in
     // its own tile (its tile load may see the row before or after the append; the LDS copy
     // replaces it), so no fence or second read of the row is needed.
     const bool holder = a.rope && pos >= k_begin && pos < k_end;
-
-    // q of the G heads (G * HD <= 1024 floats: at most one float4 per thread)
-    const int32_t q4 = G * HD / 4;
-    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < q4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(t) * dim + g * G * HD)[tid];
-    // the first tile's keys and values go out with q, before the RoPE work
-    constexpr bool TOGETHER = TF4 <= 8;
-    f4 kr[TF4], vr[TOGETHER ? TF4 : 1];
-    if (k_begin < k_end) {
-        const int32_t n4 = min(KT, k_end - k_begin) * HD / 4;
-        load_tile<TF4>(kr, a.ck + (base + k_begin) * HD, n4);
-        if constexpr (TOGETHER) load_tile<TF4>(vr, a.cv + (base + k_begin) * HD, n4);
-    }
     if (tid < G) {
         st[3 * tid] = -INFINITY;
         st[3 * tid + 1] = 0.0f;
@@ -358,6 +359,9 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         __syncthreads();
     }
 
+    // A workgroup whose key range is empty (a split past this token's keys) ran no tile,
+    // whose barriers order the running max and sum set above before the reads below.
+    if (k_begin >= k_end) __syncthreads();
     if (a.splits == 1) {
 #pragma unroll
         for (int r = 0; r < MAX_NACC; ++r) {
