@@ -174,28 +174,31 @@ __host__ __device__ constexpr int32_t lds_rec_offset(int32_t chunks) { return 4 
 __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return lds_rec_offset(chunks) + chunks * (CHUNK / RUN) * 8; }
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
 
-// glu: jobs 0 and 1 are SwiGLU's gate and up weights (same N); a workgroup's column sets
+// GLU: jobs 0 and 1 are SwiGLU's gate and up weights (same N); a workgroup's column sets
 // are pairs (gate set s, up set s), and the gate wave's epilogue writes
 // silu(gate) * up to job 0's output (silu_mul_kernel's expression) and up to job 1's.
-template <int BITS, int R, bool ZP, int XMODE>
+template <int BITS, int R, bool ZP, int XMODE, bool GLU>
 __global__ void __launch_bounds__(64 * W)
     gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
-                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate, int32_t glu) {
+                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // Everything below is shifts and masks of the arguments (K-parts and group sizes are
     // powers of two), so the first loads go out one argument fetch after the start.
+    // GLU: set slot my_cs holds weight my_cs % 2, column set my_cs / 2 of the pair range.
+    // The job's fields are the first loads (first in the source: otherwise they wait for
+    // kslog and the start costs a second scalar round trip).
+    const PJob jb = jobs.job[GLU ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & ((1 << (3 - kslog)) - 1) & 1)
+                                 : blockIdx.y];
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t cslog = 3 - kslog;  // column sets per workgroup: 1 << cslog
-    const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
-    // glu: set slot my_cs holds weight my_cs % 2, column set my_cs / 2 of the pair range
-    const PJob jb = jobs.job[glu ? (my_cs & 1) : blockIdx.y];
-    const int32_t set0 = glu ? blockIdx.x << (cslog - 1) : blockIdx.x << cslog;
+    const int32_t set0 = GLU ? blockIdx.x << (cslog - 1) : blockIdx.x << cslog;
     if (set0 >= jb.sets) return;
-    const int32_t my_set = set0 + (glu ? my_cs >> 1 : my_cs);
+    const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
+    const int32_t my_set = set0 + (GLU ? my_cs >> 1 : my_cs);
     const bool set_live = my_set < jb.sets;
     const int32_t set = set_live ? my_set : jb.sets - 1;  // a dead wave computes a copy, never writes
     const int32_t chunks = (K + CHUNK - 1) >> 7;
@@ -377,7 +380,7 @@ __global__ void __launch_bounds__(64 * W)
         for (int32_t w = 1; w < W; ++w) sq += red[W * SET + w];
         al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
     }
-    if (glu) {
+    if constexpr (GLU) {
         // the gate wave of the pair: its partner (slot my_cs + 1) holds up's sums
         if (my_cs & 1) return;
         float usum = red[(my_cs + 1) * SET + ln];
@@ -404,21 +407,33 @@ struct Forced {
 };
 Forced g_forced;
 
+template <int BITS, bool ZP, int XMODE, bool GLU>
+void launch_g(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+    // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
+    constexpr int RS = BITS == 4 ? 4 : 2;
+    if (g_forced.ring == 2)
+        gemv_packed_kernel<BITS, 2 * RS, ZP, XMODE, GLU>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+    else if (g_forced.ring == 1 || nmax > RS / 2)
+        gemv_packed_kernel<BITS, RS, ZP, XMODE, GLU>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+    else
+        gemv_packed_kernel<BITS, RS / 2, ZP, XMODE, GLU>
+            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+}
+
+// The paired gate/up form exists for the plain and RMSNorm inputs only.
 template <int BITS, bool ZP, int XMODE>
 void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
               int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax,
               int32_t glu) {
-    // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
-    constexpr int RS = BITS == 4 ? 4 : 2;
-    if (g_forced.ring == 2)
-        gemv_packed_kernel<BITS, 2 * RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
-    else if (g_forced.ring == 1 || nmax > RS / 2)
-        gemv_packed_kernel<BITS, RS, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
-    else
-        gemv_packed_kernel<BITS, RS / 2, ZP, XMODE>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate, glu);
+    if constexpr (XMODE != X_SWIGLU)
+        if (glu) {
+            launch_g<BITS, ZP, XMODE, true>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
+            return;
+        }
+    launch_g<BITS, ZP, XMODE, false>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
 }
 
 template <int BITS, bool ZP>
