@@ -145,3 +145,26 @@ def test_packed_and_plain_gemm_agree(kt, oracle_lib):
         plain = gpu_matmul(kt, x, upload_quantized(kt, q), m)
         packed = gpu_matmul(kt, x, upload_quantized(kt, q).pack(), m)
         assert normwise_rel(packed, plain) <= 1e-5
+
+
+def test_int8_with_zero_points(kt, oracle_lib):
+    """INT8 weights carrying zero points (the quantizer writes none for INT8, but a
+    QuantizedTensor may hold them: value = (q - zero) * scale with q and zero signed):
+    gemm_packed_kernel<8, true> and the reference-layout GEMM against the oracle, and the
+    one-row kernel on the copy, at g32 and g64 with ragged N."""
+    from oracle import Quantized
+    rng = np.random.default_rng(27)
+    for m, k, n, g in [(512, 2048, 1024, 32), (130, 1000, 584, 64), (1, 2048, 2048, 64)]:
+        groups = -(-k // g)
+        qdata = rng.integers(-128, 128, size=k * n, dtype=np.int64).astype(np.int8)
+        scales = (rng.random(groups * n, dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+        zeros = rng.integers(-20, 21, size=groups * n, dtype=np.int64).astype(np.int8)
+        q = Quantized(qdata, scales, zeros, k, n, 8, g)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+        banner("int8-zp", m, k, n, g)
+        plain = gpu_matmul(kt, x, upload_quantized(kt, q), m)
+        packed = gpu_matmul(kt, x, upload_quantized(kt, q).pack(), m)
+        tol = 1e-5 if m == 1 else TOL  # the one-row kernel sums exactly; the GEMMs round to fp16
+        assert normwise_rel(packed, want) <= tol, normwise_rel(packed, want)
+        assert normwise_rel(plain, want) <= tol, normwise_rel(plain, want)
