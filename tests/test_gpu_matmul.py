@@ -211,6 +211,12 @@ def test_llama8b_lm_head(kt, oracle_lib, bits):
         err = normwise_rel(got[rows], want)
         print(f"  normwise={err:.3e}", flush=True)
         assert err <= (1e-5 if m <= 2 else TOL)
+        if m >= 64:  # the column-run GEMM on the same rows (1002 column tiles)
+            packed = gpu_matmul(kt, x, qt.pack(), m)
+            qt.unpack()
+            err = normwise_rel(packed[rows], want)
+            print(f"  packed normwise={err:.3e}", flush=True)
+            assert err <= TOL
 
 
 @pytest.mark.parametrize("k,n", LLAMA8B)
