@@ -1072,10 +1072,14 @@ static void fill_jobs(GemmJobs& jobs, const WeightView* ws, float* const* cs, co
 }
 
 // The column-run kernel: every weight of the group has its copy, g % 32 == 0, and INT4
-// weights have zero points (as every INT4 quantization does).
+// weights have zero points (as every INT4 quantization does); the copy and the scales are
+// addressed with 32-bit buffer offsets, so each stays below 4 GiB.
 static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
-    for (int32_t i = 0; i < count; ++i)
+    for (int32_t i = 0; i < count; ++i) {
         if (!ws[i].p || ws[i].g % 32 != 0 || (ws[i].bits == 4 && !ws[i].z)) return false;
+        if (packed_bytes(ws[i].K, ws[i].N, ws[i].bits) > 0xFFFFFFFFll) return false;
+        if (static_cast<int64_t>(ws[i].G) * ws[i].N * 4 > 0xFFFFFFFFll) return false;
+    }
     return true;
 }
 
