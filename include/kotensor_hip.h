@@ -317,6 +317,13 @@ int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qwei
 /* Transformer.argmaxOfLastToken (K/Transformer.kt:253-266) of logits[0..n) into the
  * device int32 *index: the first index of the largest logit above -1e9, else 0. */
 int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream);
+/* One greedy decode step's bookkeeping in one launch: kt_argmax(logits, n, token), then
+ * *position += 1 (kt_position_add) and generated[*position] = *token when 0 <= *position <
+ * capacity (kt_record_token; generated may be NULL). The effect of those three calls in
+ * the order the reference's greedy loop makes them (K/Transformer.kt:224-231: take the
+ * argmax, advance the cache, hand the token out); the argmax does not read the position. */
+int32_t kt_argmax_advance(const float* logits, int32_t n, int32_t* token, int32_t* position,
+                          int32_t* generated, int32_t capacity, void* stream);
 /* KVCache.advance on the device copy of the length (K/KVCache.kt:29-35): *position += count. */
 int32_t kt_position_add(int32_t* position, int32_t count, void* stream);
 /* generated[*position] = *token when 0 <= *position < capacity: the device-side record of

@@ -124,6 +124,7 @@ SIGNATURES = {
     "kt_rmsnorm_qmatmul_group": [_P, _P, _F, _P, _I, ctypes.POINTER(_QWeight), _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _F, _P],
     "kt_rmsnorm_swiglu_gate": [_P, _P, _F, _P, _I, ctypes.POINTER(_QWeight), ctypes.POINTER(_QWeight), _P, _P, _P, _P, _P],
     "kt_argmax": [_P, _I, _P, _P],
+    "kt_argmax_advance": [_P, _I, _P, _P, _P, _I, _P],
     "kt_position_add": [_P, _I, _P],
     "kt_record_token": [_P, _P, _P, _I, _P],
     "kt_graph_begin": [_P],

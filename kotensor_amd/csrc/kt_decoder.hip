@@ -647,9 +647,13 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 
 // Each workgroup reduces a stride of the logits into partials[block]; the last one to
 // finish (counter) reduces the partials, writes the index and resets the counter.
+// advance > 0 (one greedy decode step's bookkeeping): the last workgroup also adds advance
+// to *position and records the token at the new position (position_add_kernel, then
+// record_token_kernel; the argmax does not read the position).
 __global__ void __launch_bounds__(THREADS) argmax_kernel(const float* __restrict__ logits, int32_t n,
                                                          int32_t* __restrict__ index, uint64_t* partials,
-                                                         uint32_t* counter) {
+                                                         uint32_t* counter, int32_t* position, int32_t advance,
+                                                         int32_t* generated, int32_t capacity) {
     __shared__ uint64_t part[THREADS / 64];
     __shared__ uint32_t last;
     uint64_t best = 0;
@@ -677,7 +681,13 @@ __global__ void __launch_bounds__(THREADS) argmax_kernel(const float* __restrict
     if (threadIdx.x == 0) {
         for (int i = 1; i < THREADS / 64; ++i) b = max_u64(b, part[i]);
         b = max_u64(b, part[0]);
-        *index = b == 0 ? 0 : static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(b));
+        const int32_t token = b == 0 ? 0 : static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(b));
+        *index = token;
+        if (advance) {
+            const int32_t p = *position + advance;
+            *position = p;
+            if (generated && p >= 0 && p < capacity) generated[p] = token;
+        }
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -1027,19 +1037,31 @@ int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qwei
     return qmatmul(gate, m, w, c, accumulate, alpha, bias, stream);
 }
 
-int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream) {
-    if (!logits || !index) return fail(KT_ERR_ARGUMENT, "logits or index is NULL");
-    if (n <= 0) return fail(KT_ERR_SHAPE, "argmax needs at least one logit");
-    hipStream_t st = static_cast<hipStream_t>(stream);
+static int32_t launch_argmax(const float* logits, int32_t n, int32_t* index, int32_t* position, int32_t advance,
+                             int32_t* generated, int32_t capacity, hipStream_t st) {
     int32_t blocks = ceil_div(n, 4 * THREADS);
     if (blocks > ARGMAX_BLOCKS) blocks = ARGMAX_BLOCKS;
     void* ws = nullptr;
     uint32_t* counters = nullptr;
     const int32_t status = workspace_counters(st, ARGMAX_BLOCKS * sizeof(uint64_t), 1, &ws, &counters);
     if (status) return status;
-    argmax_kernel<<<blocks, THREADS, 0, st>>>(logits, n, index, static_cast<uint64_t*>(ws), counters);
+    argmax_kernel<<<blocks, THREADS, 0, st>>>(logits, n, index, static_cast<uint64_t*>(ws), counters, position, advance,
+                                             generated, capacity);
     KT_LAUNCHED("argmax kernel");
     return KT_OK;
+}
+
+int32_t kt_argmax(const float* logits, int32_t n, int32_t* index, void* stream) {
+    if (!logits || !index) return fail(KT_ERR_ARGUMENT, "logits or index is NULL");
+    if (n <= 0) return fail(KT_ERR_SHAPE, "argmax needs at least one logit");
+    return launch_argmax(logits, n, index, nullptr, 0, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+int32_t kt_argmax_advance(const float* logits, int32_t n, int32_t* token, int32_t* position, int32_t* generated,
+                          int32_t capacity, void* stream) {
+    if (!logits || !token || !position) return fail(KT_ERR_ARGUMENT, "logits, token or position is NULL");
+    if (n <= 0) return fail(KT_ERR_SHAPE, "argmax needs at least one logit");
+    return launch_argmax(logits, n, token, position, 1, generated, capacity, static_cast<hipStream_t>(stream));
 }
 
 int32_t kt_add_inplace(float* x, const float* y, int64_t n, void* stream) {

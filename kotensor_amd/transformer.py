@@ -454,11 +454,11 @@ class Transformer:
             self._residual_projection(p + "ffn.wDown", rows.gate, rows, count, st)
 
     def _head(self, x_row_ptr: int, buffers: InferenceBuffers, st) -> None:
-        """finalNorm and lmHead of one row into buffers.logits."""
-        _lib.call("kt_rmsnorm", x_row_ptr, 1, self.dimension, self.parameters["finalNorm.weight"].ptr,
-                  ctypes.c_float(self.norm_eps), buffers.normed.ptr, st)
-        _lib.call("kt_qlinear_forward", buffers.normed.ptr, 1, ctypes.byref(self.weights["lmHead"].qweight),
-                  self._bias("lmHead"), buffers.logits.ptr, st)
+        """finalNorm and lmHead of one row into buffers.logits (one launch with the norm
+        inside the product where the one-row kernels take it)."""
+        n, ws, os_, bs = _group([self.weights["lmHead"]], [buffers.logits.ptr], [self._bias("lmHead")])
+        _lib.call("kt_rmsnorm_qmatmul_group", x_row_ptr, self.parameters["finalNorm.weight"].ptr,
+                  ctypes.c_float(self.norm_eps), buffers.normed.ptr, 1, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
 
     def _decode_step(self, cache: KVCache, buffers: InferenceBuffers, st, argmax: bool) -> None:
         """One token from buffers.tokens[0] at the device position; the host length is the
@@ -466,12 +466,15 @@ class Transformer:
         recorded in buffers.generated at its position."""
         self._embed(buffers, 1, st)
         self._layers(buffers, 1, cache, cache.max_sequence_length, st)
-        _lib.call("kt_position_add", cache.position.ptr, 1, st)
-        self._head(buffers.x.ptr, buffers, st)
         if argmax:
-            _lib.call("kt_argmax", buffers.logits.ptr, self.vocabulary_size, buffers.tokens.ptr, st)
-            _lib.call("kt_record_token", buffers.tokens.ptr, cache.position.ptr, buffers.generated.ptr,
-                      buffers.max_sequence_length, st)
+            # the head does not read the position: advance it, take the argmax and record
+            # the token in one launch after the head
+            self._head(buffers.x.ptr, buffers, st)
+            _lib.call("kt_argmax_advance", buffers.logits.ptr, self.vocabulary_size, buffers.tokens.ptr,
+                      cache.position.ptr, buffers.generated.ptr, buffers.max_sequence_length, st)
+        else:
+            _lib.call("kt_position_add", cache.position.ptr, 1, st)
+            self._head(buffers.x.ptr, buffers, st)
 
     # -- the reference's entry points ----------------------------------------------------
     def prefill(self, prompt, cache: KVCache, buffers: InferenceBuffers, stream: Stream | None = None,

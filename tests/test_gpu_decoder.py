@@ -303,6 +303,33 @@ def test_argmax(kt, oracle_lib):
             assert int(idx.download(np.int32)[0]) == oracle_lib.argmax(x), x[:4]
 
 
+def test_argmax_advance(kt, oracle_lib):
+    """kt_argmax_advance: the argmax, the position advanced by one and the token recorded
+    at the new position, as kt_argmax, kt_position_add and kt_record_token give; nothing
+    recorded past the capacity or without a record array; calls in a row each advance."""
+    from kotensor_amd import _lib
+    rng = np.random.default_rng(6)
+    capacity = 8
+    tok, pos = kt.DeviceBuffer(4), kt.DeviceBuffer(4)
+    gen = dev(kt, np.full(capacity, -7, np.int32))
+    xs = [rng.standard_normal(n).astype(np.float32) for n in (32000, 5, 151936, 1000)]
+    pos.upload(np.array([3], np.int32))
+    for i, x in enumerate(xs):
+        _lib.call("kt_argmax_advance", dev(kt, x).ptr, x.size, tok.ptr, pos.ptr, gen.ptr, capacity, None)
+        assert int(tok.download(np.int32)[0]) == oracle_lib.argmax(x)
+        assert int(pos.download(np.int32)[0]) == 4 + i
+    want = np.full(capacity, -7, np.int32)
+    want[4:8] = [oracle_lib.argmax(x) for x in xs]
+    assert np.array_equal(gen.download(np.int32), want)
+    x = xs[0]
+    _lib.call("kt_argmax_advance", dev(kt, x).ptr, x.size, tok.ptr, pos.ptr, gen.ptr, capacity, None)  # position 8
+    assert int(pos.download(np.int32)[0]) == 8 and np.array_equal(gen.download(np.int32), want)
+    _lib.call("kt_argmax_advance", dev(kt, x).ptr, x.size, tok.ptr, pos.ptr, None, 0, None)
+    assert int(pos.download(np.int32)[0]) == 9 and int(tok.download(np.int32)[0]) == oracle_lib.argmax(x)
+    with pytest.raises(kt.IllegalArgumentException):
+        _lib.call("kt_argmax_advance", dev(kt, x).ptr, x.size, tok.ptr, None, None, 0, None)
+
+
 def test_fill_normal(kt):
     from kotensor_amd import _lib
     n = 1 << 22
