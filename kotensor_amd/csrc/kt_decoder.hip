@@ -204,6 +204,20 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     const int32_t q4 = G * HD / 4;
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < q4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(t) * dim + g * G * HD)[tid];
+    // RoPE inputs (a decode token): this thread's frequency and, for the workgroup that
+    // turns out to hold the new position, its pair of the new key and value. Issued ahead
+    // of the tiles, so that the rotation below waits for them and not for the tiles.
+    const int32_t half = HD >> 1;
+    float ifr = 0.0f, kn1 = 0.0f, kn2 = 0.0f, vn1 = 0.0f, vn2 = 0.0f;
+    if (a.rope && tid < half) {
+        const float* kn = a.k_new + static_cast<size_t>(g) * HD;
+        const float* vn = a.v_new + static_cast<size_t>(g) * HD;
+        ifr = a.inv_freq[tid];
+        kn1 = kn[tid];
+        kn2 = kn[tid + half];
+        vn1 = vn[tid];
+        vn2 = vn[tid + half];
+    }
     // The first tile's keys and values go out with q and the position, before anything
     // waits: a whole tile from k_begin (rows of the cache, k_begin < max_seq), so the
     // addresses do not wait for the position; rows past the key range are never used.
@@ -235,30 +249,27 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         // one decode token: the G query heads are rotated in LDS; the holder rotates the
         // new key into LDS and appends it and the value to the cache
         if (tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
+        float* fs = vs;  // the frequencies, until the first tile lands in vs
+        if (tid < half) fs[tid] = ifr;
         __syncthreads();
-        const int32_t half = HD >> 1;
         for (int32_t e = tid; e < G * half; e += THREADS) {
             const int32_t i = e % half, hh = e / half;
             float y1, y2;
-            rope_rotate(qs[hh * HD + i], qs[hh * HD + i + half], pos, a.inv_freq[i], y1, y2);
+            rope_rotate(qs[hh * HD + i], qs[hh * HD + i + half], pos, fs[i], y1, y2);
             qs[hh * HD + i] = y1;
             qs[hh * HD + i + half] = y2;
         }
-        if (holder) {
+        if (holder && tid < half) {  // half <= THREADS: one pair per thread
             float* ckw = const_cast<float*>(a.ck) + (base + pos) * HD;
             float* cvw = const_cast<float*>(a.cv) + (base + pos) * HD;
-            const float* kn = a.k_new + static_cast<size_t>(g) * HD;
-            const float* vn = a.v_new + static_cast<size_t>(g) * HD;
-            for (int32_t i = tid; i < half; i += THREADS) {
-                float y1, y2;
-                rope_rotate(kn[i], kn[i + half], pos, a.inv_freq[i], y1, y2);
-                kn_s[i] = y1;
-                kn_s[i + half] = y2;
-                ckw[i] = y1;
-                ckw[i + half] = y2;
-                cvw[i] = vn[i];
-                cvw[i + half] = vn[i + half];
-            }
+            float y1, y2;
+            rope_rotate(kn1, kn2, pos, ifr, y1, y2);
+            kn_s[tid] = y1;
+            kn_s[tid + half] = y2;
+            ckw[tid] = y1;
+            ckw[tid + half] = y2;
+            cvw[tid] = vn1;
+            cvw[tid + half] = vn2;
         }
         __syncthreads();
     }
@@ -299,10 +310,11 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             // thread replaces elements it did not write, so the tile writes come first)
             __syncthreads();
             const int32_t j = pos - k0;
-            const float* vn = a.v_new + static_cast<size_t>(g) * HD;
-            for (int32_t d = tid; d < HD; d += THREADS) {
-                ks[j * KP + d] = kn_s[d];
-                vs[j * HD + d] = vn[d];
+            if (tid < half) {
+                ks[j * KP + tid] = kn_s[tid];
+                ks[j * KP + tid + half] = kn_s[tid + half];
+                vs[j * HD + tid] = vn1;
+                vs[j * HD + tid + half] = vn2;
             }
         }
         __syncthreads();
