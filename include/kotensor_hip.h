@@ -306,6 +306,35 @@ int32_t kt_rmsnorm_qmatmul_group(const float* x, const float* norm_weight, float
 int32_t kt_rmsnorm_swiglu_gate(const float* x, const float* norm_weight, float eps, float* normed, int32_t m,
                                const kt_qweight* w_gate, const kt_qweight* w_up, const float* bias_gate,
                                const float* bias_up, float* gate, float* up, void* stream);
+/* One step of kt_qmatmul_chain: a one-row kt_qmatmul_group over `count` weights sharing
+ * K; with norm_weight, RMSNorm of x first (kt_rmsnorm_qmatmul_group; normed is its K
+ * floats of scratch); with swiglu_gate, weights = {gate, up} and outputs = {gate, up} as
+ * kt_rmsnorm_swiglu_gate gives them (accumulate 0, alpha 1). biases is NULL or `count`
+ * pointers, each NULL or N floats. */
+typedef struct kt_qmatmul_step {
+    const float* x;
+    const float* norm_weight;
+    float eps;
+    float* normed;
+    const kt_qweight* weights;
+    int32_t count;
+    float* const* outputs;
+    const float* const* biases;
+    int32_t accumulate;
+    float alpha;
+    int32_t swiglu_gate;
+} kt_qmatmul_step;
+
+/* Dependent one-row products, in order, each free to read earlier steps' outputs and to
+ * write what earlier steps read, with the effect of calling each step on its own: a
+ * decoder layer's projections between two attention calls (K/TransformerBlock.kt:40-46:
+ * wOut and its residual add into x, norm2 and the FFN, the down projection's residual add,
+ * then the next layer's norm1 and q/k/v, K/Attention.kt:222-224). When every weight has
+ * its column-run copy and all share one width and zero-point form, the steps run as one
+ * launch in which a step's workgroups fetch their first weights while earlier steps
+ * compute and wait on device counters (in the stream's workspace) only for their input
+ * row; otherwise as the calls named, one after another. 1 to 6 steps. */
+int32_t kt_qmatmul_chain(const kt_qmatmul_step* steps, int32_t count, void* stream);
 /* SwiGLU.forwardInto's gate followed by the down projection (K/SwiGLU.kt:19-25 then
  * QuantizedLinear.forwardInto, K/QuantizedLinear.kt:16-25):
  * c = (accumulate ? c : 0) + alpha * (silu(gate) * up) . deq(W) (+ bias), gate and up

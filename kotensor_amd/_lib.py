@@ -67,6 +67,23 @@ class _QWeight(ctypes.Structure):
 QWeight = _QWeight
 
 
+class QMatmulStep(ctypes.Structure):
+    """kt_qmatmul_step: one step of kt_qmatmul_chain."""
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("norm_weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("normed", ctypes.c_void_p),
+        ("weights", ctypes.POINTER(_QWeight)),
+        ("count", ctypes.c_int32),
+        ("outputs", ctypes.POINTER(ctypes.c_void_p)),
+        ("biases", ctypes.POINTER(ctypes.c_void_p)),
+        ("accumulate", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("swiglu_gate", ctypes.c_int32),
+    ]
+
+
 class _StEntry(ctypes.Structure):
     """kt_st_entry: one tensor of a safetensors header."""
     _fields_ = [
@@ -123,6 +140,7 @@ SIGNATURES = {
     "kt_rope_attention": [_P, _P, _P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P],
     "kt_rmsnorm_qmatmul_group": [_P, _P, _F, _P, _I, ctypes.POINTER(_QWeight), _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _F, _P],
     "kt_rmsnorm_swiglu_gate": [_P, _P, _F, _P, _I, ctypes.POINTER(_QWeight), ctypes.POINTER(_QWeight), _P, _P, _P, _P, _P],
+    "kt_qmatmul_chain": [ctypes.POINTER(QMatmulStep), _I, _P],
     "kt_argmax": [_P, _I, _P, _P],
     "kt_argmax_advance": [_P, _I, _P, _P, _P, _I, _P],
     "kt_position_add": [_P, _I, _P],

@@ -153,6 +153,23 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
                            int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up = nullptr,
                            const float* norm_weight = nullptr, float eps = 0.0f, bool glu = false);
 bool gemv_packed_pair_supported(const float* a, const WeightView* ws, float* const* cs);
+// Dependent column-run GEMVs as one launch (each step's input may be an earlier step's
+// output): the arguments of one launch_gemv_packed call per step.
+struct ChainStep {
+    const float* a;
+    const WeightView* ws;
+    float* const* cs;
+    const float* const* biases;
+    int32_t count, accumulate;
+    float alpha;
+    const float* up;
+    const float* norm_weight;
+    float eps;
+    bool glu;
+};
+int32_t gemv_chain_max_steps();
+int32_t gemv_chain_max_k();  // the longest input row a chained step takes
+int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st);
 void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);

@@ -1026,6 +1026,60 @@ int32_t kt_rmsnorm_swiglu_gate(const float* x, const float* norm_weight, float e
     return kt_silu_mul(gate, up, static_cast<int64_t>(m) * views[0].N, stream);
 }
 
+// One step of kt_qmatmul_chain as the call it stands for.
+static int32_t chain_step_call(const kt_qmatmul_step& p, void* stream) {
+    if (p.swiglu_gate)
+        return kt_rmsnorm_swiglu_gate(p.x, p.norm_weight, p.eps, p.normed, 1, &p.weights[0], &p.weights[1],
+                                      p.biases ? p.biases[0] : nullptr, p.biases ? p.biases[1] : nullptr,
+                                      p.outputs[0], p.outputs[1], stream);
+    if (p.norm_weight)
+        return kt_rmsnorm_qmatmul_group(p.x, p.norm_weight, p.eps, p.normed, 1, p.weights, p.count, p.outputs,
+                                        p.biases, p.accumulate, p.alpha, stream);
+    return kt_qmatmul_group(p.x, 1, p.weights, p.count, p.outputs, p.biases, p.accumulate, p.alpha, stream);
+}
+
+int32_t kt_qmatmul_chain(const kt_qmatmul_step* steps, int32_t count, void* stream) {
+    if (!steps) return fail(KT_ERR_ARGUMENT, "steps is NULL");
+    if (count < 1 || count > gemv_chain_max_steps())
+        return fail(KT_ERR_ARGUMENT, "a chain holds 1 to %d steps, got %d", gemv_chain_max_steps(), count);
+    WeightView views[8][4];
+    ChainStep cs[8];
+    bool chain = gemv_kind() == 0 || gemv_kind() == 5;
+    for (int32_t i = 0; i < count; ++i) {
+        const kt_qmatmul_step& p = steps[i];
+        if (!p.x || !p.weights || !p.outputs) return fail(KT_ERR_ARGUMENT, "step %d: x, weights or outputs is NULL", i);
+        if (p.count < 1 || p.count > 4 || (p.swiglu_gate && p.count != 2))
+            return fail(KT_ERR_ARGUMENT, "step %d: %d weights (1 to 4; the SwiGLU gate pair takes 2)", i, p.count);
+        if (p.norm_weight && !p.normed) return fail(KT_ERR_ARGUMENT, "step %d: normed is NULL", i);
+        for (int32_t j = 0; j < p.count; ++j) {
+            if (!p.outputs[j]) return fail(KT_ERR_ARGUMENT, "step %d: output %d is NULL", i, j);
+            const int32_t status = view_weight(&p.weights[j], &views[i][j]);
+            if (status) return status;
+            const WeightView& v = views[i][j];
+            if (v.K != views[i][0].K) return fail(KT_ERR_SHAPE, "step %d: the weights must share K", i);
+            chain = chain && v.bits == views[i][0].bits && v.g == views[i][0].g &&
+                    (v.z != nullptr) == (views[i][0].z != nullptr) && gemv_packed_supported(p.x, 1, v, p.outputs[j]);
+        }
+        if (p.swiglu_gate) {
+            if (views[i][0].N != views[i][1].N) return fail(KT_ERR_SHAPE, "step %d: gate and up differ in shape", i);
+            chain = chain && !p.accumulate && p.alpha == 1.0f && gemv_packed_pair_supported(p.x, views[i], p.outputs);
+        }
+        if (p.norm_weight)
+            chain = chain && aligned(p.norm_weight, 16) && views[i][0].K <= NORM_F4 * 4 * NORM_THREADS;
+        chain = chain && views[i][0].K <= gemv_chain_max_k();
+        chain = chain && views[i][0].bits == views[0][0].bits &&
+                (views[i][0].z != nullptr) == (views[0][0].z != nullptr);
+        cs[i] = ChainStep{p.x, views[i], p.outputs, p.biases, p.count, p.accumulate, p.alpha, nullptr,
+                          p.norm_weight, p.eps, p.swiglu_gate != 0};
+    }
+    if (chain) return launch_gemv_chain(cs, count, static_cast<hipStream_t>(stream));
+    for (int32_t i = 0; i < count; ++i) {
+        const int32_t status = chain_step_call(steps[i], stream);
+        if (status) return status;
+    }
+    return KT_OK;
+}
+
 int32_t kt_swiglu_qmatmul(float* gate, const float* up, int32_t m, const kt_qweight* w, float* c, int32_t accumulate,
                           float alpha, const float* bias, void* stream) {
     if (!gate || !up || !c) return fail(KT_ERR_ARGUMENT, "gate, up or the output is NULL");

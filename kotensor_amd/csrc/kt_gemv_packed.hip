@@ -174,13 +174,77 @@ __host__ __device__ constexpr int32_t lds_rec_offset(int32_t chunks) { return 4 
 __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return lds_rec_offset(chunks) + chunks * (CHUNK / RUN) * 8; }
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
 
+// A stage of a chained launch (gemv_chain_kernel): the workgroup issues its first weight
+// loads, waits until the previous stage's flag is raised (the first stage waits for
+// nothing), then reads its input row; when its outputs are stored it counts itself in.
+// Device-scope atomics on one address run one at a time (tens of ns each), so a stage's
+// workgroups count in two levels: into one of CHAIN_PARTS partition counters, and the
+// last of each partition into the stage counter; the stage's last workgroup returns both
+// to zero, lowers the flag it waited on (every workgroup of the stage is past it) and
+// raises its own. Waiting workgroups only read the flag. Every word is zero again when
+// the launch ends.
+constexpr int CHAIN_PARTS = 16;
+constexpr int CHAIN_STRIDE = 32;  // words between counters: one 128-byte line each
+constexpr uint32_t CHAIN_SPIN_LIMIT = 1u << 22;  // polls before a wait gives up (a fault, not a schedule)
+
+struct ChainLink {
+    uint32_t* wait_flag;   // raised when the previous stage is complete (null: none)
+    uint32_t* part_count;  // this workgroup's partition counter
+    uint32_t* stage_count;
+    uint32_t* done_flag;   // raised when this stage is complete (null: the last stage)
+    uint32_t part_size;    // workgroups of this stage in this partition
+    uint32_t parts;        // partitions holding workgroups of this stage
+};
+
+__device__ __forceinline__ void chain_wait(const ChainLink& link) {
+    if (!link.wait_flag) return;
+    if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        while (__hip_atomic_load(link.wait_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0u &&
+               ++spins < CHAIN_SPIN_LIMIT)
+            __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void chain_signal(const ChainLink& link) {
+    __syncthreads();  // every wave's write-through output stores are complete
+    if (threadIdx.x != 0) return;
+    if (__hip_atomic_fetch_add(link.part_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.part_size - 1)
+        return;
+    __hip_atomic_store(link.part_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (__hip_atomic_fetch_add(link.stage_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.parts - 1)
+        return;
+    __hip_atomic_store(link.stage_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (link.wait_flag) __hip_atomic_store(link.wait_flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (link.done_flag) __hip_atomic_store(link.done_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// What crosses stages of a chain goes past the caches, so that no cache-wide write-back
+// or invalidation is needed: outputs are written through (system-scope stores), and the
+// input row and accumulated outputs are read from the coherence point (system-scope loads;
+// the buffer loads' cache policy sc0 sc1).
+constexpr int COHERENT = 1 | 16;
+template <bool CHAIN>
+__device__ __forceinline__ float load_out(const float* p) {
+    if constexpr (CHAIN) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    else return *p;
+}
+template <bool CHAIN>
+__device__ __forceinline__ void store_out(float* p, float v) {
+    if constexpr (CHAIN) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    else *p = v;
+}
+
 // GLU: jobs 0 and 1 are SwiGLU's gate and up weights (same N); a workgroup's column sets
 // are pairs (gate set s, up set s), and the gate wave's epilogue writes
 // silu(gate) * up to job 0's output (silu_mul_kernel's expression) and up to job 1's.
-template <int BITS, int R, bool ZP, int XMODE, bool GLU>
-__global__ void __launch_bounds__(64 * W)
-    gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
-                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate) {
+// (bx, by) is the workgroup's place in the launch's own grid; CHAIN adds the hooks above.
+template <int BITS, int R, bool ZP, int XMODE, bool GLU, bool CHAIN, int XS = X_SLOTS>
+__device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, const float* __restrict__ aux, float eps,
+                                                 int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog,
+                                                 float alpha, int32_t accumulate, int32_t bx, int32_t by,
+                                                 const ChainLink& link) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -191,12 +255,18 @@ __global__ void __launch_bounds__(64 * W)
     // The job's fields are the first loads (first in the source: otherwise they wait for
     // kslog and the start costs a second scalar round trip).
     const PJob jb = jobs.job[GLU ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & ((1 << (3 - kslog)) - 1) & 1)
-                                 : blockIdx.y];
+                                 : by];
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t cslog = 3 - kslog;  // column sets per workgroup: 1 << cslog
-    const int32_t set0 = GLU ? blockIdx.x << (cslog - 1) : blockIdx.x << cslog;
-    if (set0 >= jb.sets) return;
+    const int32_t set0 = GLU ? bx << (cslog - 1) : bx << cslog;
+    if (set0 >= jb.sets) {
+        if constexpr (CHAIN) {
+            chain_wait(link);
+            chain_signal(link);
+        }
+        return;
+    }
     const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
     const int32_t my_set = set0 + (GLU ? my_cs >> 1 : my_cs);
     const bool set_live = my_set < jb.sets;
@@ -215,22 +285,28 @@ __global__ void __launch_bounds__(64 * W)
     // weights with their scales and zero points.
     const int32_t n4 = K >> 2, kp4 = kpad >> 2;
     const int32_t used = (kp4 + 64 * W - 1) / (64 * W);  // slots that reach into the digit rows
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, K * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t ur =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(XMODE == X_PLAIN ? x : aux), 0, K * 4, 0x00020000);
-    float4 xv[X_SLOTS];
-    float4 uv[XMODE == X_PLAIN ? 1 : X_SLOTS];
-    static_for<0, X_SLOTS>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        if (j < used) {
-            xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (tid + 64 * W * j) * 16, 0, 0));
-            if constexpr (XMODE != X_PLAIN)
-                uv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, (tid + 64 * W * j) * 16, 0, 0));
-        } else {
-            xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if constexpr (XMODE != X_PLAIN) uv[j] = xv[j];
-        }
-    });
+    float4 xv[XS];
+    float4 uv[XMODE == X_PLAIN ? 1 : XS];
+    auto load_x = [&]() {
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, K * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t ur =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(XMODE == X_PLAIN ? x : aux), 0, K * 4, 0x00020000);
+        static_for<0, XS>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < used) {
+                xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (tid + 64 * W * j) * 16, 0,
+                                                                                         CHAIN ? COHERENT : 0));
+                if constexpr (XMODE != X_PLAIN)  // up (SwiGLU input) may come from the chain too
+                    uv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           ur, (tid + 64 * W * j) * 16, 0,
+                                                           CHAIN && XMODE == X_SWIGLU ? COHERENT : 0));
+            } else {
+                xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (XMODE != X_PLAIN) uv[j] = xv[j];
+            }
+        });
+    };
+    if constexpr (!CHAIN) load_x();  // chained: after the weights and the wait
 
     int8_t* xd = reinterpret_cast<int8_t*>(smem);
     const int32_t zoff = 4 * kpad;
@@ -263,13 +339,22 @@ __global__ void __launch_bounds__(64 * W)
 #pragma unroll
     for (int s = 0; s < R; ++s) issue(s, s);
     __builtin_amdgcn_sched_barrier(0);
+    // chained and accumulating: this lane's old output (an earlier stage may have written
+    // it) goes out with the row
+    float old_out = 0.0f;
+    if constexpr (CHAIN) {
+        chain_wait(link);
+        load_x();
+        if constexpr (!GLU)
+            if (accumulate && kp == 0 && ln < SET && set_live) old_out = load_out<true>(jb.out + col);
+    }
 
     // ---- x to digits and run records, the whole row by the whole workgroup --------------
     // (float4 slot j of thread t is float4 t + 64 W j of the row; a run's 8 float4s are 8
     // lanes of one wave). Float4s past the row give zero digits.
     if (tid < ZERO_BYTES / 4) reinterpret_cast<uint32_t*>(smem + zoff)[tid] = 0u;
     float nsum = 0.0f;  // X_NORM: this thread's share of sum x^2
-    static_for<0, X_SLOTS>([&](auto jc) {
+    static_for<0, XS>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         const int32_t i = tid + 64 * W * j;
         if (j >= used) return;
@@ -356,49 +441,76 @@ __global__ void __launch_bounds__(64 * W)
     // Unrolled over the largest range so that the ring sits in registers; the wave leaves
     // at its own chunk count. Refills past the range read zeros without memory traffic
     // and are never used.
-    static_for<0, MAX_WAVE_CHUNKS>([&](auto ci) {
-        constexpr int c = decltype(ci)::value;
-        if (c < n) {
-            process(c % R, c);
-            if constexpr (c + R < MAX_WAVE_CHUNKS) issue(c % R, c + R);
-            __builtin_amdgcn_sched_barrier(0);  // keep each refill right behind its use
-        }
-    });
+    auto ring_loop = [&]() {
+        static_for<0, MAX_WAVE_CHUNKS>([&](auto ci) {
+            constexpr int c = decltype(ci)::value;
+            if (c < n) {
+                process(c % R, c);
+                if constexpr (c + R < MAX_WAVE_CHUNKS) issue(c % R, c + R);
+                __builtin_amdgcn_sched_barrier(0);  // keep each refill right behind its use
+            }
+        });
+    };
+    if constexpr (CHAIN) {
+        // a chained stage whose whole range is already in the ring: no refills, so the
+        // chunks' reads and products may interleave
+        if (n <= R)
+            static_for<0, R>([&](auto ci) {
+                constexpr int c = decltype(ci)::value;
+                if (c < n) process(c, c);
+            });
+        else
+            ring_loop();
+    } else {
+        ring_loop();
+    }
 
     // ---- the column's four runs, then the K-parts of the column set, in fixed order ----
     y += __shfl_xor(y, 16, 64);
     y += __shfl_xor(y, 32, 64);
     if (ln < SET) red[wave * SET + ln] = y;
     __syncthreads();
-    if (kp != 0 || ln >= SET || !set_live) return;
-    const int32_t ks = 1 << kslog, cs = 1 << cslog;
-    float sum = red[my_cs * SET + ln];
-    for (int32_t p = 1; p < ks; ++p) sum += red[(p * cs + my_cs) * SET + ln];
-    float al = alpha;
-    if constexpr (XMODE == X_NORM) {
-        float sq = red[W * SET];
-        for (int32_t w = 1; w < W; ++w) sq += red[W * SET + w];
-        al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
-    }
-    if constexpr (GLU) {
-        // the gate wave of the pair: its partner (slot my_cs + 1) holds up's sums
-        if (my_cs & 1) return;
-        float usum = red[(my_cs + 1) * SET + ln];
-        for (int32_t p = 1; p < ks; ++p) usum += red[(p * cs + my_cs + 1) * SET + ln];
-        float g = fmaf(al, sum, 0.0f);
-        if (jb.bias) g += jb.bias[col];
-        const PJob& ju = jobs.job[1];
-        float u = fmaf(al, usum, 0.0f);
-        if (ju.bias) u += ju.bias[col];
-        ju.out[col] = u;
-        jb.out[col] = g / (1.0f + static_cast<float>(exp(-static_cast<double>(g)))) * u;
-        return;
-    }
-    float* dst = jb.out + col;
-    float o = accumulate ? *dst : 0.0f;
-    o = fmaf(al, sum, o);
-    if (jb.bias) o += jb.bias[col];
-    *dst = o;
+    [&]() {
+        if (kp != 0 || ln >= SET || !set_live) return;
+        const int32_t ks = 1 << kslog, cs = 1 << cslog;
+        float sum = red[my_cs * SET + ln];
+        for (int32_t p = 1; p < ks; ++p) sum += red[(p * cs + my_cs) * SET + ln];
+        float al = alpha;
+        if constexpr (XMODE == X_NORM) {
+            float sq = red[W * SET];
+            for (int32_t w = 1; w < W; ++w) sq += red[W * SET + w];
+            al = alpha * (1.0f / sqrtf(sq / static_cast<float>(K) + eps));
+        }
+        if constexpr (GLU) {
+            // the gate wave of the pair: its partner (slot my_cs + 1) holds up's sums
+            if (my_cs & 1) return;
+            float usum = red[(my_cs + 1) * SET + ln];
+            for (int32_t p = 1; p < ks; ++p) usum += red[(p * cs + my_cs + 1) * SET + ln];
+            float g = fmaf(al, sum, 0.0f);
+            if (jb.bias) g += jb.bias[col];
+            const PJob& ju = jobs.job[1];
+            float u = fmaf(al, usum, 0.0f);
+            if (ju.bias) u += ju.bias[col];
+            store_out<CHAIN>(ju.out + col, u);
+            store_out<CHAIN>(jb.out + col, g / (1.0f + static_cast<float>(exp(-static_cast<double>(g)))) * u);
+            return;
+        }
+        float* dst = jb.out + col;
+        float o = accumulate ? (CHAIN ? old_out : *dst) : 0.0f;
+        o = fmaf(al, sum, o);
+        if (jb.bias) o += jb.bias[col];
+        store_out<CHAIN>(dst, o);
+    }();
+    if constexpr (CHAIN) chain_signal(link);
+}
+
+template <int BITS, int R, bool ZP, int XMODE, bool GLU>
+__global__ void __launch_bounds__(64 * W)
+    gemv_packed_kernel(const float* __restrict__ x, const float* __restrict__ aux, float eps, int32_t K, int32_t gshift,
+                       PJobs jobs, int32_t kslog, int32_t nmax, float alpha, int32_t accumulate) {
+    (void)nmax;
+    gemv_packed_body<BITS, R, ZP, XMODE, GLU, false>(x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, blockIdx.x,
+                                                     blockIdx.y, ChainLink{});
 }
 
 struct Forced {
@@ -548,9 +660,25 @@ bool gemv_packed_pair_supported(const float* a, const WeightView* ws, float* con
     return plan.ks != 0 && plan.ks <= W / 2;  // two column sets per workgroup at least
 }
 
-int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
-                           int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up,
-                           const float* norm_weight, float eps, bool glu) {
+namespace {
+
+// One launch of the column-run GEMV, as launch_gemv_packed checks and shapes it.
+struct PackedLaunch {
+    PJobs jobs{};
+    dim3 grid;
+    size_t lds = 0;
+    int mode = X_PLAIN;
+    int32_t kslog = 0, nmax = 0, gshift = 0, bits = 0;
+    bool zp = false, glu = false;
+    const float* x = nullptr;
+    const float* aux = nullptr;
+    float eps = 0.0f, alpha = 1.0f;
+    int32_t K = 0, accumulate = 0;
+};
+
+int32_t prepare_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                            int32_t count, int32_t accumulate, float alpha, const float* up, const float* norm_weight,
+                            float eps, bool glu, PackedLaunch* out) {
     const WeightView& w0 = ws[0];
     bool zp = false;
     for (int32_t i = 0; i < count; ++i) zp = zp || ws[i].z != nullptr;
@@ -570,11 +698,11 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
     if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed gemv: no work split fits K = %d, g = %d", w0.K, w0.g);
     if (glu && (count != 2 || ws[0].N != ws[1].N || plan.ks > W / 2 || accumulate || up))
         return fail(KT_ERR_ARGUMENT, "packed gemv: the paired gate/up form needs two weights of one shape");
-    const int32_t kslog = log2_exact(plan.ks);
-    PJobs jobs{};
-    jobs.count = count;
+    PackedLaunch& L = *out;
+    L.jobs = PJobs{};
+    L.jobs.count = count;
     for (int32_t i = 0; i < count; ++i) {
-        PJob& jb = jobs.job[i];
+        PJob& jb = L.jobs.job[i];
         jb.packed = ws[i].p;
         jb.s = ws[i].s;
         jb.z = ws[i].z;
@@ -584,20 +712,179 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
         jb.sets = ws[i].N / SET;
     }
     const int32_t per_wg = glu ? W / plan.ks / 2 : W / plan.ks;  // column sets (of each weight, glu) per workgroup
-    const dim3 grid(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)),
-                    static_cast<uint32_t>(glu ? 1 : count));
-    const int32_t gshift = log2_exact(w0.g / RUN);
-    const float* aux = up ? up : norm_weight;
-    if (w0.bits == 4)
-        launch_mode<4, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                             plan.nmax, glu ? 1 : 0);
-    else if (zp)
-        launch_mode<8, true>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                             plan.nmax, glu ? 1 : 0);
+    L.grid = dim3(static_cast<uint32_t>(ceil_div(static_cast<int32_t>(sets_max), per_wg)),
+                  static_cast<uint32_t>(glu ? 1 : count));
+    L.lds = plan.lds;
+    L.mode = mode;
+    L.kslog = log2_exact(plan.ks);
+    L.nmax = plan.nmax;
+    L.gshift = log2_exact(w0.g / RUN);
+    L.bits = w0.bits;
+    L.zp = zp;
+    L.glu = glu;
+    L.x = a;
+    L.aux = up ? up : norm_weight;
+    L.eps = eps;
+    L.alpha = alpha;
+    L.K = w0.K;
+    L.accumulate = accumulate;
+    return KT_OK;
+}
+
+// ---- chained launches ---------------------------------------------------------------
+// Dependent one-row products (each step's input row may be an earlier step's output) as
+// one launch: stage s is the workgroups [begin[s], begin[s + 1]), in dispatch order after
+// every earlier stage, so its first weight loads overlap the earlier stages and only the
+// input row waits (ChainLink). A stage never waits for a later one and the workgroups of
+// a launch are dispatched in order, so every wait ends.
+constexpr int MAX_STAGES = 6;
+
+struct ChainStage {
+    PJobs jobs;
+    const float* x;
+    const float* aux;
+    float eps, alpha;
+    int32_t K, gshift, kslog, accumulate;
+    int32_t gx;    // the stage's own grid is gx x (workgroups / gx)
+    int32_t kind;  // 3 x the form (plain, RMSNorm, RMSNorm paired gate/up, plain paired, SwiGLU input) + ring
+};
+// A chained stage's wave takes its ring as deep as its chunk range where it can (RS / 2,
+// RS or 2 RS chunks: all of the range in flight before the input row is there) and holds
+// at most CHAIN_XS float4s of the row per thread (K <= 8192).
+constexpr int CHAIN_XS = 4;
+
+struct ChainArgs {
+    int32_t begin[MAX_STAGES + 1];  // first workgroup of each stage, then the launch's total
+    int32_t stages;
+    uint32_t* counters;  // per stage: CHAIN_PARTS partition counters, the stage counter, the flag
+    ChainStage st[MAX_STAGES];
+};
+
+template <int BITS, bool ZP>
+__global__ void __launch_bounds__(64 * W) gemv_chain_kernel(ChainArgs c) {
+    const int32_t b = blockIdx.x;
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_STAGES; ++i) s += (i < c.stages && b >= c.begin[i]) ? 1 : 0;
+    const ChainStage& a = c.st[s];
+    const int32_t local = b - c.begin[s];
+    const int32_t by = local / a.gx, bx = local - by * a.gx;
+    // stage s's words: CHAIN_PARTS partition counters, the stage counter, the flag
+    uint32_t* words = c.counters + s * (CHAIN_PARTS + 2) * CHAIN_STRIDE;
+    const int32_t n = c.begin[s + 1] - c.begin[s], part = local % CHAIN_PARTS;
+    ChainLink link;
+    link.wait_flag = s > 0 ? words - CHAIN_STRIDE : nullptr;
+    link.part_count = words + part * CHAIN_STRIDE;
+    link.stage_count = words + CHAIN_PARTS * CHAIN_STRIDE;
+    link.done_flag = s + 1 < c.stages ? words + (CHAIN_PARTS + 1) * CHAIN_STRIDE : nullptr;
+    link.part_size = static_cast<uint32_t>((n - part + CHAIN_PARTS - 1) / CHAIN_PARTS);
+    link.parts = static_cast<uint32_t>(min(n, CHAIN_PARTS));
+    constexpr int RS = BITS == 4 ? 4 : 2;
+#define KT_CHAIN_BODY(RING, XM, GL)                                                                                    \
+    gemv_packed_body<BITS, RING, ZP, XM, GL, true, CHAIN_XS>(a.x, a.aux, a.eps, a.K, a.gshift, a.jobs, a.kslog,        \
+                                                             a.alpha, a.accumulate, bx, by, link)
+#define KT_CHAIN_FORM(F, XM, GL)                                                                                       \
+    case 3 * F: KT_CHAIN_BODY(RS / 2, XM, GL); break;                                                                  \
+    case 3 * F + 1: KT_CHAIN_BODY(RS, XM, GL); break;                                                                  \
+    case 3 * F + 2: KT_CHAIN_BODY(2 * RS, XM, GL); break;
+    switch (a.kind) {
+        KT_CHAIN_FORM(0, X_PLAIN, false)
+        KT_CHAIN_FORM(1, X_NORM, false)
+        KT_CHAIN_FORM(2, X_NORM, true)
+        KT_CHAIN_FORM(3, X_PLAIN, true)
+        KT_CHAIN_FORM(4, X_SWIGLU, false)
+        default: break;
+    }
+#undef KT_CHAIN_FORM
+#undef KT_CHAIN_BODY
+}
+
+int32_t chain_kind(const PackedLaunch& L) {
+    const int RS = L.bits == 4 ? 4 : 2;
+    const int ring = L.nmax <= RS / 2 ? 0 : L.nmax <= RS ? 1 : 2;
+    int form = 0;
+    if (L.mode == X_SWIGLU) form = 4;
+    else if (L.mode == X_NORM) form = L.glu ? 2 : 1;
+    else form = L.glu ? 3 : 0;
+    return 3 * form + ring;
+}
+
+}  // namespace
+
+int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* cs, const float* const* biases,
+                           int32_t count, int32_t accumulate, float alpha, hipStream_t st, const float* up,
+                           const float* norm_weight, float eps, bool glu) {
+    PackedLaunch L;
+    const int32_t status = prepare_gemv_packed(a, ws, cs, biases, count, accumulate, alpha, up, norm_weight, eps, glu, &L);
+    if (status) return status;
+    if (L.bits == 4)
+        launch_mode<4, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
+                             L.accumulate, L.nmax, L.glu ? 1 : 0);
+    else if (L.zp)
+        launch_mode<8, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
+                             L.accumulate, L.nmax, L.glu ? 1 : 0);
     else
-        launch_mode<8, false>(mode, grid, plan.lds, st, a, aux, eps, w0.K, gshift, jobs, kslog, alpha, accumulate,
-                              plan.nmax, glu ? 1 : 0);
+        launch_mode<8, false>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
+                              L.accumulate, L.nmax, L.glu ? 1 : 0);
     KT_LAUNCHED("qmatmul: packed gemv kernel");
+    return KT_OK;
+}
+
+int32_t gemv_chain_max_steps() { return MAX_STAGES; }
+int32_t gemv_chain_max_k() { return CHAIN_XS * 4 * 64 * W; }
+
+int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st) {
+    if (n < 1 || n > MAX_STAGES) return fail(KT_ERR_ARGUMENT, "a chain holds 1 to %d steps, got %d", MAX_STAGES, n);
+    ChainArgs c{};
+    c.stages = n;
+    size_t lds = 0;
+    int32_t bits = 0;
+    bool zp = false;
+    int64_t total = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        const ChainStep& p = steps[i];
+        PackedLaunch L;
+        const int32_t status = prepare_gemv_packed(p.a, p.ws, p.cs, p.biases, p.count, p.accumulate, p.alpha, p.up,
+                                                   p.norm_weight, p.eps, p.glu, &L);
+        if (status) return status;
+        if (L.K > CHAIN_XS * 4 * 64 * W)
+            return fail(KT_ERR_ARGUMENT, "a chained step's row holds at most %d values, got %d", CHAIN_XS * 4 * 64 * W, L.K);
+        if (i == 0) {
+            bits = L.bits;
+            zp = L.zp;
+        } else if (L.bits != bits || L.zp != zp) {
+            return fail(KT_ERR_ARGUMENT, "a chain's weights must share one width and zero-point form");
+        }
+        ChainStage& a = c.st[i];
+        a.jobs = L.jobs;
+        a.x = L.x;
+        a.aux = L.aux;
+        a.eps = L.eps;
+        a.alpha = L.alpha;
+        a.K = L.K;
+        a.gshift = L.gshift;
+        a.kslog = L.kslog;
+        a.accumulate = L.accumulate;
+        a.gx = static_cast<int32_t>(L.grid.x);
+        a.kind = chain_kind(L);
+        c.begin[i] = static_cast<int32_t>(total);
+        total += static_cast<int64_t>(L.grid.x) * L.grid.y;
+        lds = std::max(lds, L.lds);
+    }
+    if (total > INT32_MAX) return fail(KT_ERR_SHAPE, "chain too large");
+    for (int32_t i = n; i <= MAX_STAGES; ++i) c.begin[i] = static_cast<int32_t>(total);
+    void* general = nullptr;
+    const int32_t status =
+        workspace_counters(st, 0, static_cast<size_t>(n) * (CHAIN_PARTS + 2) * CHAIN_STRIDE, &general, &c.counters);
+    if (status) return status;
+    const dim3 grid(static_cast<uint32_t>(total));
+    if (bits == 4)
+        gemv_chain_kernel<4, true><<<grid, dim3(64 * W), lds, st>>>(c);
+    else if (zp)
+        gemv_chain_kernel<8, true><<<grid, dim3(64 * W), lds, st>>>(c);
+    else
+        gemv_chain_kernel<8, false><<<grid, dim3(64 * W), lds, st>>>(c);
+    KT_LAUNCHED("qmatmul chain kernel");
     return KT_OK;
 }
 

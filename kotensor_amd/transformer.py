@@ -433,17 +433,46 @@ class Transformer:
     def _bias(self, name: str):
         return None if self._zero_bias.get(name, True) else self.parameters[name + ".bias"].ptr
 
-    def _layers(self, rows: _Rows, count: int, cache: KVCache, key_bound: int, st) -> None:
+    def _layers(self, rows: _Rows, count: int, cache: KVCache, key_bound: int, st,
+                head: InferenceBuffers | None = None) -> bool:
+        """The layers over `count` rows. For one row the projections between two attention
+        calls (wOut, norm2 and the gate pair, wDown, and the next layer's norm1 and q/k/v)
+        run as one kt_qmatmul_chain call, and with `head` the last layer's chain ends with
+        finalNorm and lmHead into head.logits; returns whether the head ran."""
+        q_ready = False  # the layer's q/k/v came from the previous layer's chain
+        headed = False
         for l in range(self.num_layers):
             p = f"block.{l}."
-            names = [p + "attention.wQ", p + "attention.wK", p + "attention.wV"]
-            n, ws, os_, bs = _group([self.weights[x] for x in names], [rows.q.ptr, rows.k.ptr, rows.v.ptr],
-                                    [self._bias(x) for x in names])
-            _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm1.weight"].ptr,
-                      ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0), st)
+            if not q_ready:
+                n, ws, os_, bs = _group([self.weights[x] for x in self._qkv_names(l)], [rows.q.ptr, rows.k.ptr, rows.v.ptr],
+                                        [self._bias(x) for x in self._qkv_names(l)])
+                _lib.call("kt_rmsnorm_qmatmul_group", rows.x.ptr, self.parameters[p + "norm1.weight"].ptr,
+                          ctypes.c_float(self.norm_eps), rows.normed.ptr, count, ws, n, os_, bs, 0, ctypes.c_float(1.0),
+                          st)
             _lib.call("kt_rope_attention", rows.q.ptr, rows.k.ptr, rows.v.ptr, self.inv_freq.ptr, count,
                       cache.position.ptr, key_bound, cache.keys.ptr, cache.values.ptr, l, cache.max_sequence_length,
                       self.num_heads, self.num_key_value_heads, self.head_dim, rows.context.ptr, st)
+            q_ready = False
+            if count == 1 and self._zero_bias.get(p + "attention.wOut", True) and \
+                    self._zero_bias.get(p + "ffn.wDown", True):
+                # a zero bias lets wOut and wDown accumulate straight into x
+                steps = [(rows.context.ptr, None, [self.weights[p + "attention.wOut"]], [rows.x.ptr], [None], 1, 0),
+                         (rows.x.ptr, self.parameters[p + "norm2.weight"].ptr,
+                          [self.weights[p + "ffn.wGate"], self.weights[p + "ffn.wUp"]], [rows.gate.ptr, rows.up.ptr],
+                          [self._bias(p + "ffn.wGate"), self._bias(p + "ffn.wUp")], 0, 1),
+                         (rows.gate.ptr, None, [self.weights[p + "ffn.wDown"]], [rows.x.ptr], [None], 1, 0)]
+                if l + 1 < self.num_layers:
+                    names = self._qkv_names(l + 1)
+                    steps.append((rows.x.ptr, self.parameters[f"block.{l + 1}.norm1.weight"].ptr,
+                                  [self.weights[x] for x in names], [rows.q.ptr, rows.k.ptr, rows.v.ptr],
+                                  [self._bias(x) for x in names], 0, 0))
+                    q_ready = True
+                elif head is not None:
+                    steps.append((rows.x.ptr, self.parameters["finalNorm.weight"].ptr, [self.weights["lmHead"]],
+                                  [head.logits.ptr], [self._bias("lmHead")], 0, 0))
+                    headed = True
+                self._chain(steps, rows.normed.ptr, st)
+                continue
             self._residual_projection(p + "attention.wOut", rows.context, rows, count, st)
             # norm2, gate and up, and the gate silu(gate) * up in one call; then the down
             # projection of the gate row with the residual
@@ -452,6 +481,31 @@ class Transformer:
                       ctypes.byref(self.weights[p + "ffn.wGate"].qweight), ctypes.byref(self.weights[p + "ffn.wUp"].qweight),
                       self._bias(p + "ffn.wGate"), self._bias(p + "ffn.wUp"), rows.gate.ptr, rows.up.ptr, st)
             self._residual_projection(p + "ffn.wDown", rows.gate, rows, count, st)
+        return headed
+
+    @staticmethod
+    def _qkv_names(l: int) -> list[str]:
+        p = f"block.{l}."
+        return [p + "attention.wQ", p + "attention.wK", p + "attention.wV"]
+
+    def _chain(self, steps, normed_ptr: int, st) -> None:
+        """kt_qmatmul_chain over (x, norm weight, weights, outputs, biases, accumulate,
+        swiglu gate pair) steps."""
+        arr = (_lib.QMatmulStep * len(steps))()
+        keep = []
+        for s, (x, nw, ws, outs, biases, acc, swiglu) in zip(arr, steps):
+            n = len(ws)
+            wa = (_lib.QWeight * n)(*[w.qweight for w in ws])
+            oa = (ctypes.c_void_p * n)(*outs)
+            ba = None if all(b is None for b in biases) else (ctypes.c_void_p * n)(*[b or 0 for b in biases])
+            keep += [wa, oa, ba]
+            s.x, s.norm_weight, s.eps, s.normed = x, nw, self.norm_eps, normed_ptr
+            s.weights = ctypes.cast(wa, ctypes.POINTER(_lib.QWeight))
+            s.count = n
+            s.outputs = ctypes.cast(oa, ctypes.POINTER(ctypes.c_void_p))
+            s.biases = ctypes.cast(ba, ctypes.POINTER(ctypes.c_void_p)) if ba is not None else None
+            s.accumulate, s.alpha, s.swiglu_gate = acc, 1.0, swiglu
+        _lib.call("kt_qmatmul_chain", arr, len(steps), st)
 
     def _head(self, x_row_ptr: int, buffers: InferenceBuffers, st) -> None:
         """finalNorm and lmHead of one row into buffers.logits (one launch with the norm
@@ -465,16 +519,16 @@ class Transformer:
         caller's to advance. With argmax the greedy token replaces buffers.tokens[0] and is
         recorded in buffers.generated at its position."""
         self._embed(buffers, 1, st)
-        self._layers(buffers, 1, cache, cache.max_sequence_length, st)
+        headed = self._layers(buffers, 1, cache, cache.max_sequence_length, st, head=buffers)
+        if not headed:
+            self._head(buffers.x.ptr, buffers, st)
         if argmax:
             # the head does not read the position: advance it, take the argmax and record
             # the token in one launch after the head
-            self._head(buffers.x.ptr, buffers, st)
             _lib.call("kt_argmax_advance", buffers.logits.ptr, self.vocabulary_size, buffers.tokens.ptr,
                       cache.position.ptr, buffers.generated.ptr, buffers.max_sequence_length, st)
         else:
             _lib.call("kt_position_add", cache.position.ptr, 1, st)
-            self._head(buffers.x.ptr, buffers, st)
 
     # -- the reference's entry points ----------------------------------------------------
     def prefill(self, prompt, cache: KVCache, buffers: InferenceBuffers, stream: Stream | None = None,

@@ -89,6 +89,18 @@ def test_argument_errors_map_to_illegal_argument():
     assert lib.kt_qweight_pack(ctypes.byref(w), None, None) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_qweight_pack(ctypes.byref(w), ctypes.c_void_p(8), None) == _lib.KT_ERR_ARGUMENT
     assert "16-byte aligned" in _lib.last_error()
+    # the chain of one-row products: its step checks come before any device access
+    steps = (_lib.QMatmulStep * 2)()
+    assert lib.kt_qmatmul_chain(None, 1, None) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qmatmul_chain(steps, 0, None) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qmatmul_chain(steps, 7, None) == _lib.KT_ERR_ARGUMENT
+    assert "1 to 6 steps" in _lib.last_error()
+    assert lib.kt_qmatmul_chain(steps, 1, None) == _lib.KT_ERR_ARGUMENT  # x, weights, outputs NULL
+    outs = (ctypes.c_void_p * 2)(16, 16)
+    steps[0].x, steps[0].weights, steps[0].outputs = 16, ctypes.pointer(w), outs
+    steps[0].count, steps[0].swiglu_gate = 1, 1
+    assert lib.kt_qmatmul_chain(steps, 1, None) == _lib.KT_ERR_ARGUMENT
+    assert "SwiGLU gate pair takes 2" in _lib.last_error()
 
 
 def test_product_does_not_reach_the_oracle():
