@@ -175,34 +175,51 @@ __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return ld
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
 
 // A stage of a chained launch (gemv_chain_kernel): the workgroup issues its first weight
-// loads, waits until the previous stage's flag is raised (the first stage waits for
-// nothing), then reads its input row; when its outputs are stored it counts itself in.
-// Device-scope atomics on one address run one at a time (tens of ns each), so a stage's
-// workgroups count in two levels: into one of CHAIN_PARTS partition counters, and the
-// last of each partition into the stage counter; the stage's last workgroup returns both
-// to zero, lowers the flag it waited on (every workgroup of the stage is past it) and
-// raises its own. Waiting workgroups only read the flag. Every word is zero again when
-// the launch ends.
+// loads, waits until every partition of the previous stage has raised its flag (the first
+// stage waits for nothing), then reads its input row; when its outputs are stored it
+// counts itself in. Device-scope atomics on one address run one at a time (tens of ns
+// each), so a stage's workgroups count in CHAIN_PARTS partition counters, each on its own
+// line; the last workgroup of a partition returns the counter to zero and raises the
+// partition's flag, and waiting workgroups read the flags (one lane each). A stage's flags
+// are lowered two stages on, by the first workgroup of stage s + 2 once it is past its own
+// wait (every workgroup of stage s + 1 is then past the flags). The last stage has no
+// waiters: its partitions' last workgroups count into one stage counter instead, and the
+// last of those lowers the previous stage's flags. Every word is zero when the launch ends.
 constexpr int CHAIN_PARTS = 16;
-constexpr int CHAIN_STRIDE = 32;  // words between counters: one 128-byte line each
+constexpr int CHAIN_STRIDE = 32;  // words between counters and flags: one 128-byte line each
+constexpr int CHAIN_WORDS = (2 * CHAIN_PARTS + 1) * CHAIN_STRIDE;  // per stage
+constexpr int CHAIN_BASE = 8192;  // the chain's words start here in the stream's counters
 constexpr uint32_t CHAIN_SPIN_LIMIT = 1u << 22;  // polls before a wait gives up (a fault, not a schedule)
 
 struct ChainLink {
-    uint32_t* wait_flag;   // raised when the previous stage is complete (null: none)
-    uint32_t* part_count;  // this workgroup's partition counter
-    uint32_t* stage_count;
-    uint32_t* done_flag;   // raised when this stage is complete (null: the last stage)
-    uint32_t part_size;    // workgroups of this stage in this partition
-    uint32_t parts;        // partitions holding workgroups of this stage
+    uint32_t* wait_flags;   // the previous stage's partition flags (null: the first stage)
+    uint32_t* lower_flags;  // stage s - 2's flags, lowered by the stage's first workgroup (or null)
+    uint32_t* part_count;   // this workgroup's partition counter
+    uint32_t* part_flag;    // its flag (null: the last stage)
+    uint32_t* stage_count;  // the last stage's counter
+    uint32_t* last_lower;   // the last stage: the previous stage's flags, lowered at the end
+    uint32_t wait_parts, lower_parts, last_lower_parts;
+    uint32_t part_size, parts;  // workgroups in this partition; partitions of this stage
 };
 
+__device__ __forceinline__ void lower_chain_flags(uint32_t* flags, uint32_t parts) {
+    for (uint32_t p = 0; p < parts; ++p)
+        __hip_atomic_store(flags + p * CHAIN_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ void chain_wait(const ChainLink& link) {
-    if (!link.wait_flag) return;
-    if (threadIdx.x == 0) {
+    if (!link.wait_flags) return;
+    if (threadIdx.x < 64) {  // wave 0: lane p reads partition p's flag
+        const uint32_t ln = threadIdx.x;
         uint32_t spins = 0;
-        while (__hip_atomic_load(link.wait_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0u &&
-               ++spins < CHAIN_SPIN_LIMIT)
+        while (true) {
+            const uint32_t v = ln < link.wait_parts ? __hip_atomic_load(link.wait_flags + ln * CHAIN_STRIDE,
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                                                    : 1u;
+            if (__all(v != 0u) || ++spins >= CHAIN_SPIN_LIMIT) break;
             __builtin_amdgcn_s_sleep(2);
+        }
+        if (threadIdx.x == 0 && link.lower_flags) lower_chain_flags(link.lower_flags, link.lower_parts);
     }
     __syncthreads();
 }
@@ -213,11 +230,14 @@ __device__ __forceinline__ void chain_signal(const ChainLink& link) {
     if (__hip_atomic_fetch_add(link.part_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.part_size - 1)
         return;
     __hip_atomic_store(link.part_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (link.part_flag) {
+        __hip_atomic_store(link.part_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
     if (__hip_atomic_fetch_add(link.stage_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.parts - 1)
         return;
     __hip_atomic_store(link.stage_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (link.wait_flag) __hip_atomic_store(link.wait_flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (link.done_flag) __hip_atomic_store(link.done_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (link.last_lower) lower_chain_flags(link.last_lower, link.last_lower_parts);
 }
 
 // What crosses stages of a chain goes past the caches, so that no cache-wide write-back
@@ -756,7 +776,7 @@ constexpr int CHAIN_XS = 4;
 struct ChainArgs {
     int32_t begin[MAX_STAGES + 1];  // first workgroup of each stage, then the launch's total
     int32_t stages;
-    uint32_t* counters;  // per stage: CHAIN_PARTS partition counters, the stage counter, the flag
+    uint32_t* counters;  // the stream's counters; the chain's words from CHAIN_BASE
     ChainStage st[MAX_STAGES];
 };
 
@@ -769,16 +789,23 @@ __global__ void __launch_bounds__(64 * W) gemv_chain_kernel(ChainArgs c) {
     const ChainStage& a = c.st[s];
     const int32_t local = b - c.begin[s];
     const int32_t by = local / a.gx, bx = local - by * a.gx;
-    // stage s's words: CHAIN_PARTS partition counters, the stage counter, the flag
-    uint32_t* words = c.counters + s * (CHAIN_PARTS + 2) * CHAIN_STRIDE;
+    // stage s's words: CHAIN_PARTS partition counters, CHAIN_PARTS flags, the stage counter
+    auto words = [&](int32_t t) { return c.counters + CHAIN_BASE + t * CHAIN_WORDS; };
+    auto parts = [&](int32_t t) { return static_cast<uint32_t>(min(c.begin[t + 1] - c.begin[t], CHAIN_PARTS)); };
     const int32_t n = c.begin[s + 1] - c.begin[s], part = local % CHAIN_PARTS;
+    const bool last = s + 1 == c.stages;
     ChainLink link;
-    link.wait_flag = s > 0 ? words - CHAIN_STRIDE : nullptr;
-    link.part_count = words + part * CHAIN_STRIDE;
-    link.stage_count = words + CHAIN_PARTS * CHAIN_STRIDE;
-    link.done_flag = s + 1 < c.stages ? words + (CHAIN_PARTS + 1) * CHAIN_STRIDE : nullptr;
+    link.wait_flags = s > 0 ? words(s - 1) + CHAIN_PARTS * CHAIN_STRIDE : nullptr;
+    link.wait_parts = s > 0 ? parts(s - 1) : 0u;
+    link.lower_flags = s > 1 && local == 0 ? words(s - 2) + CHAIN_PARTS * CHAIN_STRIDE : nullptr;
+    link.lower_parts = s > 1 ? parts(s - 2) : 0u;
+    link.part_count = words(s) + part * CHAIN_STRIDE;
+    link.part_flag = last ? nullptr : words(s) + (CHAIN_PARTS + part) * CHAIN_STRIDE;
+    link.stage_count = words(s) + 2 * CHAIN_PARTS * CHAIN_STRIDE;
+    link.last_lower = last && s > 0 ? link.wait_flags : nullptr;
+    link.last_lower_parts = link.wait_parts;
     link.part_size = static_cast<uint32_t>((n - part + CHAIN_PARTS - 1) / CHAIN_PARTS);
-    link.parts = static_cast<uint32_t>(min(n, CHAIN_PARTS));
+    link.parts = parts(s);
     constexpr int RS = BITS == 4 ? 4 : 2;
 #define KT_CHAIN_BODY(RING, XM, GL)                                                                                    \
     gemv_packed_body<BITS, RING, ZP, XM, GL, true, CHAIN_XS>(a.x, a.aux, a.eps, a.K, a.gshift, a.jobs, a.kslog,        \
@@ -875,7 +902,7 @@ int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st) {
     for (int32_t i = n; i <= MAX_STAGES; ++i) c.begin[i] = static_cast<int32_t>(total);
     void* general = nullptr;
     const int32_t status =
-        workspace_counters(st, 0, static_cast<size_t>(n) * (CHAIN_PARTS + 2) * CHAIN_STRIDE, &general, &c.counters);
+        workspace_counters(st, 0, CHAIN_BASE + static_cast<size_t>(n) * CHAIN_WORDS, &general, &c.counters);
     if (status) return status;
     const dim3 grid(static_cast<uint32_t>(total));
     if (bits == 4)
