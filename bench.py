@@ -22,7 +22,9 @@ The JSON line also carries:
                    host: faithful and FMA-contracted builds, all threads and one, the
                    median of 5 samples after 3 warm-up calls;
   extra         -- the rest of the workload family: C2, the Qwen2-0.5B layer step
-                   (grouped launches) and each projection alone at g64 and g32; C1, the
+                   (grouped launches, and the decoder's one chained launch with the
+                   norms, SwiGLU and residual adds fused) and each projection alone at
+                   g64 and g32; C1, the
                    INT8 2048 x 2048 GEMV at g64 and g32; C5's g32 rows at M = 1; the
                    INT8 group-32 prefill GEMM at M = 512 on the 2048-wide layer's four
                    shapes and their sum, each beside the vendor library's plain bf16
@@ -34,9 +36,10 @@ The JSON line also carries:
                    to end (1024-token prefill, greedy decode steps). Every timed graph
                    reads each of its weight copies (> 2x MALL).
 
---only dominant | copy | quantize | gemm runs just the headline product (or a 256 MB
-device copy, the calibration of the HBM byte counters, or kt_quantize INT4 and INT8 g64
-on 4096 x 14336, or the INT8 g32 M = 512 GEMM on 2048 -> 8192) for rocprofv3 runs.
+--only dominant | copy | quantize | gemm | decode runs just the headline product (or a
+256 MB device copy, the calibration of the HBM byte counters, or kt_quantize INT4 and
+INT8 g64 on 4096 x 14336, or the INT8 g32 M = 512 GEMM on 2048 -> 8192, or the 1B
+decoder's prefill and decode steps) for rocprofv3 runs.
 """
 from __future__ import annotations
 
@@ -307,7 +310,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--plain", action="store_true",
                     help="with --only gemm: weights without the column-run copy (the reference-layout GEMM)")
-    ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm"],
+    ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm", "decode"],
                     help="run one kernel for a rocprofv3 run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -381,6 +384,10 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
         print(json.dumps({"only": "gemm", "kernel": f"{kernel} int8 g32 M=512 2048x8192",
                           "flops": 2 * 512 * 2048 * 8192, "launches": args.steps}), flush=True)
         return 0
+    if args.only == "decode":
+        # the Llama-style 1B INT4 decoder: 1024-token prefill and 127 greedy steps, twice
+        print(json.dumps({"only": "decode", **decoder_figures(torch, stream_obj)}), flush=True)
+        return 0
     k, n, bits, g = HEADLINE
     copies = weight_copies(torch, kt_lib, k, n, bits, g, 8, stream, packed=True)
     x = torch.randn((1, k), device="cuda", dtype=torch.float32)
@@ -450,10 +457,38 @@ def gemv_row(torch, kt_lib, stream_obj, k, n, bits, g, seed, launches=64):
             "bytes": nbytes}
 
 
-def qwen_step(torch, kt_lib, stream_obj, bits, g, steps):
+def chain_steps(kt_lib, ws, bufs):
+    """The five kt_qmatmul_chain steps of one Qwen2-0.5B layer and the head, in the
+    decoder's order (TransformerBlock.kt:40-46): o accumulated into x, norm2 and the
+    SwiGLU gate/up pair, down accumulated into x, norm1 and q/k/v, the final norm and the
+    head. Returns (the step array, the arrays it points into)."""
+    b = bufs
+    spec = [(b["ctx"], None, ws[3:4], [b["x"]], 1, 0),
+            (b["x"], b["norm2"], ws[4:6], [b["gate"], b["up"]], 0, 1),
+            (b["gate"], None, ws[6:7], [b["x"]], 1, 0),
+            (b["x"], b["norm1"], ws[0:3], [b["q"], b["k"], b["v"]], 0, 0),
+            (b["x"], b["normf"], ws[7:8], [b["logits"]], 0, 0)]
+    steps = (kt_lib.QMatmulStep * len(spec))()
+    keep = []
+    for s, (x, nw, wl, outs, acc, swiglu) in zip(steps, spec):
+        wa = (kt_lib.QWeight * len(wl))(*[w.struct for w in wl])
+        oa = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+        keep += [wa, oa]
+        s.x, s.norm_weight, s.eps = x.data_ptr(), nw.data_ptr() if nw is not None else None, 1e-6
+        s.normed = b["normed"].data_ptr()
+        s.weights = ctypes.cast(wa, ctypes.POINTER(kt_lib.QWeight))
+        s.count = len(wl)
+        s.outputs = ctypes.cast(oa, ctypes.POINTER(ctypes.c_void_p))
+        s.biases, s.accumulate, s.alpha, s.swiglu_gate = None, acc, 1.0, swiglu
+    return steps, keep
+
+
+def qwen_step(torch, kt_lib, stream_obj, bits, g, steps, chained=False):
     """One Qwen2-0.5B layer's projections and the head at M = 1 on packed weights: q/k/v
-    and gate/up as one grouped launch each, o, down and the head one launch each; one
-    graph per weight copy, replayed. Returns (ms per step, bytes per step, copies)."""
+    and gate/up as one grouped launch each, o, down and the head one launch each; or,
+    chained, the decoder's single kt_qmatmul_chain launch over the same weights with the
+    norms, the SwiGLU gate and the residual adds fused. One graph per weight copy,
+    replayed. Returns (ms per step, bytes per step, copies)."""
     stream = ctypes.c_void_p(stream_obj.cuda_stream)
     base = [Weight(torch, kt_lib, k, n, bits, g, seed=1 + i, stream=stream).pack(torch, kt_lib, stream)
             for i, (_, k, n) in enumerate(QWEN)]
@@ -462,9 +497,18 @@ def qwen_step(torch, kt_lib, stream_obj, bits, g, steps):
     sets = [base] + [[w.clone(kt_lib) for w in base] for _ in range(copies - 1)]
     xs = {k: torch.randn((1, k), device="cuda", dtype=torch.float32) for k in (896, 4864)}
     ys = [torch.empty((1, n), device="cuda", dtype=torch.float32) for _, _, n in QWEN]
+    bufs = {name: torch.randn(n, device="cuda", dtype=torch.float32) * 0.1 + (1.0 if name.startswith("norm") else 0.0)
+            for name, n in (("x", 896), ("ctx", 896), ("normed", 896), ("norm1", 896), ("norm2", 896),
+                            ("normf", 896), ("gate", 4864), ("up", 4864), ("q", 896), ("k", 128), ("v", 128),
+                            ("logits", 151936))}
+    chains = [chain_steps(kt_lib, ws, bufs) for ws in sets] if chained else None
     torch.cuda.synchronize()
 
-    def step(ws):
+    def step(r):
+        ws = sets[r]
+        if chained:
+            kt_lib.call("kt_qmatmul_chain", chains[r][0], 5, stream)
+            return
         qmatmul_group(kt_lib, xs[896], 1, ws[0:3], ys[0:3], stream)
         qmatmul(kt_lib, xs[896], 1, ws[3], ys[3], stream)
         qmatmul_group(kt_lib, xs[896], 1, ws[4:6], ys[4:6], stream)
@@ -472,13 +516,13 @@ def qwen_step(torch, kt_lib, stream_obj, bits, g, steps):
         qmatmul(kt_lib, xs[896], 1, ws[7], ys[7], stream)
 
     for r in range(copies):
-        step(sets[r])
+        step(r)
     torch.cuda.synchronize()
     graphs = []
     for r in range(copies):
         gph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gph, stream=stream_obj):
-            step(sets[r])
+            step(r)
         graphs.append(gph)
     for i in range(4 * copies):
         graphs[i % copies].replay()
@@ -490,7 +534,7 @@ def qwen_step(torch, kt_lib, stream_obj, bits, g, steps):
         graphs[i % copies].replay()
     t1.record(stream_obj)
     torch.cuda.synchronize()
-    del graphs, sets, base
+    del graphs, sets, base, chains
     return t0.elapsed_time(t1) / steps, sum(gemv_bytes(1, k, n, bits, g) for _, k, n in QWEN), copies
 
 
@@ -528,6 +572,11 @@ def run(args, torch, kt_lib, stream_obj) -> int:
             gbs = b / (ms * 1e-3) / 1e9
             row = {"step": {"ms": round(ms, 5), "bytes": b, "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                             "launches": 5, "weight_copies": cp}}
+            ms, b, cp = qwen_step(torch, kt_lib, stream_obj, 4, gg, 200, chained=True)
+            gbs = b / (ms * 1e-3) / 1e9
+            row["step_chained"] = {"ms": round(ms, 5), "bytes": b, "GB/s": round(gbs, 1),
+                                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "launches": 1, "weight_copies": cp,
+                                   "fused": "norm1, norm2, final norm, SwiGLU gate, two residual adds"}
             for name, kk, nn in [("q_o", 896, 896), ("k_v", 896, 128), ("gate_up", 896, 4864), ("down", 4864, 896),
                                  ("lm_head", 896, 151936)]:
                 row[f"{name}_{kk}x{nn}"] = gemv_row(torch, kt_lib, stream_obj, kk, nn, 4, gg, 3)
