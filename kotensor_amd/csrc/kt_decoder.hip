@@ -32,18 +32,35 @@ namespace {
 constexpr int THREADS = 256;
 constexpr int KT = 64;        // keys per attention tile
 constexpr int MAX_SPLITS = 64;  // key splits of one (token, kv head); the merge holds one weight per lane
-constexpr int MAX_NACC = 4;   // (head, dim) pairs per thread: heads per kv head x head_dim <= 1024
+constexpr int MAX_NACC = 4;   // query floats per thread: heads per kv head x head_dim <= 1024
+constexpr int ACC_REGS = 8;   // per lane: query heads of its wave x dims of its lane (head_dim / 64 rounded up)
 constexpr int MAX_HD = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Sum and maximum over a wave without LDS round trips: inside each row of 16 lanes by DPP
+// exchanges (quad xor 1, quad xor 2, half-row mirror, row mirror: every lane of a row ends
+// with the same row total, the two operands of each add being the same pair), then the
+// four row totals read into scalars and combined in one fixed order, so every lane holds
+// the same bits. Needs every lane of the wave active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x141>(v);  // row_half_mirror
+    v += dpp_move<0x140>(v);  // row_mirror
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // ---- RMSNorm ---------------------------------------------------------------------
@@ -167,6 +184,11 @@ struct AttnArgs {
 // then the weighted values). With one split the workgroup writes the context; with
 // several the last split to finish merges every split's (sum of weighted values, max,
 // sum) and writes the context.
+// Wave w owns query heads w, w + 4, ...: for the scores lane l is key l of the tile (its
+// key row read from LDS 16 bytes at a time, the query row a broadcast), so the running
+// maximum and sum are wave reductions on registers; for the weighted values lane l holds
+// dims l, l + 64, ... and reads the wave's own row of exponentials back from LDS. The
+// tile is the only thing the waves share: one barrier after it lands, one before the next.
 // Every global load of a tile is issued before the first is used (unrolled, predicated
 // float4 loads into registers, then LDS), so a tile costs one memory round trip.
 // TF4: float4 per thread for a full tile (4, 8, 16 for head_dim up to 64, 128, 256).
@@ -189,11 +211,11 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     const int32_t g = blockIdx.x, s = blockIdx.y, t = blockIdx.z;
     const int32_t HD = a.head_dim, G = a.num_heads / a.num_kv_heads;
     const int32_t dim = a.num_heads * HD;
-    const int32_t KP = HD + 1;  // padded key row: lanes reading consecutive rows hit distinct banks
+    const int32_t KP = HD + 4;  // padded key row: 16-byte reads of consecutive rows hit distinct banks
     float* qs = smem;                  // [G][HD]
-    float* ks = qs + G * HD;           // [KT][HD + 1]
+    float* ks = qs + G * HD;           // [KT][HD + 4]
     float* vs = ks + KT * KP;          // [KT][HD]
-    float* sc = vs + KT * HD;          // [G][KT]
+    float* sc = vs + KT * HD;          // [G][KT] each wave's exponentials of its heads
     float* st = sc + G * KT;           // [G] x {m, l, alpha}
     float* kn_s = st + 3 * G;          // [HD] the new key after RoPE (the workgroup holding it), then one word
     const int32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -235,15 +257,17 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     // its own tile (its tile load may see the row before or after the append; the LDS copy
     // replaces it), so no fence or second read of the row is needed.
     const bool holder = a.rope && pos >= k_begin && pos < k_end;
-    if (tid < G) {
-        st[3 * tid] = -INFINITY;
-        st[3 * tid + 1] = 0.0f;
-    }
-    const int32_t pairs = G * HD;
-    const int32_t nacc = (pairs + THREADS - 1) / THREADS;
-    float acc[MAX_NACC];
+    constexpr int NW = THREADS / 64;
+    constexpr int DPL = (TF4 + 3) / 4;     // dims per lane: head_dim <= 64 DPL
+    constexpr int MAXH = ACC_REGS / DPL;   // query heads per wave
+    float acc[MAXH][DPL], mrun[MAXH], lrun[MAXH];
 #pragma unroll
-    for (int r = 0; r < MAX_NACC; ++r) acc[r] = 0.0f;
+    for (int h = 0; h < MAXH; ++h) {
+        mrun[h] = -INFINITY;
+        lrun[h] = 0.0f;
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) acc[h][dd] = 0.0f;
+    }
 
     if (a.rope) {
         // one decode token: the G query heads are rotated in LDS; the holder rotates the
@@ -289,11 +313,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             const int32_t e = tid + i * THREADS;
             if (e < n4) {
                 const int32_t j = (4 * e) / HD, d = (4 * e) % HD;
-                float* kd = ks + j * KP + d;
-                kd[0] = kr[i].x;
-                kd[1] = kr[i].y;
-                kd[2] = kr[i].z;
-                kd[3] = kr[i].w;
+                *reinterpret_cast<f4*>(ks + j * KP + d) = kr[i];
                 if constexpr (TOGETHER) reinterpret_cast<f4*>(vs)[e] = vr[i];
             }
         }
@@ -318,69 +338,73 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        // scores: pair (head i, key j)
-        for (int32_t e = tid; e < G * KT; e += THREADS) {
-            const int32_t i = e / KT, j = e % KT;
+#pragma unroll
+        for (int h = 0; h < MAXH; ++h) {
+            const int32_t hh = wave + h * NW;
+            if (hh >= G) break;
+            // score of key `lane` (four interleaved sums over the head's dims)
             float score = -INFINITY;
-            if (j < n) {
-                const float* qi = qs + i * HD;
-                const float* kj = ks + j * KP;
+            if (lane < n) {
+                const f4* qi = reinterpret_cast<const f4*>(qs + hh * HD);
+                const f4* kj = reinterpret_cast<const f4*>(ks + lane * KP);
                 float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll 4
-                for (int32_t d = 0; d < HD; d += 4) {
-                    s0 = fmaf(qi[d], kj[d], s0);
-                    s1 = fmaf(qi[d + 1], kj[d + 1], s1);
-                    s2 = fmaf(qi[d + 2], kj[d + 2], s2);
-                    s3 = fmaf(qi[d + 3], kj[d + 3], s3);
+                for (int32_t d4 = 0; d4 < HD / 4; ++d4) {
+                    const f4 qv4 = qi[d4], kv4 = kj[d4];
+                    s0 = fmaf(qv4.x, kv4.x, s0);
+                    s1 = fmaf(qv4.y, kv4.y, s1);
+                    s2 = fmaf(qv4.z, kv4.z, s2);
+                    s3 = fmaf(qv4.w, kv4.w, s3);
                 }
                 score = ((s0 + s1) + (s2 + s3)) * a.scale;
             }
-            sc[i * KT + j] = score;
-        }
-        __syncthreads();
-        // running max and sum per head: one wave per head, a lane per key
-        for (int32_t i = wave; i < G; i += THREADS / 64) {
-            const float v = sc[i * KT + lane];
-            const float m_old = st[3 * i];
-            const float m_new = fmaxf(m_old, wave_max(v));
-            const float e = lane < n ? expf(v - m_new) : 0.0f;
-            sc[i * KT + lane] = e;
-            const float sum = wave_sum(e);
-            if (lane == 0) {
-                const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-                st[3 * i] = m_new;
-                st[3 * i + 1] = st[3 * i + 1] * alpha + sum;
-                st[3 * i + 2] = alpha;
-            }
-        }
-        __syncthreads();
-        // weighted values: pair (head i, dim d), values from LDS
+            // running max and sum of the head
+            const float m_old = mrun[h];
+            const float m_new = fmaxf(m_old, wave_max_dpp(score));
+            const float ex = lane < n ? expf(score - m_new) : 0.0f;
+            const float sum = wave_sum_dpp(ex);
+            const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+            mrun[h] = m_new;
+            lrun[h] = lrun[h] * alpha + sum;
+            // weighted values: the wave's row of exponentials goes through LDS (a wave's
+            // LDS accesses complete in order; the wave barrier keeps the compiler from
+            // moving the reads above the write)
+            float* ep = sc + hh * KT;
+            ep[lane] = ex;
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int r = 0; r < MAX_NACC; ++r) {
-            const int32_t e = tid + r * THREADS;
-            if (r < nacc && e < pairs) {
-                const int32_t i = e / HD, d = e % HD;
-                float x = acc[r] * st[3 * i + 2];
-                const float* ep = sc + i * KT;
-                const float* vp = vs + d;
-#pragma unroll 8
-                for (int32_t j = 0; j < n; ++j) x = fmaf(ep[j], vp[j * HD], x);
-                acc[r] = x;
+            for (int dd = 0; dd < DPL; ++dd) {
+                const int32_t d = lane + 64 * dd;
+                if (d < HD) {
+                    float x = acc[h][dd] * alpha;
+                    const float* vp = vs + d;
+                    int32_t j = 0;
+#pragma unroll 2
+                    for (; j + 4 <= n; j += 4) {
+                        const f4 e4 = *reinterpret_cast<const f4*>(ep + j);
+                        x = fmaf(e4.x, vp[j * HD], x);
+                        x = fmaf(e4.y, vp[(j + 1) * HD], x);
+                        x = fmaf(e4.z, vp[(j + 2) * HD], x);
+                        x = fmaf(e4.w, vp[(j + 3) * HD], x);
+                    }
+                    for (; j < n; ++j) x = fmaf(ep[j], vp[j * HD], x);
+                    acc[h][dd] = x;
+                }
             }
+            __builtin_amdgcn_wave_barrier();
         }
         __syncthreads();
     }
 
-    // A workgroup whose key range is empty (a split past this token's keys) ran no tile,
-    // whose barriers order the running max and sum set above before the reads below.
-    if (k_begin >= k_end) __syncthreads();
     if (a.splits == 1) {
 #pragma unroll
-        for (int r = 0; r < MAX_NACC; ++r) {
-            const int32_t e = tid + r * THREADS;
-            if (r < nacc && e < pairs) {
-                const int32_t i = e / HD, d = e % HD;
-                a.context[static_cast<size_t>(t) * dim + (g * G + i) * HD + d] = acc[r] * (1.0f / st[3 * i + 1]);
+        for (int h = 0; h < MAXH; ++h) {
+            const int32_t hh = wave + h * NW;
+            if (hh >= G) break;
+#pragma unroll
+            for (int dd = 0; dd < DPL; ++dd) {
+                const int32_t d = lane + 64 * dd;
+                if (d < HD) a.context[static_cast<size_t>(t) * dim + (g * G + hh) * HD + d] = acc[h][dd] * (1.0f / lrun[h]);
             }
         }
         return;
@@ -393,16 +417,18 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     // on other workgroups; the merge order, and so the result, does not depend on timing.
     const size_t pbase = (static_cast<size_t>(t) * a.num_heads + g * G) * a.splits;  // (head g G, split 0)
 #pragma unroll
-    for (int r = 0; r < MAX_NACC; ++r) {
-        const int32_t e = tid + r * THREADS;
-        if (r < nacc && e < pairs) {
-            const int32_t i = e / HD, d = e % HD;
-            float* pp = a.partials + (pbase + static_cast<size_t>(i) * a.splits + s) * (HD + 2);
-            __hip_atomic_store(pp + d, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (d == 0) {
-                __hip_atomic_store(pp + HD, st[3 * i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(pp + HD + 1, st[3 * i + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
+    for (int h = 0; h < MAXH; ++h) {
+        const int32_t hh = wave + h * NW;
+        if (hh >= G) break;
+        float* pp = a.partials + (pbase + static_cast<size_t>(hh) * a.splits + s) * (HD + 2);
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) {
+            const int32_t d = lane + 64 * dd;
+            if (d < HD) __hip_atomic_store(pp + d, acc[h][dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (lane == 0) {
+            __hip_atomic_store(pp + HD, mrun[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(pp + HD + 1, lrun[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -412,7 +438,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     if (tid == 0) *last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (*last_s != static_cast<uint32_t>(a.splits - 1)) return;
-    const int32_t S = a.splits;
+    const int32_t S = a.splits, pairs = G * HD;
     float* ws = sc;  // [G][S] weights (S <= MAX_SPLITS <= KT)
     for (int32_t i = wave; i < G; i += THREADS / 64) {
         const float* pp = a.partials + (pbase + static_cast<size_t>(i) * S) * (HD + 2);
@@ -421,9 +447,9 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         const float ls = lane < S ? __hip_atomic_load(pp + lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_SYSTEM)
                                   : 0.0f;
-        const float m = wave_max(ms);
+        const float m = wave_max_dpp(ms);
         const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
-        const float l = wave_sum(w * ls);
+        const float l = wave_sum_dpp(w * ls);
         if (lane < S) ws[i * KT + lane] = w;
         if (lane == 0) st[3 * i + 1] = l;
     }
@@ -745,7 +771,7 @@ __global__ void record_token_kernel(const int32_t* token, const int32_t* positio
 constexpr int32_t ARGMAX_BLOCKS = 64;
 
 size_t attention_lds(int32_t G, int32_t HD) {
-    return sizeof(float) * (static_cast<size_t>(G) * HD + static_cast<size_t>(KT) * (HD + 1) +
+    return sizeof(float) * (static_cast<size_t>(G) * HD + static_cast<size_t>(KT) * (HD + 4) +
                             static_cast<size_t>(KT) * HD + static_cast<size_t>(G) * KT + 3 * static_cast<size_t>(G) +
                             static_cast<size_t>(HD) + 1);
 }
@@ -826,9 +852,9 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     const int32_t G = num_heads / num_kv_heads;
     if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > MAX_HD)
         return fail(KT_ERR_ARGUMENT, "head dimension %d: a multiple of 4 up to %d", head_dim, MAX_HD);
-    if (G * head_dim > MAX_NACC * THREADS)
-        return fail(KT_ERR_ARGUMENT, "%d query heads per key/value head of %d dims exceed %d", G, head_dim,
-                    MAX_NACC * THREADS);
+    if (G * head_dim > MAX_NACC * THREADS || ceil_div(G, THREADS / 64) * ceil_div(head_dim, 64) > ACC_REGS)
+        return fail(KT_ERR_ARGUMENT, "%d query heads per key/value head of %d dims: more than %d floats, or more than %d "
+                    "heads per wave", G, head_dim, MAX_NACC * THREADS, (THREADS / 64) * ACC_REGS / ceil_div(head_dim, 64));
     if (tokens < 0 || key_bound < tokens || key_bound > max_seq || layer < 0)
         return fail(KT_ERR_ARGUMENT, "key bound %d must cover the %d tokens and fit maxSequenceLength %d", key_bound,
                     tokens, max_seq);
