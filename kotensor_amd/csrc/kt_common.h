@@ -33,7 +33,10 @@ int32_t workspace(hipStream_t stream, size_t bytes, void** out);
 // The same workspace plus `count` uint32 counters that are zero on entry; a kernel
 // that takes them must leave every one at zero when it completes.
 int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters);
-constexpr size_t MAX_COUNTERS = (64 << 10) / sizeof(uint32_t);
+// The counter region holds 16384 words; the last 512 are the decode attention's RoPE
+// cache (ROPE_CACHE_WORD), which keeps its contents between calls.
+constexpr size_t MAX_COUNTERS = (64 << 10) / sizeof(uint32_t) - 512;
+constexpr size_t ROPE_CACHE_WORD = MAX_COUNTERS;
 // The counters plus `doubles` fp64 accumulators that are zero on entry; a kernel that
 // uses them leaves them at zero.
 int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs);

@@ -115,12 +115,19 @@ __global__ void __launch_bounds__(THREADS) rmsnorm_kernel(const float* __restric
 // RoPE.applyInPlace's rotation of pair (x1, x2) = (row[i], row[i + half]) at pos:
 // theta = pos * invFreq[i] in fp32, cos and sin in double rounded to float, no
 // contraction (the whole region is compiled with fp contract off).
-__device__ __forceinline__ void rope_rotate(float x1, float x2, int32_t pos, float inv_freq_i, float& y1, float& y2) {
+__device__ __forceinline__ void rope_cos_sin(int32_t pos, float inv_freq_i, float& c, float& s) {
     const float theta = static_cast<float>(pos) * inv_freq_i;
-    const float c = static_cast<float>(cos(static_cast<double>(theta)));
-    const float s = static_cast<float>(sin(static_cast<double>(theta)));
+    c = static_cast<float>(cos(static_cast<double>(theta)));
+    s = static_cast<float>(sin(static_cast<double>(theta)));
+}
+__device__ __forceinline__ void rope_apply(float x1, float x2, float c, float s, float& y1, float& y2) {
     y1 = x1 * c - x2 * s;
     y2 = x1 * s + x2 * c;
+}
+__device__ __forceinline__ void rope_rotate(float x1, float x2, int32_t pos, float inv_freq_i, float& y1, float& y2) {
+    float c, s;
+    rope_cos_sin(pos, inv_freq_i, c, s);
+    rope_apply(x1, x2, c, s, y1, y2);
 }
 __global__ void __launch_bounds__(THREADS) rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
                                                           const float* __restrict__ v, int32_t num_heads,
@@ -176,6 +183,10 @@ struct AttnArgs {
     // several splits: one counter per (token, kv head), zero on entry and on exit; the
     // split that takes it to splits - 1 merges all splits (no second kernel)
     uint32_t* counters;
+    // one decode token: per frequency i, words 4i .. 4i + 3 = (position + 1, inv_freq[i]'s
+    // bits, cos, sin) as layer 0's launch computed them; layer 0 writes them, later
+    // layers' launches use an entry whose position and frequency match (or null: none)
+    uint32_t* rope_cache;
 };
 
 // Workgroup (kv head g, key split s, token t): the G = num_heads / num_kv_heads query
@@ -231,6 +242,10 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     // of the tiles, so that the rotation below waits for them and not for the tiles.
     const int32_t half = HD >> 1;
     float ifr = 0.0f, kn1 = 0.0f, kn2 = 0.0f, vn1 = 0.0f, vn2 = 0.0f;
+    // layers after the first take cos and sin of their position from the cache layer 0's
+    // launch wrote (read past the caches: that launch wrote them through)
+    const bool cache_read = a.rope_cache && a.layer != 0;
+    uint32_t ce[4] = {0u, 0u, 0u, 0u};
     if (a.rope && tid < half) {
         const float* kn = a.k_new + static_cast<size_t>(g) * HD;
         const float* vn = a.v_new + static_cast<size_t>(g) * HD;
@@ -239,6 +254,11 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         kn2 = kn[tid + half];
         vn1 = vn[tid];
         vn2 = vn[tid + half];
+        if (cache_read) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                ce[w] = __hip_atomic_load(a.rope_cache + 4 * tid + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
     // The first tile's keys and values go out with q and the position, before anything
     // waits: a whole tile from k_begin (rows of the cache, k_begin < max_seq), so the
@@ -273,13 +293,31 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         // one decode token: the G query heads are rotated in LDS; the holder rotates the
         // new key into LDS and appends it and the value to the cache
         if (tid < q4) reinterpret_cast<float4*>(qs)[tid] = qv;
-        float* fs = vs;  // the frequencies, until the first tile lands in vs
-        if (tid < half) fs[tid] = ifr;
+        float* fc = vs;         // cos and sin of each frequency, until the first tile lands in vs
+        float* fsn = vs + half;
+        float cf = 0.0f, sf = 0.0f;
+        if (tid < half) {
+            if (cache_read && ce[0] == static_cast<uint32_t>(pos) + 1u && ce[1] == __builtin_bit_cast(uint32_t, ifr)) {
+                cf = __builtin_bit_cast(float, ce[2]);
+                sf = __builtin_bit_cast(float, ce[3]);
+            } else {
+                rope_cos_sin(pos, ifr, cf, sf);
+            }
+            fc[tid] = cf;
+            fsn[tid] = sf;
+            if (a.rope_cache && a.layer == 0 && g == 0 && s == 0) {
+                uint32_t* e = a.rope_cache + 4 * tid;
+                __hip_atomic_store(e, static_cast<uint32_t>(pos) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(e + 1, __builtin_bit_cast(uint32_t, ifr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(e + 2, __builtin_bit_cast(uint32_t, cf), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(e + 3, __builtin_bit_cast(uint32_t, sf), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
         __syncthreads();
         for (int32_t e = tid; e < G * half; e += THREADS) {
             const int32_t i = e % half, hh = e / half;
             float y1, y2;
-            rope_rotate(qs[hh * HD + i], qs[hh * HD + i + half], pos, fs[i], y1, y2);
+            rope_apply(qs[hh * HD + i], qs[hh * HD + i + half], fc[i], fsn[i], y1, y2);
             qs[hh * HD + i] = y1;
             qs[hh * HD + i + half] = y2;
         }
@@ -287,7 +325,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             float* ckw = const_cast<float*>(a.ck) + (base + pos) * HD;
             float* cvw = const_cast<float*>(a.cv) + (base + pos) * HD;
             float y1, y2;
-            rope_rotate(kn1, kn2, pos, ifr, y1, y2);
+            rope_apply(kn1, kn2, cf, sf, y1, y2);
             kn_s[tid] = y1;
             kn_s[tid + half] = y2;
             ckw[tid] = y1;
@@ -929,6 +967,9 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
             workspace_counters(st, bytes, static_cast<size_t>(tokens) * num_kv_heads, &ws, &a.counters);
         if (status) return status;
         a.partials = static_cast<float*>(ws);
+        // the RoPE cache sits in the same workspace (with one split the launch needs none
+        // and computes cos and sin itself)
+        if (a.rope) a.rope_cache = a.counters + ROPE_CACHE_WORD;
     }
     const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(a.splits), static_cast<uint32_t>(tokens));
     const size_t lds = attention_lds(G, head_dim);

@@ -60,8 +60,11 @@ thread_local const FixedWorkspace* t_fixed = nullptr;
 
 // Each workspace starts with a COUNTER_BYTES region of uint32 counters and a region of
 // fp64 accumulators, both zeroed when the allocation is made and left at zero by every
-// kernel that uses them; the general area follows.
+// kernel that uses them (the counter region's last words, from ROPE_CACHE_WORD, excepted:
+// the decode attention's RoPE cache, whose entries a zeroed word marks as empty); the
+// general area follows.
 constexpr size_t COUNTER_BYTES = 64 << 10;
+static_assert(ROPE_CACHE_WORD + 512 == COUNTER_BYTES / sizeof(uint32_t), "the RoPE cache ends the counter region");
 
 static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** out) {
     int device = 0;
@@ -130,7 +133,7 @@ int32_t workspace(hipStream_t stream, size_t bytes, void** out) {
 }
 
 int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void** general, uint32_t** counters) {
-    if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    if (count > MAX_COUNTERS) return fail(KT_ERR_SHAPE, "too many reduction counters");
     if (t_fixed) {
         double* d;
         return fixed_regions(*t_fixed, 0, bytes, counters, &d, general);
@@ -145,7 +148,7 @@ int32_t workspace_counters(hipStream_t stream, size_t bytes, size_t count, void*
 }
 
 int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs) {
-    if (count * sizeof(uint32_t) > COUNTER_BYTES) return fail(KT_ERR_SHAPE, "too many reduction counters");
+    if (count > MAX_COUNTERS) return fail(KT_ERR_SHAPE, "too many reduction counters");
     if (t_fixed) {
         void* g;
         return fixed_regions(*t_fixed, doubles, 0, counters, accs, &g);

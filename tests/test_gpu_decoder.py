@@ -184,6 +184,46 @@ def test_rope_attention_fused_equals_unfused(kt, oracle_lib):
             assert np.array_equal(a_, b_)
 
 
+@pytest.mark.parametrize("same_position", [True, False])
+def test_rope_attention_cos_sin_cache(kt, oracle_lib, same_position):
+    """Layer 0's fused launch leaves cos and sin of its position in the stream's cache;
+    a later layer's launch at that position and frequencies takes them from there (and at
+    another position computes them): either way the bits of kt_rope_kv + kt_attention."""
+    from kotensor_amd import _lib
+    rng = np.random.default_rng(22)
+    heads, kvh, hd, start, max_seq, layers = 32, 8, 64, 1100, 1200, 2
+    banner("rope cache", same_position)
+    inv = oracle_lib.rope_inv_freq(hd, 500000.0, None).astype(np.float32)
+    keys = np.zeros((layers, kvh, max_seq, hd), np.float32)
+    values = np.zeros_like(keys)
+    keys[:, :, :start + 1] = rng.standard_normal((layers, kvh, start + 1, hd))
+    values[:, :, :start + 1] = rng.standard_normal((layers, kvh, start + 1, hd))
+    qkv = [(rng.standard_normal((1, heads * hd)).astype(np.float32), rng.standard_normal((1, kvh * hd)).astype(np.float32),
+            rng.standard_normal((1, kvh * hd)).astype(np.float32)) for _ in range(layers)]
+    positions = [start, start] if same_position else [start - 1, start]
+    outs = []
+    for fused in (True, False):
+        dck, dcv, dinv = dev(kt, keys), dev(kt, values), dev(kt, inv)
+        got = []
+        for layer in range(layers):
+            q, k, v = qkv[layer]
+            dq, dk, dv = dev(kt, q), dev(kt, k), dev(kt, v)
+            pos = dev(kt, np.array([positions[layer]], np.int32))
+            ctx = kt.DeviceBuffer(q.nbytes)
+            if fused:
+                _lib.call("kt_rope_attention", dq.ptr, dk.ptr, dv.ptr, dinv.ptr, 1, pos.ptr, max_seq, dck.ptr,
+                          dcv.ptr, layer, max_seq, heads, kvh, hd, ctx.ptr, None)
+            else:
+                _lib.call("kt_rope_kv", dq.ptr, dk.ptr, dv.ptr, 1, heads, kvh, hd, dinv.ptr, pos.ptr, dck.ptr,
+                          dcv.ptr, layer, max_seq, None)
+                _lib.call("kt_attention", dq.ptr, 1, pos.ptr, max_seq, dck.ptr, dcv.ptr, layer, max_seq, heads, kvh,
+                          hd, ctx.ptr, None)
+            got.append(ctx.download(np.float32))
+        outs.append(got + [dck.download(np.float32), dcv.download(np.float32)])
+    for a_, b_ in zip(outs[0], outs[1]):
+        assert np.array_equal(a_, b_)
+
+
 def test_silu_mul_and_add(kt, oracle_lib):
     from kotensor_amd import _lib
     rng = np.random.default_rng(4)
