@@ -171,7 +171,7 @@ struct AttnArgs {
     const float* ck;
     const float* cv;
     float* context;          // [tokens x num_heads * head_dim]
-    float* partials;         // [tokens][num_heads][splits][head_dim + 2] when splits > 1
+    uint64_t* partials;      // [tokens][num_heads][splits][head_dim + 2] tagged words when splits > 1, zero between launches
     int32_t layer, max_seq, num_heads, num_kv_heads, head_dim, splits, span;
     float scale;
     // one decode token with RoPE and the cache append inside: q, k_new, v_new are the
@@ -180,9 +180,6 @@ struct AttnArgs {
     const float* v_new;
     const float* inv_freq;
     int32_t rope;
-    // several splits: one counter per (token, kv head), zero on entry and on exit; the
-    // split that takes it to splits - 1 merges all splits (no second kernel)
-    uint32_t* counters;
     // one decode token: per frequency i, words 4i .. 4i + 3 = (position + 1, inv_freq[i]'s
     // bits, cos, sin) as layer 0's launch computed them; layer 0 writes them, later
     // layers' launches use an entry whose position and frequency match (or null: none)
@@ -213,6 +210,35 @@ __device__ __forceinline__ void load_tile(f4 (&r)[TF4], const float* src, int32_
     for (int i = 0; i < TF4; ++i) {
         const int32_t e = min(static_cast<int32_t>(threadIdx.x) + i * THREADS, n4 - 1);
         r[i] = reinterpret_cast<const f4*>(src)[e];
+    }
+}
+
+// A partial of the split merge: the float's bits, the tag 1 above them.
+__device__ __forceinline__ uint64_t tagged(float v) {
+    return (uint64_t{1} << 32) | __builtin_bit_cast(uint32_t, v);
+}
+constexpr int MERGE_BATCH = 24;            // other splits' values a merging lane loads at once (over its dims)
+constexpr uint32_t MERGE_SPIN_LIMIT = 1u << 20;  // polls per merging lane, over all its waits
+__device__ __forceinline__ bool is_tagged(uint64_t w) { return (w >> 32) == 1u; }
+// Words w[u] = *(base + min(u, count - 1) * stride) (each already loaded once) until
+// every tag of u < count is 1: each round reloads all N words, unconditionally (a load
+// under a branch is waited for at the branch's end), so a round costs one memory round
+// trip whatever the count; a word stays tagged once it is. The rounds of a lane share
+// one budget, so that a fault shows as a wrong result within about a second rather than
+// as a hang.
+template <int N>
+__device__ __forceinline__ void await_tagged(uint64_t (&w)[N], uint64_t* base, int32_t stride, int32_t count,
+                                             uint32_t& budget) {
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int u = 0; u < N; ++u) all = all && (u >= count || is_tagged(w[u]));
+        if (all || budget == 0) return;
+        --budget;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < N; ++u)
+            w[u] = __hip_atomic_load(base + min(u, count - 1) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -381,18 +407,31 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             const int32_t hh = wave + h * NW;
             if (hh >= G) break;
             // score of key `lane` (four interleaved sums over the head's dims)
+            // (eight 16-byte pairs in flight per group: indices past the row repeat its last
+            // float4 and add nothing)
             float score = -INFINITY;
             if (lane < n) {
                 const f4* qi = reinterpret_cast<const f4*>(qs + hh * HD);
                 const f4* kj = reinterpret_cast<const f4*>(ks + lane * KP);
+                const int32_t HD4 = HD >> 2;
                 float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-#pragma unroll 4
-                for (int32_t d4 = 0; d4 < HD / 4; ++d4) {
-                    const f4 qv4 = qi[d4], kv4 = kj[d4];
-                    s0 = fmaf(qv4.x, kv4.x, s0);
-                    s1 = fmaf(qv4.y, kv4.y, s1);
-                    s2 = fmaf(qv4.z, kv4.z, s2);
-                    s3 = fmaf(qv4.w, kv4.w, s3);
+                for (int32_t g0 = 0; g0 < HD4; g0 += 8) {
+                    f4 qv4[8], kv4[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int32_t d4 = min(g0 + u, HD4 - 1);
+                        qv4[u] = qi[d4];
+                        kv4[u] = kj[d4];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        if (g0 + u < HD4) {
+                            s0 = fmaf(qv4[u].x, kv4[u].x, s0);
+                            s1 = fmaf(qv4[u].y, kv4[u].y, s1);
+                            s2 = fmaf(qv4[u].z, kv4[u].z, s2);
+                            s3 = fmaf(qv4[u].w, kv4[u].w, s3);
+                        }
+                    }
                 }
                 score = ((s0 + s1) + (s2 + s3)) * a.scale;
             }
@@ -417,7 +456,21 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
                     float x = acc[h][dd] * alpha;
                     const float* vp = vs + d;
                     int32_t j = 0;
-#pragma unroll 2
+                    for (; j + 16 <= n; j += 16) {  // 20 reads in flight, then the 16 in order
+                        f4 e4[4];
+                        float vv[16];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) e4[u] = *reinterpret_cast<const f4*>(ep + j + 4 * u);
+#pragma unroll
+                        for (int u = 0; u < 16; ++u) vv[u] = vp[(j + u) * HD];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            x = fmaf(e4[u].x, vv[4 * u], x);
+                            x = fmaf(e4[u].y, vv[4 * u + 1], x);
+                            x = fmaf(e4[u].z, vv[4 * u + 2], x);
+                            x = fmaf(e4[u].w, vv[4 * u + 3], x);
+                        }
+                    }
                     for (; j + 4 <= n; j += 4) {
                         const f4 e4 = *reinterpret_cast<const f4*>(ep + j);
                         x = fmaf(e4.x, vp[j * HD], x);
@@ -447,61 +500,98 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         }
         return;
     }
-    // Several splits: every split stores (sum of weighted values, max, sum) per head with
-    // write-through (system-scope) stores and waits for them; the workgroup that then
-    // takes the (token, kv head) counter to splits - 1 is the last one: it reads every
-    // split's values back past the caches and merges them in split order, as
-    // attn_combine_kernel does, then returns the counter to zero. No fence and no waiting
-    // on other workgroups; the merge order, and so the result, does not depend on timing.
-    const size_t pbase = (static_cast<size_t>(t) * a.num_heads + g * G) * a.splits;  // (head g G, split 0)
+    // Several splits: each split but the last writes its (sum of weighted values, max,
+    // sum) per head as 64-bit words, the float's bits with the tag 1 above them, written
+    // through to memory, and is done (no wait for the stores, no counter). The last split
+    // of the (token, kv head), dispatched after the others, merges: its loads of their
+    // words past the caches are the wait (a word is ready when its tag is 1, and the
+    // 64-bit store is single-copy atomic), it merges every split in split order with its
+    // own from registers, as attn_combine_kernel does, and returns each word it read to
+    // zero, so the region (the workspace's zeroed area) is zero again when the launch
+    // ends. It waits only for workgroups dispatched before it; the waits are bounded all
+    // the same. (In decode the last split usually holds no keys, the key bound being the
+    // cache's capacity, so it is free to wait from the start.)
+    const int32_t S = a.splits;
+    const size_t pbase = (static_cast<size_t>(t) * a.num_heads + g * G) * S;  // (head g G, split 0)
+    if (s != S - 1) {
+#pragma unroll
+        for (int h = 0; h < MAXH; ++h) {
+            const int32_t hh = wave + h * NW;
+            if (hh >= G) break;
+            uint64_t* pp = a.partials + (pbase + static_cast<size_t>(hh) * S + s) * (HD + 2);
+#pragma unroll
+            for (int dd = 0; dd < DPL; ++dd) {
+                const int32_t d = lane + 64 * dd;
+                if (d < HD) __hip_atomic_store(pp + d, tagged(acc[h][dd]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            if (lane == 0) {
+                __hip_atomic_store(pp + HD, tagged(mrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(pp + HD + 1, tagged(lrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        return;
+    }
+    float* ws = sc;  // [G][KT] each wave's weights of its heads (S <= MAX_SPLITS <= KT)
+    const int32_t others = S - 1;
+    constexpr int MB = MERGE_BATCH / DPL;
+    uint32_t budget = MERGE_SPIN_LIMIT;
 #pragma unroll
     for (int h = 0; h < MAXH; ++h) {
         const int32_t hh = wave + h * NW;
         if (hh >= G) break;
-        float* pp = a.partials + (pbase + static_cast<size_t>(hh) * a.splits + s) * (HD + 2);
-#pragma unroll
-        for (int dd = 0; dd < DPL; ++dd) {
-            const int32_t d = lane + 64 * dd;
-            if (d < HD) __hip_atomic_store(pp + d, acc[h][dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        uint64_t* pp = a.partials + (pbase + static_cast<size_t>(hh) * S) * (HD + 2);  // split 0 of head hh
+        // split `lane`'s max and sum (this workgroup's own in lane S - 1): the poll; the
+        // values are loaded once these have arrived (a split writes its max and sum after
+        // its values, so they are mostly there by then; loading them with the poll made
+        // every round several times slower)
+        uint64_t ml[2] = {0, 0};  // split `lane`'s max and sum words (adjacent)
+        if (lane < others) {
+            ml[0] = __hip_atomic_load(pp + lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            ml[1] = __hip_atomic_load(pp + lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
-        if (lane == 0) {
-            __hip_atomic_store(pp + HD, mrun[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(pp + HD + 1, lrun[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        float ms = -INFINITY, ls = 0.0f;
+        if (lane < others) {
+            await_tagged(ml, pp + lane * (HD + 2) + HD, 1, 2, budget);
+            ms = __builtin_bit_cast(float, static_cast<uint32_t>(ml[0]));
+            ls = __builtin_bit_cast(float, static_cast<uint32_t>(ml[1]));
+            __hip_atomic_store(pp + lane * (HD + 2) + HD, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(pp + lane * (HD + 2) + HD + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else if (lane == others) {
+            ms = mrun[h];
+            ls = lrun[h];
         }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // every thread's stores are complete before the count
-    uint32_t* counter = a.counters + static_cast<size_t>(t) * a.num_kv_heads + g;
-    uint32_t* last_s = reinterpret_cast<uint32_t*>(kn_s + HD);  // in the dynamic LDS: no static LDS
-    if (tid == 0) *last_s = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (*last_s != static_cast<uint32_t>(a.splits - 1)) return;
-    const int32_t S = a.splits, pairs = G * HD;
-    float* ws = sc;  // [G][S] weights (S <= MAX_SPLITS <= KT)
-    for (int32_t i = wave; i < G; i += THREADS / 64) {
-        const float* pp = a.partials + (pbase + static_cast<size_t>(i) * S) * (HD + 2);
-        const float ms = lane < S ? __hip_atomic_load(pp + lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
-                                  : -INFINITY;
-        const float ls = lane < S ? __hip_atomic_load(pp + lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_SYSTEM)
-                                  : 0.0f;
         const float m = wave_max_dpp(ms);
         const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
         const float l = wave_sum_dpp(w * ls);
-        if (lane < S) ws[i * KT + lane] = w;
-        if (lane == 0) st[3 * i + 1] = l;
+        ws[hh * KT + lane] = w;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) {
+            const int32_t d = lane + 64 * dd;
+            if (d >= HD) continue;
+            float x = 0.0f;
+            // batches of MB splits, each batch's words out together before its first wait
+            for (int32_t c0 = 0; c0 < others; c0 += MB) {
+                uint64_t cw[MB];
+#pragma unroll
+                for (int u = 0; u < MB; ++u)
+                    cw[u] = __hip_atomic_load(pp + min(c0 + u, others - 1) * (HD + 2) + d, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_SYSTEM);
+                await_tagged(cw, pp + c0 * (HD + 2) + d, HD + 2, others - c0, budget);
+#pragma unroll
+                for (int u = 0; u < MB; ++u) {
+                    if (c0 + u < others) {
+                        x = fmaf(__builtin_bit_cast(float, static_cast<uint32_t>(cw[u])), ws[hh * KT + c0 + u], x);
+                        __hip_atomic_store(pp + (c0 + u) * (HD + 2) + d, uint64_t{0}, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_SYSTEM);
+                    }
+                }
+            }
+            x = fmaf(acc[h][dd], ws[hh * KT + others], x);
+            a.context[static_cast<size_t>(t) * dim + (g * G + hh) * HD + d] = x * (1.0f / l);
+        }
+        __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
-    for (int32_t e = tid; e < pairs; e += THREADS) {
-        const int32_t i = e / HD, d = e % HD;
-        const float* pp = a.partials + (pbase + static_cast<size_t>(i) * S) * (HD + 2);
-        float x = 0.0f;
-        for (int32_t sp = 0; sp < S; ++sp)
-            x = fmaf(__hip_atomic_load(pp + sp * (HD + 2) + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM),
-                     ws[i * KT + sp], x);
-        a.context[static_cast<size_t>(t) * dim + (g * G + i) * HD + d] = x * (1.0f / st[3 * i + 1]);
-    }
-    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- prefill attention: blocked over queries, fp32 MFMA ---------------------------------
@@ -960,16 +1050,18 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     a.rope = k_new != nullptr ? 1 : 0;
     a.span = ceil_div(tiles, splits) * KT;
     a.splits = ceil_div(key_bound, a.span);
-    if (a.splits > 1) {  // tokens * num_kv_heads < 2 * CUs counters
-        void* ws = nullptr;
-        const size_t bytes = static_cast<size_t>(tokens) * num_heads * a.splits * (head_dim + 2) * sizeof(float);
-        const int32_t status =
-            workspace_counters(st, bytes, static_cast<size_t>(tokens) * num_kv_heads, &ws, &a.counters);
+    if (a.splits > 1) {
+        // the tagged partials live in the workspace's zeroed region (zero on entry, zero
+        // again when the launch ends)
+        uint32_t* counters = nullptr;
+        double* zeroed = nullptr;
+        const size_t words = static_cast<size_t>(tokens) * num_heads * a.splits * (head_dim + 2);
+        const int32_t status = workspace_accumulators(st, 0, words, &counters, &zeroed);
         if (status) return status;
-        a.partials = static_cast<float*>(ws);
+        a.partials = reinterpret_cast<uint64_t*>(zeroed);
         // the RoPE cache sits in the same workspace (with one split the launch needs none
         // and computes cos and sin itself)
-        if (a.rope) a.rope_cache = a.counters + ROPE_CACHE_WORD;
+        if (a.rope) a.rope_cache = counters + ROPE_CACHE_WORD;
     }
     const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(a.splits), static_cast<uint32_t>(tokens));
     const size_t lds = attention_lds(G, head_dim);
