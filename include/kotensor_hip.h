@@ -266,7 +266,11 @@ int32_t kt_rope_kv(float* q, float* k, const float* v, int32_t tokens, int32_t n
  * softmax(q . k_j / sqrt(head_dim)) over cached positions j <= that position, of the
  * kv head that serves its query head (GQA), times v, into context [tokens x
  * num_heads*head_dim]. key_bound >= *position + tokens bounds the keys (it sizes the
- * launch; a captured decode step passes max_seq). q and the caches are 16-byte aligned. */
+ * launch; a captured decode step passes max_seq). q and the caches are 16-byte aligned.
+ * For fewer than 16 tokens the keys are split over workgroups whose partials meet in the
+ * stream's workspace (its zeroed region, zero again when the launch ends); as for every
+ * call that takes the workspace, a graph is recorded after one eager call of the same
+ * shapes on the stream. */
 int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, int32_t key_bound,
                      const float* cache_k, const float* cache_v, int32_t layer, int32_t max_seq,
                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float* context,
@@ -277,7 +281,9 @@ int32_t kt_attention(const float* q, int32_t tokens, const int32_t* position, in
  * the append happen inside the attention launch: q and k are left as they were (the
  * rotated q lives in LDS) and the cache row is written by the workgroup that reads it.
  * For more tokens q and k are rotated in place, as kt_rope_kv does. Saves the RoPE
- * launch of a decode step. */
+ * launch of a decode step. A one-token call for layer 0 also leaves cos and sin of its
+ * position in the stream's workspace, and one-token calls for other layers use them when
+ * position and frequencies match (otherwise they compute them: the same bits either way). */
 int32_t kt_rope_attention(float* q, float* k, const float* v, const float* inv_freq, int32_t tokens,
                           const int32_t* position, int32_t key_bound, float* cache_k, float* cache_v,
                           int32_t layer, int32_t max_seq, int32_t num_heads, int32_t num_kv_heads,

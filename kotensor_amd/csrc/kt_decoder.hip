@@ -190,8 +190,8 @@ struct AttnArgs {
 // heads of kv head g over keys [s * span, min((s + 1) * span, position + t + 1)), in
 // tiles of 64 keys with a running maximum and sum (scores, then exp(score - max),
 // then the weighted values). With one split the workgroup writes the context; with
-// several the last split to finish merges every split's (sum of weighted values, max,
-// sum) and writes the context.
+// several the last split in dispatch order merges every split's (sum of weighted values,
+// max, sum) and writes the context.
 // Wave w owns query heads w, w + 4, ...: for the scores lane l is key l of the tile (its
 // key row read from LDS 16 bytes at a time, the query row a broadcast), so the running
 // maximum and sum are wave reductions on registers; for the weighted values lane l holds
