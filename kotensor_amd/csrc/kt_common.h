@@ -40,6 +40,10 @@ constexpr size_t ROPE_CACHE_WORD = MAX_COUNTERS;
 // The counters plus `doubles` fp64 accumulators that are zero on entry; a kernel that
 // uses them leaves them at zero.
 int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles, uint32_t** counters, double** accs);
+// The counters, `doubles` zeroed fp64 words (left at zero by the kernel, as above) and
+// `bytes` of general area, all of one stream's workspace.
+int32_t workspace_regions(hipStream_t stream, size_t doubles, size_t bytes, uint32_t** counters, double** accs,
+                          void** general);
 
 // Validated view of a kt_qweight, with the derived layout numbers.
 struct WeightView {

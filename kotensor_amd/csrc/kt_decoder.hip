@@ -171,7 +171,10 @@ struct AttnArgs {
     const float* ck;
     const float* cv;
     float* context;          // [tokens x num_heads * head_dim]
-    uint64_t* partials;      // [tokens][num_heads][splits][head_dim + 2] tagged words when splits > 1, zero between launches
+    // several splits: each split's sum of weighted values [tokens][num_heads][splits][head_dim]
+    // and its (max, sum) as tagged words [tokens][num_heads][splits][2] (zero between launches)
+    float* partials;
+    uint64_t* stats;
     int32_t layer, max_seq, num_heads, num_kv_heads, head_dim, splits, span;
     float scale;
     // one decode token with RoPE and the cache append inside: q, k_new, v_new are the
@@ -217,7 +220,8 @@ __device__ __forceinline__ void load_tile(f4 (&r)[TF4], const float* src, int32_
 __device__ __forceinline__ uint64_t tagged(float v) {
     return (uint64_t{1} << 32) | __builtin_bit_cast(uint32_t, v);
 }
-constexpr int MERGE_BATCH = 24;            // other splits' values a merging lane loads at once (over its dims)
+constexpr int MERGE_BATCH = 8;             // 16-byte loads of other splits' values a merging lane has in flight
+constexpr int COHERENT_AUX = 1 | 16;       // buffer-load cache bits sc0 sc1: read past the caches
 constexpr uint32_t MERGE_SPIN_LIMIT = 1u << 20;  // polls per merging lane, over all its waits
 __device__ __forceinline__ bool is_tagged(uint64_t w) { return (w >> 32) == 1u; }
 // Words w[u] = *(base + min(u, count - 1) * stride) (each already loaded once) until
@@ -500,17 +504,19 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         }
         return;
     }
-    // Several splits: each split but the last writes its (sum of weighted values, max,
-    // sum) per head as 64-bit words, the float's bits with the tag 1 above them, written
-    // through to memory, and is done (no wait for the stores, no counter). The last split
-    // of the (token, kv head), dispatched after the others, merges: its loads of their
-    // words past the caches are the wait (a word is ready when its tag is 1, and the
-    // 64-bit store is single-copy atomic), it merges every split in split order with its
-    // own from registers, as attn_combine_kernel does, and returns each word it read to
-    // zero, so the region (the workspace's zeroed area) is zero again when the launch
-    // ends. It waits only for workgroups dispatched before it; the waits are bounded all
-    // the same. (In decode the last split usually holds no keys, the key bound being the
-    // cache's capacity, so it is free to wait from the start.)
+    // Several splits: each split but the last writes its sums of weighted values through
+    // to memory, waits until they are there, then writes its (max, sum) as 64-bit words,
+    // the float's bits under the tag 1, and is done (no counter). The last split of the
+    // (token, kv head), dispatched after the others, merges: it polls the (max, sum) words
+    // past the caches (a word is ready when its tag is 1; the 64-bit store is single-copy
+    // atomic), whereupon that split's values are in memory, and reads those 16 bytes at a
+    // time, several splits per load instruction. It merges every split with its own from
+    // registers, as attn_combine_kernel does (each lane a strided share of the splits, the
+    // shares added in a fixed order), and returns the (max, sum) words to zero, so their
+    // region (the workspace's zeroed area) is zero again when the launch ends. It waits
+    // only for workgroups dispatched before it; the polls are bounded all the same. (In
+    // decode the last split usually holds no keys, the key bound being the cache's
+    // capacity, so it is free to wait from the start.)
     const int32_t S = a.splits;
     const size_t pbase = (static_cast<size_t>(t) * a.num_heads + g * G) * S;  // (head g G, split 0)
     if (s != S - 1) {
@@ -518,44 +524,50 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         for (int h = 0; h < MAXH; ++h) {
             const int32_t hh = wave + h * NW;
             if (hh >= G) break;
-            uint64_t* pp = a.partials + (pbase + static_cast<size_t>(hh) * S + s) * (HD + 2);
+            float* pv = a.partials + (pbase + static_cast<size_t>(hh) * S + s) * HD;
 #pragma unroll
             for (int dd = 0; dd < DPL; ++dd) {
                 const int32_t d = lane + 64 * dd;
-                if (d < HD) __hip_atomic_store(pp + d, tagged(acc[h][dd]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (d < HD) __hip_atomic_store(pv + d, acc[h][dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
+            // this wave's values are in memory before its (max, sum) words go out
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_waitcnt(0);
             if (lane == 0) {
-                __hip_atomic_store(pp + HD, tagged(mrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(pp + HD + 1, tagged(lrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                uint64_t* ps = a.stats + (pbase + static_cast<size_t>(hh) * S + s) * 2;
+                __hip_atomic_store(ps, tagged(mrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(ps + 1, tagged(lrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
         return;
     }
     float* ws = sc;  // [G][KT] each wave's weights of its heads (S <= MAX_SPLITS <= KT)
+    float* red = ks + wave * 256;  // this wave's shares of the merged values, [phases][HD]
     const int32_t others = S - 1;
-    constexpr int MB = MERGE_BATCH / DPL;
     uint32_t budget = MERGE_SPIN_LIMIT;
+    // values: lane = (phase q, float4 r of the row); a load instruction covers `phases`
+    // splits' rows (HD / 4 lanes each)
+    const int32_t quads = HD >> 2, phases = 64 / quads;
+    const int32_t q = lane / quads, r = lane - q * quads;
+    const size_t vbytes = static_cast<size_t>(gridDim.z) * a.num_heads * S * HD * sizeof(float);
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(a.partials, 0, static_cast<int32_t>(vbytes),
+                                                                        0x00020000);
 #pragma unroll
     for (int h = 0; h < MAXH; ++h) {
         const int32_t hh = wave + h * NW;
         if (hh >= G) break;
-        uint64_t* pp = a.partials + (pbase + static_cast<size_t>(hh) * S) * (HD + 2);  // split 0 of head hh
-        // split `lane`'s max and sum (this workgroup's own in lane S - 1): the poll; the
-        // values are loaded once these have arrived (a split writes its max and sum after
-        // its values, so they are mostly there by then; loading them with the poll made
-        // every round several times slower)
-        uint64_t ml[2] = {0, 0};  // split `lane`'s max and sum words (adjacent)
-        if (lane < others) {
-            ml[0] = __hip_atomic_load(pp + lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            ml[1] = __hip_atomic_load(pp + lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
+        // split `lane`'s max and sum (this workgroup's own in lane S - 1)
+        uint64_t* ps = a.stats + (pbase + static_cast<size_t>(hh) * S) * 2;  // split 0 of head hh
+        uint64_t ml[2] = {0, 0};
         float ms = -INFINITY, ls = 0.0f;
         if (lane < others) {
-            await_tagged(ml, pp + lane * (HD + 2) + HD, 1, 2, budget);
+            ml[0] = __hip_atomic_load(ps + 2 * lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            ml[1] = __hip_atomic_load(ps + 2 * lane + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            await_tagged(ml, ps + 2 * lane, 1, 2, budget);
             ms = __builtin_bit_cast(float, static_cast<uint32_t>(ml[0]));
             ls = __builtin_bit_cast(float, static_cast<uint32_t>(ml[1]));
-            __hip_atomic_store(pp + lane * (HD + 2) + HD, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(pp + lane * (HD + 2) + HD + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(ps + 2 * lane, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(ps + 2 * lane + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         } else if (lane == others) {
             ms = mrun[h];
             ls = lrun[h];
@@ -564,29 +576,42 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
         const float l = wave_sum_dpp(w * ls);
         ws[hh * KT + lane] = w;
+        // every split's (max, sum) seen: their values are in memory; no read below may
+        // move above the polls
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        // this lane's share: splits q, q + phases, ... of float4 r, in that order
+        f4 x4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        const size_t row0 = (pbase + static_cast<size_t>(hh) * S) * HD;  // split 0's row of head hh
+        for (int32_t b0 = 0; b0 < others; b0 += MERGE_BATCH * phases) {
+            f4 vv[MERGE_BATCH];
+#pragma unroll
+            for (int u = 0; u < MERGE_BATCH; ++u) {
+                const int32_t sp = min(b0 + q + u * phases, others - 1);
+                vv[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   pr, static_cast<int32_t>((row0 + static_cast<size_t>(sp) * HD + 4 * r) * 4),
+                                                   0, COHERENT_AUX));
+            }
+#pragma unroll
+            for (int u = 0; u < MERGE_BATCH; ++u) {
+                const int32_t sp = b0 + q + u * phases;
+                if (q < phases && sp < others) {
+                    const float wsp = ws[hh * KT + sp];
+                    x4.x = fmaf(vv[u].x, wsp, x4.x);
+                    x4.y = fmaf(vv[u].y, wsp, x4.y);
+                    x4.z = fmaf(vv[u].z, wsp, x4.z);
+                    x4.w = fmaf(vv[u].w, wsp, x4.w);
+                }
+            }
+        }
+        if (q < phases) *reinterpret_cast<f4*>(red + q * HD + 4 * r) = x4;
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int dd = 0; dd < DPL; ++dd) {
             const int32_t d = lane + 64 * dd;
             if (d >= HD) continue;
             float x = 0.0f;
-            // batches of MB splits, each batch's words out together before its first wait
-            for (int32_t c0 = 0; c0 < others; c0 += MB) {
-                uint64_t cw[MB];
-#pragma unroll
-                for (int u = 0; u < MB; ++u)
-                    cw[u] = __hip_atomic_load(pp + min(c0 + u, others - 1) * (HD + 2) + d, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_SYSTEM);
-                await_tagged(cw, pp + c0 * (HD + 2) + d, HD + 2, others - c0, budget);
-#pragma unroll
-                for (int u = 0; u < MB; ++u) {
-                    if (c0 + u < others) {
-                        x = fmaf(__builtin_bit_cast(float, static_cast<uint32_t>(cw[u])), ws[hh * KT + c0 + u], x);
-                        __hip_atomic_store(pp + (c0 + u) * (HD + 2) + d, uint64_t{0}, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_SYSTEM);
-                    }
-                }
-            }
+            for (int32_t p = 0; p < phases; ++p) x += red[p * HD + d];
             x = fmaf(acc[h][dd], ws[hh * KT + others], x);
             a.context[static_cast<size_t>(t) * dim + (g * G + hh) * HD + d] = x * (1.0f / l);
         }
@@ -978,8 +1003,8 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
         return fail(KT_ERR_ARGUMENT, "numHeads %d must be a multiple of numKeyValueHeads %d", num_heads, num_kv_heads);
     const int32_t G = num_heads / num_kv_heads;
-    if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > MAX_HD)
-        return fail(KT_ERR_ARGUMENT, "head dimension %d: a multiple of 4 up to %d", head_dim, MAX_HD);
+    if (head_dim < 8 || head_dim % 4 != 0 || head_dim > MAX_HD)
+        return fail(KT_ERR_ARGUMENT, "head dimension %d: a multiple of 4 from 8 to %d", head_dim, MAX_HD);
     if (G * head_dim > MAX_NACC * THREADS || ceil_div(G, THREADS / 64) * ceil_div(head_dim, 64) > ACC_REGS)
         return fail(KT_ERR_ARGUMENT, "%d query heads per key/value head of %d dims: more than %d floats, or more than %d "
                     "heads per wave", G, head_dim, MAX_NACC * THREADS, (THREADS / 64) * ACC_REGS / ceil_div(head_dim, 64));
@@ -1051,14 +1076,17 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
     a.span = ceil_div(tiles, splits) * KT;
     a.splits = ceil_div(key_bound, a.span);
     if (a.splits > 1) {
-        // the tagged partials live in the workspace's zeroed region (zero on entry, zero
-        // again when the launch ends)
+        // the tagged (max, sum) words live in the workspace's zeroed region (zero on entry,
+        // zero again when the launch ends), the values in its general area
         uint32_t* counters = nullptr;
         double* zeroed = nullptr;
-        const size_t words = static_cast<size_t>(tokens) * num_heads * a.splits * (head_dim + 2);
-        const int32_t status = workspace_accumulators(st, 0, words, &counters, &zeroed);
+        void* general = nullptr;
+        const size_t rows = static_cast<size_t>(tokens) * num_heads * a.splits;
+        const int32_t status = workspace_regions(st, 2 * rows, rows * head_dim * sizeof(float), &counters, &zeroed,
+                                                 &general);
         if (status) return status;
-        a.partials = reinterpret_cast<uint64_t*>(zeroed);
+        a.stats = reinterpret_cast<uint64_t*>(zeroed);
+        a.partials = static_cast<float*>(general);
         // the RoPE cache sits in the same workspace (with one split the launch needs none
         // and computes cos and sin itself)
         if (a.rope) a.rope_cache = counters + ROPE_CACHE_WORD;

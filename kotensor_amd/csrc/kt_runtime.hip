@@ -162,6 +162,19 @@ int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles,
     return KT_OK;
 }
 
+int32_t workspace_regions(hipStream_t stream, size_t doubles, size_t bytes, uint32_t** counters, double** accs,
+                          void** general) {
+    if (t_fixed) return fixed_regions(*t_fixed, doubles, bytes, counters, accs, general);
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Block* b = nullptr;
+    int32_t status = ensure(stream, doubles * sizeof(double), bytes, &b);
+    if (status) return status;
+    *counters = static_cast<uint32_t*>(b->ptr);
+    *accs = reinterpret_cast<double*>(static_cast<char*>(b->ptr) + COUNTER_BYTES);
+    *general = static_cast<char*>(b->ptr) + COUNTER_BYTES + b->zbytes;
+    return KT_OK;
+}
+
 int32_t cu_count() {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return 256;
