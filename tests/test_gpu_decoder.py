@@ -124,9 +124,11 @@ def test_attention(kt, oracle_lib, heads, kvh, hd):
     # one token per workgroup (with key splits) up to 15 tokens; 16 and more take the
     # query-blocked MFMA kernel for head_dim 64 and 128 (several blocks and key tiles,
     # ragged last block, a prompt continuing a cache)
-    # (2999 keys: more key splits than the merging lane loads in one batch)
+    # (2999 keys: more key splits than the merging lane loads in one batch; 10 tokens over
+    # 200 keys: several tokens, each with key splits merged)
     for start, tokens, max_seq in [(0, 1, 8), (63, 1, 64), (64, 1, 200), (1151, 1, 1152), (2999, 1, 3000),
-                                   (20, 70, 100), (0, 33, 40), (3, 15, 20), (0, 16, 16), (130, 300, 431)]:
+                                   (100, 10, 200), (20, 70, 100), (0, 33, 40), (3, 15, 20), (0, 16, 16),
+                                   (130, 300, 431)]:
         banner("attention", heads, kvh, hd, start, tokens, max_seq)
         n = layers * kvh * max_seq * hd
         keys = np.zeros(n, np.float32)
