@@ -216,7 +216,7 @@ __device__ __forceinline__ void load_tile(f4 (&r)[TF4], const float* src, int32_
     }
 }
 
-// A partial of the split merge: the float's bits, the tag 1 above them.
+// A split's max or sum word for the merge: the float's bits, the tag 1 above them.
 __device__ __forceinline__ uint64_t tagged(float v) {
     return (uint64_t{1} << 32) | __builtin_bit_cast(uint32_t, v);
 }
