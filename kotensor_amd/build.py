@@ -29,6 +29,10 @@ COMMON = [
     "-fPIC",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 16 dwords of a kernel's arguments arrive in scalar registers with the
+    # wave (the code keeps a fallback that loads them where the firmware does not), so
+    # the first dependent loads do not wait for an argument fetch
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unknown-pragmas",
