@@ -10,7 +10,9 @@
  *   - Entry points are stateless and reentrant. Compute entry points enqueue work on
  *     the given stream and return before it finishes, except kt_quantize (see there).
  *     The library keeps one internal workspace per (device, stream); calls that
- *     share a stream are ordered by it, calls on different streams never share one.
+ *     share a stream are ordered by it, and calls on different streams never share
+ *     one, with one exception: every kt_qmatmul_noalloc call on a device uses that
+ *     device's single fixed array (see there), so such calls must not overlap.
  *   - Return value: KT_OK (0) on success; a negative KT_ERR_* for an argument error
  *     (the reference raises IllegalArgumentException for the same cases) except
  *     KT_ERR_STATE; a positive value is a HIP runtime error code (the reference has no
@@ -18,7 +20,9 @@
  *     IllegalStateException. kt_last_error() returns the message of the last failure
  *     on the calling thread.
  *
- * Weight layout is the reference's, consumed without repacking:
+ * Weight layout is the reference's; every entry point reads it as it lies, and the
+ * optional device-native copy (kt_qweight.packed, written by kt_qweight_pack from these
+ * bytes) only adds a faster read path for some products:
  *   qdata  [rows x bytes_per_row], row-major. 8-bit: bytes_per_row = columns, each
  *          byte a two's-complement int8. 4-bit: bytes_per_row = (columns + columns%2)/2
  *          and split-half packing: column c < bytes_per_row is the LOW nibble of byte c,
@@ -105,7 +109,21 @@ int32_t kt_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int32_t kt_memset(void* dst, int32_t value, size_t bytes, void* stream);
 int32_t kt_stream_create(void** stream);
 int32_t kt_stream_destroy(void* stream);
+/* kt_stream_sync and kt_memcpy_d2h (which synchronizes) also report a bounded wait
+ * inside a kernel that gave up since the stream's last synchronization (the chained
+ * stages of kt_qmatmul_chain, the split merge of kt_attention / kt_rope_attention: a
+ * fault, never a schedule): KT_ERR_STATE, returned once, after the stream's internal
+ * counters are cleared; the outputs of the calls since the last synchronization are
+ * then not valid. No counterpart in the reference (its kernels do not wait on each
+ * other). */
 int32_t kt_stream_sync(void* stream);
+/* Test hook for that report, no counterpart in the reference: spin_limit replaces the
+ * polls a wait makes before it gives up (0 = the kernels' own limits) and withhold = 1
+ * makes the producers of those waits (a chained stage's partition flags, an attention
+ * split's tagged sums) withhold their signals, so that every wait gives up while every
+ * kernel still exits normally. Process-wide; read when a call is enqueued (recorded
+ * graphs keep the values they were recorded with). */
+int32_t kt_debug_wait_limits(uint32_t spin_limit, int32_t withhold);
 /* HIP graphs: kernels enqueued on `stream` between kt_graph_begin and kt_graph_end are
  * recorded (not run) and instantiated into *graph, which kt_graph_launch replays on a
  * stream. The replacement for a tracing compiler on the decode path: one decode step

@@ -118,6 +118,7 @@ SIGNATURES = {
     "kt_stream_create": [ctypes.POINTER(_P)],
     "kt_stream_destroy": [_P],
     "kt_stream_sync": [_P],
+    "kt_debug_wait_limits": [ctypes.c_uint32, _I],
     "kt_qweight_layout": [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
     "kt_qweight_check": [ctypes.POINTER(_QWeight)],
     "kt_qweight_packed_bytes": [_I, _I, _I, ctypes.POINTER(ctypes.c_int64)],

@@ -45,6 +45,22 @@ int32_t workspace_accumulators(hipStream_t stream, size_t count, size_t doubles,
 int32_t workspace_regions(hipStream_t stream, size_t doubles, size_t bytes, uint32_t** counters, double** accs,
                           void** general);
 
+// Give-up reports of bounded waits. A kernel whose wait runs out of polls stores a
+// nonzero code into its stream's fault word (pinned host memory mapped into the device;
+// nullptr for calls on a caller's fixed workspace, which run no waiting kernel), goes on,
+// and the stream's next kt_stream_sync / kt_memcpy_d2h returns KT_ERR_STATE after
+// re-zeroing the stream's counters (a late producer may have left words behind).
+constexpr int32_t FAULT_CHAIN_WAIT = 1;  // a chained stage's wait for the previous stage's flags
+constexpr int32_t FAULT_MERGE_WAIT = 2;  // the decode attention's wait for other splits' sums
+int32_t stream_fault_word(hipStream_t stream, int32_t** dev_word);
+// The poll budget of the waits (0 = each kernel's own default) and whether producers
+// withhold their signals, both set by kt_debug_wait_limits for tests of the give-up path.
+struct WaitLimits {
+    uint32_t spin_limit;
+    int32_t withhold;
+};
+WaitLimits wait_limits();
+
 // Validated view of a kt_qweight, with the derived layout numbers.
 struct WeightView {
     const uint8_t* q;

@@ -187,6 +187,11 @@ struct AttnArgs {
     // bits, cos, sin) as layer 0's launch computed them; layer 0 writes them, later
     // layers' launches use an entry whose position and frequency match (or null: none)
     uint32_t* rope_cache;
+    // the merge's bounded wait: the stream's fault word (set when it gives up), its poll
+    // budget, and the test hook that makes the other splits withhold their tagged words
+    int32_t* fault;
+    uint32_t spin_limit;
+    int32_t withhold;
 };
 
 // Workgroup (kv head g, key split s, token t): the G = num_heads / num_kv_heads query
@@ -230,14 +235,16 @@ __device__ __forceinline__ bool is_tagged(uint64_t w) { return (w >> 32) == 1u; 
 // trip whatever the count; a word stays tagged once it is. The rounds of a lane share
 // one budget, so that a fault shows as a wrong result within about a second rather than
 // as a hang.
+// Returns whether every word is tagged (false: the budget ran out first).
 template <int N>
-__device__ __forceinline__ void await_tagged(uint64_t (&w)[N], uint64_t* base, int32_t stride, int32_t count,
+__device__ __forceinline__ bool await_tagged(uint64_t (&w)[N], uint64_t* base, int32_t stride, int32_t count,
                                              uint32_t& budget) {
     for (;;) {
         bool all = true;
 #pragma unroll
         for (int u = 0; u < N; ++u) all = all && (u >= count || is_tagged(w[u]));
-        if (all || budget == 0) return;
+        if (all) return true;
+        if (budget == 0) return false;
         --budget;
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
@@ -533,7 +540,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
             // this wave's values are in memory before its (max, sum) words go out
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_s_waitcnt(0);
-            if (lane == 0) {
+            if (lane == 0 && !a.withhold) {
                 uint64_t* ps = a.stats + (pbase + static_cast<size_t>(hh) * S + s) * 2;
                 __hip_atomic_store(ps, tagged(mrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(ps + 1, tagged(lrun[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -544,7 +551,7 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
     float* ws = sc;  // [G][KT] each wave's weights of its heads (S <= MAX_SPLITS <= KT)
     float* red = ks + wave * 256;  // this wave's shares of the merged values, [phases][HD]
     const int32_t others = S - 1;
-    uint32_t budget = MERGE_SPIN_LIMIT;
+    uint32_t budget = a.spin_limit;
     // values: lane = (phase q, float4 r of the row); a load instruction covers `phases`
     // splits' rows (HD / 4 lanes each)
     const int32_t quads = HD >> 2, phases = 64 / quads;
@@ -563,7 +570,8 @@ __global__ void __launch_bounds__(THREADS) attention_kernel(AttnArgs a) {
         if (lane < others) {
             ml[0] = __hip_atomic_load(ps + 2 * lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             ml[1] = __hip_atomic_load(ps + 2 * lane + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            await_tagged(ml, ps + 2 * lane, 1, 2, budget);
+            if (!await_tagged(ml, ps + 2 * lane, 1, 2, budget) && a.fault)
+                __hip_atomic_store(a.fault, FAULT_MERGE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             ms = __builtin_bit_cast(float, static_cast<uint32_t>(ml[0]));
             ls = __builtin_bit_cast(float, static_cast<uint32_t>(ml[1]));
             __hip_atomic_store(ps + 2 * lane, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1090,6 +1098,10 @@ static int32_t attention_launch(const float* q, int32_t tokens, const int32_t* p
         // the RoPE cache sits in the same workspace (with one split the launch needs none
         // and computes cos and sin itself)
         if (a.rope) a.rope_cache = counters + ROPE_CACHE_WORD;
+        if (const int32_t fs = stream_fault_word(st, &a.fault)) return fs;
+        const WaitLimits limits = wait_limits();
+        a.spin_limit = limits.spin_limit ? limits.spin_limit : MERGE_SPIN_LIMIT;
+        a.withhold = limits.withhold;
     }
     const dim3 grid(static_cast<uint32_t>(num_kv_heads), static_cast<uint32_t>(a.splits), static_cast<uint32_t>(tokens));
     const size_t lds = attention_lds(G, head_dim);

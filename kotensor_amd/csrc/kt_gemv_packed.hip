@@ -192,6 +192,9 @@ constexpr int CHAIN_BASE = 8192;  // the chain's words start here in the stream'
 constexpr uint32_t CHAIN_SPIN_LIMIT = 1u << 22;  // polls before a wait gives up (a fault, not a schedule)
 
 struct ChainLink {
+    int32_t* fault;         // the stream's fault word (or null): set when the wait gives up
+    uint32_t spin_limit;    // polls before the wait gives up
+    int32_t withhold;       // test hook: never raise the partition flags
     uint32_t* wait_flags;   // the previous stage's partition flags (null: the first stage)
     uint32_t* lower_flags;  // stage s - 2's flags, lowered by the stage's first workgroup (or null)
     uint32_t* part_count;   // this workgroup's partition counter
@@ -207,31 +210,51 @@ __device__ __forceinline__ void lower_chain_flags(uint32_t* flags, uint32_t part
         __hip_atomic_store(flags + p * CHAIN_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Ordering. What one stage hands the next (its output row) is written with system-scope
+// stores, which write through the caches; chain_signal makes every wave wait until its
+// own stores are complete (s_waitcnt 0, behind a release fence that keeps the compiler
+// from sinking a store past it) before the workgroup barrier, so the partition counter
+// is incremented, and the flag raised, only after every output store of the partition
+// is in memory. The waiter's flag loads are system-scope (past the caches); its input
+// loads are issued only after the flags' values were seen (the loop's exit depends on
+// them, then a barrier and an acquire fence keep the compiler from hoisting a load),
+// and those loads read past the caches too, so they see the stored row.
 __device__ __forceinline__ void chain_wait(const ChainLink& link) {
     if (!link.wait_flags) return;
     if (threadIdx.x < 64) {  // wave 0: lane p reads partition p's flag
         const uint32_t ln = threadIdx.x;
         uint32_t spins = 0;
+        bool gave_up = false;
         while (true) {
             const uint32_t v = ln < link.wait_parts ? __hip_atomic_load(link.wait_flags + ln * CHAIN_STRIDE,
                                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
                                                     : 1u;
-            if (__all(v != 0u) || ++spins >= CHAIN_SPIN_LIMIT) break;
+            if (__all(v != 0u)) break;
+            if (++spins >= link.spin_limit) {
+                gave_up = true;
+                break;
+            }
             __builtin_amdgcn_s_sleep(2);
         }
+        if (gave_up && threadIdx.x == 0 && link.fault)
+            __hip_atomic_store(link.fault, FAULT_CHAIN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (threadIdx.x == 0 && link.lower_flags) lower_chain_flags(link.lower_flags, link.lower_parts);
     }
     __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 __device__ __forceinline__ void chain_signal(const ChainLink& link) {
-    __syncthreads();  // every wave's write-through output stores are complete
+    // this wave's write-through output stores are complete before the workgroup counts in
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (threadIdx.x != 0) return;
     if (__hip_atomic_fetch_add(link.part_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.part_size - 1)
         return;
     __hip_atomic_store(link.part_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     if (link.part_flag) {
-        __hip_atomic_store(link.part_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (!link.withhold) __hip_atomic_store(link.part_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         return;
     }
     if (__hip_atomic_fetch_add(link.stage_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != link.parts - 1)
@@ -777,6 +800,9 @@ struct ChainArgs {
     int32_t begin[MAX_STAGES + 1];  // first workgroup of each stage, then the launch's total
     int32_t stages;
     uint32_t* counters;  // the stream's counters; the chain's words from CHAIN_BASE
+    int32_t* fault;      // the stream's fault word
+    uint32_t spin_limit;
+    int32_t withhold;
     ChainStage st[MAX_STAGES];
 };
 
@@ -795,6 +821,9 @@ __global__ void __launch_bounds__(64 * W) gemv_chain_kernel(ChainArgs c) {
     const int32_t n = c.begin[s + 1] - c.begin[s], part = local % CHAIN_PARTS;
     const bool last = s + 1 == c.stages;
     ChainLink link;
+    link.fault = c.fault;
+    link.spin_limit = c.spin_limit;
+    link.withhold = c.withhold;
     link.wait_flags = s > 0 ? words(s - 1) + CHAIN_PARTS * CHAIN_STRIDE : nullptr;
     link.wait_parts = s > 0 ? parts(s - 1) : 0u;
     link.lower_flags = s > 1 && local == 0 ? words(s - 2) + CHAIN_PARTS * CHAIN_STRIDE : nullptr;
@@ -904,6 +933,10 @@ int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st) {
     const int32_t status =
         workspace_counters(st, 0, CHAIN_BASE + static_cast<size_t>(n) * CHAIN_WORDS, &general, &c.counters);
     if (status) return status;
+    if (const int32_t fs = stream_fault_word(st, &c.fault)) return fs;
+    const WaitLimits limits = wait_limits();
+    c.spin_limit = limits.spin_limit ? limits.spin_limit : CHAIN_SPIN_LIMIT;
+    c.withhold = limits.withhold;
     const dim3 grid(static_cast<uint32_t>(total));
     if (bits == 4)
         gemv_chain_kernel<4, true><<<grid, dim3(64 * W), lds, st>>>(c);

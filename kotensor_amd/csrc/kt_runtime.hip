@@ -36,6 +36,7 @@ struct Block {
     size_t bytes = 0;       // whole allocation
     size_t zbytes = 0;      // the zeroed accumulator region after the counters
     bool captured = false;  // handed to a kernel recorded into a graph
+    int32_t fault = -1;     // the stream's slot of the fault words, once a kernel took it
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Block> g_ws;
@@ -88,7 +89,9 @@ static int32_t ensure(hipStream_t stream, size_t zbytes, size_t bytes, Block** o
             KT_HIP(hipStreamSynchronize(stream));
             if (b.captured) g_retired.push_back(b.ptr);  // a graph may still address it
             else KT_HIP(hipFree(b.ptr));
+            const int32_t fault = b.fault;
             b = Block{};
+            b.fault = fault;
         }
         KT_HIP(hipMalloc(&b.ptr, want));
         KT_HIP(hipMemsetAsync(b.ptr, 0, COUNTER_BYTES + zcap, stream));
@@ -186,6 +189,78 @@ int32_t cu_count() {
         cus = 256;
     g_cus[device] = cus;
     return cus;
+}
+
+// ---- fault words of bounded waits ----------------------------------------------------
+// One pinned host array mapped into every device; a stream takes the next slot the first
+// time a waiting kernel is launched on it and keeps it (slots are not reused: a graph
+// recorded on a stream keeps the address after the stream is gone; past FAULT_SLOTS
+// streams, slots are shared, so a report may name a neighbouring stream too).
+constexpr int32_t FAULT_SLOTS = 4096;
+static int32_t* g_fault_host = nullptr;
+static int32_t* g_fault_dev = nullptr;
+static int32_t g_fault_next = 0;
+
+static WaitLimits g_wait_limits{0u, 0};
+
+WaitLimits wait_limits() { return g_wait_limits; }
+
+int32_t stream_fault_word(hipStream_t stream, int32_t** dev_word) {
+    *dev_word = nullptr;
+    if (t_fixed) return KT_OK;  // the fixed workspace's calls run no waiting kernel
+    int device = 0;
+    KT_HIP(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if (!g_fault_host) {
+        void* h = nullptr;
+        KT_HIP(hipHostMalloc(&h, FAULT_SLOTS * sizeof(int32_t), hipHostMallocPortable | hipHostMallocMapped));
+        memset(h, 0, FAULT_SLOTS * sizeof(int32_t));
+        void* d = nullptr;
+        const hipError_t err = hipHostGetDevicePointer(&d, h, 0);
+        if (err != hipSuccess) {
+            (void)hipHostFree(h);
+            return hip_fail(err, "fault words: hipHostGetDevicePointer");
+        }
+        g_fault_host = static_cast<int32_t*>(h);
+        g_fault_dev = static_cast<int32_t*>(d);
+    }
+    Block& b = g_ws[std::make_pair(device, stream)];
+    if (b.fault < 0) b.fault = g_fault_next++ % FAULT_SLOTS;
+    *dev_word = g_fault_dev + b.fault;
+    return KT_OK;
+}
+
+// After a synchronization of `stream`: a give-up reported by a kernel on it is returned
+// as KT_ERR_STATE, once, and the stream's counters and zeroed words are cleared, since
+// a producer that arrived after its waiter gave up may have left flags or tagged words
+// set that the next launch would take as its own.
+static int32_t check_fault(hipStream_t stream) {
+    int device = 0;
+    KT_HIP(hipGetDevice(&device));
+    int32_t code = 0;
+    void* ptr = nullptr;
+    size_t clear = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        auto it = g_ws.find(std::make_pair(device, stream));
+        if (it == g_ws.end() || it->second.fault < 0 || !g_fault_host) return KT_OK;
+        int32_t* word = g_fault_host + it->second.fault;
+        code = __atomic_load_n(word, __ATOMIC_ACQUIRE);
+        if (code == 0) return KT_OK;
+        __atomic_store_n(word, 0, __ATOMIC_RELEASE);
+        ptr = it->second.ptr;
+        clear = COUNTER_BYTES + it->second.zbytes;
+    }
+    if (ptr) {
+        KT_HIP(hipMemsetAsync(ptr, 0, clear, stream));
+        KT_HIP(hipStreamSynchronize(stream));
+    }
+    return fail(KT_ERR_STATE,
+                "a kernel's bounded wait gave up (code %d: %s); outputs of the calls on this stream since its last "
+                "synchronization are not valid",
+                code, code == FAULT_CHAIN_WAIT ? "a chained stage's input never arrived"
+                      : code == FAULT_MERGE_WAIT ? "an attention split's sums never arrived"
+                                                 : "unknown wait");
 }
 
 // ---- kt_qmatmul_noalloc's workspace -----------------------------------------------
@@ -343,7 +418,10 @@ int32_t kt_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
 }
 
 int32_t kt_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
-    return copy(dst, src, bytes, hipMemcpyDeviceToHost, stream);
+    const int32_t st = copy(dst, src, bytes, hipMemcpyDeviceToHost, stream);
+    if (st) return st;
+    if (bytes == 0) KT_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return check_fault(static_cast<hipStream_t>(stream));
 }
 
 int32_t kt_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
@@ -387,6 +465,12 @@ int32_t kt_stream_destroy(void* stream) {
 
 int32_t kt_stream_sync(void* stream) {
     KT_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return check_fault(static_cast<hipStream_t>(stream));
+}
+
+int32_t kt_debug_wait_limits(uint32_t spin_limit, int32_t withhold) {
+    if (withhold != 0 && withhold != 1) return fail(KT_ERR_ARGUMENT, "withhold must be 0 or 1, got %d", withhold);
+    g_wait_limits = WaitLimits{spin_limit, withhold};
     return KT_OK;
 }
 

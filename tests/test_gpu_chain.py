@@ -127,6 +127,8 @@ CASES = [  # dim, hidden, kv, bits, g, qkv bias, head
     (2048, 8192, 512, 4, 64, False, 0),  # Llama-3.2-1B
     (2048, 8192, 512, 8, 32, False, 0),
     (896, 4864, 128, 4, 64, True, 151936),  # Qwen2-0.5B, the last layer with the head
+    (896, 4864, 128, 4, 32, True, 151936),  # the same at the group size of 32
+    (896, 4864, 128, 8, 32, True, 151936),
     (4096, 14336, 1024, 4, 64, False, 0),  # Llama-3-8B
 ]
 
@@ -184,3 +186,34 @@ def test_chain_without_the_copy_and_argument_checks(kt, oracle_lib):
     steps[1].count = 3  # the SwiGLU pair takes two weights
     with pytest.raises(kt.IllegalArgumentException):
         _lib.call("kt_qmatmul_chain", steps, 4, None)
+
+
+def test_a_wait_that_gives_up_is_reported(kt, oracle_lib):
+    """A chained stage whose input never arrives (the test hook makes every stage withhold
+    its partition flags) gives up after a small poll budget; every kernel still exits,
+    the stream's next synchronization raises IllegalStateException once, and the
+    stream's counters are clear again: the next chain gives the separate calls' bits."""
+    from kotensor_amd import _lib
+    layer = Layer(kt, oracle_lib, 896, 4864, 128, 4, 64, 10)
+    layer.reset()
+    _separate(kt, layer)
+    want = layer.results()
+    banner("chain give-up")
+    layer.reset()
+    steps, keep = _struct(kt, layer)
+    _lib.call("kt_debug_wait_limits", 64, 1)
+    try:
+        _lib.call("kt_qmatmul_chain", steps, len(steps), None)
+    finally:
+        _lib.call("kt_debug_wait_limits", 0, 0)
+    with pytest.raises(kt.IllegalStateException, match="gave up"):
+        kt.synchronize()
+    kt.synchronize()  # reported once
+    with pytest.raises(kt.IllegalArgumentException):
+        _lib.call("kt_debug_wait_limits", 0, 2)
+    layer.reset()
+    steps, keep = _struct(kt, layer)
+    _lib.call("kt_qmatmul_chain", steps, len(steps), None)
+    got = layer.results()
+    del keep
+    assert all(same_bits(got[k], want[k]) for k in want)

@@ -19,8 +19,9 @@ only, and the logits agree to a normwise 1e-4 (the reference's own PrefillTest b
 1e-4 absolute). Prompts of three or more rows go through the prefill GEMM, whose fp16
 operands (x with a per-row power-of-two scale, deq(W) with the group scale) hold each
 product to about 2^-12, inside the 2e-3 per-matmul criterion; through the layers of a
-model that leaves the logits within a normwise 1e-2 of the oracle, and those comparisons
-use that bound. Runs that take the same kernels (chunkings of three or more rows,
+model that leaves the logits within a normwise 1e-2 of the oracle on the small test
+models (weights ~N(0, 0.3), measured up to 4e-3), and those comparisons use that bound;
+the full-size 1B decoder has its own, FULL_1B_TOL = 5e-3 (measured 2.6e-3). Runs that take the same kernels (chunkings of three or more rows,
 graph and eager decoding) are compared tightly.
 """
 
@@ -147,6 +148,39 @@ def test_attention(kt, oracle_lib, heads, kvh, hd):
             got = out.download(np.float32).reshape(q.shape)
             want = oracle_lib.attend(q, start, keys, values, layer, heads, kvh, hd, max_seq)
             np.testing.assert_allclose(got, want, rtol=0, atol=5e-6 * max(1.0, np.abs(want).max()))
+
+
+def test_attention_merge_that_gives_up_is_reported(kt, oracle_lib):
+    """The decode attention's merge waits for the other key splits' tagged sums; when the
+    test hook makes them withhold those words, the wait gives up after a small budget,
+    the kernel still exits, the stream's next synchronization raises
+    IllegalStateException once, and the next launch meets the oracle again (its zeroed
+    words were cleared)."""
+    from kotensor_amd import _lib
+    heads, kvh, hd, start, max_seq, layer = 32, 8, 64, 1151, 1152, 0
+    rng = np.random.default_rng(31)
+    n = kvh * max_seq * hd
+    keys = rng.standard_normal(n).astype(np.float32)
+    values = rng.standard_normal(n).astype(np.float32)
+    q = rng.standard_normal((1, heads * hd)).astype(np.float32)
+    out = kt.DeviceBuffer(q.nbytes)
+    pos = dev(kt, np.array([start], np.int32))
+    dq, dk, dv = dev(kt, q), dev(kt, keys), dev(kt, values)
+    banner("attention give-up")
+    _lib.call("kt_debug_wait_limits", 16, 1)
+    try:
+        _lib.call("kt_attention", dq.ptr, 1, pos.ptr, max_seq, dk.ptr, dv.ptr, layer, max_seq, heads, kvh, hd,
+                  out.ptr, None)
+    finally:
+        _lib.call("kt_debug_wait_limits", 0, 0)
+    with pytest.raises(kt.IllegalStateException, match="gave up"):
+        kt.synchronize()
+    kt.synchronize()
+    _lib.call("kt_attention", dq.ptr, 1, pos.ptr, max_seq, dk.ptr, dv.ptr, layer, max_seq, heads, kvh, hd, out.ptr,
+              None)
+    got = out.download(np.float32).reshape(q.shape)
+    want = oracle_lib.attend(q, start, keys, values, layer, heads, kvh, hd, max_seq)
+    np.testing.assert_allclose(got, want, rtol=0, atol=5e-6 * max(1.0, np.abs(want).max()))
 
 
 def test_rope_attention_fused_equals_unfused(kt, oracle_lib):
@@ -627,22 +661,30 @@ def test_llama_1b_shape_consistency(kt):
     assert a == model.generate(prompt[:64], 16)
 
 
+# The 1B decoder's own bound: every prefill projection holds each product to about 2^-12
+# (normwise ~3.3e-4 per matmul against the oracle, measured); through 16 layers of seven
+# projections, attention and the norms the logits were measured at 2.6e-3 (prefill) and
+# 1.5e-3 to 1.7e-3 (decode steps reading the prefill's cache).
+FULL_1B_TOL = 5e-3
+
+
 @pytest.mark.timeout(600)
 def test_llama_1b_full_size_against_the_oracle(kt):
     """The 1B INT4 decoder at its configured size (16 layers, 2048, 32/8 heads, SwiGLU
     8192, vocab 32000, RMSNorm eps 1e-5, RoPE theta 5e5, weights ~N(0, 0.02) INT4 g64): the
-    logits of a 1024-token random-id prefill and of 8 teacher-forced decode steps after it
-    against the oracle's RefTransformer on the same quantized weights (dense mode: the
+    logits of a 1024-token random-id prefill and of 32 teacher-forced decode steps after
+    it against the oracle's RefTransformer on the same quantized weights (dense mode: the
     dequantized weights through BLAS and float64 attention, which the CPU tests hold to
-    the restated loops within 1e-5). Bound: the prefill GEMM's, normwise 1e-2 (every
-    prefill projection rounds x to fp16; the decode steps read the cache that prefill
-    wrote). The greedy tokens agree wherever the oracle's top two logits are apart."""
+    the restated loops within 1e-5), normwise within FULL_1B_TOL. The greedy tokens agree
+    wherever the oracle's top two logits are apart, and the graph-replayed greedy
+    generation from the same prompt produces the oracle's greedy tokens up to the first
+    near-tie."""
     import time
     model = kt.Transformer(32000, 2048, 16, 32, 8192, 8, norm_eps=1e-5, rope_theta=500000.0,
                            quantization=kt.Quantization.INT4, seed=1)
     rng = np.random.default_rng(24)
     prompt = rng.integers(0, 32000, 1024).tolist()
-    steps = 8
+    steps = 32
     banner("1b full: device prefill")
     cache, buffers = model.new_cache(1024 + steps), model.new_inference_buffers(1024 + steps)
     got = model.prefill(prompt, cache, buffers).logits_numpy()
@@ -655,16 +697,31 @@ def test_llama_1b_full_size_against_the_oracle(kt):
     want = ref.prefill(prompt, rc)
     err = normwise_rel(got, want)
     banner(f"1b full: prefill logits normwise {err:.2e} ({time.time() - t0:.1f} s)")
-    assert err <= tolerance(1024)
-    assert normwise_rel(cache.keys_numpy(), rc.keys) <= tolerance(1024)
+    assert err <= FULL_1B_TOL
+    assert normwise_rel(cache.keys_numpy(), rc.keys) <= FULL_1B_TOL
+    oracle_tokens, tie_at = [], None
     for step in range(steps):
         token = oracle_argmax_or_near_tie(want, got)
+        if tie_at is None and near_tie(want):
+            tie_at = step
+        oracle_tokens.append(token)
         got = model.decode(token, cache, buffers).logits_numpy()
         want = ref.decode(token, rc)
         err = normwise_rel(got, want)
         banner(f"1b full: decode step {step} token {token} normwise {err:.2e}")
-        assert err <= tolerance(1024)
+        assert err <= FULL_1B_TOL
     assert cache.length == rc.length == 1024 + steps
+    banner("1b full: graph-replayed greedy generation")
+    generated = model.generate(prompt, steps)[len(prompt):]
+    agree = steps if tie_at is None else tie_at
+    print(f"  graph tokens equal the oracle's for the first {agree} steps", flush=True)
+    assert generated[:agree] == oracle_tokens[:agree]
+
+
+def near_tie(want: np.ndarray) -> bool:
+    """Whether the oracle's top two logits are within the comparison's reach."""
+    top = np.sort(want.ravel())[-2:]
+    return bool(top[1] - top[0] <= 1e-2 * np.abs(want).max())
 
 
 def oracle_argmax_or_near_tie(want: np.ndarray, got: np.ndarray) -> int:

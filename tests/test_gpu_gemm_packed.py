@@ -1,7 +1,8 @@
 """The prefill GEMM on the column-run copy (gemm_packed_kernel in kt_gemm.hip).
 
 A weight with its column-run copy (kt_qweight_pack) and a group size that is a multiple of
-32 takes this kernel for M >= 3 (MatMul.multiplyQuantized's M > 1 branch,
+32 takes this kernel for M >= 17 (smaller M go to the one-row and few-row kernels;
+MatMul.multiplyQuantized's M > 1 branch,
 MatMul.kt:479-485 -> computeQuantizedTile :830-881). Its operands are the fp16 values the
 other prefill GEMM uses (a scaled per row by a power of two, (q - zero) * scale rounded
 once), so it meets the oracle to the same normwise 2e-3 (measured near 3e-4), on every
@@ -55,7 +56,7 @@ LLAMA1B = [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]
 
 
 @pytest.mark.parametrize("k,n", LLAMA1B)
-@pytest.mark.parametrize("m", [3, 17, 128, 512])
+@pytest.mark.parametrize("m", [17, 64, 128, 512])
 @pytest.mark.parametrize("bits,g", [(8, 32), (4, 32), (8, 128), (4, 64)])
 def test_packed_gemm_matches_the_oracle(kt, oracle_lib, m, k, n, bits, g):
     rng = np.random.default_rng(m + k + n + bits + g)
@@ -63,6 +64,21 @@ def test_packed_gemm_matches_the_oracle(kt, oracle_lib, m, k, n, bits, g):
     q = _weights(oracle_lib, k, n, bits, g, 3)
     qt, got = _check(kt, oracle_lib, q, x, "llama1b")
     assert same_bits(got, gpu_matmul(kt, x, qt, m))  # repeat: same bits
+
+
+LLAMA8B = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
+
+
+@pytest.mark.parametrize("k,n", LLAMA8B)
+@pytest.mark.parametrize("m", [64, 512])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_packed_gemm_llama8b_shapes(kt, oracle_lib, m, k, n, bits):
+    """The Llama-3-8B projection shapes at the prefill row counts the bench times (g64,
+    the reference's default group), every row of every tile against the oracle."""
+    rng = np.random.default_rng(m + k + n + bits)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    q = _weights(oracle_lib, k, n, bits, 64, 11)
+    _check(kt, oracle_lib, q, x, "llama8b")
 
 
 def test_packed_gemm_large_shapes(kt, oracle_lib):
