@@ -104,7 +104,7 @@ class Weight:
     def pack(self, torch, kt_lib, stream):
         """Adds the column-run copy (kt_qweight_pack) that the one-row kernel streams."""
         nbytes = ctypes.c_int64()
-        kt_lib.call("kt_qweight_packed_bytes", self.k, self.n, self.bits, ctypes.byref(nbytes))
+        kt_lib.call("kt_qweight_packed_bytes", self.k, self.n, self.bits, self.g, ctypes.byref(nbytes))
         self.p = torch.empty(nbytes.value, dtype=torch.uint8, device="cuda")
         self._bind(kt_lib)
         kt_lib.call("kt_qweight_pack", ctypes.byref(self.struct), self.p.data_ptr(), stream)

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KT_ABI_VERSION 2
+#define KT_ABI_VERSION 3
 
 /* Status codes. */
 #define KT_OK 0
@@ -155,13 +155,16 @@ int32_t kt_qweight_check(const kt_qweight* w);
  * 16-column blocks (1 KB per 128 k for 4-bit, 2 KB for 8-bit), so the one-row kernel
  * reads whole columns with no cross-workgroup sums; the prefill GEMM (three or more
  * rows, group_size % 32 == 0) reads each lane's MFMA operand bytes from it as 16 or 8
- * contiguous bytes. It is a device-side accelerator next to qdata, not a format: files,
- * quantize and the accessors keep using qdata. Write it once after qdata is final (and
- * again if qdata changes), then set kt_qweight.packed. Size: ceil(columns / 16) * ceil(rows / 128)
- * * (bits == 4 ? 1024 : 2048) bytes, 16-byte aligned. */
-int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int64_t* bytes);
-/* Writes the copy of w's qdata into `packed` (kt_qweight_packed_bytes bytes of device
- * memory, 16-byte aligned); w->packed is ignored. Asynchronous. */
+ * contiguous bytes. After the weight blocks come the scales and zero points of every
+ * 16-column set as rows [set][group][16] (fp32, then bytes), so that a wave reads the
+ * groups of its K range as contiguous bytes. It is a device-side accelerator next to
+ * qdata, scales and zeros, not a format: files, quantize and the accessors keep using
+ * those. Write it once after they are final (and again if they change), then set
+ * kt_qweight.packed. Size: sets * ceil(rows / 128) * (bits == 4 ? 1024 : 2048) + sets *
+ * ceil(rows / group_size) * 80 bytes with sets = ceil(columns / 16), 16-byte aligned. */
+int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size, int64_t* bytes);
+/* Writes the copy of w's qdata, scales and zeros into `packed` (kt_qweight_packed_bytes
+ * bytes of device memory, 16-byte aligned); w->packed is ignored. Asynchronous. */
 int32_t kt_qweight_pack(const kt_qweight* w, void* packed, void* stream);
 
 /* ---- quantize + pack ---------------------------------------------------------- */

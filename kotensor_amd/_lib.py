@@ -121,7 +121,7 @@ SIGNATURES = {
     "kt_debug_wait_limits": [ctypes.c_uint32, _I],
     "kt_qweight_layout": [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
     "kt_qweight_check": [ctypes.POINTER(_QWeight)],
-    "kt_qweight_packed_bytes": [_I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
+    "kt_qweight_packed_bytes": [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)],
     "kt_qweight_pack": [ctypes.POINTER(_QWeight), _P, _P],
     "kt_quantize": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "kt_qmatmul": [_P, _I, ctypes.POINTER(_QWeight), _P, _I, _F, _P],

@@ -167,7 +167,8 @@ bool gemv_strip_preferred(const WeightView* ws, int32_t count);
 // up = SwiGLU's up row, norm_weight = RMSNorm's weight, as in launch_gemv_wide) and its
 // knobs (K-parts per column set, waves per workgroup, ring depth 4 or 8 = 8 or 16 KB per
 // wave; 0 = automatic).
-int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits);
+int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size);
+int64_t packed_weight_bytes(int32_t rows, int32_t columns, int32_t bits);  // the weight blocks alone
 int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st);
 bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
 // glu: ws[0], ws[1] are SwiGLU's gate and up weights; cs[0] receives silu(gate) * up and

@@ -1077,7 +1077,7 @@ static void fill_jobs(GemmJobs& jobs, const WeightView* ws, float* const* cs, co
 static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
     for (int32_t i = 0; i < count; ++i) {
         if (!ws[i].p || ws[i].g % 32 != 0 || (ws[i].bits == 4 && !ws[i].z)) return false;
-        if (packed_bytes(ws[i].K, ws[i].N, ws[i].bits) > 0xFFFFFFFFll) return false;
+        if (packed_weight_bytes(ws[i].K, ws[i].N, ws[i].bits) > 0xFFFFFFFFll) return false;
         if (static_cast<int64_t>(ws[i].G) * ws[i].N * 4 > 0xFFFFFFFFll) return false;
     }
     return true;

@@ -43,6 +43,7 @@
 // how the columns or the K range are divided among waves.
 #include "kt_common.h"
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace kt {
@@ -57,6 +58,7 @@ constexpr int RUN = 32;      // k per lane run
 constexpr int MAX_JOBS = 4;
 constexpr int MAX_K = 16384;  // eight waves of at most 2048 k each
 constexpr int ZERO_BYTES = 32;
+constexpr int NONTEMPORAL = 2;  // buffer-load cache policy: streamed data, read once
 
 __host__ __device__ constexpr int block_bytes(int bits) { return bits == 4 ? 1024 : 2048; }
 
@@ -67,8 +69,8 @@ __host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4
 
 struct PJob {
     const uint8_t* packed;
-    const float* s;
-    const int8_t* z;
+    const float* s;   // the copy's scale rows [set][group][16]
+    const int8_t* z;  // the copy's zero-point rows (null: no zero points)
     float* out;
     const float* bias;
     int32_t N, sets;
@@ -123,6 +125,24 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// Writes the copy's scale and zero-point rows: [column set][group][16] fp32 scales, then
+// [column set][group][16] zero points (0 without zero points, and past the last column).
+__global__ void __launch_bounds__(256)
+    pack_scales_kernel(const float* __restrict__ s, const int8_t* __restrict__ z, int32_t G, int32_t N, int64_t rows,
+                       float* __restrict__ ps, int8_t* __restrict__ pz) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < rows;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t set_group = i / SET;
+        const int32_t n = static_cast<int32_t>(i - set_group * SET);
+        const int32_t set = static_cast<int32_t>(set_group / G);
+        const int32_t grp = static_cast<int32_t>(set_group - static_cast<int64_t>(set) * G);
+        const int32_t col = set * SET + n;
+        const int64_t at = static_cast<int64_t>(grp) * N + col;
+        ps[i] = col < N ? s[at] : 0.0f;
+        pz[i] = z && col < N ? z[at] : static_cast<int8_t>(0);
+    }
+}
+
 // Max over the 8 lanes of an aligned group (quad swaps, then the half-row mirror).
 __device__ __forceinline__ float max8(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
@@ -169,10 +189,23 @@ constexpr int MAX_WAVE_CHUNKS = 16;   // a wave's K range: at most 2048
 constexpr int X_SLOTS = MAX_K / (256 * W);  // float4s of x per thread
 
 // The workgroup's LDS: digit rows [4][kp] (kp = 128 chunks bytes), 32 zero bytes, run
-// records [4 chunks] x 8 bytes, then the meeting area: [W][16] sums and [W] sums of squares.
+// records [4 chunks] x 8 bytes, the meeting area: [W][16] sums and [W] sums of squares,
+// then each wave's staged scales and zero points: rows [stage_rows][16] fp32, then
+// [stage_rows][16] bytes (the quantization groups its K range touches, its 16 columns).
 __host__ __device__ constexpr int32_t lds_rec_offset(int32_t chunks) { return 4 * chunks * CHUNK + ZERO_BYTES; }
 __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return lds_rec_offset(chunks) + chunks * (CHUNK / RUN) * 8; }
-__host__ __device__ constexpr int32_t lds_bytes(int32_t chunks) { return lds_red_offset(chunks) + W * (SET + 1) * 4; }
+__host__ __device__ constexpr int32_t lds_stage_offset(int32_t chunks) {
+    return (lds_red_offset(chunks) + W * (SET + 1) * 4 + 15) & ~15;
+}
+// Groups a wave's range of at most nmax chunks touches (g = 32 << gshift): whole groups
+// per chunk up to g = 128; beyond that a range may start inside a group, one row more.
+__host__ __device__ constexpr int32_t stage_rows(int32_t nmax, int32_t gshift) {
+    return gshift <= 2 ? nmax << (2 - gshift) : ((nmax << 2) + (1 << gshift) - 1) / (1 << gshift) + 1;
+}
+constexpr int32_t STAGE_ROW_BYTES = SET * 4 + SET;  // scales and zero points of one group row
+__host__ __device__ constexpr int32_t lds_bytes(int32_t chunks, int32_t nmax, int32_t gshift) {
+    return lds_stage_offset(chunks) + W * stage_rows(nmax, gshift) * STAGE_ROW_BYTES;
+}
 
 // A stage of a chained launch (gemv_chain_kernel): the workgroup issues its first weight
 // loads, waits until every partition of the previous stage has raised its flag (the first
@@ -324,8 +357,8 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     const int32_t kpad = chunks * CHUNK;  // digit row stride
 
     // ---- loads, in the order they complete: this thread's share of x (buffer loads:
-    // slots past the row read zeros without memory traffic), then the first R chunks of
-    // weights with their scales and zero points.
+    // slots past the row read zeros without memory traffic), the wave's scales and zero
+    // points, then the first R chunks of weights.
     const int32_t n4 = K >> 2, kp4 = kpad >> 2;
     const int32_t used = (kp4 + 64 * W - 1) / (64 * W);  // slots that reach into the digit rows
     float4 xv[XS];
@@ -355,30 +388,52 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     const int32_t zoff = 4 * kpad;
     int2* rec = reinterpret_cast<int2*>(smem + lds_rec_offset(chunks));
 
-    // the wave's blocks are contiguous; chunks past its range read as zeros without
-    // touching memory
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(jb.packed + (static_cast<int64_t>(set) * chunks + c_begin) * BB), 0, n * BB, 0x00020000);
-    // a chunk's scale and zero point for this lane's run and column travel with its
-    // weights (a run past K, padding of the last chunk, takes the last group's: its digits
-    // are zero, so it adds nothing)
+    // The wave's scales and zero points: group rows g0 .. g0 + rows - 1 of its column
+    // set in the copy's [set][group][16] rows (contiguous: 64 bytes of scales and 16 of
+    // zero points a row), in a few 16-byte loads per lane (sixteen rows of scales per
+    // load: four lanes a row; a row of zero points per lane); rows past G read zeros
+    // without memory traffic. They go to the wave's rows in LDS with the digit pass, and
+    // each chunk reads its lane's pair there. Measured at 4096 -> 14336 / 14336 -> 4096
+    // INT4: one 4-byte and one 1-byte load per chunk from the [G x N] arrays 7.9 / 10.7
+    // us, these rows gathered from the [G x N] arrays 8.2-8.5 / 10.3-11.0, from the
+    // copy's contiguous rows 8.0 / 8.8.
+    const int32_t g0 = k0 >> (gshift + 5);
+    const int32_t rows = stage_rows((chunks + (1 << kslog) - 1) >> kslog, gshift);
     const __amdgpu_buffer_rsrc_t sr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(jb.s), 0, G * jb.N * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(ZP ? jb.z : reinterpret_cast<const int8_t*>(jb.s)), 0, G * jb.N, 0x00020000);
+    u32x4 sst[4];
+    u32x4 zst;
+    auto issue_stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int32_t r = g0 + 16 * i + (ln >> 2);
+            const int32_t off = r < G ? ((set * G + r) * SET + 4 * (ln & 3)) * 4 : G * jb.N * 4;
+            sst[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+        }
+        if constexpr (ZP) {
+            const int32_t r = g0 + ln;
+            zst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                zr, r < G ? (set * G + r) * SET : G * jb.N, 0, 0));
+        }
+    };
+    if constexpr (!CHAIN) issue_stage();
+
+    // the wave's blocks are contiguous; chunks past its range read as zeros without
+    // touching memory. Weights are read once: non-temporal loads (measured 8.7 -> 7.9 us
+    // at 4096 x 14336 before the staging above; a plain read of the same bytes 7.1 -> 6.5).
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(jb.packed + (static_cast<int64_t>(set) * chunks + c_begin) * BB), 0, n * BB, 0x00020000);
     const int32_t run_base = (k0 >> 5) + kb;  // this lane's run in chunk 0 of its range
     u32x4 wb[R][NB];
-    float sc[R];
-    int32_t zz[ZP ? R : 1];
     auto issue = [&](int slot, int32_t cc) {
 #pragma unroll
         for (int h = 0; h < NB; ++h)
             wb[slot][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        wr, cc * BB + h * 1024 + 16 * ln, 0, 0));
-        const int32_t at = min((run_base + cc * (CHUNK / RUN)) >> gshift, G - 1) * jb.N + col;
-        sc[slot] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, at * 4, 0, 0));
-        if constexpr (ZP) zz[slot] = static_cast<int8_t>(__builtin_amdgcn_raw_buffer_load_b8(zr, at, 0, 0));
+                                                        wr, cc * BB + h * 1024 + 16 * ln, 0, NONTEMPORAL));
     };
+    if constexpr (CHAIN) issue_stage();
 #pragma unroll
     for (int s = 0; s < R; ++s) issue(s, s);
     __builtin_amdgcn_sched_barrier(0);
@@ -443,6 +498,13 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         const float w2 = norm_wave_sum(nsum);
         if (ln == 0) red[W * SET + wave] = w2;
     }
+    // the staged rows (only this wave reads them)
+    unsigned char* stg = smem + lds_stage_offset(chunks) + wave * rows * STAGE_ROW_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (16 * i + (ln >> 2) < rows) *reinterpret_cast<u32x4*>(stg + i * 1024 + 16 * ln) = sst[i];
+    if constexpr (ZP)
+        if (ln < rows) *reinterpret_cast<u32x4*>(stg + rows * SET * 4 + 16 * ln) = zst;
     __syncthreads();
 
     // ---- main loop: R chunks in flight ----------------------------------------------
@@ -471,8 +533,11 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         i32x4 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
         const int2 rc = rec[run_base + cc * (CHUNK / RUN)];
-        const float scale = sc[s];
-        const float zero = ZP ? static_cast<float>(zz[s]) : 0.0f;
+        // the lane's group row (a run past K, padding of the last chunk, takes the last
+        // group's: its digits are zero, so it adds nothing)
+        const int32_t r = min((run_base + cc * (CHUNK / RUN)) >> gshift, G - 1) - g0;
+        const float scale = *reinterpret_cast<const float*>(stg + r * (SET * 4) + nl * 4);
+        const float zero = ZP ? static_cast<float>(static_cast<int8_t>(stg[rows * SET * 4 + r * SET + nl])) : 0.0f;
         // digit pairs in integer (exact: |D_p| < 2^16 for INT4, so D_0 + 256 D_1 < 2^24;
         // INT8 sums round once in the conversion), then one fma: u = D_23 + D_01 / 2^16
         // with D_23 = D_2 + 256 D_3, D_01 = D_0 + 256 D_1; the run record holds E - 14
@@ -556,51 +621,74 @@ __global__ void __launch_bounds__(64 * W)
                                                      blockIdx.y, ChainLink{});
 }
 
+constexpr size_t LDS_DEFAULT = 64 << 10, LDS_MAX = 160 << 10;
+// Raises the dynamic-LDS attribute of kernel KERN to LDS_MAX once, when a launch needs
+// more than the default.
+template <auto KERN>
+int32_t allow_lds(size_t lds) {
+    static std::atomic<bool> raised{false};
+    if (lds <= LDS_DEFAULT || raised.load(std::memory_order_acquire)) return KT_OK;
+    KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(LDS_MAX)));
+    raised.store(true, std::memory_order_release);
+    return KT_OK;
+}
+
 struct Forced {
     int ks = 0;
     int ring = 0;  // 1: 4 KB of weights in flight per wave, 2: 8 KB, 0: automatic
 };
 Forced g_forced;
 
+template <int BITS, int R, bool ZP, int XMODE, bool GLU>
+int32_t launch_k(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+                 int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+    if (const int32_t status = allow_lds<&gemv_packed_kernel<BITS, R, ZP, XMODE, GLU>>(lds)) return status;
+    gemv_packed_kernel<BITS, R, ZP, XMODE, GLU>
+        <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+    return KT_OK;
+}
+
 template <int BITS, bool ZP, int XMODE, bool GLU>
-void launch_g(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
-              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+int32_t launch_g(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+                 int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
     // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
     constexpr int RS = BITS == 4 ? 4 : 2;
     if (g_forced.ring == 2)
-        gemv_packed_kernel<BITS, 2 * RS, ZP, XMODE, GLU>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
-    else if (g_forced.ring == 1 || nmax > RS / 2)
-        gemv_packed_kernel<BITS, RS, ZP, XMODE, GLU>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
-    else
-        gemv_packed_kernel<BITS, RS / 2, ZP, XMODE, GLU>
-            <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
+        return launch_k<BITS, 2 * RS, ZP, XMODE, GLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha,
+                                                      accumulate, nmax);
+    if (g_forced.ring == 1 || nmax > RS / 2)
+        return launch_k<BITS, RS, ZP, XMODE, GLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha,
+                                                  accumulate, nmax);
+    return launch_k<BITS, RS / 2, ZP, XMODE, GLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha,
+                                                  accumulate, nmax);
 }
 
 // The paired gate/up form exists for the plain and RMSNorm inputs only.
 template <int BITS, bool ZP, int XMODE>
-void launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
-              int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax,
-              int32_t glu) {
+int32_t launch_r(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
+                 int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax,
+                 int32_t glu) {
     if constexpr (XMODE != X_SWIGLU)
-        if (glu) {
-            launch_g<BITS, ZP, XMODE, true>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
-            return;
-        }
-    launch_g<BITS, ZP, XMODE, false>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax);
+        if (glu)
+            return launch_g<BITS, ZP, XMODE, true>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha,
+                                                   accumulate, nmax);
+    return launch_g<BITS, ZP, XMODE, false>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate,
+                                            nmax);
 }
 
 template <int BITS, bool ZP>
-void launch_mode(int mode, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
-                 int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate,
-                 int32_t nmax, int32_t glu) {
+int32_t launch_mode(int mode, dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps,
+                    int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate,
+                    int32_t nmax, int32_t glu) {
     if (mode == X_SWIGLU)
-        launch_r<BITS, ZP, X_SWIGLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
-    else if (mode == X_NORM)
-        launch_r<BITS, ZP, X_NORM>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
-    else
-        launch_r<BITS, ZP, X_PLAIN>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax, glu);
+        return launch_r<BITS, ZP, X_SWIGLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate,
+                                            nmax, glu);
+    if (mode == X_NORM)
+        return launch_r<BITS, ZP, X_NORM>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax,
+                                          glu);
+    return launch_r<BITS, ZP, X_PLAIN>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate, nmax,
+                                       glu);
 }
 
 int32_t log2_exact(int32_t v) {
@@ -611,19 +699,32 @@ int32_t log2_exact(int32_t v) {
 
 }  // namespace
 
-int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits) {
+int64_t packed_weight_bytes(int32_t rows, int32_t columns, int32_t bits) {
     const int64_t sets = ceil_div(columns, SET), chunks = ceil_div(rows, CHUNK);
     return sets * chunks * block_bytes(bits);
 }
 
+int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size) {
+    const int64_t sets = ceil_div(columns, SET), groups = ceil_div(rows, group_size);
+    return packed_weight_bytes(rows, columns, bits) + sets * groups * STAGE_ROW_BYTES;
+}
+
 int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st) {
     const int32_t chunks = ceil_div(w.K, CHUNK);
-    const int64_t dwords = packed_bytes(w.K, w.N, w.bits) / 4;
+    const int64_t wbytes = packed_weight_bytes(w.K, w.N, w.bits);
+    const int64_t dwords = wbytes / 4;
     int64_t blocks = (dwords + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     pack_kernel<<<static_cast<uint32_t>(blocks), 256, 0, st>>>(w.q, w.K, w.N, w.bits, w.bpr, chunks, dwords,
                                                                static_cast<uint32_t*>(packed));
     KT_LAUNCHED("qweight pack kernel");
+    const int32_t sets = ceil_div(w.N, SET);
+    const int64_t rows = static_cast<int64_t>(sets) * w.G * SET;
+    float* ps = reinterpret_cast<float*>(static_cast<uint8_t*>(packed) + wbytes);
+    int8_t* pz = reinterpret_cast<int8_t*>(ps + rows);
+    blocks = std::min<int64_t>((rows + 255) / 256, 65536);
+    pack_scales_kernel<<<static_cast<uint32_t>(blocks), 256, 0, st>>>(w.s, w.z, w.G, w.N, rows, ps, pz);
+    KT_LAUNCHED("qweight pack kernel (scales)");
     return KT_OK;
 }
 
@@ -635,19 +736,9 @@ void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring) {
 
 namespace {
 
-// Largest LDS block the device gives a workgroup (cached per device).
-size_t lds_limit() {
-    static int32_t cached[64] = {};
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 64 << 10;
-    if (!cached[device]) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess || v <= 0)
-            v = 64 << 10;
-        cached[device] = v;
-    }
-    return static_cast<size_t>(cached[device]);
-}
+// gfx950 gives a workgroup up to 160 KB of LDS; a kernel asks for more than 64 KB of
+// dynamic LDS by raising its attribute first (allow_lds).
+size_t lds_limit() { return LDS_MAX; }
 
 struct PackedPlan {
     int32_t ks = 0, nmax = 0;
@@ -662,6 +753,7 @@ struct PackedPlan {
 // 4-chunk waves beat 128 of 8-chunk ones). ks = 0 when nothing fits.
 PackedPlan plan_packed(int32_t K, int32_t g, int64_t sets_total) {
     PackedPlan p;
+    if (g % RUN != 0 || log2_exact(g / RUN) < 0) return p;
     const int32_t chunks = ceil_div(K, CHUNK);
     int32_t ks = 1;
     while (ks < W && ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) ks *= 2;
@@ -673,8 +765,7 @@ PackedPlan plan_packed(int32_t K, int32_t g, int64_t sets_total) {
         while (ks < W && 2 * ks <= chunks && 5 * ((sets_total * ks + W - 1) / W) < 4 * cu_count()) ks *= 2;
     }
     const int32_t nmax = ceil_div(chunks, ks);
-    (void)g;
-    const size_t lds = static_cast<size_t>(lds_bytes(chunks));
+    const size_t lds = static_cast<size_t>(lds_bytes(chunks, nmax, log2_exact(g / RUN)));
     if (lds > lds_limit()) return p;
     p.ks = ks;
     p.nmax = nmax;
@@ -690,6 +781,7 @@ bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const
     if (w.K % RUN != 0 || w.K > MAX_K) return false;             // whole runs; the digits fit LDS
     if (w.g % RUN != 0 || log2_exact(w.g / RUN) < 0) return false;  // a run lies in one group
     if (w.N % SET != 0) return false;                             // whole column sets
+    if (static_cast<int64_t>(w.G) * w.N * 4 > INT32_MAX) return false;  // scale offsets in 32 bits
     if (!aligned(w.p, 16) || !aligned(a, 16) || !aligned(w.s, 16) || (w.z && !aligned(w.z, 16))) return false;
     return plan_packed(w.K, w.g, w.N / SET).ks != 0;
 }
@@ -747,8 +839,10 @@ int32_t prepare_gemv_packed(const float* a, const WeightView* ws, float* const* 
     for (int32_t i = 0; i < count; ++i) {
         PJob& jb = L.jobs.job[i];
         jb.packed = ws[i].p;
-        jb.s = ws[i].s;
-        jb.z = ws[i].z;
+        // the copy's scale and zero-point rows follow its weight blocks
+        jb.s = reinterpret_cast<const float*>(ws[i].p + packed_weight_bytes(ws[i].K, ws[i].N, ws[i].bits));
+        jb.z = ws[i].z ? reinterpret_cast<const int8_t*>(jb.s + static_cast<int64_t>(ws[i].N / SET) * ws[i].G * SET)
+                       : nullptr;
         jb.out = cs[i];
         jb.bias = biases ? biases[i] : nullptr;
         jb.N = ws[i].N;
@@ -873,15 +967,17 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
     PackedLaunch L;
     const int32_t status = prepare_gemv_packed(a, ws, cs, biases, count, accumulate, alpha, up, norm_weight, eps, glu, &L);
     if (status) return status;
+    int32_t launched = KT_OK;
     if (L.bits == 4)
-        launch_mode<4, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
-                             L.accumulate, L.nmax, L.glu ? 1 : 0);
+        launched = launch_mode<4, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog,
+                                        L.alpha, L.accumulate, L.nmax, L.glu ? 1 : 0);
     else if (L.zp)
-        launch_mode<8, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
-                             L.accumulate, L.nmax, L.glu ? 1 : 0);
+        launched = launch_mode<8, true>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog,
+                                        L.alpha, L.accumulate, L.nmax, L.glu ? 1 : 0);
     else
-        launch_mode<8, false>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog, L.alpha,
-                              L.accumulate, L.nmax, L.glu ? 1 : 0);
+        launched = launch_mode<8, false>(L.mode, L.grid, L.lds, st, L.x, L.aux, L.eps, L.K, L.gshift, L.jobs, L.kslog,
+                                         L.alpha, L.accumulate, L.nmax, L.glu ? 1 : 0);
+    if (launched) return launched;
     KT_LAUNCHED("qmatmul: packed gemv kernel");
     return KT_OK;
 }
@@ -938,12 +1034,16 @@ int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st) {
     c.spin_limit = limits.spin_limit ? limits.spin_limit : CHAIN_SPIN_LIMIT;
     c.withhold = limits.withhold;
     const dim3 grid(static_cast<uint32_t>(total));
-    if (bits == 4)
+    if (bits == 4) {
+        if (const int32_t ls = allow_lds<&gemv_chain_kernel<4, true>>(lds)) return ls;
         gemv_chain_kernel<4, true><<<grid, dim3(64 * W), lds, st>>>(c);
-    else if (zp)
+    } else if (zp) {
+        if (const int32_t ls = allow_lds<&gemv_chain_kernel<8, true>>(lds)) return ls;
         gemv_chain_kernel<8, true><<<grid, dim3(64 * W), lds, st>>>(c);
-    else
+    } else {
+        if (const int32_t ls = allow_lds<&gemv_chain_kernel<8, false>>(lds)) return ls;
         gemv_chain_kernel<8, false><<<grid, dim3(64 * W), lds, st>>>(c);
+    }
     KT_LAUNCHED("qmatmul chain kernel");
     return KT_OK;
 }

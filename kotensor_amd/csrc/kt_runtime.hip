@@ -525,11 +525,12 @@ int32_t kt_qweight_check(const kt_qweight* w) {
     return view_weight(w, &v);
 }
 
-int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int64_t* bytes) {
+int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size, int64_t* bytes) {
     if (!bytes) return fail(KT_ERR_ARGUMENT, "bytes is NULL");
     if (bits != 4 && bits != 8) return fail(KT_ERR_ARGUMENT, "bits must be 4 or 8, got %d", bits);
+    if (group_size <= 0) return fail(KT_ERR_ARGUMENT, "groupSize must be positive");
     if (rows <= 0 || columns <= 0) return fail(KT_ERR_SHAPE, "QuantizedTensor needs a 2-D shape, got [%d, %d]", rows, columns);
-    *bytes = packed_bytes(rows, columns, bits);
+    *bytes = packed_bytes(rows, columns, bits, group_size);
     return KT_OK;
 }
 

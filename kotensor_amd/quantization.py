@@ -120,14 +120,14 @@ class QuantizedTensor:
         return self._p
 
     def pack(self, stream: Stream | None = None) -> "QuantizedTensor":
-        """Writes the device-native column-run copy of qdata (``kt_qweight_pack``) and
-        points the weight at it, so one-row products (and, for group sizes that are
-        multiples of 32, the prefill GEMM) read it instead of qdata. qdata stays the format
-        of record (files, accessors, the other kernels). Costs
-        ``kt_qweight_packed_bytes`` more device memory (about the size of qdata); call it
-        again after qdata changes. Returns self."""
+        """Writes the device-native column-run copy of qdata, scales and zeros
+        (``kt_qweight_pack``) and points the weight at it, so one-row products (and, for
+        group sizes that are multiples of 32, the prefill GEMM) read it instead of qdata.
+        qdata, scales and zeros stay the format of record (files, accessors, the other
+        kernels). Costs ``kt_qweight_packed_bytes`` more device memory (about the size of
+        qdata plus the scales and zeros); call it again after they change. Returns self."""
         n = ctypes.c_int64()
-        _lib.call("kt_qweight_packed_bytes", self.rows, self.columns, self.bits, ctypes.byref(n))
+        _lib.call("kt_qweight_packed_bytes", self.rows, self.columns, self.bits, self.group_size, ctypes.byref(n))
         if self._p is None or self._p.nbytes != n.value:
             self._p = DeviceBuffer(n.value)
         self._struct.packed = None

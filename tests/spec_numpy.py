@@ -99,8 +99,9 @@ def decode(qdata, scales, zeros, K, N, bits, group_size) -> np.ndarray:
     return (s * (raw - z).astype(np.float32)).astype(np.float32)
 
 
-def pack_column_runs(qdata, K: int, N: int, bits: int) -> np.ndarray:
-    """The column-run copy of qdata (kt_qweight_pack), restated with numpy reshapes.
+def pack_column_runs(qdata, K: int, N: int, bits: int, scales=None, zeros=None, g: int = 0) -> np.ndarray:
+    """The column-run copy (kt_qweight_pack), restated with numpy reshapes: the weight
+    blocks, then (with scales and g given) the scale and zero-point rows.
 
     Blocks [column set of 16][chunk of 128 k]; in a block, lane l = 16 kb + n owns 16
     bytes (INT8: two halves of 1 KB, lane bytes at h * 1024 + 16 l) for column 16 set + n
@@ -120,7 +121,20 @@ def pack_column_runs(qdata, K: int, N: int, bits: int) -> np.ndarray:
     V[:K, :N] = vals
     if bits == 8:
         R = V.reshape(chunks, 4, 2, 16, sets, 16)           # c, kb, h, b, set, n
-        return np.ascontiguousarray(R.transpose(4, 0, 2, 1, 5, 3)).reshape(-1)  # set, c, h, kb, n, b
-    R = V.reshape(chunks, 4, 2, 2, 2, 4, sets, 16)          # c, kb, m, hh, lohi, t, set, n
-    byte = R[:, :, :, :, 0] | (R[:, :, :, :, 1] << 4)       # c, kb, m, hh, t, set, n
-    return np.ascontiguousarray(byte.transpose(5, 0, 1, 6, 2, 3, 4)).reshape(-1)  # set, c, kb, n, m, hh, t
+        blocks = np.ascontiguousarray(R.transpose(4, 0, 2, 1, 5, 3)).reshape(-1)  # set, c, h, kb, n, b
+    else:
+        R = V.reshape(chunks, 4, 2, 2, 2, 4, sets, 16)      # c, kb, m, hh, lohi, t, set, n
+        byte = R[:, :, :, :, 0] | (R[:, :, :, :, 1] << 4)   # c, kb, m, hh, t, set, n
+        blocks = np.ascontiguousarray(byte.transpose(5, 0, 1, 6, 2, 3, 4)).reshape(-1)  # set, c, kb, n, m, hh, t
+    if scales is None:
+        return blocks
+    # [set][group][16] rows: fp32 scales, then zero-point bytes (0 past N or without zeros)
+    G = -(-K // g)
+    S = np.zeros((G, sets * 16), dtype=np.float32)
+    S[:, :N] = np.asarray(scales, dtype=np.float32).reshape(G, N)
+    Z = np.zeros((G, sets * 16), dtype=np.uint8)
+    if zeros is not None:
+        Z[:, :N] = np.asarray(zeros).view(np.uint8).reshape(G, N)
+    srows = np.ascontiguousarray(S.reshape(G, sets, 16).transpose(1, 0, 2)).view(np.uint8).reshape(-1)
+    zrows = np.ascontiguousarray(Z.reshape(G, sets, 16).transpose(1, 0, 2)).reshape(-1)
+    return np.concatenate([blocks, srows, zrows])

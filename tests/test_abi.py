@@ -81,11 +81,12 @@ def test_argument_errors_map_to_illegal_argument():
     assert lib.kt_last_error(buf, 8) == 0 and len(buf.value) <= 7
     # the column-run copy: size formula, and its checks before any device access
     n = ctypes.c_int64()
-    assert lib.kt_qweight_packed_bytes(4096, 14336, 4, ctypes.byref(n)) == _lib.KT_OK
-    assert n.value == (14336 // 16) * (4096 // 128) * 1024
-    assert lib.kt_qweight_packed_bytes(300, 2100, 8, ctypes.byref(n)) == _lib.KT_OK
-    assert n.value == 132 * 3 * 2048  # ceil(2100 / 16) sets, ceil(300 / 128) chunks
-    assert lib.kt_qweight_packed_bytes(300, 2100, 5, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qweight_packed_bytes(4096, 14336, 4, 64, ctypes.byref(n)) == _lib.KT_OK
+    assert n.value == (14336 // 16) * (4096 // 128) * 1024 + (14336 // 16) * 64 * 80
+    assert lib.kt_qweight_packed_bytes(300, 2100, 8, 32, ctypes.byref(n)) == _lib.KT_OK
+    assert n.value == 132 * 3 * 2048 + 132 * 10 * 80  # ceil(2100 / 16) sets, ceil(300 / 128) chunks, 10 groups
+    assert lib.kt_qweight_packed_bytes(300, 2100, 5, 32, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
+    assert lib.kt_qweight_packed_bytes(300, 2100, 8, 0, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_qweight_pack(ctypes.byref(w), None, None) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_qweight_pack(ctypes.byref(w), ctypes.c_void_p(8), None) == _lib.KT_ERR_ARGUMENT
     assert "16-byte aligned" in _lib.last_error()

@@ -34,14 +34,14 @@ def _packed(kt, q):
     return upload_quantized(kt, q).pack()
 
 
-@pytest.mark.parametrize("k,n,bits", [(300, 2100, 4), (300, 2100, 8), (896, 4864, 4), (128, 16, 8), (200, 33, 4),
-                                      (4096, 1024, 8), (70, 9, 4)])
-def test_pack_layout_bit_exact(kt, oracle_lib, k, n, bits):
-    q = _weights(oracle_lib, k, n, bits, 64, k + n)
-    banner("pack", k, n, bits)
+@pytest.mark.parametrize("k,n,bits,g", [(300, 2100, 4, 64), (300, 2100, 8, 32), (896, 4864, 4, 32), (128, 16, 8, 64),
+                                        (200, 33, 4, 64), (4096, 1024, 8, 128), (70, 9, 4, 64), (1000, 48, 4, 96)])
+def test_pack_layout_bit_exact(kt, oracle_lib, k, n, bits, g):
+    q = _weights(oracle_lib, k, n, bits, g, k + n)
+    banner("pack", k, n, bits, g)
     qt = _packed(kt, q)
     got = qt.packed_buffer.download(np.uint8)
-    assert same_bits(got, pack_column_runs(q.qdata, k, n, bits))
+    assert same_bits(got, pack_column_runs(q.qdata, k, n, bits, q.scales, q.zeros, g))
 
 
 SHAPES = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 151936), (2048, 2048), (2048, 512), (2048, 8192),

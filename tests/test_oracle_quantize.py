@@ -201,3 +201,21 @@ def test_column_run_spec_matches_its_definition():
                 d, t = rng.integers(4), rng.integers(4)
                 k = run + 16 * (d >> 1) + 8 * (d & 1) + t
                 assert P[(s * chunks + c) * BB + 16 * lane + 4 * d + t] == val(k, col) | (val(k + 4, col) << 4)
+        # the scale and zero-point rows after the blocks: row (set, group) holds the 16
+        # columns of the set, fp32 scales first, then the zero points' bytes
+        for g in (32, 64, 96):
+            G = -(-K // g)
+            sc = rng.standard_normal(G * N).astype(np.float32)
+            zs = rng.integers(0, 16, size=G * N, dtype=np.uint8)
+            P = pack_column_runs(q, K, N, bits, sc, zs, g)
+            base = sets * chunks * BB
+            assert P.size == base + sets * G * 80
+            srows = P[base:base + sets * G * 64].view(np.float32)
+            zrows = P[base + sets * G * 64:]
+            for _ in range(500):
+                s, grp, n = rng.integers(sets), rng.integers(G), rng.integers(16)
+                col = 16 * s + n
+                want_s = sc[grp * N + col] if col < N else 0.0
+                want_z = zs[grp * N + col] if col < N else 0
+                assert srows[(s * G + grp) * 16 + n] == want_s
+                assert zrows[(s * G + grp) * 16 + n] == want_z
