@@ -200,7 +200,7 @@ __host__ __device__ constexpr int32_t lds_stage_offset(int32_t chunks) {
 // Groups a wave's range of at most nmax chunks touches (g = 32 << gshift): whole groups
 // per chunk up to g = 128; beyond that a range may start inside a group, one row more.
 __host__ __device__ constexpr int32_t stage_rows(int32_t nmax, int32_t gshift) {
-    return gshift <= 2 ? nmax << (2 - gshift) : ((nmax << 2) + (1 << gshift) - 1) / (1 << gshift) + 1;
+    return gshift <= 2 ? nmax << (2 - gshift) : (((nmax << 2) + (1 << gshift) - 1) >> gshift) + 1;
 }
 constexpr int32_t STAGE_ROW_BYTES = SET * 4 + SET;  // scales and zero points of one group row
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks, int32_t nmax, int32_t gshift) {
@@ -515,7 +515,10 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     const int32_t a_step = diag ? CHUNK : 0;
     const uint32_t mask = 0x0F0F0F0Fu;
     float y = 0.0f;
-    auto process = [&](int s, int32_t cc) {
+    // live = false: a chunk past the wave's range (its weights read as zeros), which adds
+    // nothing; its LDS reads stay inside the wave's rows
+    auto process = [&](int s, int32_t cc, bool live) {
+        cc = live ? cc : n - 1;
         const int8_t* pa = xd + a_base + cc * a_step;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(pa);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(pa + 16);
@@ -544,20 +547,25 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         const int32_t d01 = acc[0] + (acc[1] << 8), d23 = acc[2] + (acc[3] << 8);
         const float u = fmaf(static_cast<float>(d01), 1.0f / 65536.0f, static_cast<float>(d23));
         const float v = fmaf(-zero, __int_as_float(rc.y), ldexpf(u, rc.x));
-        y = fmaf(scale, v, y);
+        const float yn = fmaf(scale, v, y);
+        y = live ? yn : y;
     };
-    // Unrolled over the largest range so that the ring sits in registers; the wave leaves
-    // at its own chunk count. Refills past the range read zeros without memory traffic
-    // and are never used.
+    // The ring: a loop over groups of R chunks, each slot's refill (chunk c + R) issued
+    // right behind its use. The refills cross the loop's back edge, so the compiler
+    // cannot sink them to their uses: with the chunks unrolled under per-chunk range
+    // tests it did exactly that in some instantiations (each load then waited for at
+    // once, one chunk in flight: 4096 x 14336 INT4 11.4 us instead of 8.0). Refills past
+    // the range read zeros without memory traffic; chunks past it are masked.
     auto ring_loop = [&]() {
-        static_for<0, MAX_WAVE_CHUNKS>([&](auto ci) {
-            constexpr int c = decltype(ci)::value;
-            if (c < n) {
-                process(c % R, c);
-                if constexpr (c + R < MAX_WAVE_CHUNKS) issue(c % R, c + R);
+#pragma nounroll
+        for (int32_t c0 = 0; c0 < n; c0 += R) {
+            static_for<0, R>([&](auto si) {
+                constexpr int sl = decltype(si)::value;
+                process(sl, c0 + sl, c0 + sl < n);
+                issue(sl, c0 + sl + R);
                 __builtin_amdgcn_sched_barrier(0);  // keep each refill right behind its use
-            }
-        });
+            });
+        }
     };
     if constexpr (CHAIN) {
         // a chained stage whose whole range is already in the ring: no refills, so the
@@ -565,7 +573,7 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         if (n <= R)
             static_for<0, R>([&](auto ci) {
                 constexpr int c = decltype(ci)::value;
-                if (c < n) process(c, c);
+                if (c < n) process(c, c, true);
             });
         else
             ring_loop();
@@ -634,6 +642,32 @@ int32_t allow_lds(size_t lds) {
     return KT_OK;
 }
 
+// One weight (the common call): everything the first loads depend on is in the first
+// 16 dwords of the arguments, which arrive in scalar registers with the wave, and the
+// copy's scale and zero-point rows are found from its size, so no wave waits for an
+// argument fetch before its first loads (a job table indexed by blockIdx.y, and the
+// K-part shift after it, are read from memory). shifts = kslog | gshift << 4.
+template <int BITS, int R, bool ZP, int XMODE>
+__global__ void __launch_bounds__(64 * W)
+    gemv_packed_single(const uint8_t* __restrict__ packed, const float* __restrict__ x, int32_t N, int32_t K,
+                       int32_t shifts, float alpha, float* out, int32_t accumulate, const float* bias,
+                       const float* __restrict__ aux, float eps) {
+    const int32_t kslog = shifts & 15, gshift = shifts >> 4;
+    const int32_t sets = N >> 4, chunks = (K + CHUNK - 1) >> 7, G = (K + (RUN << gshift) - 1) >> (gshift + 5);
+    PJobs jobs;
+    jobs.count = 1;
+    PJob& jb = jobs.job[0];
+    jb.packed = packed;
+    jb.s = reinterpret_cast<const float*>(packed + static_cast<int64_t>(sets) * chunks * block_bytes(BITS));
+    jb.z = ZP ? reinterpret_cast<const int8_t*>(jb.s + static_cast<int64_t>(sets) * G * SET) : nullptr;
+    jb.out = out;
+    jb.bias = bias;
+    jb.N = N;
+    jb.sets = sets;
+    gemv_packed_body<BITS, R, ZP, XMODE, false, false>(x, aux, eps, K, gshift, jobs, kslog, alpha, accumulate,
+                                                       blockIdx.x, 0, ChainLink{});
+}
+
 struct Forced {
     int ks = 0;
     int ring = 0;  // 1: 4 KB of weights in flight per wave, 2: 8 KB, 0: automatic
@@ -643,6 +677,15 @@ Forced g_forced;
 template <int BITS, int R, bool ZP, int XMODE, bool GLU>
 int32_t launch_k(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
                  int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
+    if constexpr (!GLU) {
+        if (jobs.count == 1) {
+            if (const int32_t status = allow_lds<&gemv_packed_single<BITS, R, ZP, XMODE>>(lds)) return status;
+            const PJob& jb = jobs.job[0];
+            gemv_packed_single<BITS, R, ZP, XMODE><<<grid, dim3(64 * W), lds, st>>>(
+                jb.packed, x, jb.N, K, kslog | gshift << 4, alpha, jb.out, accumulate, jb.bias, aux, eps);
+            return KT_OK;
+        }
+    }
     if (const int32_t status = allow_lds<&gemv_packed_kernel<BITS, R, ZP, XMODE, GLU>>(lds)) return status;
     gemv_packed_kernel<BITS, R, ZP, XMODE, GLU>
         <<<grid, dim3(64 * W), lds, st>>>(x, aux, eps, K, gshift, jobs, kslog, nmax, alpha, accumulate);
