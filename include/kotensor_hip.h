@@ -82,13 +82,13 @@ int32_t kt_set_device(int32_t device);
 /* Kernel selection knobs, the counterpart of MatMul's runtime knobs
  * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they choose how the
  * small-M kernels split their work, never their result beyond fp32 rounding order.
- * gemv_kind: 0 = automatic (for one row the column-run kernel when the weight has a
- *            packed copy, else the column-strip kernel up to a size and the wide-strip
- *            MFMA kernel above it; the row-block MFMA kernel for 2 to 16 rows, where the
- *            layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA GEMV for M > 1:
- *            those go to the GEMM), 2 = row-block MFMA kernel for M <= 16, 3 = wide-strip
- *            MFMA kernel for M == 1, 4 = column-strip kernel for M == 1, 5 = column-run
- *            kernel for M == 1 (needs the packed copy);
+ * gemv_kind: 0 = automatic (the column-run kernels for 1 to 16 rows when the weight has
+ *            a packed copy; otherwise for one row the column-strip kernel up to a size and
+ *            the wide-strip MFMA kernel above it, and the row-block MFMA kernel for 2 to 16
+ *            rows, where the layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA
+ *            GEMV for M > 1: those go to the GEMM), 2 = row-block MFMA kernel for M <= 16,
+ *            3 = wide-strip MFMA kernel for M == 1, 4 = column-strip kernel for M == 1,
+ *            5 = column-run kernels for M <= 16 (need the packed copy);
  * gemv_vec: vector-ALU kernel bytes per lane per row (4 or 8; 0 = automatic); for the
  *            column-run kernel, the KB of weights in flight per wave (4 or 8);
  * gemv_splits: workgroups along K per column tile (0 = automatic); for the column-run

@@ -196,6 +196,13 @@ int32_t gemv_chain_max_k();  // the longest input row a chained step takes
 int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st);
 void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 
+// 2 to 16 rows on the column-run copy (kt_gemv_rows_packed.hip): support check and launch
+// (up to four weights sharing the input: one preparation of x, one launch per weight).
+bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                hipStream_t st);
+
 // Whether the fast GEMV / GEMM kernels accept this weight (layout and alignment);
 // otherwise the generic kernel runs.
 bool gemv_supported(const float* a, const WeightView& w, const float* c);

@@ -42,6 +42,7 @@
 // A column's result therefore depends only on x and that column's weights, never on
 // how the columns or the K range are divided among waves.
 #include "kt_common.h"
+#include "kt_packed.h"
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -52,15 +53,10 @@ namespace {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int SET = 16;      // columns per column set
-constexpr int CHUNK = 128;   // k per chunk
-constexpr int RUN = 32;      // k per lane run
 constexpr int MAX_JOBS = 4;
 constexpr int MAX_K = 16384;  // eight waves of at most 2048 k each
 constexpr int ZERO_BYTES = 32;
-constexpr int NONTEMPORAL = 2;  // buffer-load cache policy: streamed data, read once
 
-__host__ __device__ constexpr int block_bytes(int bits) { return bits == 4 ? 1024 : 2048; }
 
 // The s_waitcnt immediate that waits until at most n vector memory operations are
 // outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at
@@ -174,15 +170,6 @@ constexpr int X_PLAIN = 0, X_SWIGLU = 1, X_NORM = 2;
 // by each wave for its own K-part alone, or units of one wave meeting through memory,
 // were measured slower: more x traffic ahead of the first weights, or a memory round trip
 // after the last.)
-// Calls f(std::integral_constant<int, I>) for I = B .. E - 1, so register arrays indexed by
-// I stay in registers.
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
 
 constexpr int W = 8;                  // waves per workgroup
 constexpr int MAX_WAVE_CHUNKS = 16;   // a wave's K range: at most 2048
@@ -197,12 +184,6 @@ __host__ __device__ constexpr int32_t lds_red_offset(int32_t chunks) { return ld
 __host__ __device__ constexpr int32_t lds_stage_offset(int32_t chunks) {
     return (lds_red_offset(chunks) + W * (SET + 1) * 4 + 15) & ~15;
 }
-// Groups a wave's range of at most nmax chunks touches (g = 32 << gshift): whole groups
-// per chunk up to g = 128; beyond that a range may start inside a group, one row more.
-__host__ __device__ constexpr int32_t stage_rows(int32_t nmax, int32_t gshift) {
-    return gshift <= 2 ? nmax << (2 - gshift) : (((nmax << 2) + (1 << gshift) - 1) >> gshift) + 1;
-}
-constexpr int32_t STAGE_ROW_BYTES = SET * 4 + SET;  // scales and zero points of one group row
 __host__ __device__ constexpr int32_t lds_bytes(int32_t chunks, int32_t nmax, int32_t gshift) {
     return lds_stage_offset(chunks) + W * stage_rows(nmax, gshift) * STAGE_ROW_BYTES;
 }
@@ -629,18 +610,6 @@ __global__ void __launch_bounds__(64 * W)
                                                      blockIdx.y, ChainLink{});
 }
 
-constexpr size_t LDS_DEFAULT = 64 << 10, LDS_MAX = 160 << 10;
-// Raises the dynamic-LDS attribute of kernel KERN to LDS_MAX once, when a launch needs
-// more than the default.
-template <auto KERN>
-int32_t allow_lds(size_t lds) {
-    static std::atomic<bool> raised{false};
-    if (lds <= LDS_DEFAULT || raised.load(std::memory_order_acquire)) return KT_OK;
-    KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(LDS_MAX)));
-    raised.store(true, std::memory_order_release);
-    return KT_OK;
-}
 
 // One weight (the common call): everything the first loads depend on is in the first
 // 16 dwords of the arguments, which arrive in scalar registers with the wave, and the
@@ -734,11 +703,6 @@ int32_t launch_mode(int mode, dim3 grid, size_t lds, hipStream_t st, const float
                                        glu);
 }
 
-int32_t log2_exact(int32_t v) {
-    int32_t s = 0;
-    while ((1 << s) < v) ++s;
-    return (1 << s) == v ? s : -1;
-}
 
 }  // namespace
 
@@ -777,16 +741,8 @@ void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring) {
     g_forced.ring = ring == 4 ? 1 : ring == 8 ? 2 : 0;
 }
 
-namespace {
 
-// gfx950 gives a workgroup up to 160 KB of LDS; a kernel asks for more than 64 KB of
-// dynamic LDS by raising its attribute first (allow_lds).
-size_t lds_limit() { return LDS_MAX; }
 
-struct PackedPlan {
-    int32_t ks = 0, nmax = 0;
-    size_t lds = 0;
-};
 
 // K-parts per column set for a launch over weights with K rows, groups of g and
 // sets_total column sets in all: the smallest power of two that keeps a wave's range
@@ -809,14 +765,14 @@ PackedPlan plan_packed(int32_t K, int32_t g, int64_t sets_total) {
     }
     const int32_t nmax = ceil_div(chunks, ks);
     const size_t lds = static_cast<size_t>(lds_bytes(chunks, nmax, log2_exact(g / RUN)));
-    if (lds > lds_limit()) return p;
+    if (lds > LDS_MAX) return p;
     p.ks = ks;
     p.nmax = nmax;
     p.lds = lds;
     return p;
 }
 
-}  // namespace
+
 
 bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
     (void)c;

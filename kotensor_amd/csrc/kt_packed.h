@@ -1,0 +1,69 @@
+// kt_packed.h -- the column-run copy's layout constants and helpers, shared by the
+// kernels that read it (kt_gemv_packed.hip: one row; kt_gemv_rows_packed.hip: 2 to 16).
+// Layout: blocks of one 16-column set x one 128-k chunk, ordered [set][chunk] (INT4 1 KB,
+// INT8 2 KB), lane l = 16 kb + n of a reading wave owning column 16 set + n over the
+// 32-k run [128 chunk + 32 kb, + 32); after the blocks, the scale and zero-point rows
+// [set][group][16] (fp32, then bytes).
+#pragma once
+
+#include <atomic>
+#include <type_traits>
+
+#include "kt_common.h"
+
+namespace kt {
+
+constexpr int SET = 16;         // columns per column set
+constexpr int CHUNK = 128;      // k per chunk
+constexpr int RUN = 32;         // k per lane run
+constexpr int NONTEMPORAL = 2;  // buffer-load cache policy: streamed data, read once
+__host__ __device__ constexpr int block_bytes(int bits) { return bits == 4 ? 1024 : 2048; }
+
+// Calls f(std::integral_constant<int, I>) for I = B .. E - 1, so register arrays indexed by
+// I stay in registers.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Groups a wave's range of at most nmax chunks touches (g = 32 << gshift): whole groups
+// per chunk up to g = 128; beyond that a range may start inside a group, one row more.
+__host__ __device__ constexpr int32_t stage_rows(int32_t nmax, int32_t gshift) {
+    return gshift <= 2 ? nmax << (2 - gshift) : (((nmax << 2) + (1 << gshift) - 1) >> gshift) + 1;
+}
+constexpr int32_t STAGE_ROW_BYTES = SET * 4 + SET;  // scales and zero points of one group row
+
+// gfx950 gives a workgroup up to 160 KB of LDS; a kernel asks for more than 64 KB of
+// dynamic LDS by raising its attribute first (allow_lds).
+constexpr size_t LDS_DEFAULT = 64 << 10, LDS_MAX = 160 << 10;
+// Raises the dynamic-LDS attribute of kernel KERN to LDS_MAX once, when a launch needs
+// more than the default.
+template <auto KERN>
+int32_t allow_lds(size_t lds) {
+    static std::atomic<bool> raised{false};
+    if (lds <= LDS_DEFAULT || raised.load(std::memory_order_acquire)) return KT_OK;
+    KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(LDS_MAX)));
+    raised.store(true, std::memory_order_release);
+    return KT_OK;
+}
+
+inline int32_t log2_exact(int32_t v) {
+    int32_t s = 0;
+    while ((1 << s) < v) ++s;
+    return (1 << s) == v ? s : -1;
+}
+
+// The work split of a launch over weights with K rows, groups of g and sets_total column
+// sets: ks K-parts per column set (a workgroup of eight waves holds 8 / ks sets), nmax
+// chunks at most per wave, and the one-row kernel's LDS (kt_gemv_packed.hip).
+struct PackedPlan {
+    int32_t ks = 0, nmax = 0;
+    size_t lds = 0;
+};
+PackedPlan plan_packed(int32_t K, int32_t g, int64_t sets_total);
+
+}  // namespace kt

@@ -601,6 +601,8 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
     const float* biases[1] = {bias};
     if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_packed_supported(a, m, v, c))
         return launch_gemv_packed(a, &v, &c, biases, 1, accumulate, alpha, st);
+    if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_rows_packed_supported(a, m, v, c))
+        return launch_gemv_rows_packed(a, m, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 4 || (g_gemv_kind == 0 && gemv_strip_preferred(&v, 1))) && gemv_strip_supported(a, m, v, c))
         return launch_gemv_strip(a, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 3 || (g_gemv_kind == 0 && gemv_wide_preferred(&v, 1))) && gemv_wide_supported(a, m, v, c))
@@ -626,6 +628,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         bool wide = (g_gemv_kind == 0 || g_gemv_kind == 3) && a != nullptr;
         bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
         bool packed = (g_gemv_kind == 0 || g_gemv_kind == 5) && a != nullptr;
+        bool rows_packed = packed && m >= 2;
         bool gemm = m > 2 && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
@@ -640,6 +643,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
             strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
             packed = packed && gemv_packed_supported(a, m, v, outputs[start + i]);
+            rows_packed = rows_packed && gemv_rows_packed_supported(a, m, v, outputs[start + i]);
             gemm = gemm && gemm_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 16)) &&
                    (v.z != nullptr) == (views[0].z != nullptr);
         }
@@ -652,6 +656,9 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         if (packed) {
             status = launch_gemv_packed(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,
                                         alpha, st);
+        } else if (rows_packed) {
+            status = launch_gemv_rows_packed(a, m, views, outputs + start, biases ? biases + start : nullptr, n,
+                                             accumulate, alpha, st);
         } else if (strip) {
             status = launch_gemv_strip(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate, alpha, st);
         } else if (wide) {

@@ -35,7 +35,9 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.kt_abi_version() == 2
+    header = (ROOT / "include" / "kotensor_hip.h").read_text()
+    declared = int(re.search(r"#define KT_ABI_VERSION (\d+)", header).group(1))
+    assert lib.kt_abi_version() == declared == 3
     assert kotensor_amd.LIBRARY_PATH.name == "libkotensor_hip.so"
 
 

@@ -265,3 +265,107 @@ def test_packed_swiglu_gate_pairs(kt, oracle_lib):
         _lib.call("kt_rmsnorm_swiglu_gate", dx.ptr, None, ctypes.c_float(1e-5), None, 1, ctypes.byref(small.qweight),
                   ctypes.byref(_packed(kt, qu).qweight), None, None, kt.DeviceBuffer(n * 4).ptr,
                   kt.DeviceBuffer(n * 4).ptr, None)
+
+
+# ---- 2 to 16 rows on the copy (kt_gemv_rows_packed.hip) ------------------------------
+
+ROW_SHAPES = [(896, 896), (896, 4864), (4864, 896), (2048, 2048), (2048, 8192), (8192, 2048), (4096, 14336),
+              (14336, 4096)]
+
+
+@pytest.mark.parametrize("k,n", ROW_SHAPES)
+@pytest.mark.parametrize("bits,g", [(4, 64), (8, 32), (4, 32), (8, 64)])
+def test_packed_rows_match_the_oracle(kt, oracle_lib, k, n, bits, g):
+    """2, 3, 8 and 16 rows on the copy against the oracle's tile kernel (MatMul.kt:830-881),
+    row by row (rows scaled by 1e-6 .. 1e5, one row zero): x is held to 22 bits of its
+    row's largest value and the products are exact, so each row meets the oracle to the
+    one-row kernels' normwise 1e-5."""
+    q = _weights(oracle_lib, k, n, bits, g, 13)
+    qt = _packed(kt, q)
+    rng = np.random.default_rng(k + n + bits + g + 1)
+    for m in (2, 3, 8, 16):
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        x *= (np.float32(10.0) ** rng.integers(-6, 6, size=(m, 1))).astype(np.float32)
+        if m > 2:
+            x[m // 2] = 0.0
+        banner("packed-rows", k, n, bits, g, m)
+        got = gpu_matmul(kt, x, qt, m)
+        want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+        errs = [normwise_rel(got[r], want[r]) for r in range(m)]
+        print(f"  worst row normwise={max(errs):.2e}", flush=True)
+        assert max(errs) <= TOL, errs
+
+
+def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
+    """QuantizationTest.kt:110-134: a and W ~ U(-0.5, 0.5), INT4 g64; m copies of one row
+    give its one-row result within 1e-4 (absolute) -- here within normwise 1e-6, since
+    both sides are exact products with fp32 sums. Beyond the reference's bound, a row's
+    bits on the copy do not depend on how many rows share the call or on what they hold:
+    each row is prepared and multiplied by itself."""
+    rng = np.random.default_rng(41)
+    for k, n in ((320, 2112), (4096, 14336)):
+        a = (rng.random((1, k), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+        w = (rng.random((k, n), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+        st, q = oracle_lib.quantize(w, 4, 64)
+        assert st == 0
+        qt = _packed(kt, q)
+        single = gpu_matmul(kt, a, qt, 1)
+        ref = None
+        for m in (2, 3, 5, 8, 9, 16):
+            banner("packed-rows-batched", k, n, m)
+            batched = gpu_matmul(kt, np.tile(a, (m, 1)), qt, m)
+            diff = float(np.abs(batched - single).max())
+            print(f"  max |batched - single| = {diff:.2e}", flush=True)
+            assert diff < 1e-4 and normwise_rel(batched, np.tile(single, (m, 1))) <= 1e-6, (k, n, m, diff)
+            ref = batched[0] if ref is None else ref
+            assert all(same_bits(batched[r], ref) for r in range(m)), m
+        x = rng.standard_normal((16, k)).astype(np.float32)
+        full = gpu_matmul(kt, x, qt, 16)
+        for rows in ([0, 5, 15], [7, 3], [2, 9, 11, 4, 13]):
+            part = gpu_matmul(kt, x[rows], qt, len(rows))
+            assert all(same_bits(part[i], full[r]) for i, r in enumerate(rows)), rows
+
+
+def test_packed_rows_grouped_accumulate_and_bias(kt, oracle_lib):
+    """Grouped weights of one input (q/k/v, gate/up) at 2..16 rows: one preparation of x,
+    a launch per weight; accumulate, alpha and biases."""
+    rng = np.random.default_rng(42)
+    for m in (2, 5, 16):
+        for k, ns, bits, g in [(2048, (2048, 512, 512), 8, 32), (4096, (14336, 14336), 4, 64), (896, (896, 128, 128), 4, 64)]:
+            banner("packed-rows-group", m, k, ns, bits, g)
+            qs = [_weights(oracle_lib, k, n, bits, g, 50 + i) for i, n in enumerate(ns)]
+            qts = [_packed(kt, q) for q in qs]
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            biases = [rng.standard_normal(n).astype(np.float32) for n in ns]
+            c0 = [rng.standard_normal((m, n)).astype(np.float32) for n in ns]
+            outs = [kt.DeviceBuffer.from_numpy(c) for c in c0]
+            dbias = [kt.DeviceBuffer.from_numpy(b) for b in biases]
+            kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(x), qts, outs, m, accumulate=True,
+                                               alpha=-0.75, biases=dbias)
+            kt.synchronize()
+            for q, o, b, c, n in zip(qs, outs, biases, c0, ns):
+                got = o.download(np.float32).reshape(m, n)
+                want = oracle_lib.multiply_quantized(x, q, m, c=c, accumulate=True, alpha=-0.75, threads=16) + b[None, :]
+                assert normwise_rel(got, want) <= TOL
+
+
+def test_packed_rows_work_splits_agree(kt, oracle_lib):
+    """Every split of a column set's K range over 1, 2, 4 or 8 waves (and the x tiles in
+    one phase or several) gives the oracle's result at 4 and 16 rows."""
+    rng = np.random.default_rng(43)
+    try:
+        for k, n, bits in [(4096, 14336, 4), (2048, 2048, 8), (8192, 2048, 4)]:
+            q = _weights(oracle_lib, k, n, bits, 64, 44)
+            qt = _packed(kt, q)
+            for m in (4, 16):
+                x = rng.standard_normal((m, k), dtype=np.float32)
+                want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+                for ks in (1, 2, 4, 8):
+                    if -(-k // 128) > 16 * ks:
+                        continue
+                    banner("packed-rows-split", k, n, bits, m, ks)
+                    kt.MatMul.set_kernel_config(5, 0, ks, 0, 0)
+                    got = gpu_matmul(kt, x, qt, m)
+                    assert normwise_rel(got, want) <= TOL, (m, ks)
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
