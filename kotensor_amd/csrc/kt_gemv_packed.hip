@@ -37,8 +37,10 @@
 //     then one fp32 fma), sum x q = u * 2^(E - 14), and y += scale * (sum x q - zero *
 //     sum x): the reference's combineGroup, scale * (acc - zero * rowSum)
 //     (MatMul.kt:804-828), applied per run;
-//   * the four lanes of a column (its four runs of a chunk) and the waves that split K
-//     meet by fixed-order sums inside the workgroup.
+//   * K is cut into eight fixed sub-parts (kt_packed.h); a sub-part's sum is its lanes'
+//     runs in K order, then the column's four lanes, and the sub-parts add in a fixed
+//     balanced tree, whose lower levels the wave covering them forms and whose top the
+//     waves that split K form in LDS.
 // A column's result therefore depends only on x and that column's weights, never on
 // how the columns or the K range are divided among waves.
 #include "kt_common.h"
@@ -172,7 +174,6 @@ constexpr int X_PLAIN = 0, X_SWIGLU = 1, X_NORM = 2;
 // after the last.)
 
 constexpr int W = 8;                  // waves per workgroup
-constexpr int MAX_WAVE_CHUNKS = 16;   // a wave's K range: at most 2048
 constexpr int X_SLOTS = MAX_K / (256 * W);  // float4s of x per thread
 
 // The workgroup's LDS: digit rows [4][kp] (kp = 128 chunks bytes), 32 zero bytes, run
@@ -496,9 +497,28 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     const int32_t a_step = diag ? CHUNK : 0;
     const uint32_t mask = 0x0F0F0F0Fu;
     float y = 0.0f;
+    // K is cut into SUB_PARTS sub-parts at chunk (j chunks) / SUB_PARTS, j = 0 .. SUB_PARTS;
+    // a wave's range is SUB_PARTS / ks of them. A sub-part's sum (each lane's runs in K
+    // order, then the column's four lanes, (l0 + l1) + (l2 + l3), by two lane swaps)
+    // enters a balanced tree over the sub-parts in K order: the wave completes the
+    // subtree of its range, the meet adds the top levels. So the result does not depend
+    // on ks, only on K.
+    const int32_t sp_count = SUB_PARTS >> kslog, sp0 = kp * sp_count;
+    int32_t sp = 0;                                                   // the current sub-part
+    int32_t sp_end = (((sp0 + 1) * chunks) >> SUB_LOG) - c_begin;    // its end (wave's chunks)
+    float tree[3] = {0.0f, 0.0f, 0.0f};
+    float part = 0.0f;
+    auto close_sub_part = [&]() {
+        part = tree_push(tree, sp, lanes4_sum(y));
+        y = 0.0f;
+        ++sp;
+        sp_end = (((sp0 + sp + 1) * chunks) >> SUB_LOG) - c_begin;
+    };
     // live = false: a chunk past the wave's range (its weights read as zeros), which adds
     // nothing; its LDS reads stay inside the wave's rows
     auto process = [&](int s, int32_t cc, bool live) {
+        if (live)
+            while (cc >= sp_end) close_sub_part();
         cc = live ? cc : n - 1;
         const int8_t* pa = xd + a_base + cc * a_step;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(pa);
@@ -562,16 +582,14 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         ring_loop();
     }
 
-    // ---- the column's four runs, then the K-parts of the column set, in fixed order ----
-    y += __shfl_xor(y, 16, 64);
-    y += __shfl_xor(y, 32, 64);
-    if (ln < SET) red[wave * SET + ln] = y;
+    // ---- the last sub-parts, then the K-parts of the column set (the tree's top) --------
+    while (sp < sp_count) close_sub_part();
+    if (ln < SET) red[wave * SET + ln] = part;
     __syncthreads();
     [&]() {
         if (kp != 0 || ln >= SET || !set_live) return;
-        const int32_t ks = 1 << kslog, cs = 1 << cslog;
-        float sum = red[my_cs * SET + ln];
-        for (int32_t p = 1; p < ks; ++p) sum += red[(p * cs + my_cs) * SET + ln];
+        const int32_t cs = 1 << cslog;
+        const float sum = tree_top(red + my_cs * SET + ln, cs * SET, kslog);
         float al = alpha;
         if constexpr (XMODE == X_NORM) {
             float sq = red[W * SET];
@@ -581,8 +599,7 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         if constexpr (GLU) {
             // the gate wave of the pair: its partner (slot my_cs + 1) holds up's sums
             if (my_cs & 1) return;
-            float usum = red[(my_cs + 1) * SET + ln];
-            for (int32_t p = 1; p < ks; ++p) usum += red[(p * cs + my_cs + 1) * SET + ln];
+            const float usum = tree_top(red + (my_cs + 1) * SET + ln, cs * SET, kslog);
             float g = fmaf(al, sum, 0.0f);
             if (jb.bias) g += jb.bias[col];
             const PJob& ju = jobs.job[1];

@@ -25,7 +25,8 @@
 //     rows 4 kb .. 4 kb + 3 of column n, and y += scale(group, n) * D per run
 //     (combineGroup, MatMul.kt:804-828, per run); INT4 high nibbles enter as 16 (q - z),
 //     so the prep divides x's parts at those positions by 16 (exact);
-//   * the K-parts of a column set meet in LDS in K-part order, then y * 2^-s_m.
+//   * K's sub-parts (kt_packed.h) are summed alone and added in a fixed tree, whatever
+//     the K split; then y * 2^-s_m.
 // A row's result therefore differs from the one-row kernel's only by the rounding of x to
 // 22 bits and the order of fp32 sums (normwise near 1e-7 against the oracle), and does
 // not depend on the other rows of the call (QuantizationTest.kt:110-134 asks 1e-4).
@@ -267,6 +268,22 @@ __global__ void __launch_bounds__(64 * W)
     // own A rows, and rows past M are never stored
     const int32_t a_lane = kb * M * 16 + min(nl, M - 1) * 16;
     float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // sub-parts of K, each summed alone and added in a balanced tree in K order (the
+    // one-row kernel's scheme): the result does not depend on ks
+    const int32_t sp_count = SUB_PARTS >> kslog, sp0 = kp * sp_count;
+    int32_t sp = 0;
+    int32_t sp_end = (((sp0 + 1) * chunks) >> SUB_LOG) - c_begin;
+    float tree[4][3] = {};
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto close_sub_part = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            part[i] = tree_push(tree[i], sp, y[i]);
+            y[i] = 0.0f;
+        }
+        ++sp;
+        sp_end = (((sp0 + sp + 1) * chunks) >> SUB_LOG) - c_begin;
+    };
     const int32_t run0 = k0 >> 5;  // the wave's first run
     // the slot's weights, transposed: t[r] = k 8 kb .. 8 kb + 7 of run r of the chunk
     // (INT8: t2[r] the next 8 bytes) -- taken out of the ring so the slot refills at once
@@ -292,6 +309,8 @@ __global__ void __launch_bounds__(64 * W)
         }
     };
     auto process = [&](const uint32_t (&t)[4], const uint32_t (&t2)[4], int32_t cl, bool live, int32_t ph) {
+        if (live)
+            while (cl >= sp_end) close_sub_part();
         // a chunk past the wave's range adds nothing; its reads stay in the phase's tiles
         // and the wave's staged rows (the phase's first chunk is below nmax)
         const int32_t cc = live ? cl : ph * cpp;
@@ -374,10 +393,12 @@ __global__ void __launch_bounds__(64 * W)
         }
     }
 
-    // ---- the K-parts of each column set, in K-part order; the row shifts; the stores ----
+    // ---- the last sub-parts; the K-parts of each column set (the tree's top); the row
+    // shifts; the stores
+    while (sp < sp_count) close_sub_part();
     float* red = reinterpret_cast<float*>(smem + rows_lds_red(ks, cpp, M, rows));  // [W][16 rows][16 cols]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * kb + i) * 16 + nl] = y[i];
+    for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * kb + i) * 16 + nl] = part[i];
     __syncthreads();
     if (kp != 0 || !set_live) return;
     const int32_t cs = 1 << cslog;
@@ -385,8 +406,7 @@ __global__ void __launch_bounds__(64 * W)
     for (int i = 0; i < 4; ++i) {
         const int32_t m = 4 * kb + i;
         if (m >= M) continue;
-        float sum = red[(my_cs * 16 + m) * 16 + nl];
-        for (int32_t p = 1; p < ks; ++p) sum += red[((p * cs + my_cs) * 16 + m) * 16 + nl];
+        const float sum = tree_top(red + (my_cs * 16 + m) * 16 + nl, cs * 256, kslog);
         float* dst = out + static_cast<size_t>(m) * N + col;
         float o = accumulate ? *dst : 0.0f;
         const int32_t sh[4] = {rsh.x, rsh.y, rsh.z, rsh.w};
@@ -398,19 +418,34 @@ __global__ void __launch_bounds__(64 * W)
 
 }  // namespace
 
-// The x tiles a phase holds: chunks per phase (a multiple of R, the wave's range rounded
-// up to R when all of it fits in what LDS the staged rows and the meeting area leave),
-// and the LDS of the launch; 0 chunks when not even R chunks fit.
-static int32_t rows_plan(int32_t M, const PackedPlan& plan, int32_t gshift, size_t* lds) {
+// The launch: the one-row kernel's K split (plan_packed), or the largest smaller one
+// whose x tiles fit (the result does not depend on the split); the x tiles a phase holds
+// (chunks per phase: a multiple of R, the wave's range rounded up to R when all of it
+// fits in what LDS the staged rows and the meeting area leave); the LDS. ks = 0: none fits.
+struct RowsPlan {
+    int32_t ks = 0, cpp = 0;
+    size_t lds = 0;
+};
+static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets) {
+    RowsPlan r;
+    const PackedPlan plan = plan_packed(K, g, sets);
+    const int32_t gshift = log2_exact(g / RUN), chunks = ceil_div(K, CHUNK);
     const int32_t tile = run_tile_bytes(M);
-    const int32_t rows = stage_rows(plan.nmax, gshift);
-    const int32_t fixed = rows_lds_bytes(plan.ks, 0, M, rows);
-    if (fixed >= static_cast<int32_t>(LDS_MAX)) return 0;
-    int32_t cpp = (static_cast<int32_t>(LDS_MAX) - fixed) / (plan.ks * 4 * tile);
-    cpp = std::min(cpp, (plan.nmax + R - 1) / R * R) / R * R;
-    if (cpp < R) return 0;
-    *lds = static_cast<size_t>(rows_lds_bytes(plan.ks, cpp, M, rows));
-    return *lds <= LDS_MAX ? cpp : 0;
+    for (int32_t ks = plan.ks; ks >= 1; ks /= 2) {
+        const int32_t nmax = ceil_div(chunks, ks);
+        if (nmax > MAX_WAVE_CHUNKS) break;
+        const int32_t rows = stage_rows(nmax, gshift);
+        const int32_t fixed = rows_lds_bytes(ks, 0, M, rows);
+        if (fixed >= static_cast<int32_t>(LDS_MAX)) continue;
+        int32_t cpp = (static_cast<int32_t>(LDS_MAX) - fixed) / (ks * 4 * tile);
+        cpp = std::min(cpp, (nmax + R - 1) / R * R) / R * R;
+        if (cpp < R) continue;
+        r.ks = ks;
+        r.cpp = cpp;
+        r.lds = static_cast<size_t>(rows_lds_bytes(ks, cpp, M, rows));
+        return r;
+    }
+    return r;
 }
 
 bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
@@ -421,10 +456,7 @@ bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, 
     if (w.N % SET != 0) return false;
     if (static_cast<int64_t>(w.G) * w.N * 4 > INT32_MAX) return false;
     if (!aligned(w.p, 16) || !aligned(a, 16) || !aligned(c, 4)) return false;
-    const PackedPlan plan = plan_packed(w.K, w.g, w.N / SET);
-    if (!plan.ks) return false;
-    size_t lds = 0;
-    return rows_plan(m, plan, log2_exact(w.g / RUN), &lds) != 0;
+    return rows_plan(m, w.K, w.g, w.N / SET).ks != 0;
 }
 
 int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
@@ -445,11 +477,11 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
     KT_LAUNCHED("qmatmul: rows prep kernel");
     for (int32_t i = 0; i < count; ++i) {
         const WeightView& w = ws[i];
-        const PackedPlan plan = plan_packed(w.K, w.g, w.N / SET);
+        const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET);
         const int32_t gshift = log2_exact(w.g / RUN);
-        size_t lds = 0;
-        const int32_t cpp = plan.ks ? rows_plan(m, plan, gshift, &lds) : 0;
-        if (!cpp) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
+        const size_t lds = plan.lds;
+        const int32_t cpp = plan.cpp;
+        if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
         const int32_t kslog = log2_exact(plan.ks);
         const dim3 grid(static_cast<uint32_t>(ceil_div(w.N / SET, W / plan.ks)));
         const int32_t shifts = kslog | gshift << 4;

@@ -17,6 +17,7 @@ constexpr int SET = 16;         // columns per column set
 constexpr int CHUNK = 128;      // k per chunk
 constexpr int RUN = 32;         // k per lane run
 constexpr int NONTEMPORAL = 2;  // buffer-load cache policy: streamed data, read once
+constexpr int MAX_WAVE_CHUNKS = 16;  // a wave's K range: at most 2048 (its staged group rows fit 64)
 __host__ __device__ constexpr int block_bytes(int bits) { return bits == 4 ? 1024 : 2048; }
 
 // Calls f(std::integral_constant<int, I>) for I = B .. E - 1, so register arrays indexed by
@@ -27,6 +28,56 @@ __device__ __forceinline__ void static_for(F&& f) {
         f(std::integral_constant<int, B>{});
         static_for<B + 1, E>(f);
     }
+}
+
+// Sums that do not depend on how K is split: K's chunks are cut into SUB_PARTS sub-parts
+// (sub-part j: chunks [j chunks / SUB_PARTS, (j + 1) chunks / SUB_PARTS)), every
+// sub-part's sum is formed alone, and the sub-parts add as a balanced binary tree in K
+// order. A wave that covers an aligned block of 2^b sub-parts pushes them in order
+// (tree_push) and holds that block's subtree at the end; the K-parts' subtrees then meet
+// in the tree's top levels (tree_top).
+constexpr int SUB_LOG = 3;
+constexpr int SUB_PARTS = 1 << SUB_LOG;  // the largest K split
+
+// Pushes sub-part i's sum v (i: index within the wave's block); t holds the pending left
+// subtrees of sizes 1, 2 and 4. Returns the subtree that v completes (after the block's
+// last push: the block's sum).
+__device__ __forceinline__ float tree_push(float (&t)[3], int32_t i, float v) {
+    if (i & 1) {
+        v = t[0] + v;
+        if (i & 2) {
+            v = t[1] + v;
+            if (i & 4) v = t[2] + v;
+            else t[2] = v;
+        } else {
+            t[1] = v;
+        }
+    } else {
+        t[0] = v;
+    }
+    return v;
+}
+
+// (v_l + v_l^16) + (v_l^32 + v_l^48), the same value in the four lanes: the lane groups'
+// sum in a fixed order by two lane swaps (no LDS path).
+__device__ __forceinline__ float lanes4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // rows (0, 1) and (2, 3)
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// The top levels: the 2^kslog K-parts' subtrees p[0], p[stride], ... added pairwise.
+__device__ __forceinline__ float tree_top(const float* p, int32_t stride, int32_t kslog) {
+    float v[SUB_PARTS];
+#pragma unroll
+    for (int q = 0; q < SUB_PARTS; ++q) v[q] = q < (1 << kslog) ? p[q * stride] : 0.0f;
+#pragma unroll
+    for (int l = 0; l < SUB_LOG; ++l)
+        if (l < kslog)
+#pragma unroll
+            for (int q = 0; q < SUB_PARTS; q += 2 << l) v[q] = v[q] + v[q + (1 << l)];
+    return v[0];
 }
 
 // Groups a wave's range of at most nmax chunks touches (g = 32 << gshift): whole groups
