@@ -23,13 +23,11 @@
 //     are exact, and so is sum(part * (q - z)) = fma(-(1024 + z), sum(part), that sum);
 //   * per unit: res += scale * 2^e * (hi + mid + lo), on every lane (16 columns each);
 //   * a workgroup is 2, 4 or 8 waves on one tile; its waves take the units of its
-//     K-slice round-robin and meet in LDS. With several K-slices, every workgroup adds its
-//     column sums into fp64 accumulators with atomics and the last one of the tile (a
-//     per-tile counter) takes the totals, resetting them to zero. fp32 sums whose
-//     magnitudes lie within 2^(29 - log2 slices) of each other add exactly in fp64, so
-//     the result does not depend on the order of arrival; otherwise the fp64 total can
-//     differ in its last bit, which reaches the fp32 result only when the total lies
-//     within that bit of an fp32 rounding boundary.
+//     K-slice round-robin and meet in LDS. With several K-slices, every workgroup writes
+//     its column sums to its slice's row of partial sums (written through to memory) and
+//     counts in on a per-tile counter; the last one of the tile adds the slices' rows in
+//     slice order and resets the counter. The result therefore does not depend on the
+//     order in which the workgroups finish.
 //
 // Grid shape: one workgroup is one tile x one K-slice. A workgroup's bandwidth is
 // limited (about 45 GB/s for 8 waves on MI355X), so the launcher takes as many K-slices
@@ -57,8 +55,8 @@ struct Job {
     const int8_t* z;
     float* out;
     const float* bias;
-    double* accum;       // [N] fp64 column totals, zero on entry and exit, when slices > 1
-    uint32_t* counters;  // [tiles] when slices > 1
+    float* partial;      // [slices][N] the slices' column sums, when slices > 1
+    uint32_t* counters;  // [tiles], zero on entry and exit, when slices > 1
     int32_t N, bpr, tiles, slices, units_per_slice;
 };
 
@@ -398,29 +396,49 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
 
     if (jb.slices > 1) {
-        // The slices of the tile meet in the fp64 accumulators; the adds are complete
-        // (s_waitcnt) before the counter is taken, and the last workgroup's exchanges
-        // follow its counter read, so it sees every add. Each column is added by one
-        // thread per workgroup: the workgroup's sums are contiguous columns.
+        // The slices of the tile meet through their rows of partial sums. The rows are
+        // written with system-scope stores (written through the caches), and every
+        // thread waits until its own stores are complete (s_waitcnt 0, behind a release
+        // fence that keeps the compiler from sinking a store past it) before the
+        // barrier, so the counter is taken only after the workgroup's row is in memory.
+        // The last workgroup's reads are system-scope loads (past the caches), issued
+        // after it has seen the count (a barrier and an acquire fence keep the compiler
+        // from hoisting them), so they see every slice's row.
+        float* row = jb.partial + static_cast<size_t>(slice) * N;
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i)
-            if (live[i])
-                __hip_atomic_fetch_add(jb.accum + colg[i], static_cast<double>(sum[i]), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+            if (live[i]) __hip_atomic_store(row + colg[i], sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ uint32_t last;
         if (t == 0)
-            last = __hip_atomic_fetch_add(jb.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            last = __hip_atomic_fetch_add(jb.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
                    static_cast<uint32_t>(jb.slices - 1);
         __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         if (!last) return;
+        // eight slices' loads per column in flight at once, then added in slice order
+        constexpr int BATCH = 8;
 #pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i)
-            sum[i] = live[i] ? static_cast<float>(__hip_atomic_exchange(jb.accum + colg[i], 0.0, __ATOMIC_RELAXED,
-                                                                        __HIP_MEMORY_SCOPE_AGENT))
-                             : 0.0f;
-        if (t == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = 0; i < PER_THREAD; ++i) sum[i] = 0.0f;
+        for (int32_t s0 = 0; s0 < jb.slices; s0 += BATCH) {
+            float pv[PER_THREAD][BATCH];
+#pragma unroll
+            for (int i = 0; i < PER_THREAD; ++i)
+#pragma unroll
+                for (int j = 0; j < BATCH; ++j)
+                    pv[i][j] = live[i] && s0 + j < jb.slices
+                                   ? __hip_atomic_load(jb.partial + static_cast<size_t>(s0 + j) * N + colg[i],
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                                   : 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER_THREAD; ++i)
+#pragma unroll
+                for (int j = 0; j < BATCH; ++j)
+                    if (s0 + j < jb.slices) sum[i] = s0 + j == 0 ? pv[i][j] : sum[i] + pv[i][j];
+        }
+        if (t == 0) __hip_atomic_store(jb.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     const float al = XMODE == X_NORM ? alpha * norm_scale(npart, K, eps) : alpha;
 #pragma unroll
@@ -561,16 +579,19 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
         return fail(KT_ERR_ARGUMENT, "wide gemv: K-slice of %d units too long for the x area", plan.ups);
     const int32_t slices = plan.slices;
 
-    size_t n_accs = 0;
+    size_t n_partial = 0;  // floats: each weight's [slices][N]
     if (slices > 1)
-        for (int32_t i = 0; i < count; ++i) n_accs += static_cast<size_t>(ws[i].N);
-    double* accs = nullptr;
+        for (int32_t i = 0; i < count; ++i) n_partial += static_cast<size_t>(slices) * ws[i].N;
+    float* partials = nullptr;
     uint32_t* counters = nullptr;
     if (slices > 1) {
         if (static_cast<size_t>(tiles_total) > MAX_COUNTERS)
             return fail(KT_ERR_ARGUMENT, "wide gemv: too many tiles for the counters");
-        const int32_t status = workspace_accumulators(st, static_cast<size_t>(tiles_total), n_accs, &counters, &accs);
+        void* general = nullptr;
+        const int32_t status = workspace_counters(st, n_partial * sizeof(float), static_cast<size_t>(tiles_total),
+                                                  &general, &counters);
         if (status) return status;
+        partials = static_cast<float*>(general);
     }
     Jobs jobs{};
     jobs.count = count;
@@ -588,9 +609,9 @@ int32_t launch_gemv_wide(const float* a, const WeightView* ws, float* const* cs,
         jb.tiles = ceil_div(ws[i].bpr, TILE);
         jb.slices = slices;
         jb.units_per_slice = plan.ups;
-        jb.accum = slices > 1 ? accs + offset : nullptr;
+        jb.partial = slices > 1 ? partials + offset : nullptr;
         jb.counters = slices > 1 ? counters + coffset : nullptr;
-        offset += static_cast<size_t>(ws[i].N);
+        offset += static_cast<size_t>(slices) * ws[i].N;
         coffset += jb.tiles;
         if (jb.tiles * slices > blocks) blocks = jb.tiles * slices;
     }

@@ -269,7 +269,9 @@ def test_results_are_bit_reproducible(kt, oracle_lib):
 
 
 def test_gemv_work_splits_agree(kt, oracle_lib):
-    """Every lane width and split count of the M == 1 kernel gives the reference's result."""
+    """Every lane width and split count of the M == 1 kernels gives the reference's result,
+    and a repeat gives the same bits (every multi-slice meet adds the slices' partial sums
+    in slice order, whatever order the workgroups finish in)."""
     rng = np.random.default_rng(11)
     try:
         for (k, n, bits) in [(896, 4864, 4), (4096, 1024, 8), (512, 2048, 4)]:
