@@ -37,6 +37,7 @@
 #include <type_traits>
 
 #include "kt_common.h"
+#include "kt_packed.h"
 
 namespace kt {
 namespace {
@@ -653,18 +654,22 @@ __global__ void __launch_bounds__(256)
 // of a column lie in one scale group.
 // Dequantization and scaling are those of gemm_kernel (same fp16 values of the weights and
 // of a, the same powers of two); only the order of the fp32 sums differs.
-constexpr int PT = 128;                  // tile rows and columns
+// Tiles are TM x TN with TM, TN in {64, 128}: 128 x 128 when the tiles fill the CUs,
+// 64-row tiles for M <= 64 (no padded rows), 64-column tiles when 128-column ones leave
+// CUs idle (narrow M).
 constexpr int PTHREADS = 256;
 constexpr int PDEPTH = 3;                // slabs a wave holds or has in flight
-constexpr int PSLAB = PT * 32 * 2;       // bytes of fp16 a per (row tile, slab)
-constexpr int MPITCH = PT + 4;           // floats per row of the epilogue's meet
-constexpr size_t PLDS = 4 * 64 * MPITCH * sizeof(float);  // the meet: four waves x 64 rows, 132 KiB
+__host__ __device__ constexpr int pslab_bytes(int tm) { return tm * 32 * 2; }  // fp16 a per (row tile, slab)
+__host__ __device__ constexpr int mpitch(int tn) { return tn + 4; }            // floats per row of the meet
+// the epilogue's meet: four waves x 64 rows (132 KiB at TN = 128)
+__host__ __device__ constexpr size_t plds_bytes(int tn) { return 4 * 64 * mpitch(tn) * sizeof(float); }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Rows of a in the tiled fp16 order above, one wave per row (blocks [0, Mp / 4)), then the
-// scale slices as gemm_prep. S = slabs (K rounded up to 128, over 32).
-template <int BITS>
+// Rows of a in the tiled fp16 order above (row tiles of TM rows), one wave per row
+// (blocks [0, Mp / 4)), then the scale slices as gemm_prep. S = slabs (K rounded up to
+// 128, over 32).
+template <int BITS, int TM>
 __global__ void __launch_bounds__(256)
     gemm_prep_tiled(const float* __restrict__ a, int32_t M, int32_t K, int32_t S, int32_t vec_rows, int32_t Mp,
                     GemmJobs jobs, _Float16* __restrict__ a16t, int32_t* __restrict__ er, float* __restrict__ smax) {
@@ -676,13 +681,14 @@ __global__ void __launch_bounds__(256)
     }
     const int32_t m = b * 4 + (threadIdx.x >> 6);
     const int32_t ln = threadIdx.x & 63;
-    const int32_t tm = m / PT, r = m % PT, rb = r / 32, rl = r % 32;
+    const int32_t tm = m / TM, r = m % TM, rb = r / 32, rl = r % 32;
     // the piece holding k = 32 sp + 8 o8 .. + 8 of this row
     auto piece = [&](int32_t sp, int32_t o8) -> u32x4* {
         const int32_t q = o8 >> 1, i = o8 & 1;
         const int32_t slab = BITS == 8 ? sp : 2 * (sp >> 1) + q;
         const int32_t hl = BITS == 8 ? q : (sp & 1);
-        return reinterpret_cast<u32x4*>(a16t) + ((static_cast<size_t>(tm) * S + slab) * 8 + rb * 2 + i) * 64 + rl + 32 * hl;
+        return reinterpret_cast<u32x4*>(a16t) + ((static_cast<size_t>(tm) * S + slab) * (TM / 16) + rb * 2 + i) * 64 +
+               rl + 32 * hl;
     };
     if (m >= M) {
         for (int32_t sp = ln; sp < S; sp += 64)
@@ -738,27 +744,29 @@ __global__ void __launch_bounds__(256)
     if (ln == 0) er[m] = e;
 }
 
-// One slab of a wave: a pieces (2 rb + i), the weight bytes of its four column blocks, and
+// One slab of a wave: a pieces (2 rb + i), the weight bytes of its CB column blocks, and
 // their scales and zero points.
-template <int BITS>
+template <int BITS, int RB, int CB>
 struct PSlab {
-    u32x4 a[8];
-    typename std::conditional<BITS == 8, u32x4, u32x2>::type w[4];
-    float s[4];
-    uint32_t z[4];  // the dword holding the column's zero byte
+    u32x4 a[2 * RB];
+    typename std::conditional<BITS == 8, u32x4, u32x2>::type w[CB];
+    float s[CB];
+    uint32_t z[CB];  // the dword holding the column's zero byte
 };
 
 // v_perm_b32 selectors: bytes (0, 1) or (2, 3) of a word into the low bytes of its halves.
 constexpr uint32_t SEL01 = 0x0c010c00u, SEL23 = 0x0c030c02u;
 
-template <int BITS, bool ZP>
+template <int BITS, bool ZP, int TM, int TN>
 __global__ void __launch_bounds__(PTHREADS, 1)
     gemm_packed_kernel(const _Float16* __restrict__ a16t, const int32_t* __restrict__ er,
                        const float* __restrict__ smax_all, GemmJobs jobs, int32_t M, int32_t K, int32_t S, int32_t g,
                        int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t slabs_per_split, float alpha,
                        int32_t accumulate) {
-    extern __shared__ f32x4 meet[];  // the epilogue's meet, PLDS bytes
-    __shared__ int32_t er_s[PT];
+    constexpr int RB = TM / 32, CB = TN / 32;  // 32 x 32 row and column blocks
+    constexpr int PSLAB = pslab_bytes(TM), MPITCH = mpitch(TN);
+    extern __shared__ f32x4 meet[];  // the epilogue's meet, plds_bytes(TN)
+    __shared__ int32_t er_s[TM];
     __shared__ float red[4];
 
     // Block -> (tile_n, tile_m, slice) as gemm_kernel: the workgroups of one weight tile on one XCD.
@@ -773,15 +781,15 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     const int32_t rem = jx % per_n;
     const int32_t tile_m = rem % tiles_m;
     const int32_t sp = rem / tiles_m;
-    const int32_t col0 = (tile_n - jb.tile_begin) * PT;
-    const int32_t m0 = tile_m * PT;
+    const int32_t col0 = (tile_n - jb.tile_begin) * TN;
+    const int32_t m0 = tile_m * TM;
     const int32_t t = threadIdx.x, ln = t & 63, hl = ln >> 5;
     const int32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int32_t s_begin = sp * slabs_per_split;
     const int32_t n_mine = (min(S, s_begin + slabs_per_split) - s_begin) / 4;  // >= 1: the host keeps slices whole
 
     const float smx = t < nsb ? smax_all[jb.smax_begin + t] : 0.0f;  // nsb <= 256
-    const int32_t erv = t < PT && m0 + t < M ? er[m0 + t] : 0;
+    const int32_t erv = t < TM && m0 + t < M ? er[m0 + t] : 0;
 
     const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(a16t) + static_cast<size_t>(tile_m) * S * (PSLAB / 2), 0, S * PSLAB, 0x00020000);
@@ -793,10 +801,10 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         const_cast<int8_t*>(ZP ? jb.z : nullptr), 0, ZP ? static_cast<uint32_t>(G) * N : 0u, 0x00020000);
 
     // Lane offsets fixed for the whole loop.
-    uint32_t w_off[4], z_shift[4];
-    int32_t col_c[4];
+    uint32_t w_off[CB], z_shift[CB];
+    int32_t col_c[CB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < CB; ++j) {
         const int32_t col = col0 + 32 * j + (ln & 31);
         const int32_t set = min(col >> 4, sets - 1);  // past the last column: any valid bytes, outputs dropped
         w_off[j] = static_cast<uint32_t>(set) * chunks * (BITS == 8 ? 2048u : 1024u) +
@@ -804,14 +812,14 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         col_c[j] = min(col, N - 1);
         z_shift[j] = 8u * (col_c[j] & 3);
     }
-    auto load = [&](PSlab<BITS>& d, int32_t x) {
+    auto load = [&](PSlab<BITS, RB, CB>& d, int32_t x) {
         const int32_t s = s_begin + wave + 4 * min(x, n_mine - 1);
 #pragma unroll
-        for (int pc = 0; pc < 8; ++pc)
+        for (int pc = 0; pc < 2 * RB; ++pc)
             d.a[pc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, (pc * 64 + ln) * 16, s * PSLAB, 0));
         const int32_t wso = BITS == 8 ? (s >> 2) * 2048 + (s & 3) * 256 : (s >> 2) * 1024 + ((s >> 1) & 1) * 512 + (s & 1) * 8;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < CB; ++j) {
             if constexpr (BITS == 8)
                 d.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, w_off[j], wso, 0));
             else
@@ -820,7 +828,7 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         const int32_t kg = BITS == 8 ? 32 * s : 64 * (s >> 1) + 32 * hl;  // first k of the lane's run
         const int32_t grp = min(kg / g, G - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < CB; ++j) {
             const uint32_t at = static_cast<uint32_t>(grp) * N + col_c[j];
             d.s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, at * 4, 0, 0));
             // the dword holding the zero byte (N % 4 == 0: it lies inside the array); a byte
@@ -829,31 +837,31 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         }
     };
 
-    PSlab<BITS> sl[PDEPTH];
+    PSlab<BITS, RB, CB> sl[PDEPTH];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d + 1 < PDEPTH; ++d) {
         load(sl[d], d);  // in slab order: the loop's waits count on it
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (t < PT) er_s[t] = erv;
+    if (t < TM) er_s[t] = erv;
     const int32_t ew = scale_exponent(block_max<PTHREADS / 64>(smx, red), 7);
     __builtin_amdgcn_sched_barrier(0);
 
-    float16v acc[4][4];
+    float16v acc[RB][CB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < CB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     // Dequantizes sub-product i of one slab's weights (the fp16 values gemm_kernel's
     // store_piece makes): column block j's operand into b[j]. Sub-product 0 also turns the
     // slab's scales and zero points into their fp16 forms, kept in s and z for sub-product 1.
-    auto dequant = [&](PSlab<BITS>& d, int i, half8 (&b)[4]) {
+    auto dequant = [&](PSlab<BITS, RB, CB>& d, int i, half8 (&b)[CB]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < CB; ++j) {
             if constexpr (BITS == 8) {
                 if (i == 0) {
                     const float sc = ldexpf(d.s[j], -ew);
@@ -901,13 +909,13 @@ __global__ void __launch_bounds__(PTHREADS, 1)
             }
         }
     };
-    // The 16 products of sub-product i of one slab.
-    auto multiply = [&](const PSlab<BITS>& d, int i, const half8 (&b)[4]) {
+    // The RB x CB products of sub-product i of one slab.
+    auto multiply = [&](const PSlab<BITS, RB, CB>& d, int i, const half8 (&b)[CB]) {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             const half8 av = __builtin_bit_cast(half8, d.a[rb * 2 + i]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < CB; ++j)
                 acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[j], acc[rb][j], 0, 0, 0);
         }
     };
@@ -917,32 +925,28 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     // sub-product is dequantized. One MFMA, then a few vector ALU and memory instructions, in
     // turn (sched_group_barrier), so the matrix unit is not left idle while operands are
     // prepared and the loads go out spread over the step.
-    half8 b0[4], b1[4];
-    constexpr int NLOADS = 8 + 4 + 4 + (ZP ? 4 : 0);  // vector memory instructions per slab
-    auto step = [&](PSlab<BITS>& d, PSlab<BITS>& nx, PSlab<BITS>& refill, int32_t refill_x) {
+    half8 b0[CB], b1[CB];
+    constexpr int NLOADS = 2 * RB + 2 * CB + (ZP ? CB : 0);  // vector memory instructions per slab
+    constexpr int NMF = RB * CB;                             // MFMAs per sub-product
+    constexpr int VPER = (20 * CB + NMF - 1) / NMF;          // dequantization VALU per MFMA (about)
+    auto step = [&](PSlab<BITS, RB, CB>& d, PSlab<BITS, RB, CB>& nx, PSlab<BITS, RB, CB>& refill, int32_t refill_x) {
         multiply(d, 0, b0);
         dequant(d, 1, b1);
         load(refill, refill_x);  // past the end: the last slab again, never used
-#pragma unroll
-        for (int k = 0; k < NLOADS - 16; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // vector ALU
-            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // loads
-        }
-#pragma unroll
-        for (int k = NLOADS - 16; k < 16; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
+        static_for<0, NMF>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int nl = NLOADS / NMF + (k < NLOADS % NMF ? 1 : 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, VPER - 1, 0);          // vector ALU
+            if constexpr (nl > 0) __builtin_amdgcn_sched_group_barrier(0x020, nl, 0);  // loads
+        });
         __builtin_amdgcn_sched_barrier(0);
         multiply(d, 1, b1);
         dequant(nx, 0, b0);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
+        static_for<0, NMF>([&](auto) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-        }
+            __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
+        });
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -975,29 +979,30 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     const float* bs = jb.partials ? nullptr : jb.bias;
     const float al = jb.partials ? 1.0f : alpha;
     const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
-        out + static_cast<size_t>(m0) * N, 0, static_cast<uint32_t>(min(M - m0, PT)) * N * 4, 0x00020000);
+        out + static_cast<size_t>(m0) * N, 0, static_cast<uint32_t>(min(M - m0, TM)) * N * 4, 0x00020000);
     float* mt = reinterpret_cast<float*>(meet);  // [wave][64 rows][MPITCH]
-    const int32_t c4 = t & 31, rsub = t >> 5;      // this thread's column quad and row within 8
+    constexpr int QPR = TN / 4, RPI = PTHREADS / QPR, ITEMS = 64 / RPI;  // quads a row, rows an item, items
+    const int32_t c4 = t % QPR, rsub = t / QPR;  // this thread's column quad and row within RPI
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < TM / 64; ++half) {
         __syncthreads();  // er_s written; the previous half's meet read
 #pragma unroll
         for (int rl = 0; rl < 2; ++rl)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < CB; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int32_t r = rl * 32 + (e >> 2) * 8 + (ln >> 5) * 4 + (e & 3);
                     mt[(wave * 64 + r) * MPITCH + j * 32 + (ln & 31)] = acc[half * 2 + rl][j][e];
                 }
         __syncthreads();
-        // item it: row it * 8 + rsub of the half, columns 4 c4 .. 4 c4 + 3
+        // item it: row it * RPI + rsub of the half, columns 4 c4 .. 4 c4 + 3
         auto offset = [&](int it) -> uint32_t {
-            const int32_t rt = half * 64 + it * 8 + rsub;  // tile row
+            const int32_t rt = half * 64 + it * RPI + rsub;  // tile row
             return m0 + rt < M && col0 + 4 * c4 < N ? static_cast<uint32_t>(rt * N + col0 + 4 * c4) * 4u : 0x80000000u;
         };
         auto total = [&](int it) -> f32x4 {
-            const int32_t r = it * 8 + rsub;
+            const int32_t r = it * RPI + rsub;
             const int32_t idx = r * MPITCH + 4 * c4;
             f32x4 v = *reinterpret_cast<const f32x4*>(mt + idx);
 #pragma unroll
@@ -1006,17 +1011,17 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         };
         auto store = [&](auto loads) {
             constexpr bool LOADS = decltype(loads)::value;
-            f32x4 old[8];
+            f32x4 old[ITEMS];
             f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             if constexpr (LOADS) {
                 if (bs) bv = *reinterpret_cast<const f32x4*>(bs + min(col0 + 4 * c4, N - 4));
 #pragma unroll
-                for (int it = 0; it < 8; ++it)
+                for (int it = 0; it < ITEMS; ++it)
                     old[it] = add ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(orr, offset(it), 0, 0))
                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
 #pragma unroll
-            for (int it = 0; it < 8; ++it) {
+            for (int it = 0; it < ITEMS; ++it) {
                 const f32x4 sm = total(it);
                 f32x4 v;
 #pragma unroll
@@ -1083,21 +1088,25 @@ static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
     return true;
 }
 
-static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
-                                  const float* const* biases, int32_t count, int32_t accumulate, float alpha,
-                                  hipStream_t st) {
+// The launch of one tile shape: the prep (a in the tiled fp16 order of TM-row tiles, the
+// scale maxima), the kernel, and the slices' reduction when K is split.
+template <int TM, int TN>
+static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                        const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                        hipStream_t st) {
     const WeightView& w = ws[0];
-    const int32_t Mp = ceil_div(m, PT) * PT;
+    const int32_t Mp = ceil_div(m, TM) * TM;
     const int32_t chunks = ceil_div(w.K, 128);
     const int32_t S = chunks * 4;
     int32_t tiles_n = 0;
-    for (int32_t i = 0; i < count; ++i) tiles_n += ceil_div(ws[i].N, PT);
-    const int32_t tiles_m = Mp / PT;
-    // Split K (in whole 128-k chunks, at least two per slice) when the tiles leave CUs idle.
+    for (int32_t i = 0; i < count; ++i) tiles_n += ceil_div(ws[i].N, TN);
+    const int32_t tiles_m = Mp / TM;
+    // Split K (in whole 128-k chunks, at least two per slice) when the tiles leave CUs
+    // idle, into as many slices as keep one round of workgroups (one per CU).
     int32_t splits = 1;
     const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
     const int32_t cus = cu_count();
-    if (tiles < cus) splits = static_cast<int32_t>((cus + tiles - 1) / tiles);
+    if (tiles < cus) splits = static_cast<int32_t>(cus / tiles);
     const int32_t cap = chunks / 2 > 1 ? chunks / 2 : 1;
     if (splits > cap) splits = cap;
     if (splits > MAX_SPLITS) splits = MAX_SPLITS;
@@ -1107,7 +1116,7 @@ static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* w
     GemmJobs jobs;
     int32_t nsb_total = 0;
     size_t part_elems = 0;
-    fill_jobs(jobs, ws, cs, biases, count, PT, true, splits, m, &nsb_total, &part_elems);
+    fill_jobs(jobs, ws, cs, biases, count, TN, true, splits, m, &nsb_total, &part_elems);
     auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t a16_bytes = round256(static_cast<size_t>(Mp) * S * 64);
     const size_t er_bytes = round256(static_cast<size_t>(Mp) * 4);
@@ -1127,25 +1136,27 @@ static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* w
     const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
     const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4 + nsb_total);
     if (w.bits == 4)
-        gemm_prep_tiled<4><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+        gemm_prep_tiled<4, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
     else
-        gemm_prep_tiled<8><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+        gemm_prep_tiled<8, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
     KT_LAUNCHED("qmatmul: tiled gemm prep");
+    constexpr size_t lds = plds_bytes(TN);
     static bool raised = false;
-    if (!raised) {  // the epilogue's 128 KiB meet is beyond the default dynamic LDS limit
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<4, true>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, true>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, false>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(PLDS)));
+    if (!raised && lds > LDS_DEFAULT) {  // the meet is beyond the default dynamic LDS limit (exactly
+        // what it needs: the kernel's static LDS comes on top)
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<4, true, TM, TN>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, true, TM, TN>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, false, TM, TN>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         raised = true;
     }
     const uint32_t blocks = static_cast<uint32_t>(ceil_div(tiles_n, XCDS) * XCDS * tiles_m * splits);
 #define KT_GEMM_ARGS a16t, er, smax, jobs, m, w.K, S, w.g, tiles_m, tiles_n, splits, chunks_per_split * 4, alpha, accumulate
-    if (w.bits == 4) gemm_packed_kernel<4, true><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
-    else if (w.z) gemm_packed_kernel<8, true><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
-    else gemm_packed_kernel<8, false><<<blocks, PTHREADS, PLDS, st>>>(KT_GEMM_ARGS);
+    if (w.bits == 4) gemm_packed_kernel<4, true, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
+    else if (w.z) gemm_packed_kernel<8, true, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
+    else gemm_packed_kernel<8, false, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
 #undef KT_GEMM_ARGS
     KT_LAUNCHED("qmatmul: packed gemm kernel");
     for (int32_t i = 0; i < count && splits > 1; ++i) {
@@ -1155,6 +1166,22 @@ static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* w
         KT_LAUNCHED("qmatmul: gemm reduce");
     }
     return KT_OK;
+}
+
+// Tile shape: 64-row tiles when M <= 64 (a 128-row tile would be half padding), 64-column
+// tiles when 128-column ones number fewer than the CUs.
+static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                  const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                  hipStream_t st) {
+    const bool rows64 = m <= 64;
+    int64_t tiles128 = 0;
+    for (int32_t i = 0; i < count; ++i) tiles128 += ceil_div(ws[i].N, 128);
+    tiles128 *= ceil_div(m, rows64 ? 64 : 128);
+    const bool cols64 = tiles128 < cu_count();
+    if (rows64 && cols64) return launch_gemm_packed_tiles<64, 64>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    if (rows64) return launch_gemm_packed_tiles<64, 128>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    if (cols64) return launch_gemm_packed_tiles<128, 64>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    return launch_gemm_packed_tiles<128, 128>(a, m, ws, cs, biases, count, accumulate, alpha, st);
 }
 
 int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float* const* cs, const float* const* biases,
