@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KT_ABI_VERSION 3
+#define KT_ABI_VERSION 4
 
 /* Status codes. */
 #define KT_OK 0
@@ -160,8 +160,10 @@ int32_t kt_qweight_check(const kt_qweight* w);
  * groups of its K range as contiguous bytes. It is a device-side accelerator next to
  * qdata, scales and zeros, not a format: files, quantize and the accessors keep using
  * those. Write it once after they are final (and again if they change), then set
- * kt_qweight.packed. Size: sets * ceil(rows / 128) * (bits == 4 ? 1024 : 2048) + sets *
- * ceil(rows / group_size) * 80 bytes with sets = ceil(columns / 16), 16-byte aligned. */
+ * kt_qweight.packed. It ends in a 16-byte trailer: the weight's largest |scale| (fp32,
+ * NaNs ignored), which the prefill GEMM takes as its dequantization range, then zeros.
+ * Size: sets * ceil(rows / 128) * (bits == 4 ? 1024 : 2048) + sets * ceil(rows /
+ * group_size) * 80 + 16 bytes with sets = ceil(columns / 16), 16-byte aligned. */
 int32_t kt_qweight_packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size, int64_t* bytes);
 /* Writes the copy of w's qdata, scales and zeros into `packed` (kt_qweight_packed_bytes
  * bytes of device memory, 16-byte aligned); w->packed is ignored. Asynchronous. */

@@ -169,6 +169,9 @@ bool gemv_strip_preferred(const WeightView* ws, int32_t count);
 // wave; 0 = automatic).
 int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size);
 int64_t packed_weight_bytes(int32_t rows, int32_t columns, int32_t bits);  // the weight blocks alone
+// The copy ends in a 16-byte trailer: the largest |scale| of the weight (fp32), then zeros.
+constexpr int64_t PACKED_TRAILER_BYTES = 16;
+const float* packed_scale_max(const WeightView& w);  // the trailer's maximum (device address)
 int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st);
 bool gemv_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
 // glu: ws[0], ws[1] are SwiGLU's gate and up weights; cs[0] receives silu(gate) * up and

@@ -76,7 +76,8 @@ constexpr int MAX_GEMM_JOBS = 4;
 // smax[smax_begin .. smax_begin + nsb).
 struct GemmJob {
     const uint8_t* q;
-    const uint8_t* p;  // the column-run copy (gemm_packed_kernel)
+    const uint8_t* p;     // the column-run copy (gemm_packed_kernel)
+    const float* pmax;    // its largest |scale| (the copy's trailer)
     const float* s;
     const int8_t* z;
     float* c;
@@ -658,7 +659,6 @@ __global__ void __launch_bounds__(256)
 // 64-row tiles for M <= 64 (no padded rows), 64-column tiles when 128-column ones leave
 // CUs idle (narrow M).
 constexpr int PTHREADS = 256;
-constexpr int PDEPTH = 3;                // slabs a wave holds or has in flight
 __host__ __device__ constexpr int pslab_bytes(int tm) { return tm * 32 * 2; }  // fp16 a per (row tile, slab)
 __host__ __device__ constexpr int mpitch(int tn) { return tn + 4; }            // floats per row of the meet
 // the epilogue's meet: four waves x 64 rows (132 KiB at TN = 128)
@@ -667,19 +667,14 @@ __host__ __device__ constexpr size_t plds_bytes(int tn) { return 4 * 64 * mpitch
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Rows of a in the tiled fp16 order above (row tiles of TM rows), one wave per row
-// (blocks [0, Mp / 4)), then the scale slices as gemm_prep. S = slabs (K rounded up to
-// 128, over 32).
+// (Mp / 4 blocks; the weights' scale maxima come from their copies). S = slabs (K rounded
+// up to 128, over 32).
 template <int BITS, int TM>
 __global__ void __launch_bounds__(256)
     gemm_prep_tiled(const float* __restrict__ a, int32_t M, int32_t K, int32_t S, int32_t vec_rows, int32_t Mp,
-                    GemmJobs jobs, _Float16* __restrict__ a16t, int32_t* __restrict__ er, float* __restrict__ smax) {
-    __shared__ float red[4];
-    const int32_t b = blockIdx.x;
-    if (b >= Mp / 4) {
-        scale_slice_max(jobs, b - Mp / 4, red, smax);
-        return;
-    }
-    const int32_t m = b * 4 + (threadIdx.x >> 6);
+                    _Float16* __restrict__ a16t, int32_t* __restrict__ er) {
+    (void)Mp;
+    const int32_t m = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int32_t ln = threadIdx.x & 63;
     const int32_t tm = m / TM, r = m % TM, rb = r / 32, rl = r % 32;
     // the piece holding k = 32 sp + 8 o8 .. + 8 of this row
@@ -718,8 +713,7 @@ __global__ void __launch_bounds__(256)
                 v[h][c] = sp < S ? row_chunk(row, sp * 8 + c, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 mx = fmaxf(mx, absmax(v[h][c]));
             }
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        mx = wave_max64(mx);
         const int32_t e = scale_exponent(mx, 15);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -733,8 +727,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int c = 0; c < 8; ++c) mx = fmaxf(mx, absmax(row_chunk(row, sp * 8 + c, K, vec)));
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max64(mx);
     const int32_t e = scale_exponent(mx, 15);
     for (int32_t sp = ln; sp < S; sp += 64) {
 #pragma unroll
@@ -757,17 +750,18 @@ struct PSlab {
 // v_perm_b32 selectors: bytes (0, 1) or (2, 3) of a word into the low bytes of its halves.
 constexpr uint32_t SEL01 = 0x0c010c00u, SEL23 = 0x0c030c02u;
 
-template <int BITS, bool ZP, int TM, int TN>
+// PDEPTH: slabs a wave holds or has in flight (3 for the larger tiles; the 64 x 64 tile of
+// narrow M, whose waves have few registers of sums and a long K range each, holds 8).
+template <int BITS, bool ZP, int TM, int TN, int PDEPTH>
 __global__ void __launch_bounds__(PTHREADS, 1)
-    gemm_packed_kernel(const _Float16* __restrict__ a16t, const int32_t* __restrict__ er,
-                       const float* __restrict__ smax_all, GemmJobs jobs, int32_t M, int32_t K, int32_t S, int32_t g,
+    gemm_packed_kernel(const _Float16* __restrict__ a16t, const int32_t* __restrict__ er, GemmJobs jobs, int32_t M,
+                       int32_t K, int32_t S, int32_t g,
                        int32_t tiles_m, int32_t tiles_n, int32_t splits, int32_t slabs_per_split, float alpha,
                        int32_t accumulate) {
     constexpr int RB = TM / 32, CB = TN / 32;  // 32 x 32 row and column blocks
     constexpr int PSLAB = pslab_bytes(TM), MPITCH = mpitch(TN);
     extern __shared__ f32x4 meet[];  // the epilogue's meet, plds_bytes(TN)
     __shared__ int32_t er_s[TM];
-    __shared__ float red[4];
 
     // Block -> (tile_n, tile_m, slice) as gemm_kernel: the workgroups of one weight tile on one XCD.
     const int32_t pid = blockIdx.x;
@@ -776,7 +770,7 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     const int32_t tile_n = (jx / per_n) * XCDS + pid % XCDS;
     if (tile_n >= tiles_n) return;
     const GemmJob& jb = jobs.job[job_of_tile(jobs, tile_n)];
-    const int32_t N = jb.N, nsb = jb.nsb;
+    const int32_t N = jb.N;
     const int32_t sets = (N + 15) / 16, chunks = S / 4, G = (K + g - 1) / g;
     const int32_t rem = jx % per_n;
     const int32_t tile_m = rem % tiles_m;
@@ -788,7 +782,7 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     const int32_t s_begin = sp * slabs_per_split;
     const int32_t n_mine = (min(S, s_begin + slabs_per_split) - s_begin) / 4;  // >= 1: the host keeps slices whole
 
-    const float smx = t < nsb ? smax_all[jb.smax_begin + t] : 0.0f;  // nsb <= 256
+    const float smx = *jb.pmax;  // the weight's largest |scale|, from its copy
     const int32_t erv = t < TM && m0 + t < M ? er[m0 + t] : 0;
 
     const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
@@ -845,7 +839,7 @@ __global__ void __launch_bounds__(PTHREADS, 1)
         __builtin_amdgcn_sched_barrier(0);
     }
     if (t < TM) er_s[t] = erv;
-    const int32_t ew = scale_exponent(block_max<PTHREADS / 64>(smx, red), 7);
+    const int32_t ew = scale_exponent(smx, 7);
     __builtin_amdgcn_sched_barrier(0);
 
     float16v acc[RB][CB];
@@ -1057,6 +1051,7 @@ static void fill_jobs(GemmJobs& jobs, const WeightView* ws, float* const* cs, co
         GemmJob& jb = jobs.job[i];
         jb.q = ws[i].q;
         jb.p = ws[i].p;
+        jb.pmax = ws[i].p ? packed_scale_max(ws[i]) : nullptr;
         jb.s = ws[i].s;
         jb.z = ws[i].z;
         jb.c = cs[i];
@@ -1090,7 +1085,7 @@ static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
 
 // The launch of one tile shape: the prep (a in the tiled fp16 order of TM-row tiles, the
 // scale maxima), the kernel, and the slices' reduction when K is split.
-template <int TM, int TN>
+template <int TM, int TN, int PD>
 static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightView* ws, float* const* cs,
                                         const float* const* biases, int32_t count, int32_t accumulate, float alpha,
                                         hipStream_t st) {
@@ -1114,49 +1109,47 @@ static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightV
     splits = ceil_div(chunks, chunks_per_split);
 
     GemmJobs jobs;
-    int32_t nsb_total = 0;
+    int32_t nsb_total = 0;  // the scale maxima come from the copies' trailers: no scale blocks
     size_t part_elems = 0;
     fill_jobs(jobs, ws, cs, biases, count, TN, true, splits, m, &nsb_total, &part_elems);
     auto round256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t a16_bytes = round256(static_cast<size_t>(Mp) * S * 64);
     const size_t er_bytes = round256(static_cast<size_t>(Mp) * 4);
-    const size_t smax_bytes = round256(static_cast<size_t>(nsb_total) * 4);
     void* wsp = nullptr;
-    int32_t status = workspace(st, a16_bytes + er_bytes + smax_bytes + part_elems * sizeof(float), &wsp);
+    int32_t status = workspace(st, a16_bytes + er_bytes + part_elems * sizeof(float), &wsp);
     if (status) return status;
     char* base = static_cast<char*>(wsp);
     _Float16* a16t = reinterpret_cast<_Float16*>(base);
     int32_t* er = reinterpret_cast<int32_t*>(base + a16_bytes);
-    float* smax = reinterpret_cast<float*>(base + a16_bytes + er_bytes);
-    float* part = reinterpret_cast<float*>(base + a16_bytes + er_bytes + smax_bytes);
+    float* part = reinterpret_cast<float*>(base + a16_bytes + er_bytes);
     for (int32_t i = 0; i < count && splits > 1; ++i) {
         jobs.job[i].partials = part;
         part += static_cast<size_t>(splits) * m * ws[i].N;
     }
     const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
-    const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4 + nsb_total);
+    const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4);
     if (w.bits == 4)
-        gemm_prep_tiled<4, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+        gemm_prep_tiled<4, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
     else
-        gemm_prep_tiled<8, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, jobs, a16t, er, smax);
+        gemm_prep_tiled<8, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
     KT_LAUNCHED("qmatmul: tiled gemm prep");
     constexpr size_t lds = plds_bytes(TN);
     static bool raised = false;
     if (!raised && lds > LDS_DEFAULT) {  // the meet is beyond the default dynamic LDS limit (exactly
         // what it needs: the kernel's static LDS comes on top)
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<4, true, TM, TN>),
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<4, true, TM, TN, PD>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, true, TM, TN>),
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, true, TM, TN, PD>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, false, TM, TN>),
+        KT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_packed_kernel<8, false, TM, TN, PD>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         raised = true;
     }
     const uint32_t blocks = static_cast<uint32_t>(ceil_div(tiles_n, XCDS) * XCDS * tiles_m * splits);
-#define KT_GEMM_ARGS a16t, er, smax, jobs, m, w.K, S, w.g, tiles_m, tiles_n, splits, chunks_per_split * 4, alpha, accumulate
-    if (w.bits == 4) gemm_packed_kernel<4, true, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
-    else if (w.z) gemm_packed_kernel<8, true, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
-    else gemm_packed_kernel<8, false, TM, TN><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
+#define KT_GEMM_ARGS a16t, er, jobs, m, w.K, S, w.g, tiles_m, tiles_n, splits, chunks_per_split * 4, alpha, accumulate
+    if (w.bits == 4) gemm_packed_kernel<4, true, TM, TN, PD><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
+    else if (w.z) gemm_packed_kernel<8, true, TM, TN, PD><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
+    else gemm_packed_kernel<8, false, TM, TN, PD><<<blocks, PTHREADS, lds, st>>>(KT_GEMM_ARGS);
 #undef KT_GEMM_ARGS
     KT_LAUNCHED("qmatmul: packed gemm kernel");
     for (int32_t i = 0; i < count && splits > 1; ++i) {
@@ -1168,6 +1161,7 @@ static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightV
     return KT_OK;
 }
 
+constexpr int GEMM_NARROW_DEPTH = 5;  // the 64 x 64 tile's ring (3, 5, 8 measured alike; 5 a little ahead)
 // Tile shape: 64-row tiles when M <= 64 (a 128-row tile would be half padding), 64-column
 // tiles when 128-column ones number fewer than the CUs.
 static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
@@ -1178,10 +1172,11 @@ static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* w
     for (int32_t i = 0; i < count; ++i) tiles128 += ceil_div(ws[i].N, 128);
     tiles128 *= ceil_div(m, rows64 ? 64 : 128);
     const bool cols64 = tiles128 < cu_count();
-    if (rows64 && cols64) return launch_gemm_packed_tiles<64, 64>(a, m, ws, cs, biases, count, accumulate, alpha, st);
-    if (rows64) return launch_gemm_packed_tiles<64, 128>(a, m, ws, cs, biases, count, accumulate, alpha, st);
-    if (cols64) return launch_gemm_packed_tiles<128, 64>(a, m, ws, cs, biases, count, accumulate, alpha, st);
-    return launch_gemm_packed_tiles<128, 128>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    if (rows64 && cols64)
+        return launch_gemm_packed_tiles<64, 64, GEMM_NARROW_DEPTH>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    if (rows64) return launch_gemm_packed_tiles<64, 128, 3>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    if (cols64) return launch_gemm_packed_tiles<128, 64, 3>(a, m, ws, cs, biases, count, accumulate, alpha, st);
+    return launch_gemm_packed_tiles<128, 128, 3>(a, m, ws, cs, biases, count, accumulate, alpha, st);
 }
 
 int32_t launch_gemm_group(const float* a, int32_t m, const WeightView* ws, float* const* cs, const float* const* biases,

@@ -124,10 +124,15 @@ __global__ void __launch_bounds__(256)
 }
 
 // Writes the copy's scale and zero-point rows: [column set][group][16] fp32 scales, then
-// [column set][group][16] zero points (0 without zero points, and past the last column).
+// [column set][group][16] zero points (0 without zero points, and past the last column);
+// and the largest |scale| into the trailer word smax (zero beforehand): fmaxf's maximum
+// (NaNs ignored, infinities kept), as the bits of a non-negative float, whose unsigned
+// order is the float order, by one atomic maximum per workgroup (order-free).
 __global__ void __launch_bounds__(256)
     pack_scales_kernel(const float* __restrict__ s, const int8_t* __restrict__ z, int32_t G, int32_t N, int64_t rows,
-                       float* __restrict__ ps, int8_t* __restrict__ pz) {
+                       float* __restrict__ ps, int8_t* __restrict__ pz, uint32_t* smax) {
+    __shared__ uint32_t red[4];
+    uint32_t mx = 0u;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < rows;
          i += static_cast<int64_t>(gridDim.x) * 256) {
         const int64_t set_group = i / SET;
@@ -136,9 +141,25 @@ __global__ void __launch_bounds__(256)
         const int32_t grp = static_cast<int32_t>(set_group - static_cast<int64_t>(set) * G);
         const int32_t col = set * SET + n;
         const int64_t at = static_cast<int64_t>(grp) * N + col;
-        ps[i] = col < N ? s[at] : 0.0f;
+        const float v = col < N ? s[at] : 0.0f;
+        ps[i] = v;
         pz[i] = z && col < N ? z[at] : static_cast<int8_t>(0);
+        const uint32_t b = __float_as_uint(fabsf(v));
+        mx = b <= 0x7F800000u ? max(mx, b) : mx;
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o, 64)));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mx = max(max(red[0], red[1]), max(red[2], red[3]));
+        __hip_atomic_fetch_max(smax, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Zeroes the copy's 16-byte trailer before the maximum is taken into its first word.
+__global__ void zero_trailer(uint32_t* w) {
+    if (threadIdx.x < PACKED_TRAILER_BYTES / 4) w[threadIdx.x] = 0u;
 }
 
 // Max over the 8 lanes of an aligned group (quad swaps, then the half-row mirror).
@@ -730,7 +751,12 @@ int64_t packed_weight_bytes(int32_t rows, int32_t columns, int32_t bits) {
 
 int64_t packed_bytes(int32_t rows, int32_t columns, int32_t bits, int32_t group_size) {
     const int64_t sets = ceil_div(columns, SET), groups = ceil_div(rows, group_size);
-    return packed_weight_bytes(rows, columns, bits) + sets * groups * STAGE_ROW_BYTES;
+    return packed_weight_bytes(rows, columns, bits) + sets * groups * STAGE_ROW_BYTES + PACKED_TRAILER_BYTES;
+}
+
+const float* packed_scale_max(const WeightView& w) {
+    return reinterpret_cast<const float*>(static_cast<const uint8_t*>(w.p) + packed_bytes(w.K, w.N, w.bits, w.g) -
+                                          PACKED_TRAILER_BYTES);
 }
 
 int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st) {
@@ -746,8 +772,11 @@ int32_t launch_pack(const WeightView& w, void* packed, hipStream_t st) {
     const int64_t rows = static_cast<int64_t>(sets) * w.G * SET;
     float* ps = reinterpret_cast<float*>(static_cast<uint8_t*>(packed) + wbytes);
     int8_t* pz = reinterpret_cast<int8_t*>(ps + rows);
+    uint32_t* smax = reinterpret_cast<uint32_t*>(pz + rows);  // the trailer: 16-byte aligned (rows % 16 == 0)
+    zero_trailer<<<1, 64, 0, st>>>(smax);
+    KT_LAUNCHED("qweight pack kernel (trailer)");
     blocks = std::min<int64_t>((rows + 255) / 256, 65536);
-    pack_scales_kernel<<<static_cast<uint32_t>(blocks), 256, 0, st>>>(w.s, w.z, w.G, w.N, rows, ps, pz);
+    pack_scales_kernel<<<static_cast<uint32_t>(blocks), 256, 0, st>>>(w.s, w.z, w.G, w.N, rows, ps, pz, smax);
     KT_LAUNCHED("qweight pack kernel (scales)");
     return KT_OK;
 }

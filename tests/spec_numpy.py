@@ -101,7 +101,8 @@ def decode(qdata, scales, zeros, K, N, bits, group_size) -> np.ndarray:
 
 def pack_column_runs(qdata, K: int, N: int, bits: int, scales=None, zeros=None, g: int = 0) -> np.ndarray:
     """The column-run copy (kt_qweight_pack), restated with numpy reshapes: the weight
-    blocks, then (with scales and g given) the scale and zero-point rows.
+    blocks, then (with scales and g given) the scale and zero-point rows and the trailer
+    (the largest |scale|).
 
     Blocks [column set of 16][chunk of 128 k]; in a block, lane l = 16 kb + n owns 16
     bytes (INT8: two halves of 1 KB, lane bytes at h * 1024 + 16 l) for column 16 set + n
@@ -137,4 +138,7 @@ def pack_column_runs(qdata, K: int, N: int, bits: int, scales=None, zeros=None, 
         Z[:, :N] = np.asarray(zeros).view(np.uint8).reshape(G, N)
     srows = np.ascontiguousarray(S.reshape(G, sets, 16).transpose(1, 0, 2)).view(np.uint8).reshape(-1)
     zrows = np.ascontiguousarray(Z.reshape(G, sets, 16).transpose(1, 0, 2)).reshape(-1)
-    return np.concatenate([blocks, srows, zrows])
+    # the trailer: the largest |scale| (fmax: NaNs ignored), then 12 zero bytes
+    trailer = np.zeros(4, dtype=np.float32)
+    trailer[0] = np.fmax.reduce(np.abs(S.ravel()), initial=np.float32(0))
+    return np.concatenate([blocks, srows, zrows, trailer.view(np.uint8)])

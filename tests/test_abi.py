@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     header = (ROOT / "include" / "kotensor_hip.h").read_text()
     declared = int(re.search(r"#define KT_ABI_VERSION (\d+)", header).group(1))
-    assert lib.kt_abi_version() == declared == 3
+    assert lib.kt_abi_version() == declared == 4
     assert kotensor_amd.LIBRARY_PATH.name == "libkotensor_hip.so"
 
 
@@ -84,9 +84,10 @@ def test_argument_errors_map_to_illegal_argument():
     # the column-run copy: size formula, and its checks before any device access
     n = ctypes.c_int64()
     assert lib.kt_qweight_packed_bytes(4096, 14336, 4, 64, ctypes.byref(n)) == _lib.KT_OK
-    assert n.value == (14336 // 16) * (4096 // 128) * 1024 + (14336 // 16) * 64 * 80
+    assert n.value == (14336 // 16) * (4096 // 128) * 1024 + (14336 // 16) * 64 * 80 + 16
     assert lib.kt_qweight_packed_bytes(300, 2100, 8, 32, ctypes.byref(n)) == _lib.KT_OK
-    assert n.value == 132 * 3 * 2048 + 132 * 10 * 80  # ceil(2100 / 16) sets, ceil(300 / 128) chunks, 10 groups
+    # ceil(2100 / 16) sets, ceil(300 / 128) chunks, 10 groups, the 16-byte trailer
+    assert n.value == 132 * 3 * 2048 + 132 * 10 * 80 + 16
     assert lib.kt_qweight_packed_bytes(300, 2100, 5, 32, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_qweight_packed_bytes(300, 2100, 8, 0, ctypes.byref(n)) == _lib.KT_ERR_ARGUMENT
     assert lib.kt_qweight_pack(ctypes.byref(w), None, None) == _lib.KT_ERR_ARGUMENT

@@ -209,9 +209,12 @@ def test_column_run_spec_matches_its_definition():
             zs = rng.integers(0, 16, size=G * N, dtype=np.uint8)
             P = pack_column_runs(q, K, N, bits, sc, zs, g)
             base = sets * chunks * BB
-            assert P.size == base + sets * G * 80
+            assert P.size == base + sets * G * 80 + 16
             srows = P[base:base + sets * G * 64].view(np.float32)
-            zrows = P[base + sets * G * 64:]
+            zrows = P[base + sets * G * 64:base + sets * G * 80]
+            # the trailer: the largest |scale| over every scale (columns past N hold 0)
+            trailer = P[base + sets * G * 80:].view(np.float32)
+            assert trailer[0] == np.abs(sc).max() and not trailer[1:].any()
             for _ in range(500):
                 s, grp, n = rng.integers(sets), rng.integers(G), rng.integers(16)
                 col = 16 * s + n
