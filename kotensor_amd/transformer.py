@@ -260,6 +260,10 @@ class Transformer:
             self.set_parameter(f"block.{l}.norm2.weight", np.ones(dimension, np.float32), stream)
         self.set_parameter("finalNorm.weight", np.ones(dimension, np.float32), stream)
         self._graph = None
+        # one-row steps: the projections between two attention calls as one chained launch
+        # (kt_qmatmul_chain) when True, else as separate launches (the default: at the
+        # 1B decoder's shapes measured 0.488 ms per token separate, 0.538 chained)
+        self.chain_one_row = False
         # column-run copies of the projections for the one-row (decode) products
         self.packed = packed
         if packed and seed is not None:
@@ -453,7 +457,7 @@ class Transformer:
                       cache.position.ptr, key_bound, cache.keys.ptr, cache.values.ptr, l, cache.max_sequence_length,
                       self.num_heads, self.num_key_value_heads, self.head_dim, rows.context.ptr, st)
             q_ready = False
-            if count == 1 and self._zero_bias.get(p + "attention.wOut", True) and \
+            if count == 1 and self.chain_one_row and self._zero_bias.get(p + "attention.wOut", True) and \
                     self._zero_bias.get(p + "ffn.wDown", True):
                 # a zero bias lets wOut and wDown accumulate straight into x
                 steps = [(rows.context.ptr, None, [self.weights[p + "attention.wOut"]], [rows.x.ptr], [None], 1, 0),

@@ -35,6 +35,7 @@ import numpy as np
 import pytest
 
 from conftest import normwise_rel
+from gpu_helpers import same_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -487,6 +488,33 @@ def test_prefill_and_decode_match_the_oracle(kt, oracle_lib, bits, tied, biases)
             want = ref.decode(token, rc)
             assert normwise_rel(got, want) <= tol
         assert cache.length == rc.length == length + steps
+
+
+@pytest.mark.parametrize("bits,tied", [(4, False), (8, True)])
+def test_chained_decode_steps_equal_separate_launches(kt, oracle_lib, bits, tied):
+    """One-row decode steps with the projections between two attention calls chained in
+    one launch (kt_qmatmul_chain) give the same bits as the same products launched one by
+    one (the default), and both meet the oracle step by step."""
+    model = small(kt, bits, tied)
+    ref = to_oracle(kt, model)
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, model.vocabulary_size, 33).tolist()
+    tokens = rng.integers(0, model.vocabulary_size, 5).tolist()
+    runs = {}
+    for chained in (False, True):
+        banner("chained decode", bits, tied, chained)
+        model.chain_one_row = chained
+        cache = model.new_cache(len(prompt) + len(tokens))
+        buffers = model.new_inference_buffers(len(prompt) + len(tokens))
+        model.prefill(prompt, cache, buffers)
+        runs[chained] = [model.decode(t, cache, buffers).logits_numpy().copy() for t in tokens]
+    model.chain_one_row = False
+    rc = ref.new_cache(len(prompt) + len(tokens))
+    ref.prefill(prompt, rc)
+    for i, t in enumerate(tokens):
+        want = ref.decode(t, rc)
+        assert same_bits(runs[True][i], runs[False][i]), i
+        assert normwise_rel(runs[True][i], want) <= tolerance(len(prompt) + i + 1)
 
 
 def test_chunked_prefill_equals_one_chunk_and_continues_a_cache(kt, oracle_lib):
