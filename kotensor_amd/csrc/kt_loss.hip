@@ -3,16 +3,20 @@
 // (Engine/kotensor/src/main/kotlin/Loss.kt:114-219), forward loss and the gradients its
 // backward closure adds for an upstream gradient of 1.
 //
-// Like the reference, the rows go through in chunks of 2^22 / N logits (Loss.kt:133),
-// so the logits never exist for all rows at once. Per chunk: the logits by kt_qmatmul
+// Like the reference, the active rows (those whose target is not ignore_index) are
+// gathered in order and go through in chunks of 2^22 / N of them (activeRows,
+// projectRows, Loss.kt:129-133, :236-260), so the logits never exist for all rows at
+// once, and a chunk's rows, and with them the kernel that makes its logits, do not depend
+// on how many ignored rows lie between them. Per chunk: the logits by kt_qmatmul
 // (the prefill GEMM or the small-M kernels, with the bias), one workgroup per row for the
 // row's max, sum of exponentials, loss and (in place) its logit gradients
 // scale * (softmax - onehot) (logitGradients, Loss.kt:275-291), then the bias gradient as
 // column sums in row order and the hidden gradient by the transposed product
 // (MatMul.multiplyByQuantizedTransposed, K/MatMul.kt:954-981). exp and ln are Kotlin's
-// Float forms: the double function rounded to float. Rows whose target is ignore_index
-// get zero logit gradients, so they add nothing. The per-row losses are added in a fixed
-// order at the end, so the result does not depend on timing.
+// Float forms: the double function rounded to float. The hidden gradient of a chunk goes
+// back to its rows' places; ignored rows get zero (or keep theirs, accumulating). The
+// per-row losses are added in a fixed order at the end, so the result does not depend
+// on timing.
 #include "kt_common.h"
 
 #include <vector>
@@ -105,6 +109,24 @@ __global__ void __launch_bounds__(CE_THREADS)
     if (threadIdx.x == 0) *loss = active > 0 ? s / static_cast<float>(active) : 0.0f;
 }
 
+// dst[r] = src[rows[r]] for the chunk's rows (K floats each): the gathered input.
+__global__ void __launch_bounds__(256)
+    gather_rows_kernel(const float* __restrict__ src, int32_t K, const int32_t* __restrict__ rows,
+                       float* __restrict__ dst) {
+    const float* s = src + static_cast<int64_t>(rows[blockIdx.x]) * K;
+    float* d = dst + static_cast<int64_t>(blockIdx.x) * K;
+    for (int32_t k = threadIdx.x; k < K; k += 256) d[k] = s[k];
+}
+
+// dst[rows[r]] (+)= src[r]: the chunk's hidden gradient back to its rows' places.
+__global__ void __launch_bounds__(256)
+    scatter_rows_kernel(const float* __restrict__ src, int32_t K, const int32_t* __restrict__ rows,
+                        float* __restrict__ dst, int32_t accumulate) {
+    const float* s = src + static_cast<int64_t>(blockIdx.x) * K;
+    float* d = dst + static_cast<int64_t>(rows[blockIdx.x]) * K;
+    for (int32_t k = threadIdx.x; k < K; k += 256) d[k] = accumulate ? d[k] + s[k] : s[k];
+}
+
 __global__ void fill_kernel(float* __restrict__ p, int64_t n, float value) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
         p[i] = value;
@@ -132,13 +154,16 @@ extern "C" int32_t kt_fused_cross_entropy(const float* hidden, int32_t rows, con
     if (rows <= 0 || !targets) return fail(KT_ERR_ARGUMENT, "targets cannot be empty");
     if (!hidden || !loss) return fail(KT_ERR_ARGUMENT, "fused cross-entropy with a NULL hidden or loss");
     const int32_t V = w.N, K = w.K;
-    // activeRows (Loss.kt:236-249): every target is ignore_index or in [0, V)
-    int32_t active = 0;
+    // activeRows (Loss.kt:236-249): every target is ignore_index or in [0, V); the active
+    // rows' indices, then their targets, in row order
+    std::vector<int32_t> act;
     for (int32_t i = 0; i < rows; ++i) {
         if (targets[i] == ignore_index) continue;
         if (targets[i] < 0 || targets[i] >= V) return fail(KT_ERR_ARGUMENT, "target %d out of bounds %d", targets[i], V);
-        ++active;
+        act.push_back(i);
     }
+    const int32_t active = static_cast<int32_t>(act.size());
+    for (int32_t i = 0; i < active; ++i) act.push_back(targets[act[i]]);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool grads = hidden_grad || bias_grad;
     if (active == 0) {  // emptyLoss(): no gradient flows
@@ -148,21 +173,33 @@ extern "C" int32_t kt_fused_cross_entropy(const float* hidden, int32_t rows, con
         if (!accumulate && bias_grad && (status = fill(bias_grad, V, 0.0f, st))) return status;
         return KT_OK;
     }
-    const int32_t chunk = std::max(1, std::min(FUSED_CHUNK_ELEMENTS / V, rows));
-    // device scratch for this call: the chunk's logits, the per-row losses, the targets
+    const int32_t chunk = std::max(1, std::min(FUSED_CHUNK_ELEMENTS / V, active));  // chunkRows
+    // device scratch for this call: the chunk's logits, its gathered rows and their hidden
+    // gradient, the per-row losses, the active rows' indices and targets
     const size_t logit_bytes = static_cast<size_t>(chunk) * V * sizeof(float);
-    const size_t bytes = logit_bytes + static_cast<size_t>(rows) * (sizeof(float) + sizeof(int32_t));
+    const size_t row_bytes = static_cast<size_t>(chunk) * K * sizeof(float);
+    const size_t bytes = logit_bytes + 2 * row_bytes + static_cast<size_t>(active) * (sizeof(float) + 2 * sizeof(int32_t));
     void* scratch = nullptr;
     KT_HIP(hipMallocAsync(&scratch, bytes, st));
     float* logits = static_cast<float*>(scratch);
-    float* row_loss = reinterpret_cast<float*>(static_cast<char*>(scratch) + logit_bytes);
-    int32_t* dtargets = reinterpret_cast<int32_t*>(row_loss + rows);
+    float* inputs = reinterpret_cast<float*>(static_cast<char*>(scratch) + logit_bytes);
+    float* chunk_grad = reinterpret_cast<float*>(static_cast<char*>(scratch) + logit_bytes + row_bytes);
+    float* row_loss = reinterpret_cast<float*>(static_cast<char*>(scratch) + logit_bytes + 2 * row_bytes);
+    int32_t* drows = reinterpret_cast<int32_t*>(row_loss + active);
+    int32_t* dtargets = drows + active;
     status = [&]() -> int32_t {
-        KT_HIP(hipMemcpyAsync(dtargets, targets, static_cast<size_t>(rows) * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        // pageable source: the copy has read it when the call returns
+        KT_HIP(hipMemcpyAsync(drows, act.data(), act.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        if (hidden_grad && !accumulate) {  // ignored rows' gradient is zero
+            const int32_t f = fill(hidden_grad, static_cast<int64_t>(rows) * K, 0.0f, st);
+            if (f) return f;
+        }
         const float scale = 1.0f / static_cast<float>(active);
-        for (int32_t start = 0; start < rows; start += chunk) {
-            const int32_t count = std::min(chunk, rows - start);
-            int32_t s = qmatmul(hidden + static_cast<int64_t>(start) * K, count, head, logits, 0, 1.0f, bias, st);
+        for (int32_t start = 0; start < active; start += chunk) {
+            const int32_t count = std::min(chunk, active - start);
+            gather_rows_kernel<<<count, 256, 0, st>>>(hidden, K, drows + start, inputs);
+            KT_LAUNCHED("fused cross-entropy: gather rows");
+            int32_t s = qmatmul(inputs, count, head, logits, 0, 1.0f, bias, st);
             if (s) return s;
             ce_rows_kernel<<<count, CE_THREADS, 0, st>>>(logits, V, dtargets + start, ignore_index, scale,
                                                          row_loss + start, grads ? 1 : 0);
@@ -173,11 +210,13 @@ extern "C" int32_t kt_fused_cross_entropy(const float* hidden, int32_t rows, con
                 KT_LAUNCHED("fused cross-entropy: bias gradient");
             }
             if (hidden_grad) {
-                s = launch_transposed(logits, count, w, hidden_grad + static_cast<int64_t>(start) * K, accumulate, st);
+                s = launch_transposed(logits, count, w, chunk_grad, 0, st);
                 if (s) return s;
+                scatter_rows_kernel<<<count, 256, 0, st>>>(chunk_grad, K, drows + start, hidden_grad, accumulate);
+                KT_LAUNCHED("fused cross-entropy: scatter rows");
             }
         }
-        ce_loss_kernel<<<1, CE_THREADS, 0, st>>>(row_loss, rows, active, loss);
+        ce_loss_kernel<<<1, CE_THREADS, 0, st>>>(row_loss, active, active, loss);
         KT_LAUNCHED("fused cross-entropy: loss");
         return KT_OK;
     }();

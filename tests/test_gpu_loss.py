@@ -2,7 +2,7 @@
 kt_loss.hip) against the oracle's restatement of fusedCrossEntropyLoss
 (K/Loss.kt:114-219): the loss, d loss / d hidden and d loss / d bias, with ignored rows,
 chunking (the vocabulary's 2^22 / N rows per chunk), accumulate, the reference's argument
-errors and repeat calls.
+errors and repeat calls; ignored rows never change the active rows' results.
 
 Bound: the logits come from the library's products (fp32 combine for up to 16 rows, the
 prefill GEMM's fp16 operands above: about 3e-4 normwise per product), so the loss is held
@@ -65,6 +65,25 @@ def test_matches_the_oracle(kt, oracle_lib, k, n, rows, bits, g, ignore_every):
     # repeat: the same bits (fixed-order sums, no atomics)
     loss2, hg2, bg2 = _run(kt, head, hidden, targets)
     assert loss2 == loss and same_bits(hg, hg2) and same_bits(bg, bg2)
+
+
+def test_ignored_rows_do_not_change_the_active_rows(kt, oracle_lib):
+    """Chunks are taken over the active rows (Loss.kt:129-133): ignored rows interleaved
+    between the same active rows leave the loss and every active row's gradients bit for
+    bit as they were, although without compaction the chunks' row counts would change
+    (at the Qwen2 head, 27 rows a chunk: 40 active rows are chunks of 27 and 13, the
+    prefill GEMM and the small-M kernels), and the ignored rows' gradient is zero."""
+    banner("fused-ce-ignored-rows")
+    q, head, bias, hidden, targets = _setup(kt, oracle_lib, 896, 151936, 40, 4, 64, 31)
+    loss, hg, bg = _run(kt, head, hidden, targets)
+    rng = np.random.default_rng(32)
+    spread = np.sort(rng.choice(100, 40, replace=False))  # the active rows' places among 100
+    hidden2 = rng.standard_normal((100, 896)).astype(np.float32)
+    targets2 = np.full(100, IGNORE, np.int32)
+    hidden2[spread], targets2[spread] = hidden, targets
+    loss2, hg2, bg2 = _run(kt, head, hidden2, targets2)
+    assert loss2 == loss and same_bits(hg2[spread], hg) and same_bits(bg2, bg)
+    assert not np.delete(hg2, spread, axis=0).any()
 
 
 def test_accumulate_and_loss_only(kt, oracle_lib):
