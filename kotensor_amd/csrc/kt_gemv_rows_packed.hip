@@ -55,17 +55,26 @@ __host__ __device__ constexpr int32_t run_tile_bytes(int32_t M) { return 2 * 4 *
 constexpr int PREP_THREADS = 256;
 constexpr int MAX_PIECES = 16;  // 16-byte pieces of x tiles a thread moves per round
 
-// x [M x K] -> the A tiles [K / 32 runs][part][lane group kb][row][8 halves] and the row
-// shifts s_m (16 ints, zero past M): one workgroup per row, once per call, so that the
-// product's workgroups only copy tiles. K % 32 == 0.
+// x [M x K] -> the A tiles [K / 32 runs][part][lane group kb][row][8 halves] of MT rows
+// (rows M .. MT - 1 zero) and the row shifts s_m (16 ints, zero past M): one workgroup per
+// tile row, once per call, so that the product's workgroups only copy tiles. K % 32 == 0.
 template <int BITS>
 __global__ void __launch_bounds__(PREP_THREADS)
-    rows_prep_kernel(const float* __restrict__ x, int32_t M, int32_t K, _Float16* __restrict__ at,
+    rows_prep_kernel(const float* __restrict__ x, int32_t M, int32_t MT, int32_t K, _Float16* __restrict__ at,
                      int32_t* __restrict__ shifts) {
     __shared__ float red[PREP_THREADS / 64];
     const int32_t m = blockIdx.x, t = threadIdx.x;
-    const float* row = x + static_cast<size_t>(m) * K;
     const int32_t units = K >> 3;  // 8 k per unit
+    if (m >= M) {  // a padding row of the tiles
+        for (int32_t u = t; u < units; u += PREP_THREADS) {
+            _Float16* base = at + static_cast<size_t>(u >> 2) * (2 * 4 * 8 * MT);
+            *reinterpret_cast<u32x4*>(base + (0 * 4 + (u & 3)) * MT * 8 + m * 8) = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(base + (1 * 4 + (u & 3)) * MT * 8 + m * 8) = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (t == 0) shifts[m] = 0;
+        return;
+    }
+    const float* row = x + static_cast<size_t>(m) * K;
     // the row's largest |x| (a NaN or an infinity compares above every finite value)
     uint32_t mb = 0u;
     for (int32_t u = t; u < units; u += PREP_THREADS) {
@@ -99,14 +108,14 @@ __global__ void __launch_bounds__(PREP_THREADS)
             lv[j] = static_cast<_Float16>((xs - static_cast<float>(h)) * f);  // the difference is exact
         }
         const int32_t run = u >> 2, kb = u & 3;
-        _Float16* base = at + static_cast<size_t>(run) * (2 * 4 * 8 * M);
-        *reinterpret_cast<half8*>(base + (0 * 4 + kb) * M * 8 + m * 8) = hv;
-        *reinterpret_cast<half8*>(base + (1 * 4 + kb) * M * 8 + m * 8) = lv;
+        _Float16* base = at + static_cast<size_t>(run) * (2 * 4 * 8 * MT);
+        *reinterpret_cast<half8*>(base + (0 * 4 + kb) * MT * 8 + m * 8) = hv;
+        *reinterpret_cast<half8*>(base + (1 * 4 + kb) * MT * 8 + m * 8) = lv;
     }
     if (t == 0) {
         shifts[m] = s;
         if (m == 0)
-            for (int32_t r = M; r < MAX_ROWS; ++r) shifts[r] = 0;
+            for (int32_t r = MT; r < MAX_ROWS; ++r) shifts[r] = 0;
     }
 }
 
@@ -151,7 +160,10 @@ __device__ __forceinline__ void transpose4(uint32_t (&v)[4]) {
     v[3] = d[1];
 }
 
-template <int BITS, bool ZP>
+// GS: the group size's class (0: g = 32, a group per run; 1: g = 64, a group per two
+// runs; 2: g >= 128, one group per chunk), MT: rows of the x tiles (4, 8 or 16; rows M ..
+// MT - 1 are zero).
+template <int BITS, bool ZP, int GS, int MT>
 __global__ void __launch_bounds__(64 * W)
     gemv_rows_packed_kernel(const uint8_t* __restrict__ packed, const _Float16* __restrict__ at,
                             const int32_t* __restrict__ shifts_m, int32_t M, int32_t N, int32_t K, int32_t shifts,
@@ -179,7 +191,7 @@ __global__ void __launch_bounds__(64 * W)
     const int32_t col = set * SET + nl;
     const int32_t phases = (nmax + cpp - 1) / cpp;
     const int32_t rows = stage_rows(nmax, gshift);
-    const int32_t tile = run_tile_bytes(M);
+    constexpr int32_t tile = run_tile_bytes(MT);
 
     // ---- loads, in the order they complete: the first phase's x tiles (16 bytes per
     // thread and step), the wave's scale and zero-point rows, the first R chunks of weights.
@@ -256,7 +268,7 @@ __global__ void __launch_bounds__(64 * W)
         load_round(0, rd);
         store_round(rd);
     }
-    unsigned char* stg = smem + rows_lds_stage(ks, cpp, M) + wave * rows * STAGE_ROW_BYTES;
+    unsigned char* stg = smem + rows_lds_stage(ks, cpp, MT) + wave * rows * STAGE_ROW_BYTES;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         if (16 * i + (ln >> 2) < rows) *reinterpret_cast<u32x4*>(stg + i * 1024 + 16 * ln) = sst[i];
@@ -264,9 +276,9 @@ __global__ void __launch_bounds__(64 * W)
         if (ln < rows) *reinterpret_cast<u32x4*>(stg + rows * SET * 4 + 16 * ln) = zst;
     __syncthreads();
 
-    // lanes of rows past M read row 0's operand: an MFMA's output rows depend only on their
-    // own A rows, and rows past M are never stored
-    const int32_t a_lane = kb * M * 16 + min(nl, M - 1) * 16;
+    // lanes of rows past MT read row MT - 1's operand: an MFMA's output rows depend only
+    // on their own A rows, and rows past M are never stored
+    const int32_t a_lane = kb * MT * 16 + min(nl, MT - 1) * 16;
     float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // sub-parts of K, each summed alone and added in a balanced tree in K order (the
     // one-row kernel's scheme): the result does not depend on ks
@@ -308,6 +320,8 @@ __global__ void __launch_bounds__(64 * W)
             transpose4(t2);
         }
     };
+    constexpr int NGC = GS == 0 ? 4 : GS == 1 ? 2 : 1;  // quantization groups a chunk touches
+    constexpr int RPG = 4 / NGC;                        // runs per group
     auto process = [&](const uint32_t (&t)[4], const uint32_t (&t2)[4], int32_t cl, bool live, int32_t ph) {
         if (live)
             while (cl >= sp_end) close_sub_part();
@@ -315,26 +329,45 @@ __global__ void __launch_bounds__(64 * W)
         // and the wave's staged rows (the phase's first chunk is below nmax)
         const int32_t cc = live ? cl : ph * cpp;
         const unsigned char* tc = smem + (kp * cpp + (cc - ph * cpp)) * 4 * tile + a_lane;
-        float sc[4];
-        uint32_t zc[4];
+        float sc[NGC];
+        uint32_t zc[NGC];
         half8 ah[4], al[4];
 #pragma unroll
+        for (int gi = 0; gi < NGC; ++gi) {
+            // the group row of runs gi RPG .. (a run past K, the padding of the last chunk,
+            // takes the last group's; its x is zero)
+            const int32_t gr = min((run0 + cc * 4 + gi * RPG) >> gshift, G - 1) - g0;
+            sc[gi] = *reinterpret_cast<const float*>(stg + gr * (SET * 4) + nl * 4);
+            zc[gi] = ZP ? stg[rows * SET * 4 + gr * SET + nl] : 0u;
+        }
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int32_t gr = min((run0 + cc * 4 + r) >> gshift, G - 1) - g0;  // the run's group row
-            sc[r] = *reinterpret_cast<const float*>(stg + gr * (SET * 4) + nl * 4);
-            zc[r] = ZP ? stg[rows * SET * 4 + gr * SET + nl] : 0u;
             ah[r] = *reinterpret_cast<const half8*>(tc + r * tile);
-            al[r] = *reinterpret_cast<const half8*>(tc + r * tile + 4 * M * 16);
+            al[r] = *reinterpret_cast<const half8*>(tc + r * tile + 4 * MT * 16);
+        }
+        // the exact fp16 offsets of each group: 1024 + z (INT4 also 1024 + 16 z), 1152 + z
+        half2v ol[NGC], oh[NGC];
+#pragma unroll
+        for (int gi = 0; gi < NGC; ++gi) {
+            if constexpr (BITS == 4) {
+                const uint32_t zz = zc[gi] | (zc[gi] << 16);
+                ol[gi] = as_h2(zz | 0x64006400u);
+                oh[gi] = as_h2((zz << 4) | 0x64006400u);
+            } else {
+                const uint32_t zz = (zc[gi] ^ 0x80u) | ((zc[gi] ^ 0x80u) << 16);
+                ol[gi] = as_h2(zz | 0x64006400u);
+                oh[gi] = ol[gi];
+            }
         }
         half8 b[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             uint32_t bw[4];
+            const half2v o_lo = ol[r / RPG], o_hi = oh[r / RPG];
             if constexpr (BITS == 4) {
                 // halves 0..3: low nibbles, the bits of 1024 + q; 4..7: high nibbles, 1024 + 16 q;
                 // minus 1024 + z and 1024 + 16 z (the bits 0x6400 | z, 0x6400 | z << 4)
-                const uint32_t zz = zc[r] | (zc[r] << 16);
-                const half2v ol = as_h2(zz | 0x64006400u), oh = as_h2((zz << 4) | 0x64006400u);
+                const half2v ol = o_lo, oh = o_hi;
                 const uint32_t p01 = perm(0u, t[r], 0x0c010c00u), p23 = perm(0u, t[r], 0x0c030c02u);
                 bw[0] = as_u(as_h2(and_or(p01, 0x000F000Fu, 0x64006400u)) - ol);
                 bw[1] = as_u(as_h2(and_or(p23, 0x000F000Fu, 0x64006400u)) - ol);
@@ -342,8 +375,7 @@ __global__ void __launch_bounds__(64 * W)
                 bw[3] = as_u(as_h2(and_or(p23, 0x00F000F0u, 0x64006400u)) - oh);
             } else {
                 // byte b: (b ^ 0x80) + 1024 = 1152 + q; minus 1152 + z, the bits 0x6400 | (z ^ 0x80)
-                const uint32_t zz = (zc[r] ^ 0x80u) | ((zc[r] ^ 0x80u) << 16);
-                const half2v o = as_h2(zz | 0x64006400u);
+                const half2v o = o_lo;
                 bw[0] = as_u(as_h2(perm(0u, t[r], 0x0c010c00u) ^ 0x64806480u) - o);
                 bw[1] = as_u(as_h2(perm(0u, t[r], 0x0c030c02u) ^ 0x64806480u) - o);
                 bw[2] = as_u(as_h2(perm(0u, t2[r], 0x0c010c00u) ^ 0x64806480u) - o);
@@ -351,12 +383,15 @@ __global__ void __launch_bounds__(64 * W)
             }
             b[r] = __builtin_bit_cast(half8, u32x4{bw[0], bw[1], bw[2], bw[3]});
         }
-        f32x4 acc[4];
+        // one accumulator per group: its runs' hi and lo products in run order
+        f32x4 acc[NGC];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], b[r], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        for (int gi = 0; gi < NGC; ++gi) acc[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[r], b[r], acc[r], 0, 0, 0);
+        for (int r = 0; r < 4; ++r) {
+            acc[r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], b[r], acc[r / RPG], 0, 0, 0);
+            acc[r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[r], b[r], acc[r / RPG], 0, 0, 0);
+        }
         // a chunk past the wave's range may have read tiles no phase wrote: its whole
         // contribution is dropped by a select, never scaled by zero (0 * NaN)
         float cy[4];
@@ -364,7 +399,7 @@ __global__ void __launch_bounds__(64 * W)
         for (int i = 0; i < 4; ++i) {
             cy[i] = y[i];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cy[i] = fmaf(sc[r], acc[r][i], cy[i]);
+            for (int gi = 0; gi < NGC; ++gi) cy[i] = fmaf(sc[gi], acc[gi][i], cy[i]);
             y[i] = live ? cy[i] : y[i];
         }
     };
@@ -396,7 +431,7 @@ __global__ void __launch_bounds__(64 * W)
     // ---- the last sub-parts; the K-parts of each column set (the tree's top); the row
     // shifts; the stores
     while (sp < sp_count) close_sub_part();
-    float* red = reinterpret_cast<float*>(smem + rows_lds_red(ks, cpp, M, rows));  // [W][16 rows][16 cols]
+    float* red = reinterpret_cast<float*>(smem + rows_lds_red(ks, cpp, MT, rows));  // [W][16 rows][16 cols]
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * kb + i) * 16 + nl] = part[i];
     __syncthreads();
@@ -426,10 +461,14 @@ struct RowsPlan {
     int32_t ks = 0, cpp = 0;
     size_t lds = 0;
 };
+// Rows of the x tiles for M rows: 4, 8 or 16.
+static int32_t tile_rows(int32_t M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+
 static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets) {
     RowsPlan r;
     const PackedPlan plan = plan_packed(K, g, sets);
     const int32_t gshift = log2_exact(g / RUN), chunks = ceil_div(K, CHUNK);
+    M = tile_rows(M);
     const int32_t tile = run_tile_bytes(M);
     for (int32_t ks = plan.ks; ks >= 1; ks /= 2) {
         const int32_t nmax = ceil_div(chunks, ks);
@@ -459,46 +498,74 @@ bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, 
     return rows_plan(m, w.K, w.g, w.N / SET).ks != 0;
 }
 
+template <int GS, int MT>
+static int32_t launch_rows(int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st, const uint8_t* p,
+                           const _Float16* at, const int32_t* sh, int32_t m, int32_t N, int32_t K, int32_t shifts,
+                           int32_t cpp, float alpha, float* c, int32_t accumulate, const float* bias) {
+    if (bits == 4) {
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<4, true, GS, MT>>(lds)) return ls;
+        gemv_rows_packed_kernel<4, true, GS, MT>
+            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+    } else if (zp) {
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, true, GS, MT>>(lds)) return ls;
+        gemv_rows_packed_kernel<8, true, GS, MT>
+            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+    } else {
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, false, GS, MT>>(lds)) return ls;
+        gemv_rows_packed_kernel<8, false, GS, MT>
+            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+    }
+    return KT_OK;
+}
+
+template <int MT>
+static int32_t launch_rows_g(int32_t gshift, int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st,
+                             const uint8_t* p, const _Float16* at, const int32_t* sh, int32_t m, int32_t N, int32_t K,
+                             int32_t shifts, int32_t cpp, float alpha, float* c, int32_t accumulate, const float* bias) {
+    if (gshift == 0)
+        return launch_rows<0, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+    if (gshift == 1)
+        return launch_rows<1, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+    return launch_rows<2, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+}
+
 int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
                                 const float* const* biases, int32_t count, int32_t accumulate, float alpha,
                                 hipStream_t st) {
     // one preparation of x for every weight of the call (same K, bits)
     const WeightView& w0 = ws[0];
+    const int32_t mt = tile_rows(m);
     void* general = nullptr;
-    const size_t tiles = static_cast<size_t>(w0.K / RUN) * run_tile_bytes(m);
+    const size_t tiles = static_cast<size_t>(w0.K / RUN) * run_tile_bytes(mt);
     if (const int32_t status = workspace(st, tiles + 64 + 256, &general)) return status;
     char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(general) + 255) & ~uintptr_t{255});
     _Float16* at = reinterpret_cast<_Float16*>(base);
     int32_t* sh = reinterpret_cast<int32_t*>(base + tiles);
     if (w0.bits == 4)
-        rows_prep_kernel<4><<<m, PREP_THREADS, 0, st>>>(a, m, w0.K, at, sh);
+        rows_prep_kernel<4><<<mt, PREP_THREADS, 0, st>>>(a, m, mt, w0.K, at, sh);
     else
-        rows_prep_kernel<8><<<m, PREP_THREADS, 0, st>>>(a, m, w0.K, at, sh);
+        rows_prep_kernel<8><<<mt, PREP_THREADS, 0, st>>>(a, m, mt, w0.K, at, sh);
     KT_LAUNCHED("qmatmul: rows prep kernel");
     for (int32_t i = 0; i < count; ++i) {
         const WeightView& w = ws[i];
         const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET);
         const int32_t gshift = log2_exact(w.g / RUN);
-        const size_t lds = plan.lds;
-        const int32_t cpp = plan.cpp;
         if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
         const int32_t kslog = log2_exact(plan.ks);
         const dim3 grid(static_cast<uint32_t>(ceil_div(w.N / SET, W / plan.ks)));
         const int32_t shifts = kslog | gshift << 4;
         const float* bias = biases ? biases[i] : nullptr;
-        if (w.bits == 4) {
-            if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<4, true>>(lds)) return ls;
-            gemv_rows_packed_kernel<4, true><<<grid, 64 * W, lds, st>>>(w.p, at, sh, m, w.N, w.K, shifts, cpp, alpha,
-                                                                         cs[i], accumulate, bias);
-        } else if (w.z) {
-            if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, true>>(lds)) return ls;
-            gemv_rows_packed_kernel<8, true><<<grid, 64 * W, lds, st>>>(w.p, at, sh, m, w.N, w.K, shifts, cpp, alpha,
-                                                                         cs[i], accumulate, bias);
-        } else {
-            if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, false>>(lds)) return ls;
-            gemv_rows_packed_kernel<8, false><<<grid, 64 * W, lds, st>>>(w.p, at, sh, m, w.N, w.K, shifts, cpp, alpha,
-                                                                          cs[i], accumulate, bias);
-        }
+        int32_t status;
+        if (mt == 4)
+            status = launch_rows_g<4>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
+                                      shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+        else if (mt == 8)
+            status = launch_rows_g<8>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
+                                      shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+        else
+            status = launch_rows_g<16>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
+                                       shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+        if (status) return status;
         KT_LAUNCHED("qmatmul: packed rows gemv kernel");
     }
     return KT_OK;
