@@ -202,6 +202,7 @@ void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 // 2 to 16 rows on the column-run copy (kt_gemv_rows_packed.hip): support check and launch
 // (up to four weights sharing the input: one preparation of x, one launch per weight).
 bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c);
+bool gemv_rows_packed_preferred(const WeightView& w);  // the automatic choice takes it
 int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
                                 const float* const* biases, int32_t count, int32_t accumulate, float alpha,
                                 hipStream_t st);

@@ -487,6 +487,12 @@ static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets) {
     return r;
 }
 
+// The automatic choice: wide weights only. With column sets at least 16 times the 128-k
+// chunks (the 8B gate/up, the heads) this kernel is well ahead of the row-block kernel;
+// for narrow ones (8192 -> 2048, 14336 -> 4096, 4096 -> 4096) its grid is small and its x
+// tiles take several phases, and the row-block kernel is faster (measured at M = 2..16).
+bool gemv_rows_packed_preferred(const WeightView& w) { return w.N / SET >= 16 * ceil_div(w.K, CHUNK); }
+
 bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
     if (m < 2 || m > MAX_ROWS || !w.p) return false;
     if (w.K % RUN != 0 || w.K > 16384) return false;

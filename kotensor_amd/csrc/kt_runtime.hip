@@ -601,7 +601,8 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
     const float* biases[1] = {bias};
     if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_packed_supported(a, m, v, c))
         return launch_gemv_packed(a, &v, &c, biases, 1, accumulate, alpha, st);
-    if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_rows_packed_supported(a, m, v, c))
+    if ((g_gemv_kind == 5 || (g_gemv_kind == 0 && gemv_rows_packed_preferred(v))) &&
+        gemv_rows_packed_supported(a, m, v, c))
         return launch_gemv_rows_packed(a, m, &v, &c, biases, 1, accumulate, alpha, st);
     if ((g_gemv_kind == 4 || (g_gemv_kind == 0 && gemv_strip_preferred(&v, 1))) && gemv_strip_supported(a, m, v, c))
         return launch_gemv_strip(a, &v, &c, biases, 1, accumulate, alpha, st);
@@ -643,7 +644,8 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
             strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
             packed = packed && gemv_packed_supported(a, m, v, outputs[start + i]);
-            rows_packed = rows_packed && gemv_rows_packed_supported(a, m, v, outputs[start + i]);
+            rows_packed = rows_packed && gemv_rows_packed_supported(a, m, v, outputs[start + i]) &&
+                          (g_gemv_kind == 5 || gemv_rows_packed_preferred(v));
             gemm = gemm && gemm_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 16)) &&
                    (v.z != nullptr) == (views[0].z != nullptr);
         }

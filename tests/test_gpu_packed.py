@@ -289,17 +289,23 @@ def test_packed_rows_match_the_oracle(kt, oracle_lib, k, n, bits, g):
     q = _weights(oracle_lib, k, n, bits, g, 13)
     qt = _packed(kt, q)
     rng = np.random.default_rng(k + n + bits + g + 1)
-    for m in (2, 3, 8, 16):
-        x = rng.standard_normal((m, k), dtype=np.float32)
-        x *= (np.float32(10.0) ** rng.integers(-6, 6, size=(m, 1))).astype(np.float32)
-        if m > 2:
-            x[m // 2] = 0.0
-        banner("packed-rows", k, n, bits, g, m)
-        got = gpu_matmul(kt, x, qt, m)
-        want = oracle_lib.multiply_quantized(x, q, m, threads=16)
-        errs = [normwise_rel(got[r], want[r]) for r in range(m)]
-        print(f"  worst row normwise={max(errs):.2e}", flush=True)
-        assert max(errs) <= TOL, errs
+    try:
+        # the column-run kernel itself, also at the narrow shapes where the automatic
+        # choice takes the row-block kernel
+        kt.MatMul.set_kernel_config(5, 0, 0, 0, 0)
+        for m in (2, 3, 8, 16):
+            x = rng.standard_normal((m, k), dtype=np.float32)
+            x *= (np.float32(10.0) ** rng.integers(-6, 6, size=(m, 1))).astype(np.float32)
+            if m > 2:
+                x[m // 2] = 0.0
+            banner("packed-rows", k, n, bits, g, m)
+            got = gpu_matmul(kt, x, qt, m)
+            want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+            errs = [normwise_rel(got[r], want[r]) for r in range(m)]
+            print(f"  worst row normwise={max(errs):.2e}", flush=True)
+            assert max(errs) <= TOL, errs
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
 
 def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
@@ -334,11 +340,20 @@ def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
 
 def test_packed_rows_grouped_accumulate_and_bias(kt, oracle_lib):
     """Grouped weights of one input (q/k/v, gate/up) at 2..16 rows: one preparation of x,
-    a launch per weight; accumulate, alpha and biases."""
+    a launch per weight; accumulate, alpha and biases -- on the column-run kernel (forced
+    where the automatic choice takes the row-block kernel) and on the automatic choice."""
     rng = np.random.default_rng(42)
-    for m in (2, 5, 16):
+    try:
+        _grouped_rows_cases(kt, oracle_lib, rng)
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
+
+
+def _grouped_rows_cases(kt, oracle_lib, rng):
+    for m, kind in ((2, 5), (5, 5), (16, 5), (5, 0)):
         for k, ns, bits, g in [(2048, (2048, 512, 512), 8, 32), (4096, (14336, 14336), 4, 64), (896, (896, 128, 128), 4, 64)]:
-            banner("packed-rows-group", m, k, ns, bits, g)
+            banner("packed-rows-group", m, kind, k, ns, bits, g)
+            kt.MatMul.set_kernel_config(kind, 0, 0, 0, 0)
             qs = [_weights(oracle_lib, k, n, bits, g, 50 + i) for i, n in enumerate(ns)]
             qts = [_packed(kt, q) for q in qs]
             x = rng.standard_normal((m, k)).astype(np.float32)
@@ -349,6 +364,7 @@ def test_packed_rows_grouped_accumulate_and_bias(kt, oracle_lib):
             kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(x), qts, outs, m, accumulate=True,
                                                alpha=-0.75, biases=dbias)
             kt.synchronize()
+            kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
             for q, o, b, c, n in zip(qs, outs, biases, c0, ns):
                 got = o.download(np.float32).reshape(m, n)
                 want = oracle_lib.multiply_quantized(x, q, m, c=c, accumulate=True, alpha=-0.75, threads=16) + b[None, :]
