@@ -310,7 +310,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--plain", action="store_true",
                     help="with --only gemm: weights without the column-run copy (the reference-layout GEMM)")
-    ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm", "decode"],
+    ap.add_argument("--only", choices=["dominant", "copy", "quantize", "gemm", "decode", "c1", "rows", "narrow"],
                     help="run one kernel for a rocprofv3 run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -388,6 +388,22 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
         # the Llama-style 1B INT4 decoder: 1024-token prefill and 127 greedy steps, twice
         print(json.dumps({"only": "decode", **decoder_figures(torch, stream_obj)}), flush=True)
         return 0
+    if args.only in ("c1", "rows", "narrow"):
+        # c1: the INT8 g64 one-row product on 2048 x 2048; rows: M = 8 and narrow: M = 64 on
+        # the Llama-3-8B gate/up shape, INT4 g64; packed weights in rotation
+        k, n, bits, g, m = {"c1": (2048, 2048, 8, 64, 1), "rows": (4096, 14336, 4, 64, 8),
+                            "narrow": (4096, 14336, 4, 64, 64)}[args.only]
+        cs = weight_copies(torch, kt_lib, k, n, bits, g, 5, stream, packed=True)
+        x = torch.randn((m, k), device="cuda", dtype=torch.float32)
+        y = torch.empty((m, n), device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            qmatmul(kt_lib, x, m, cs[i % len(cs)], y, stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "shape": f"{k}x{n} int{bits} g{g} M={m}",
+                          "algorithmic_bytes": gemv_bytes(m, k, n, bits, g), "flops": 2 * m * k * n,
+                          "launches": args.steps}), flush=True)
+        return 0
     k, n, bits, g = HEADLINE
     copies = weight_copies(torch, kt_lib, k, n, bits, g, 8, stream, packed=True)
     x = torch.randn((1, k), device="cuda", dtype=torch.float32)
@@ -396,7 +412,7 @@ def run_only(args, torch, kt_lib, stream_obj) -> int:
     for i in range(args.steps):
         qmatmul(kt_lib, x, 1, copies[i % len(copies)], y, stream)
     torch.cuda.synchronize()
-    print(json.dumps({"only": "dominant", "kernel": "gemv_packed_kernel INT4 g64 M=1 4096x14336",
+    print(json.dumps({"only": "dominant", "kernel": "gemv_packed_single INT4 g64 M=1 4096x14336",
                       "algorithmic_bytes": gemv_bytes(1, k, n, bits, g), "launches": args.steps}), flush=True)
     return 0
 
@@ -556,7 +572,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "gemv_packed_kernel<4,4,true,0> (INT4 g64 M=1 4096x14336, packed copy)",
+                "kernel": "gemv_packed_single<4,4,true,0> (INT4 g64 M=1 4096x14336, packed copy)",
                 "algorithmic_bytes": step_bytes, "avg_us": round(ms_per_step * 1e3, 3)}
     copies_head = len(head)
     del head
@@ -607,6 +623,8 @@ def run(args, torch, kt_lib, stream_obj) -> int:
                 qmatmul(kt_lib, xg, 512, w, yg, stream)
             ag = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), cg, 32)
             plain = [w.without_copy(kt_lib) for w in cg]
+            for w in plain[:2]:  # eager calls size the stream's workspace before recording
+                qmatmul(kt_lib, xg, 512, w, yg, stream)
             ap = time_graph_launches(torch, stream_obj, lambda w: qmatmul(kt_lib, xg, 512, w, yg, stream), plain, 32)
             flops = 2.0 * 512 * k * n
             tflops = flops / (ag * 1e-3) / 1e12
@@ -658,7 +676,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
         del cm, wm
 
         # Llama-3-8B projection shapes (q/o 4096 -> 4096, k/v 4096 -> 1024, gate/up
-        # 4096 -> 14336, down 14336 -> 4096), INT4 and INT8 at group 64, M = 1, 8, 64, 512
+        # 4096 -> 14336, down 14336 -> 4096), INT4 and INT8 at group 64, M = 1, 8, 16, 64, 512
         l8 = {}
         for bits in (4, 8):
             for (k, n) in [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]:
@@ -666,7 +684,7 @@ def run(args, torch, kt_lib, stream_obj) -> int:
                 nl = max(2, -(-2 * MALL_BYTES // wl.nbytes))
                 cl = [wl] + [wl.clone(kt_lib) for _ in range(nl - 1)]
                 row = {}
-                for mm in (1, 8, 64, 512):
+                for mm in (1, 8, 16, 64, 512):
                     xl = torch.randn((mm, k), generator=gen, device="cuda", dtype=torch.float32)
                     yl = torch.empty((mm, n), device="cuda", dtype=torch.float32)
                     for w in cl[:2]:

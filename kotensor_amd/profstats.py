@@ -168,7 +168,9 @@ def main(argv=None) -> int:
     t.add_argument("--copy-bytes-read", type=float, required=True)
     t.add_argument("--copy-bytes-written", type=float, required=True)
     t.add_argument("--pattern", required=True)
-    t.add_argument("--copy-pattern", default="")
+    # the calibration run's copy kernel only (its source buffer is filled by another kernel
+    # first, whose counters must not enter the average)
+    t.add_argument("--copy-pattern", default="copyBuffer")
     t.add_argument("--algorithmic", type=int, default=0)
     t.add_argument("--out", default="")
     args = ap.parse_args(argv)
