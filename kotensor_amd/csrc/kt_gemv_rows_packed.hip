@@ -7,31 +7,38 @@
 // eight waves owns 8 / ks column sets over ks K-parts, each wave streams its set's 1 KB
 // (INT8 2 KB) chunks with four in flight (non-temporal loads) and reads its scales and
 // zero points from rows staged in LDS; so a call moves the weight bytes once, whatever M.
+// One launch per weight: x is converted inside every workgroup.
 //
 // Arithmetic (exact products, fp32 sums, the reference's per-group combine):
-//   * x: one launch before the product (rows_prep_kernel, a workgroup per row) scales each
-//     row by a power of two, 2^s_m, so that its largest |x| lies in [2^14, 2^15), and
-//     splits it into two fp16 parts, hi = fp16(x 2^s) and lo = fp16(x 2^s - hi): 22
-//     significant bits, written as the MFMA's A operands, 16 bytes per (run, part, lane
-//     group, row), which the product's workgroups copy into LDS. (Converting x inside
-//     every workgroup instead repeats M K conversions per workgroup: slower at M = 8.)
+//   * x: each row's 128-k chunk gets its own power of two, 2^s (its largest |x| into
+//     [2^14, 2^15)), and x 2^s splits into two fp16 parts, hi = fp16(x 2^s) and
+//     lo = fp16(x 2^s - hi): 22 significant bits. The parts of up to eight rows make the
+//     16 rows of one MFMA A tile (rows 0..7 hi, 8..15 lo; four rows: 0..3 and 4..7), so one
+//     MFMA per run covers both parts; sixteen rows take an A tile per part, two MFMAs per
+//     run into one accumulator. The workgroup converts the chunks of its K range into LDS
+//     once for all its waves, or (sixteen rows, or more workgroups than CUs) copies them
+//     from one conversion launch before the product;
 //   * weights: the exact integers q - z as fp16 (the bits of 1024 + q from the nibble or
 //     byte, minus 1024 + z in one packed fp16 add). The chunk's 16-byte lane pieces hold
 //     one run each (lane group kb: run kb); four lane swaps across the lane groups
 //     (v_permlane32_swap, v_permlane16_swap) transpose them so that lane group kb holds
-//     k 8 kb .. 8 kb + 7 of every run, and each MFMA step covers one run, one group;
-//   * v_mfma_f32_16x16x32_f16, hi then lo into one accumulator per run: every product is
-//     exact in fp32 (11-bit x part times an integer of at most 9 bits); lane (kb, n) gets
-//     rows 4 kb .. 4 kb + 3 of column n, and y += scale(group, n) * D per run
-//     (combineGroup, MatMul.kt:804-828, per run); INT4 high nibbles enter as 16 (q - z),
-//     so the prep divides x's parts at those positions by 16 (exact);
-//   * K's sub-parts (kt_packed.h) are summed alone and added in a fixed tree, whatever
-//     the K split; then y * 2^-s_m.
+//     k 8 kb .. 8 kb + 7 of every run. INT4 takes the nibbles as they lie (low nibbles of
+//     bytes 0 and 2, high nibbles of 0 and 2, then bytes 1 and 3 after a shift), so the A
+//     tiles hold x in that order: k 0, 2, 4, 6, 1, 3, 5, 7 of the eight;
+//   * v_mfma_f32_16x16x32_f16, one per run and A tile into one accumulator per group:
+//     every product is exact in fp32 (11-bit x part times an integer of at most 9 bits);
+//     INT4 high nibbles enter as 16 (q - z), so x's parts at those positions carry 2^(s-4).
+//     Lane (kb, n) gets A rows 4 kb .. 4 kb + 3 of column n, and per chunk
+//     y += 2^-s (sum over the chunk's groups of scale(group, n) * D) (combineGroup,
+//     MatMul.kt:804-828, per group and chunk);
+//   * K's sub-parts (kt_packed.h) are summed alone and added in a fixed tree, whatever the
+//     K split; with the parts in the rows, a row's result is its hi sum plus its lo sum.
 // A row's result therefore differs from the one-row kernel's only by the rounding of x to
 // 22 bits and the order of fp32 sums (normwise near 1e-7 against the oracle), and does
-// not depend on the other rows of the call (QuantizationTest.kt:110-134 asks 1e-4).
+// not depend on the other rows of the call (QuantizationTest.kt:110-134 asks 1e-4): its
+// bits are the same for every call of 2..8 rows, and for every call of 9..16 rows.
 // The x tiles live in LDS for the whole K range a workgroup covers when they fit, else in
-// phases: at a phase change the workgroup meets at a barrier and copies the next ones
+// phases: at a phase change the workgroup meets at a barrier and converts the next ones
 // (their loads then queue behind the weight loads in flight).
 #include "kt_common.h"
 #include "kt_packed.h"
@@ -43,96 +50,46 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-constexpr int W = 8;                  // waves per workgroup
-constexpr int R = 4;                  // chunks in flight per wave
+constexpr int W = 8;  // waves per workgroup
+constexpr int R = 4;  // chunks in flight per wave (eight measured slower at 2..16 rows)
 constexpr int MAX_ROWS = 16;
+constexpr int MAX_PASSES = 8;  // x conversion tasks a wave takes per phase
 
-// Bytes of x tiles per run: two parts x four lane groups x M rows x 16 bytes.
-__host__ __device__ constexpr int32_t run_tile_bytes(int32_t M) { return 2 * 4 * 16 * M; }
-constexpr int PREP_THREADS = 256;
-constexpr int MAX_PIECES = 16;  // 16-byte pieces of x tiles a thread moves per round
-
-// x [M x K] -> the A tiles [K / 32 runs][part][lane group kb][row][8 halves] of MT rows
-// (rows M .. MT - 1 zero) and the row shifts s_m (16 ints, zero past M): one workgroup per
-// tile row, once per call, so that the product's workgroups only copy tiles. K % 32 == 0.
-template <int BITS>
-__global__ void __launch_bounds__(PREP_THREADS)
-    rows_prep_kernel(const float* __restrict__ x, int32_t M, int32_t MT, int32_t K, _Float16* __restrict__ at,
-                     int32_t* __restrict__ shifts) {
-    __shared__ float red[PREP_THREADS / 64];
-    const int32_t m = blockIdx.x, t = threadIdx.x;
-    const int32_t units = K >> 3;  // 8 k per unit
-    if (m >= M) {  // a padding row of the tiles
-        for (int32_t u = t; u < units; u += PREP_THREADS) {
-            _Float16* base = at + static_cast<size_t>(u >> 2) * (2 * 4 * 8 * MT);
-            *reinterpret_cast<u32x4*>(base + (0 * 4 + (u & 3)) * MT * 8 + m * 8) = u32x4{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(base + (1 * 4 + (u & 3)) * MT * 8 + m * 8) = u32x4{0u, 0u, 0u, 0u};
-        }
-        if (t == 0) shifts[m] = 0;
-        return;
-    }
-    const float* row = x + static_cast<size_t>(m) * K;
-    // the row's largest |x| (a NaN or an infinity compares above every finite value)
-    uint32_t mb = 0u;
-    for (int32_t u = t; u < units; u += PREP_THREADS) {
-        const float4 a = reinterpret_cast<const float4*>(row)[2 * u];
-        const float4 b = reinterpret_cast<const float4*>(row)[2 * u + 1];
-        mb = max(mb, max(max(max(__float_as_uint(fabsf(a.x)), __float_as_uint(fabsf(a.y))),
-                             max(__float_as_uint(fabsf(a.z)), __float_as_uint(fabsf(a.w)))),
-                         max(max(__float_as_uint(fabsf(b.x)), __float_as_uint(fabsf(b.y))),
-                             max(__float_as_uint(fabsf(b.z)), __float_as_uint(fabsf(b.w))))));
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mb = max(mb, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mb), o, 64)));
-    if ((t & 63) == 0) red[t >> 6] = __uint_as_float(mb);
-    __syncthreads();
-    mb = max(max(__float_as_uint(red[0]), __float_as_uint(red[1])), max(__float_as_uint(red[2]), __float_as_uint(red[3])));
-    // largest |x| into [2^14, 2^15); a zero or non-finite row is not scaled (non-finite
-    // values then make non-finite outputs, as the reference's sums do)
-    const int32_t s = mb == 0u || mb >= 0x7F800000u ? 0 : 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(mb));
-    for (int32_t u = t; u < units; u += PREP_THREADS) {
-        const float4 a = reinterpret_cast<const float4*>(row)[2 * u];
-        const float4 b = reinterpret_cast<const float4*>(row)[2 * u + 1];
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        half8 hv, lv;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float xs = ldexpf(v[j], s);
-            const _Float16 h = static_cast<_Float16>(xs);
-            // INT4: positions 4..7 of the 8 meet high nibbles, which enter as 16 (q - z)
-            const float f = BITS == 4 && j >= 4 ? 0.0625f : 1.0f;
-            hv[j] = static_cast<_Float16>(static_cast<float>(h) * f);
-            lv[j] = static_cast<_Float16>((xs - static_cast<float>(h)) * f);  // the difference is exact
-        }
-        const int32_t run = u >> 2, kb = u & 3;
-        _Float16* base = at + static_cast<size_t>(run) * (2 * 4 * 8 * MT);
-        *reinterpret_cast<half8*>(base + (0 * 4 + kb) * MT * 8 + m * 8) = hv;
-        *reinterpret_cast<half8*>(base + (1 * 4 + kb) * MT * 8 + m * 8) = lv;
-    }
-    if (t == 0) {
-        shifts[m] = s;
-        if (m == 0)
-            for (int32_t r = MT; r < MAX_ROWS; ++r) shifts[r] = 0;
-    }
+// Two arrangements of x's parts. Up to eight rows: both parts in the rows of one A tile
+// (rows 0..7 hi, 8..15 lo; four rows: 0..3 and 4..7), one MFMA per run. Sixteen rows: an
+// A tile per part, [part][lane group kb][row][8 halves], both MFMAs into one accumulator
+// (half the values per lane to combine that two tiles of eight rows would hold).
+__host__ __device__ constexpr bool parts_in_k(int32_t MT) { return MT == 16; }
+// x rows per A tile.
+__host__ __device__ constexpr int32_t tile_x_rows(int32_t MT) { return MT < 8 ? MT : MT == 8 ? 8 : 16; }
+// Bytes of x tiles per run: MT rows x two parts x 32 k x 2 bytes; with the parts in the
+// rows, per A tile [lane group kb][A row, swizzled][8 halves].
+__host__ __device__ constexpr int32_t run_tile_bytes(int32_t MT) { return 2 * 4 * 16 * MT; }
+// The 16-byte slot of (lane group kb, A row a) in an A tile of HR x rows: a ^ 4 kb (HR = 4:
+// a ^ 4 (kb / 2)), so that the conversion's stores (lanes: four rows x the four lane
+// groups) meet 16 different bank groups, as the MFMA's reads (lanes: the A rows of one lane
+// group) do without it.
+template <int HR>
+__device__ __forceinline__ int32_t a_slot(int32_t kb, int32_t a) {
+    return kb * (2 * HR) + (a ^ (HR == 8 ? 4 * kb : 4 * (kb >> 1)));
 }
 
-// The workgroup's LDS: the x tiles of one phase [ks][cpp chunks][4 runs][tile], each tile
-// [part][lane group kb][row][8 halves]; each wave's staged scale and zero-point rows; the
-// meeting area [W][16 rows][16 columns] floats.
-__host__ __device__ constexpr int32_t rows_lds_a(int32_t ks, int32_t cpp, int32_t M) {
-    return ks * cpp * 4 * run_tile_bytes(M);
+// The workgroup's LDS: the x tiles of one phase [ks][cpp chunks][4 runs][tile]; the
+// chunks' factors 2^-s [ks][cpp][MT] floats; each wave's staged scale and zero-point rows.
+// At the end the meeting area [W][A tiles][16 A rows][16 columns] floats takes the tiles'
+// place (it is never larger).
+__host__ __device__ constexpr int32_t rows_lds_p(int32_t ks, int32_t cpp, int32_t MT) {
+    return ks * cpp * 4 * run_tile_bytes(MT);
 }
-__host__ __device__ constexpr int32_t rows_lds_stage(int32_t ks, int32_t cpp, int32_t M) {
-    return rows_lds_a(ks, cpp, M);
+__host__ __device__ constexpr int32_t rows_lds_stage(int32_t ks, int32_t cpp, int32_t MT) {
+    return rows_lds_p(ks, cpp, MT) + ks * cpp * MT * 4;
 }
-__host__ __device__ constexpr int32_t rows_lds_red(int32_t ks, int32_t cpp, int32_t M, int32_t rows) {
-    return rows_lds_stage(ks, cpp, M) + W * rows * STAGE_ROW_BYTES;
-}
-__host__ __device__ constexpr int32_t rows_lds_bytes(int32_t ks, int32_t cpp, int32_t M, int32_t rows) {
-    return rows_lds_red(ks, cpp, M, rows) + W * 16 * 16 * 4;
+__host__ __device__ constexpr int32_t rows_lds_bytes(int32_t ks, int32_t cpp, int32_t MT, int32_t rows) {
+    return rows_lds_stage(ks, cpp, MT) + W * rows * STAGE_ROW_BYTES;
 }
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -160,19 +117,92 @@ __device__ __forceinline__ void transpose4(uint32_t (&v)[4]) {
     v[3] = d[1];
 }
 
-// GS: the group size's class (0: g = 32, a group per run; 1: g = 64, a group per two
-// runs; 2: g >= 128, one group per chunk), MT: rows of the x tiles (4, 8 or 16; rows M ..
-// MT - 1 are zero).
-template <int BITS, bool ZP, int GS, int MT>
+// hi and lo fp16 parts of two floats (RNE; the differences are exact in fp32)
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const half2v h = __builtin_convertvector(f32x2{a, b}, half2v);
+    const half2v l = __builtin_convertvector(f32x2{a - static_cast<float>(h[0]), b - static_cast<float>(h[1])}, half2v);
+    hi = as_u(h);
+    lo = as_u(l);
+}
+
+// x conversion, a task at a time: a task is four rows' one chunk, a wave's lane (row
+// 4 q + (ln & 3), 8-k slice (ln >> 2) & 3, run ln >> 4) holding its 8 floats (zeros past M
+// and K). Returns 2^-s of the lane's row and chunk and its hi and lo parts in the A order:
+// INT4 k 0, 2, 4, 6, 1, 3, 5, 7 of the eight (4..7 meet high nibbles: 2^(s - 4)), INT8
+// k 0..7.
+template <int BITS>
+__device__ __forceinline__ float convert_task(const float4& a, const float4& b, uint32_t (&hw)[4], uint32_t (&lw)[4]) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float mx = fabsf(v[0]);
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    mx = rows4_max(row_stride4_max(mx));  // the row's 16 slices of the chunk
+    // largest |x| into [2^14, 2^15); a zero or non-finite chunk is not scaled (non-finite
+    // values then make non-finite outputs, as the reference's sums do); at most 2^126, so
+    // that 2^-s stays a normal float
+    const bool finite = mx <= 3.402823466e38f;
+    const int32_t s = finite && mx > 0.0f ? min(15 - __builtin_amdgcn_frexp_expf(mx), 126) : 0;
+    constexpr int ORD4[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {
+        const int e0 = BITS == 4 ? ORD4[2 * pr] : 2 * pr, e1 = BITS == 4 ? ORD4[2 * pr + 1] : 2 * pr + 1;
+        split2(ldexpf(v[e0], BITS == 4 && e0 >= 4 ? s - 4 : s), ldexpf(v[e1], BITS == 4 && e1 >= 4 ? s - 4 : s), hw[pr],
+               lw[pr]);
+    }
+    return ldexpf(1.0f, -s);
+}
+// Byte offset of x row `row`'s part (0 hi, 1 lo) for lane group kb in a run's tiles.
+template <int MT>
+__device__ __forceinline__ int32_t tile_offset(int32_t row, int32_t kb, int32_t part) {
+    constexpr int HR = tile_x_rows(MT);
+    if constexpr (parts_in_k(MT)) return part * 1024 + (kb * 16 + row) * 16;
+    return (row / HR) * (128 * HR) + a_slot<HR>(kb, part * HR + row % HR) * 16;
+}
+
+// x [M x K] -> the A tiles of every chunk [chunks][4 runs][tile], then their factors 2^-s
+// [chunks][MT] floats: a task per wave, once per call, for the products that copy tiles
+// instead of converting x themselves. Quads past M are not written (their A rows reach only
+// output rows that are never stored).
+template <int BITS, int MT>
 __global__ void __launch_bounds__(64 * W)
-    gemv_rows_packed_kernel(const uint8_t* __restrict__ packed, const _Float16* __restrict__ at,
-                            const int32_t* __restrict__ shifts_m, int32_t M, int32_t N, int32_t K, int32_t shifts,
-                            int32_t cpp, float alpha, float* out, int32_t accumulate, const float* bias) {
+    rows_prep_kernel(const float* __restrict__ x, int32_t M, int32_t K, unsigned char* __restrict__ xt) {
+    constexpr int32_t tile = run_tile_bytes(MT);
+    const int32_t chunks = (K + CHUNK - 1) >> 7, ln = threadIdx.x & 63;
+    const int32_t j = blockIdx.x * W + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (j >= ((M + 3) >> 2) * chunks) return;
+    const int32_t quad = j / chunks, c = j - quad * chunks;
+    const int32_t xrow = ln & 3, xsl = (ln >> 2) & 3, xrun = ln >> 4;
+    const int32_t row = 4 * quad + xrow, k = c * CHUNK + xrun * RUN + xsl * 8;
+    const int32_t xoob = M * K * 4;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, xoob, 0x00020000);
+    const int32_t off = row < M && k < K ? (row * K + k) * 4 : xoob;
+    const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 16, 0));
+    uint32_t hw[4], lw[4];
+    const float f = convert_task<BITS>(a, b, hw, lw);
+    unsigned char* d = xt + static_cast<size_t>(c * 4 + xrun) * tile;
+    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    if ((ln >> 2) == 0) reinterpret_cast<float*>(xt + static_cast<size_t>(chunks) * 4 * tile)[c * MT + row] = f;
+}
+
+// GS: the group size's class (0: g = 32, a group per run; 1: g = 64, a group per two
+// runs; 2: g >= 128, one group per chunk), MT: rows of the x tiles (4, 8 or 16; rows
+// M .. MT - 1 reach only output rows that are never stored). COPY: x is rows_prep_kernel's
+// output, which the workgroup copies; otherwise the workgroup converts x itself.
+template <int BITS, bool ZP, int GS, int MT, bool COPY>
+__global__ void __launch_bounds__(64 * W)
+    gemv_rows_packed_kernel(const uint8_t* __restrict__ packed, const float* __restrict__ x, int32_t M, int32_t N,
+                            int32_t K, int32_t shifts, float alpha, float* out, int32_t accumulate, const float* bias) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
+    constexpr bool PK = parts_in_k(MT);
+    // x rows per A tile, A tiles of x rows, A rows used, A operands per run
+    constexpr int HR = tile_x_rows(MT), NT = MT / HR, AR = PK ? 16 : 2 * HR, NA = PK ? 2 : NT;
+    constexpr int32_t tile = run_tile_bytes(MT);
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int32_t kslog = shifts & 15, gshift = shifts >> 4;
-    const int32_t ks = 1 << kslog;
+    const int32_t kslog = shifts & 15, gshift = (shifts >> 4) & 15, cpplog = shifts >> 8;
+    const int32_t ks = 1 << kslog, cpp = 1 << cpplog;
     const int32_t sets = N >> 4, chunks = (K + CHUNK - 1) >> 7, G = (K + (RUN << gshift) - 1) >> (gshift + 5);
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -191,44 +221,107 @@ __global__ void __launch_bounds__(64 * W)
     const int32_t col = set * SET + nl;
     const int32_t phases = (nmax + cpp - 1) / cpp;
     const int32_t rows = stage_rows(nmax, gshift);
-    constexpr int32_t tile = run_tile_bytes(MT);
 
-    // ---- loads, in the order they complete: the first phase's x tiles (16 bytes per
-    // thread and step), the wave's scale and zero-point rows, the first R chunks of weights.
-    const int32_t piece_count = ks * cpp * 4 * tile / 16;  // 16-byte pieces of a phase
-    const __amdgpu_buffer_rsrc_t ar =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(at), 0, (K >> 5) * tile, 0x00020000);
-    // piece p of phase ph: part p / per_part, then that part's chunks [begin + ph cpp, ...)
-    // in run order, contiguous in the prep's output; runs past K (the padding of the last
-    // chunk) and chunks past the part read zeros
-    auto piece_offset = [&](int32_t p, int32_t ph) -> int32_t {
-        const int32_t per_part = cpp * 4 * tile / 16;
-        const int32_t part = p / per_part, within = p - part * per_part;
-        const int32_t cb = ((part * chunks) >> kslog) + ph * cpp;
+    // ---- x into the phase's tiles. Converting: task j of a phase is quad j / (ks cpp),
+    // phase chunk j % (ks cpp) (powers of two: shifts and masks), MAX_PASSES tasks per wave
+    // at most. Copying: 16-byte pieces of the prep's tiles and factors, each part's chunks
+    // of the phase contiguous there and here.
+    const int32_t ppr = ks * cpp;               // a phase's chunks over the K-parts
+    const int32_t tasks = ((M + 3) >> 2) * ppr;  // quads past M are not converted
+    const int32_t xrow = ln & 3, xsl = (ln >> 2) & 3, xrun = ln >> 4;
+    const int32_t xoob = COPY ? chunks * (4 * tile + MT * 4) : M * K * 4;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, xoob, 0x00020000);
+    float4 xv[MAX_PASSES][2];
+    // the task's quad and phase chunk (wave-uniform), and the lane's byte offset in x
+    // (rows past M, runs past K and chunks past the part read zeros without memory traffic)
+    auto task_of = [&](int32_t j, int32_t ph, int32_t& quad, int32_t& ch) -> int32_t {
+        quad = j >> (kslog + cpplog);
+        ch = j & (ppr - 1);
+        const int32_t part = ch >> cpplog;
+        const int32_t c = ph * cpp + (ch & (cpp - 1));
+        const int32_t cg = ((part * chunks) >> kslog) + c;
         const int32_t ce = ((part + 1) * chunks) >> kslog;
-        const int32_t off = cb * 4 * tile + within * 16;
-        return off < ce * 4 * tile ? off : 0x7FFFFFF0;
+        const int32_t row = 4 * quad + xrow, k = cg * CHUNK + xrun * RUN + xsl * 8;
+        return cg < ce && row < M && k < K ? (row * K + k) * 4 : xoob;
     };
-    const int32_t rounds = (piece_count + 64 * W * MAX_PIECES - 1) / (64 * W * MAX_PIECES);
-    u32x4 ap[MAX_PIECES];
-    auto load_round = [&](int32_t ph, int32_t rd) {
+    // copy pieces: a part's phase is 2^(cpplog + 5 + log2 MT) pieces of tiles (32 MT per
+    // chunk); the factors ks cpp MT / 4 pieces (MT / 4 per chunk)
+    constexpr int MTLOG = MT == 4 ? 2 : MT == 8 ? 3 : 4;
+    const int32_t tile_pieces = ks << (cpplog + 5 + MTLOG);
+    auto piece_off = [&](int32_t q, int32_t ph) -> int32_t {  // the prep's byte offset of tile piece q, or xoob
+        const int32_t part = q >> (cpplog + 5 + MTLOG), within = q & ((1 << (cpplog + 5 + MTLOG)) - 1);
+        const int32_t cg = ((part * chunks) >> kslog) + ph * cpp + (within >> (5 + MTLOG));
+        return cg < (((part + 1) * chunks) >> kslog) ? (cg << (5 + MTLOG)) * 16 + (within & ((32 << MTLOG) - 1)) * 16
+                                                     : xoob;
+    };
+    // factor piece q (at most 128 of them: one per thread, with the first round)
+    const int32_t factor_pieces = ks << (cpplog + MTLOG - 2);
+    auto factor_off = [&](int32_t q, int32_t ph) -> int32_t {
+        const int32_t part = q >> (cpplog + MTLOG - 2), within = q & ((1 << (cpplog + MTLOG - 2)) - 1);
+        const int32_t cg = ((part * chunks) >> kslog) + ph * cpp + (within >> (MTLOG - 2));
+        return cg < (((part + 1) * chunks) >> kslog)
+                   ? chunks * 4 * tile + (cg * MT + (within & ((MT >> 2) - 1)) * 4) * 4
+                   : xoob;
+    };
+    const int32_t copy_rounds = (tile_pieces + 2 * 64 * W * MAX_PASSES - 1) / (2 * 64 * W * MAX_PASSES);
+    float4 fv;
+    auto load_x = [&](int32_t ph, int32_t rd) {
+        if constexpr (COPY)
+            if (rd == 0 && tid < factor_pieces)
+                fv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, factor_off(tid, ph), 0, 0));
 #pragma unroll
-        for (int i = 0; i < MAX_PIECES; ++i) {
-            const int32_t p = tid + 64 * W * (MAX_PIECES * rd + i);
-            ap[i] = p < piece_count
-                        ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, piece_offset(p, ph), 0, 0))
-                        : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < MAX_PASSES; ++i) {
+            if constexpr (COPY) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int32_t q = tid + 64 * W * (2 * MAX_PASSES * rd + 2 * i + h);
+                    if (q < tile_pieces)
+                        xv[i][h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, piece_off(q, ph), 0, 0));
+                }
+            } else {
+                const int32_t j = i * W + wave;
+                if (j < tasks) {
+                    int32_t quad, ch;
+                    const int32_t off = task_of(j, ph, quad, ch);
+                    xv[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+                    xv[i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 16, 0));
+                }
+            }
         }
     };
-    auto store_round = [&](int32_t rd) {
+    float* pl = reinterpret_cast<float*>(smem + rows_lds_p(ks, cpp, MT));  // [ks cpp][MT]: 2^-s
+    auto store_x = [&](int32_t ph, int32_t rd) {
+        if constexpr (COPY)
+            if (rd == 0 && tid < factor_pieces) reinterpret_cast<float4*>(pl)[tid] = fv;
 #pragma unroll
-        for (int i = 0; i < MAX_PIECES; ++i) {
-            const int32_t p = tid + 64 * W * (MAX_PIECES * rd + i);
-            if (p < piece_count) reinterpret_cast<u32x4*>(smem)[p] = ap[i];
+        for (int i = 0; i < MAX_PASSES; ++i) {
+            if constexpr (COPY) {
+                // the phase's tiles are contiguous in LDS as in the piece order
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int32_t q = tid + 64 * W * (2 * MAX_PASSES * rd + 2 * i + h);
+                    if (q < tile_pieces) reinterpret_cast<float4*>(smem)[q] = xv[i][h];
+                }
+            } else {
+                const int32_t j = i * W + wave;
+                if (j >= tasks) break;
+                int32_t quad, ch;
+                task_of(j, ph, quad, ch);
+                uint32_t hw[4], lw[4];
+                const float f = convert_task<BITS>(xv[i][0], xv[i][1], hw, lw);
+                const int32_t row = 4 * quad + xrow;  // < MT
+                unsigned char* d = smem + (ch * 4 + xrun) * tile;
+                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if ((ln >> 2) == 0) pl[ch * MT + row] = f;
+            }
         }
     };
-    load_round(0, 0);
+    const int32_t x_rounds = COPY ? copy_rounds : 1;
 
+    // ---- loads, in the order they complete: the first phase's x, the wave's scale and
+    // zero-point rows, the first R chunks of weights.
+    load_x(0, 0);
     const float* ps = reinterpret_cast<const float*>(packed + static_cast<int64_t>(sets) * chunks * BB);
     const int8_t* pz = reinterpret_cast<const int8_t*>(ps + static_cast<int64_t>(sets) * G * SET);
     const int32_t g0 = k0 >> (gshift + 5);
@@ -260,13 +353,12 @@ __global__ void __launch_bounds__(64 * W)
     };
 #pragma unroll
     for (int s = 0; s < R; ++s) issue(s, s);
-    const int4 rsh = *reinterpret_cast<const int4*>(shifts_m + 4 * kb);  // rows 4 kb .. 4 kb + 3
 
-    // ---- into LDS: the x tiles, the wave's staged rows ---------------------------------
-    store_round(0);
-    for (int32_t rd = 1; rd < rounds; ++rd) {  // a phase larger than one round
-        load_round(0, rd);
-        store_round(rd);
+    // ---- into LDS: the first phase's x tiles, the wave's staged rows ----------------------
+    store_x(0, 0);
+    for (int32_t rd = 1; rd < x_rounds; ++rd) {  // a phase larger than one round of pieces
+        load_x(0, rd);
+        store_x(0, rd);
     }
     unsigned char* stg = smem + rows_lds_stage(ks, cpp, MT) + wave * rows * STAGE_ROW_BYTES;
 #pragma unroll
@@ -276,29 +368,33 @@ __global__ void __launch_bounds__(64 * W)
         if (ln < rows) *reinterpret_cast<u32x4*>(stg + rows * SET * 4 + 16 * ln) = zst;
     __syncthreads();
 
-    // lanes of rows past MT read row MT - 1's operand: an MFMA's output rows depend only
-    // on their own A rows, and rows past M are never stored
-    const int32_t a_lane = kb * MT * 16 + min(nl, MT - 1) * 16;
-    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // lanes of A rows past AR (four x rows) read A row AR - 1: an MFMA's output rows depend
+    // only on their own A rows, and those are never stored
+    const int32_t a_lane = PK ? (kb * 16 + nl) * 16 : a_slot<HR>(kb, min(nl, AR - 1)) * 16;
+    const int32_t p_row = (4 * kb) % HR;  // the x row of the lane's first A row
+    float y[NT][4] = {};
     // sub-parts of K, each summed alone and added in a balanced tree in K order (the
     // one-row kernel's scheme): the result does not depend on ks
     const int32_t sp_count = SUB_PARTS >> kslog, sp0 = kp * sp_count;
     int32_t sp = 0;
     int32_t sp_end = (((sp0 + 1) * chunks) >> SUB_LOG) - c_begin;
-    float tree[4][3] = {};
-    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float tree[NT][4][3] = {};
+    float part[NT][4] = {};
     auto close_sub_part = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            part[i] = tree_push(tree[i], sp, y[i]);
-            y[i] = 0.0f;
-        }
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                part[tt][i] = tree_push(tree[tt][i], sp, y[tt][i]);
+                y[tt][i] = 0.0f;
+            }
         ++sp;
         sp_end = (((sp0 + sp + 1) * chunks) >> SUB_LOG) - c_begin;
     };
     const int32_t run0 = k0 >> 5;  // the wave's first run
     // the slot's weights, transposed: t[r] = k 8 kb .. 8 kb + 7 of run r of the chunk
-    // (INT8: t2[r] the next 8 bytes) -- taken out of the ring so the slot refills at once
+    // (INT8: t[r] k 8 kb .. 8 kb + 3, t2[r] the next 4) -- taken out of the ring so the
+    // slot refills at once
     auto take = [&](int s, uint32_t (&t)[4], uint32_t (&t2)[4]) {
         if constexpr (BITS == 4) {
             t[0] = wb[s][0][0];
@@ -328,10 +424,12 @@ __global__ void __launch_bounds__(64 * W)
         // a chunk past the wave's range adds nothing; its reads stay in the phase's tiles
         // and the wave's staged rows (the phase's first chunk is below nmax)
         const int32_t cc = live ? cl : ph * cpp;
-        const unsigned char* tc = smem + (kp * cpp + (cc - ph * cpp)) * 4 * tile + a_lane;
+        const int32_t chl = kp * cpp + (cc - ph * cpp);  // the chunk's place in the phase
+        const unsigned char* tc = smem + chl * 4 * tile + a_lane;
         float sc[NGC];
         uint32_t zc[NGC];
-        half8 ah[4], al[4];
+        half8 a[NA][4];  // [A tile or part][run]
+        f32x4 pf[NT];
 #pragma unroll
         for (int gi = 0; gi < NGC; ++gi) {
             // the group row of runs gi RPG .. (a run past K, the padding of the last chunk,
@@ -341,11 +439,14 @@ __global__ void __launch_bounds__(64 * W)
             zc[gi] = ZP ? stg[rows * SET * 4 + gr * SET + nl] : 0u;
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            ah[r] = *reinterpret_cast<const half8*>(tc + r * tile);
-            al[r] = *reinterpret_cast<const half8*>(tc + r * tile + 4 * MT * 16);
-        }
-        // the exact fp16 offsets of each group: 1024 + z (INT4 also 1024 + 16 z), 1152 + z
+        for (int u = 0; u < NA; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                a[u][r] = *reinterpret_cast<const half8*>(tc + r * tile + u * (PK ? 1024 : 128 * HR));
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) pf[tt] = *reinterpret_cast<const f32x4*>(pl + chl * MT + tt * HR + p_row);
+        // the exact fp16 offsets of each group: 1024 + z (INT4 also 1024 + 16 z); INT8
+        // 1152 + z (its bytes enter as 1152 + q)
         half2v ol[NGC], oh[NGC];
 #pragma unroll
         for (int gi = 0; gi < NGC; ++gi) {
@@ -365,52 +466,61 @@ __global__ void __launch_bounds__(64 * W)
             uint32_t bw[4];
             const half2v o_lo = ol[r / RPG], o_hi = oh[r / RPG];
             if constexpr (BITS == 4) {
-                // halves 0..3: low nibbles, the bits of 1024 + q; 4..7: high nibbles, 1024 + 16 q;
-                // minus 1024 + z and 1024 + 16 z (the bits 0x6400 | z, 0x6400 | z << 4)
-                const half2v ol = o_lo, oh = o_hi;
-                const uint32_t p01 = perm(0u, t[r], 0x0c010c00u), p23 = perm(0u, t[r], 0x0c030c02u);
-                bw[0] = as_u(as_h2(and_or(p01, 0x000F000Fu, 0x64006400u)) - ol);
-                bw[1] = as_u(as_h2(and_or(p23, 0x000F000Fu, 0x64006400u)) - ol);
-                bw[2] = as_u(as_h2(and_or(p01, 0x00F000F0u, 0x64006400u)) - oh);
-                bw[3] = as_u(as_h2(and_or(p23, 0x00F000F0u, 0x64006400u)) - oh);
+                // halves: the bits of 1024 + q (low nibbles) or 1024 + 16 q (high nibbles),
+                // minus 1024 + z or 1024 + 16 z: bytes 0 and 2, then 1 and 3
+                const uint32_t w = t[r], w8 = t[r] >> 8;
+                bw[0] = as_u(as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) - o_lo);   // k 0, 2
+                bw[1] = as_u(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)) - o_hi);   // k 4, 6
+                bw[2] = as_u(as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)) - o_lo);  // k 1, 3
+                bw[3] = as_u(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)) - o_hi);  // k 5, 7
             } else {
-                // byte b: (b ^ 0x80) + 1024 = 1152 + q; minus 1152 + z, the bits 0x6400 | (z ^ 0x80)
-                const half2v o = o_lo;
-                bw[0] = as_u(as_h2(perm(0u, t[r], 0x0c010c00u) ^ 0x64806480u) - o);
-                bw[1] = as_u(as_h2(perm(0u, t[r], 0x0c030c02u) ^ 0x64806480u) - o);
-                bw[2] = as_u(as_h2(perm(0u, t2[r], 0x0c010c00u) ^ 0x64806480u) - o);
-                bw[3] = as_u(as_h2(perm(0u, t2[r], 0x0c030c02u) ^ 0x64806480u) - o);
+                // byte b (signed q): 0x64 above b ^ 0x80 is 1152 + q; minus 1152 + z
+                const uint32_t u0 = t[r] ^ 0x80808080u, u1 = t2[r] ^ 0x80808080u;
+                bw[0] = as_u(as_h2(perm(0x64646464u, u0, 0x04010400u)) - o_lo);
+                bw[1] = as_u(as_h2(perm(0x64646464u, u0, 0x04030402u)) - o_lo);
+                bw[2] = as_u(as_h2(perm(0x64646464u, u1, 0x04010400u)) - o_lo);
+                bw[3] = as_u(as_h2(perm(0x64646464u, u1, 0x04030402u)) - o_lo);
             }
             b[r] = __builtin_bit_cast(half8, u32x4{bw[0], bw[1], bw[2], bw[3]});
         }
-        // one accumulator per group: its runs' hi and lo products in run order
-        f32x4 acc[NGC];
+        // one accumulator per A tile and group: its runs' products in run order
+        f32x4 acc[NT][NGC];
 #pragma unroll
-        for (int gi = 0; gi < NGC; ++gi) acc[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int gi = 0; gi < NGC; ++gi) acc[tt][gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            acc[r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], b[r], acc[r / RPG], 0, 0, 0);
-            acc[r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[r], b[r], acc[r / RPG], 0, 0, 0);
+            if constexpr (PK) {  // hi, then lo
+                acc[0][r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][r], b[r], acc[0][r / RPG], 0, 0, 0);
+                acc[0][r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][r], b[r], acc[0][r / RPG], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt)
+                    acc[tt][r / RPG] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][r], b[r], acc[tt][r / RPG], 0, 0, 0);
+            }
         }
         // a chunk past the wave's range may have read tiles no phase wrote: its whole
         // contribution is dropped by a select, never scaled by zero (0 * NaN)
-        float cy[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            cy[i] = y[i];
+        for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-            for (int gi = 0; gi < NGC; ++gi) cy[i] = fmaf(sc[gi], acc[gi][i], cy[i]);
-            y[i] = live ? cy[i] : y[i];
-        }
+            for (int i = 0; i < 4; ++i) {
+                float cy = sc[0] * acc[tt][0][i];
+#pragma unroll
+                for (int gi = 1; gi < NGC; ++gi) cy = fmaf(sc[gi], acc[tt][gi][i], cy);
+                const float yn = fmaf(pf[tt][i], cy, y[tt][i]);
+                y[tt][i] = live ? yn : y[tt][i];
+            }
     };
     // The ring over each phase's chunks (refills cross the loop's back edge, as in the
     // one-row kernel; cpp is a multiple of R, so the ring's slots line up with phases).
     for (int32_t ph = 0; ph < phases; ++ph) {
         if (ph > 0) {
             __syncthreads();  // every wave is done with the previous phase's tiles
-            for (int32_t rd = 0; rd < rounds; ++rd) {
-                load_round(ph, rd);
-                store_round(rd);
+            for (int32_t rd = 0; rd < x_rounds; ++rd) {
+                load_x(ph, rd);
+                store_x(ph, rd);
             }
             __syncthreads();
         }
@@ -428,24 +538,29 @@ __global__ void __launch_bounds__(64 * W)
         }
     }
 
-    // ---- the last sub-parts; the K-parts of each column set (the tree's top); the row
-    // shifts; the stores
+    // ---- the last sub-parts; the K-parts of each column set (the tree's top), a row's
+    // hi and lo sums; the stores. The meeting area takes the x tiles' place.
     while (sp < sp_count) close_sub_part();
-    float* red = reinterpret_cast<float*>(smem + rows_lds_red(ks, cpp, MT, rows));  // [W][16 rows][16 cols]
+    __syncthreads();  // every wave is done with the tiles
+    float* red = reinterpret_cast<float*>(smem);  // [W][NT][16 A rows][16 columns]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * kb + i) * 16 + nl] = part[i];
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[((wave * NT + tt) * 16 + 4 * kb + i) * 16 + nl] = part[tt][i];
     __syncthreads();
     if (kp != 0 || !set_live) return;
     const int32_t cs = 1 << cslog;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int32_t m = 4 * kb + i;
+    for (int j = 0; j < MT / 4; ++j) {
+        const int32_t m = 4 * j + kb;  // lane group kb stores rows kb, kb + 4, ...
         if (m >= M) continue;
-        const float sum = tree_top(red + (my_cs * 16 + m) * 16 + nl, cs * 256, kslog);
+        const float* base = red + (my_cs * NT + m / HR) * 256 + nl;
+        const float sum = PK ? tree_top(base + m * 16, cs * NT * 256, kslog)
+                             : tree_top(base + (m % HR) * 16, cs * NT * 256, kslog) +
+                                   tree_top(base + (HR + m % HR) * 16, cs * NT * 256, kslog);  // hi + lo
         float* dst = out + static_cast<size_t>(m) * N + col;
         float o = accumulate ? *dst : 0.0f;
-        const int32_t sh[4] = {rsh.x, rsh.y, rsh.z, rsh.w};
-        o = fmaf(alpha, ldexpf(sum, -sh[i]), o);
+        o = fmaf(alpha, sum, o);
         if (bias) o += bias[col];
         *dst = o;
     }
@@ -455,8 +570,9 @@ __global__ void __launch_bounds__(64 * W)
 
 // The launch: the one-row kernel's K split (plan_packed), or the largest smaller one
 // whose x tiles fit (the result does not depend on the split); the x tiles a phase holds
-// (chunks per phase: a multiple of R, the wave's range rounded up to R when all of it
-// fits in what LDS the staged rows and the meeting area leave); the LDS. ks = 0: none fits.
+// (chunks per phase: a power of two, at least R, at most what the waves convert in
+// MAX_PASSES tasks each, no more than the wave's range needs, within what LDS
+// the staged rows leave); the LDS. ks = 0: none fits.
 struct RowsPlan {
     int32_t ks = 0, cpp = 0;
     size_t lds = 0;
@@ -468,20 +584,22 @@ static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets) {
     RowsPlan r;
     const PackedPlan plan = plan_packed(K, g, sets);
     const int32_t gshift = log2_exact(g / RUN), chunks = ceil_div(K, CHUNK);
-    M = tile_rows(M);
-    const int32_t tile = run_tile_bytes(M);
+    const int32_t mt = tile_rows(M), quads = ceil_div(M, 4);
+    const int32_t tile = run_tile_bytes(mt);
     for (int32_t ks = plan.ks; ks >= 1; ks /= 2) {
         const int32_t nmax = ceil_div(chunks, ks);
         if (nmax > MAX_WAVE_CHUNKS) break;
         const int32_t rows = stage_rows(nmax, gshift);
-        const int32_t fixed = rows_lds_bytes(ks, 0, M, rows);
+        const int32_t fixed = rows_lds_bytes(ks, 0, mt, rows);
         if (fixed >= static_cast<int32_t>(LDS_MAX)) continue;
-        int32_t cpp = (static_cast<int32_t>(LDS_MAX) - fixed) / (ks * 4 * tile);
-        cpp = std::min(cpp, (nmax + R - 1) / R * R) / R * R;
-        if (cpp < R) continue;
+        int32_t cap = (static_cast<int32_t>(LDS_MAX) - fixed) / (ks * (4 * tile + mt * 4));
+        cap = std::min(cap, W * MAX_PASSES / (quads * ks));
+        int32_t cpp = R;
+        while (cpp * 2 <= cap && cpp < nmax) cpp *= 2;
+        if (cpp > cap) continue;
         r.ks = ks;
         r.cpp = cpp;
-        r.lds = static_cast<size_t>(rows_lds_bytes(ks, cpp, M, rows));
+        r.lds = static_cast<size_t>(rows_lds_bytes(ks, cpp, mt, rows));
         return r;
     }
     return r;
@@ -496,7 +614,6 @@ bool gemv_rows_packed_preferred(const WeightView& w) { return w.N / SET >= 16 * 
 bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
     if (m < 2 || m > MAX_ROWS || !w.p) return false;
     if (w.K % RUN != 0 || w.K > 16384) return false;
-    if (static_cast<int64_t>(w.K / RUN) * run_tile_bytes(m) > INT32_MAX) return false;
     if (w.g % RUN != 0 || log2_exact(w.g / RUN) < 0) return false;
     if (w.N % SET != 0) return false;
     if (static_cast<int64_t>(w.G) * w.N * 4 > INT32_MAX) return false;
@@ -504,54 +621,83 @@ bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, 
     return rows_plan(m, w.K, w.g, w.N / SET).ks != 0;
 }
 
-template <int GS, int MT>
+template <int GS, int MT, bool COPY>
 static int32_t launch_rows(int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st, const uint8_t* p,
-                           const _Float16* at, const int32_t* sh, int32_t m, int32_t N, int32_t K, int32_t shifts,
-                           int32_t cpp, float alpha, float* c, int32_t accumulate, const float* bias) {
+                           const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts, float alpha, float* c,
+                           int32_t accumulate, const float* bias) {
     if (bits == 4) {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<4, true, GS, MT>>(lds)) return ls;
-        gemv_rows_packed_kernel<4, true, GS, MT>
-            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<4, true, GS, MT, COPY>>(lds)) return ls;
+        gemv_rows_packed_kernel<4, true, GS, MT, COPY>
+            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
     } else if (zp) {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, true, GS, MT>>(lds)) return ls;
-        gemv_rows_packed_kernel<8, true, GS, MT>
-            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, true, GS, MT, COPY>>(lds)) return ls;
+        gemv_rows_packed_kernel<8, true, GS, MT, COPY>
+            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
     } else {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, false, GS, MT>>(lds)) return ls;
-        gemv_rows_packed_kernel<8, false, GS, MT>
-            <<<grid, 64 * W, lds, st>>>(p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, false, GS, MT, COPY>>(lds)) return ls;
+        gemv_rows_packed_kernel<8, false, GS, MT, COPY>
+            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
     }
     return KT_OK;
 }
 
-template <int MT>
+template <int MT, bool COPY>
 static int32_t launch_rows_g(int32_t gshift, int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st,
-                             const uint8_t* p, const _Float16* at, const int32_t* sh, int32_t m, int32_t N, int32_t K,
-                             int32_t shifts, int32_t cpp, float alpha, float* c, int32_t accumulate, const float* bias) {
+                             const uint8_t* p, const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts,
+                             float alpha, float* c, int32_t accumulate, const float* bias) {
     if (gshift == 0)
-        return launch_rows<0, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+        return launch_rows<0, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
     if (gshift == 1)
-        return launch_rows<1, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
-    return launch_rows<2, MT>(bits, zp, grid, lds, st, p, at, sh, m, N, K, shifts, cpp, alpha, c, accumulate, bias);
+        return launch_rows<1, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
+    return launch_rows<2, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
 }
 
+template <int MT>
+static int32_t launch_rows_mt(bool copy, int32_t gshift, int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st,
+                              const uint8_t* p, const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts,
+                              float alpha, float* c, int32_t accumulate, const float* bias) {
+    if (MT == 16 || copy)  // 16 rows always copy
+        return launch_rows_g<MT, true>(gshift, bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
+    if constexpr (MT != 16)
+        return launch_rows_g<MT, false>(gshift, bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
+    return KT_OK;
+}
+
+// Converting x in every workgroup saves the prep's launch; copying prepared tiles is
+// cheaper for 16 rows (two phases of conversion per workgroup) and when the workgroups
+// outnumber the CUs (the conversion repeats per round of workgroups).
 int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
                                 const float* const* biases, int32_t count, int32_t accumulate, float alpha,
                                 hipStream_t st) {
-    // one preparation of x for every weight of the call (same K, bits)
     const WeightView& w0 = ws[0];
     const int32_t mt = tile_rows(m);
-    void* general = nullptr;
-    const size_t tiles = static_cast<size_t>(w0.K / RUN) * run_tile_bytes(mt);
-    if (const int32_t status = workspace(st, tiles + 64 + 256, &general)) return status;
-    char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(general) + 255) & ~uintptr_t{255});
-    _Float16* at = reinterpret_cast<_Float16*>(base);
-    int32_t* sh = reinterpret_cast<int32_t*>(base + tiles);
-    if (w0.bits == 4)
-        rows_prep_kernel<4><<<mt, PREP_THREADS, 0, st>>>(a, m, mt, w0.K, at, sh);
-    else
-        rows_prep_kernel<8><<<mt, PREP_THREADS, 0, st>>>(a, m, mt, w0.K, at, sh);
-    KT_LAUNCHED("qmatmul: rows prep kernel");
+    int64_t wgs = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const RowsPlan plan = rows_plan(m, ws[i].K, ws[i].g, ws[i].N / SET);
+        if (plan.ks) wgs = std::max<int64_t>(wgs, ceil_div(ws[i].N / SET, W / plan.ks));
+    }
+    const bool copy = mt == 16 || wgs > cu_count();
+    const float* src = a;
+    if (copy) {  // one preparation of x for every weight of the call (same K, bits)
+        const int32_t chunks = ceil_div(w0.K, CHUNK);
+        void* general = nullptr;
+        const size_t bytes = static_cast<size_t>(chunks) * (4 * run_tile_bytes(mt) + mt * 4);
+        if (const int32_t status = workspace(st, bytes + 256, &general)) return status;
+        unsigned char* xt =
+            reinterpret_cast<unsigned char*>((reinterpret_cast<uintptr_t>(general) + 255) & ~uintptr_t{255});
+        const uint32_t blocks = static_cast<uint32_t>(ceil_div(ceil_div(m, 4) * chunks, W));
+        if (w0.bits == 4) {
+            if (mt == 4) rows_prep_kernel<4, 4><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+            else if (mt == 8) rows_prep_kernel<4, 8><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+            else rows_prep_kernel<4, 16><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+        } else {
+            if (mt == 4) rows_prep_kernel<8, 4><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+            else if (mt == 8) rows_prep_kernel<8, 8><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+            else rows_prep_kernel<8, 16><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+        }
+        KT_LAUNCHED("qmatmul: rows prep kernel");
+        src = reinterpret_cast<const float*>(xt);
+    }
     for (int32_t i = 0; i < count; ++i) {
         const WeightView& w = ws[i];
         const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET);
@@ -559,18 +705,19 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
         if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
         const int32_t kslog = log2_exact(plan.ks);
         const dim3 grid(static_cast<uint32_t>(ceil_div(w.N / SET, W / plan.ks)));
-        const int32_t shifts = kslog | gshift << 4;
+        const int32_t shifts = kslog | gshift << 4 | log2_exact(plan.cpp) << 8;
         const float* bias = biases ? biases[i] : nullptr;
         int32_t status;
+        const bool zp = w.z != nullptr;
         if (mt == 4)
-            status = launch_rows_g<4>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
-                                      shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+            status = launch_rows_mt<4>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
+                                       alpha, cs[i], accumulate, bias);
         else if (mt == 8)
-            status = launch_rows_g<8>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
-                                      shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+            status = launch_rows_mt<8>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
+                                       alpha, cs[i], accumulate, bias);
         else
-            status = launch_rows_g<16>(gshift, w.bits, w.z != nullptr, grid, plan.lds, st, w.p, at, sh, m, w.N, w.K,
-                                       shifts, plan.cpp, alpha, cs[i], accumulate, bias);
+            status = launch_rows_mt<16>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
+                                        alpha, cs[i], accumulate, bias);
         if (status) return status;
         KT_LAUNCHED("qmatmul: packed rows gemv kernel");
     }

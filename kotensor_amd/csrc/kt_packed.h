@@ -67,20 +67,33 @@ __device__ __forceinline__ float lanes4_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// The largest value over the wave's 64 lanes, in every lane, without the LDS path: DPP
-// within rows of 16 (quad swaps, half-row and row mirrors), then the two lane swaps.
-__device__ __forceinline__ float wave_max64(float v) {
 #define KT_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false))
+// The largest value over each row of 16 lanes, in every lane of the row: DPP quad swaps,
+// then the half-row and row mirrors.
+__device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, KT_DPP(v, 0xB1));   // quad_perm [1, 0, 3, 2]
     v = fmaxf(v, KT_DPP(v, 0x4E));   // quad_perm [2, 3, 0, 1]
     v = fmaxf(v, KT_DPP(v, 0x141));  // row_half_mirror: 8 lanes
-    v = fmaxf(v, KT_DPP(v, 0x140));  // row_mirror: 16 lanes
+    return fmaxf(v, KT_DPP(v, 0x140));  // row_mirror: 16 lanes
+}
+// The largest value over lanes l, l ^ 4, l ^ 8, l ^ 12 of each row of 16 (the lanes that
+// agree in bits 0 and 1), in each of them: two row rotations.
+__device__ __forceinline__ float row_stride4_max(float v) {
+    v = fmaxf(v, KT_DPP(v, 0x124));     // row_ror:4
+    return fmaxf(v, KT_DPP(v, 0x128));  // row_ror:8
+}
 #undef KT_DPP
+// The largest value over the four rows of 16 (lanes l, l ^ 16, l ^ 32, l ^ 48), in each of
+// them: the two lane swaps.
+__device__ __forceinline__ float rows4_max(float v) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+
+// The largest value over the wave's 64 lanes, in every lane, without the LDS path.
+__device__ __forceinline__ float wave_max64(float v) { return rows4_max(row16_max(v)); }
 
 // The top levels: the 2^kslog K-parts' subtrees p[0], p[stride], ... added pairwise.
 __device__ __forceinline__ float tree_top(const float* p, int32_t stride, int32_t kslog) {

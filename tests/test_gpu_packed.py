@@ -283,9 +283,9 @@ ROW_SHAPES = [(896, 896), (896, 4864), (4864, 896), (2048, 2048), (2048, 8192), 
 @pytest.mark.parametrize("bits,g", [(4, 64), (8, 32), (4, 32), (8, 64)])
 def test_packed_rows_match_the_oracle(kt, oracle_lib, k, n, bits, g):
     """2, 3, 8 and 16 rows on the copy against the oracle's tile kernel (MatMul.kt:830-881),
-    row by row (rows scaled by 1e-6 .. 1e5, one row zero): x is held to 22 bits of its
-    row's largest value and the products are exact, so each row meets the oracle to the
-    one-row kernels' normwise 1e-5."""
+    row by row (rows scaled by 1e-6 .. 1e5, one row zero): x is held to 22 bits of each
+    128-k chunk's largest value and the products are exact, so each row meets the oracle
+    to the one-row kernels' normwise 1e-5."""
     q = _weights(oracle_lib, k, n, bits, g, 13)
     qt = _packed(kt, q)
     rng = np.random.default_rng(k + n + bits + g + 1)
@@ -312,8 +312,9 @@ def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
     """QuantizationTest.kt:110-134: a and W ~ U(-0.5, 0.5), INT4 g64; m copies of one row
     give its one-row result within 1e-4 (absolute) -- here within normwise 1e-6, since
     both sides are exact products with fp32 sums. Beyond the reference's bound, a row's
-    bits on the copy do not depend on how many rows share the call or on what they hold:
-    each row is prepared and multiplied by itself."""
+    bits on the copy do not depend on what the other rows of the call hold: they are the
+    same for every call of 2..8 rows and for every call of 9..16 rows (the two tile
+    arrangements add x's hi and lo parts in different orders)."""
     rng = np.random.default_rng(41)
     for k, n in ((320, 2112), (4096, 14336)):
         a = (rng.random((1, k), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
@@ -322,20 +323,49 @@ def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
         assert st == 0
         qt = _packed(kt, q)
         single = gpu_matmul(kt, a, qt, 1)
-        ref = None
-        for m in (2, 3, 5, 8, 9, 16):
+        ref = {}
+        for m in (2, 3, 5, 8, 9, 12, 16):
             banner("packed-rows-batched", k, n, m)
             batched = gpu_matmul(kt, np.tile(a, (m, 1)), qt, m)
             diff = float(np.abs(batched - single).max())
             print(f"  max |batched - single| = {diff:.2e}", flush=True)
             assert diff < 1e-4 and normwise_rel(batched, np.tile(single, (m, 1))) <= 1e-6, (k, n, m, diff)
-            ref = batched[0] if ref is None else ref
-            assert all(same_bits(batched[r], ref) for r in range(m)), m
+            cls = m > 8
+            ref.setdefault(cls, batched[0])
+            assert all(same_bits(batched[r], ref[cls]) for r in range(m)), m
         x = rng.standard_normal((16, k)).astype(np.float32)
-        full = gpu_matmul(kt, x, qt, 16)
-        for rows in ([0, 5, 15], [7, 3], [2, 9, 11, 4, 13]):
+        full16 = gpu_matmul(kt, x, qt, 16)
+        full8 = gpu_matmul(kt, x[:8], qt, 8)
+        for rows, full in (([0, 5, 7], full8), ([7, 3], full8), ([2, 6, 1, 4, 0], full8),
+                           ([9, 0, 15, 3, 11, 4, 8, 13, 1, 6], full16), ([14, 2, 5, 10, 12, 7, 0, 9, 11], full16)):
             part = gpu_matmul(kt, x[rows], qt, len(rows))
             assert all(same_bits(part[i], full[r]) for i, r in enumerate(rows)), rows
+
+
+@pytest.mark.parametrize("bits,g", [(4, 64), (8, 32)])
+def test_packed_rows_many_workgroups_copy_prepared_tiles(kt, oracle_lib, bits, g):
+    """512 x 65536: more workgroups than CUs, where the kernel copies x tiles prepared by
+    one launch instead of converting x in every workgroup. At 2, 5 and 8 rows it meets the
+    oracle, and its first 4096 columns have the bits of the same columns as a weight of
+    their own (few workgroups: x converted in each), whose split differs too."""
+    k, n, part = 512, 65536, 4096
+    rng = np.random.default_rng(47 + bits)
+    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    st, q = oracle_lib.quantize(w, bits, g)
+    assert st == 0
+    st, qp = oracle_lib.quantize(np.ascontiguousarray(w[:, :part]), bits, g)
+    assert st == 0
+    del w
+    qt, qtp = _packed(kt, q), _packed(kt, qp)
+    for m in (2, 5, 8):
+        banner("packed-rows-copy", k, n, bits, g, m)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        got = gpu_matmul(kt, x, qt, m)
+        want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+        errs = [normwise_rel(got[r], want[r]) for r in range(m)]
+        print(f"  worst row normwise={max(errs):.2e}", flush=True)
+        assert max(errs) <= TOL, errs
+        assert same_bits(gpu_matmul(kt, x, qtp, m), np.ascontiguousarray(got[:, :part])), m
 
 
 def test_packed_rows_grouped_accumulate_and_bias(kt, oracle_lib):
