@@ -695,44 +695,53 @@ __global__ void __launch_bounds__(256)
     const float* row = a + static_cast<size_t>(m) * K;
     const bool vec = vec_rows != 0;
     auto absmax = [](const f32x4& v) { return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))); };
-    auto put = [&](int32_t sp, int o8, const f32x4& v0, const f32x4& v1, int32_t e) {
-        *piece(sp, o8) = u32x4{pack_half2(ldexpf(v0[0], -e), ldexpf(v0[1], -e)),
-                               pack_half2(ldexpf(v0[2], -e), ldexpf(v0[3], -e)),
-                               pack_half2(ldexpf(v1[0], -e), ldexpf(v1[1], -e)),
-                               pack_half2(ldexpf(v1[2], -e), ldexpf(v1[3], -e))};
+    // float4 f of the row (lanes take f = ln + 64 j: each load a contiguous KiB) holds
+    // elements 4 (f % 8) .. + 3 of span f / 8: half f % 2 of piece (f / 8, (f % 8) / 2)
+    auto put_half = [&](int32_t f, const f32x4& v, int32_t e) {
+        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(piece(f >> 3, (f & 7) >> 1)) + 8 * (f & 1)) =
+            u32x2{pack_half2(ldexpf(v[0], -e), ldexpf(v[1], -e)), pack_half2(ldexpf(v[2], -e), ldexpf(v[3], -e))};
     };
     float mx = 0.0f;
     if (S <= 2 * 64) {
-        // K <= 4096: the lane's (at most two) spans stay in registers, the row is read once
-        f32x4 v[2][8];
+        // K <= 4096: the row read once, into registers
+        f32x4 v[16];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const int32_t sp = ln + 64 * h;
-                v[h][c] = sp < S ? row_chunk(row, sp * 8 + c, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                mx = fmaxf(mx, absmax(v[h][c]));
-            }
+        for (int j = 0; j < 16; ++j) {
+            const int32_t f = ln + 64 * j;
+            v[j] = f < 8 * S ? row_chunk(row, f, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mx = fmaxf(mx, absmax(v[j]));
+        }
         mx = wave_max64(mx);
         const int32_t e = scale_exponent(mx, 15);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            if (ln + 64 * h < S)
-#pragma unroll
-                for (int o8 = 0; o8 < 4; ++o8) put(ln + 64 * h, o8, v[h][2 * o8], v[h][2 * o8 + 1], e);
+        for (int j = 0; j < 16; ++j)
+            if (ln + 64 * j < 8 * S) put_half(ln + 64 * j, v[j], e);
         if (ln == 0) er[m] = e;
         return;
     }
-    for (int32_t sp = ln; sp < S; sp += 64) {
+    // longer rows: read twice (the maximum, then the halves), 16 loads in flight per lane
+    for (int32_t f0 = 0; f0 < 8 * S; f0 += 16 * 64) {
+        f32x4 v[16];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) mx = fmaxf(mx, absmax(row_chunk(row, sp * 8 + c, K, vec)));
+        for (int j = 0; j < 16; ++j) {
+            const int32_t f = f0 + ln + 64 * j;
+            v[j] = f < 8 * S ? row_chunk(row, f, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, absmax(v[j]));
     }
     mx = wave_max64(mx);
     const int32_t e = scale_exponent(mx, 15);
-    for (int32_t sp = ln; sp < S; sp += 64) {
+    for (int32_t f0 = 0; f0 < 8 * S; f0 += 16 * 64) {
+        f32x4 v[16];
 #pragma unroll
-        for (int o8 = 0; o8 < 4; ++o8)
-            put(sp, o8, row_chunk(row, sp * 8 + 2 * o8, K, vec), row_chunk(row, sp * 8 + 2 * o8 + 1, K, vec), e);
+        for (int j = 0; j < 16; ++j) {
+            const int32_t f = f0 + ln + 64 * j;
+            v[j] = f < 8 * S ? row_chunk(row, f, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (f0 + ln + 64 * j < 8 * S) put_half(f0 + ln + 64 * j, v[j], e);
     }
     if (ln == 0) er[m] = e;
 }
