@@ -781,6 +781,7 @@ __global__ void __launch_bounds__(PTHREADS, 1)
     const GemmJob& jb = jobs.job[job_of_tile(jobs, tile_n)];
     const int32_t N = jb.N;
     const int32_t sets = (N + 15) / 16, chunks = S / 4, G = (K + g - 1) / g;
+    const int32_t gsh = __builtin_ctz(static_cast<uint32_t>(g));  // g = 32 << k
     const int32_t rem = jx % per_n;
     const int32_t tile_m = rem % tiles_m;
     const int32_t sp = rem / tiles_m;
@@ -828,11 +829,16 @@ __global__ void __launch_bounds__(PTHREADS, 1)
             else
                 d.w[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, w_off[j], wso, 0));
         }
-        const int32_t kg = BITS == 8 ? 32 * s : 64 * (s >> 1) + 32 * hl;  // first k of the lane's run
-        const int32_t grp = min(kg / g, G - 1);
+        // the group row of the lane's run (first k: 64 (s / 2) + 32 hl; INT8 32 s), offset
+        // into the [G x N] arrays: scalars for the two lane halves (g a power of two), one
+        // select per lane
+        const int32_t kg0 = BITS == 8 ? 32 * s : 64 * (s >> 1);
+        const uint32_t row0 = static_cast<uint32_t>(min(kg0 >> gsh, G - 1)) * N;
+        const uint32_t row1 = BITS == 8 ? row0 : static_cast<uint32_t>(min((kg0 + 32) >> gsh, G - 1)) * N;
+        const uint32_t row_off = hl ? row1 : row0;
 #pragma unroll
         for (int j = 0; j < CB; ++j) {
-            const uint32_t at = static_cast<uint32_t>(grp) * N + col_c[j];
+            const uint32_t at = row_off + col_c[j];
             d.s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, at * 4, 0, 0));
             // the dword holding the zero byte (N % 4 == 0: it lies inside the array); a byte
             // load's extension would be placed ahead of the loop and wait for every load
@@ -1085,7 +1091,7 @@ static void fill_jobs(GemmJobs& jobs, const WeightView* ws, float* const* cs, co
 // addressed with 32-bit buffer offsets, so each stays below 4 GiB.
 static bool gemm_packed_usable(const WeightView* ws, int32_t count) {
     for (int32_t i = 0; i < count; ++i) {
-        if (!ws[i].p || ws[i].g % 32 != 0 || (ws[i].bits == 4 && !ws[i].z)) return false;
+        if (!ws[i].p || ws[i].g % 32 != 0 || log2_exact(ws[i].g / 32) < 0 || (ws[i].bits == 4 && !ws[i].z)) return false;
         if (packed_weight_bytes(ws[i].K, ws[i].N, ws[i].bits) > 0xFFFFFFFFll) return false;
         if (static_cast<int64_t>(ws[i].G) * ws[i].N * 4 > 0xFFFFFFFFll) return false;
     }
