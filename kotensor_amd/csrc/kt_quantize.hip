@@ -4,10 +4,12 @@
 //
 // HBM-bound: reads 4 B per weight once, writes 1 B (INT8) or 0.5 B (INT4) plus
 // the per-(group, column) scale and zero. Layout of the work:
-//   * a workgroup owns one group and 64 column units (a 1-D grid, group-major);
-//     a column unit is 4 adjacent columns (INT8) or 4 adjacent bytes (INT4: the
-//     low-nibble columns b..b+3 and the high-nibble columns half+b..half+b+3);
-//   * the group's rows are split over the workgroup's waves, RPW rows each, and
+//   * an item is one group and 64 column units (group-major); a column unit is 4
+//     adjacent columns (INT8) or 4 adjacent bytes (INT4: the low-nibble columns
+//     b..b+3 and the high-nibble columns half+b..half+b+3); the workgroups are one
+//     resident round and take the items in turn, the next item's loads in flight
+//     while the current one is reduced;
+//   * an item's rows are split over the workgroup's waves, RPW rows each, and
 //     stay in registers between the min/max pass and the rounding pass, so every
 //     input float is read from HBM exactly once (each wave row is 1 KB contiguous);
 //   * per-column min/max partials are combined across waves through LDS, and each
