@@ -394,12 +394,14 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     // The wave's scales and zero points: group rows g0 .. g0 + rows - 1 of its column
     // set in the copy's [set][group][16] rows (contiguous: 64 bytes of scales and 16 of
     // zero points a row), in a few 16-byte loads per lane (sixteen rows of scales per
-    // load: four lanes a row; a row of zero points per lane); rows past G read zeros
-    // without memory traffic. They go to the wave's rows in LDS with the digit pass, and
-    // each chunk reads its lane's pair there. Measured at 4096 -> 14336 / 14336 -> 4096
-    // INT4: one 4-byte and one 1-byte load per chunk from the [G x N] arrays 7.9 / 10.7
-    // us, these rows gathered from the [G x N] arrays 8.2-8.5 / 10.3-11.0, from the
-    // copy's contiguous rows 8.0 / 8.8.
+    // load: four lanes a row; a row of zero points per lane); rows past the wave's range or
+    // past G read zeros without memory traffic, and the last two loads go out only for a
+    // range of more than 32 rows (measured at 14336 -> 4096 INT4: 9.4 -> 9.0 us against
+    // reading the next wave's rows too). They go to the wave's rows in LDS with the digit
+    // pass, and each chunk reads its lane's pair there. Measured at 4096 -> 14336 /
+    // 14336 -> 4096 INT4: one 4-byte and one 1-byte load per chunk from the [G x N] arrays
+    // 7.9 / 10.7 us, these rows gathered from the [G x N] arrays 8.2-8.5 / 10.3-11.0, from
+    // the copy's contiguous rows 8.0 / 8.8.
     const int32_t g0 = k0 >> (gshift + 5);
     const int32_t rows = stage_rows((chunks + (1 << kslog) - 1) >> kslog, gshift);
     const __amdgpu_buffer_rsrc_t sr =
@@ -408,17 +410,21 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
         const_cast<int8_t*>(ZP ? jb.z : reinterpret_cast<const int8_t*>(jb.s)), 0, G * jb.N, 0x00020000);
     u32x4 sst[4];
     u32x4 zst;
+    const int32_t rlim = min(G, g0 + rows);
     auto issue_stage = [&]() {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int32_t r = g0 + 16 * i + (ln >> 2);
-            const int32_t off = r < G ? ((set * G + r) * SET + 4 * (ln & 3)) * 4 : G * jb.N * 4;
-            sst[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+            const int32_t off = r < rlim ? ((set * G + r) * SET + 4 * (ln & 3)) * 4 : G * jb.N * 4;
+            if (i < 2 || 16 * i < rows)  // (the first two unconditional: measured faster)
+                sst[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+            else
+                sst[i] = u32x4{0u, 0u, 0u, 0u};
         }
         if constexpr (ZP) {
             const int32_t r = g0 + ln;
             zst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                zr, r < G ? (set * G + r) * SET : G * jb.N, 0, 0));
+                                                zr, r < rlim ? (set * G + r) * SET : G * jb.N, 0, 0));
         }
     };
     if constexpr (!CHAIN) issue_stage();
