@@ -84,7 +84,8 @@ int32_t kt_set_device(int32_t device);
  * small-M kernels split their work, never their result beyond fp32 rounding order.
  * gemv_kind: 0 = automatic (the column-run kernel for one row when the weight has a
  *            packed copy, and for 2 to 16 rows when it also has at least 16 column sets
- *            of 16 per 128 rows of K; otherwise for one row the column-strip kernel up to
+ *            of 16 per 128 rows of K, or K >= 4096 and at least 256 column sets;
+ *            otherwise for one row the column-strip kernel up to
  *            a size and the wide-strip MFMA kernel above it, and the row-block MFMA kernel
  *            for 2 to 16 rows, where the layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA
  *            GEMV for M > 1: those go to the GEMM), 2 = row-block MFMA kernel for M <= 16,
@@ -97,7 +98,9 @@ int32_t kt_set_device(int32_t device);
  * gemv_waves: waves per workgroup (2, 4 or 8; 0 = automatic; the column-run kernel
  *            always runs eight);
  * gemv_reduce: how split sums meet (0 = automatic, 1 = a second kernel, 2 = inside the
- * kernel). Process-wide. */
+ *            kernel); for the column-run kernel at 2 to 16 rows, how the K-parts of a
+ *            column set meet (1 = inside one workgroup, 2 = across workgroups, through
+ *            memory; the same bits either way). Process-wide. */
 int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_splits,
                              int32_t gemv_waves, int32_t gemv_reduce);
 

@@ -792,6 +792,7 @@ void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring) {
     (void)waves;  // eight per workgroup
     g_forced.ring = ring == 4 ? 1 : ring == 8 ? 2 : 0;
 }
+int32_t packed_forced_ks() { return g_forced.ks; }
 
 
 

@@ -190,10 +190,17 @@ __global__ void __launch_bounds__(64 * W)
 // runs; 2: g >= 128, one group per chunk), MT: rows of the x tiles (4, 8 or 16; rows
 // M .. MT - 1 reach only output rows that are never stored). COPY: x is rows_prep_kernel's
 // output, which the workgroup copies; otherwise the workgroup converts x itself.
-template <int BITS, bool ZP, int GS, int MT, bool COPY>
+// SPLIT: the ks K-parts of a column set are workgroups (blockIdx.y), each of eight column
+// sets over one K-part, so a workgroup converts only its part of x; every wave writes its
+// subtree of sums to `partials` (write-through), the workgroup counts itself in at
+// counters[blockIdx.x], and the last of the ks workgroups adds the parts in the tree's
+// fixed order: the same bits as the parts meeting inside one workgroup.
+template <int BITS, bool ZP, int GS, int MT, bool COPY, bool SPLIT>
 __global__ void __launch_bounds__(64 * W)
     gemv_rows_packed_kernel(const uint8_t* __restrict__ packed, const float* __restrict__ x, int32_t M, int32_t N,
-                            int32_t K, int32_t shifts, float alpha, float* out, int32_t accumulate, const float* bias) {
+                            int32_t K, int32_t shifts, float alpha, float* out, int32_t accumulate, const float* bias,
+                            float* partials, uint32_t* counters) {
+    static_assert(!(SPLIT && COPY), "split workgroups convert their own part of x");
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     constexpr bool PK = parts_in_k(MT);
@@ -203,13 +210,15 @@ __global__ void __launch_bounds__(64 * W)
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int32_t kslog = shifts & 15, gshift = (shifts >> 4) & 15, cpplog = shifts >> 8;
     const int32_t ks = 1 << kslog, cpp = 1 << cpplog;
+    const int32_t kinlog = SPLIT ? 0 : kslog, kin = 1 << kinlog;  // K-parts inside the workgroup
     const int32_t sets = N >> 4, chunks = (K + CHUNK - 1) >> 7, G = (K + (RUN << gshift) - 1) >> (gshift + 5);
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int32_t cslog = 3 - kslog;
+    const int32_t cslog = 3 - kinlog;
     const int32_t set0 = blockIdx.x << cslog;
-    if (set0 >= sets) return;
-    const int32_t my_cs = wave & ((1 << cslog) - 1), kp = wave >> cslog;
+    if (set0 >= sets) return;  // (split: never, the grid's column-set groups all hold a set)
+    const int32_t my_cs = wave & ((1 << cslog) - 1), kp = SPLIT ? static_cast<int32_t>(blockIdx.y) : wave >> cslog;
+    const int32_t kpl = SPLIT ? 0 : kp;  // the K-part's place in the workgroup's tiles
     const int32_t my_set = set0 + my_cs;
     const bool set_live = my_set < sets;
     const int32_t set = set_live ? my_set : sets - 1;
@@ -222,11 +231,11 @@ __global__ void __launch_bounds__(64 * W)
     const int32_t phases = (nmax + cpp - 1) / cpp;
     const int32_t rows = stage_rows(nmax, gshift);
 
-    // ---- x into the phase's tiles. Converting: task j of a phase is quad j / (ks cpp),
-    // phase chunk j % (ks cpp) (powers of two: shifts and masks), MAX_PASSES tasks per wave
-    // at most. Copying: 16-byte pieces of the prep's tiles and factors, each part's chunks
-    // of the phase contiguous there and here.
-    const int32_t ppr = ks * cpp;               // a phase's chunks over the K-parts
+    // ---- x into the phase's tiles. Converting: task j of a phase is quad j / (kin cpp),
+    // phase chunk j % (kin cpp) (powers of two: shifts and masks), MAX_PASSES tasks per
+    // wave at most. Copying: 16-byte pieces of the prep's tiles and factors, each part's
+    // chunks of the phase contiguous there and here.
+    const int32_t ppr = kin * cpp;              // a phase's chunks over the workgroup's K-parts
     const int32_t tasks = ((M + 3) >> 2) * ppr;  // quads past M are not converted
     const int32_t xrow = ln & 3, xsl = (ln >> 2) & 3, xrun = ln >> 4;
     const int32_t xoob = COPY ? chunks * (4 * tile + MT * 4) : M * K * 4;
@@ -235,9 +244,9 @@ __global__ void __launch_bounds__(64 * W)
     // the task's quad and phase chunk (wave-uniform), and the lane's byte offset in x
     // (rows past M, runs past K and chunks past the part read zeros without memory traffic)
     auto task_of = [&](int32_t j, int32_t ph, int32_t& quad, int32_t& ch) -> int32_t {
-        quad = j >> (kslog + cpplog);
+        quad = j >> (kinlog + cpplog);
         ch = j & (ppr - 1);
-        const int32_t part = ch >> cpplog;
+        const int32_t part = (SPLIT ? kp : 0) + (ch >> cpplog);
         const int32_t c = ph * cpp + (ch & (cpp - 1));
         const int32_t cg = ((part * chunks) >> kslog) + c;
         const int32_t ce = ((part + 1) * chunks) >> kslog;
@@ -247,7 +256,7 @@ __global__ void __launch_bounds__(64 * W)
     // copy pieces: a part's phase is 2^(cpplog + 5 + log2 MT) pieces of tiles (32 MT per
     // chunk); the factors ks cpp MT / 4 pieces (MT / 4 per chunk)
     constexpr int MTLOG = MT == 4 ? 2 : MT == 8 ? 3 : 4;
-    const int32_t tile_pieces = ks << (cpplog + 5 + MTLOG);
+    const int32_t tile_pieces = kin << (cpplog + 5 + MTLOG);
     auto piece_off = [&](int32_t q, int32_t ph) -> int32_t {  // the prep's byte offset of tile piece q, or xoob
         const int32_t part = q >> (cpplog + 5 + MTLOG), within = q & ((1 << (cpplog + 5 + MTLOG)) - 1);
         const int32_t cg = ((part * chunks) >> kslog) + ph * cpp + (within >> (5 + MTLOG));
@@ -255,7 +264,7 @@ __global__ void __launch_bounds__(64 * W)
                                                      : xoob;
     };
     // factor piece q (at most 128 of them: one per thread, with the first round)
-    const int32_t factor_pieces = ks << (cpplog + MTLOG - 2);
+    const int32_t factor_pieces = kin << (cpplog + MTLOG - 2);
     auto factor_off = [&](int32_t q, int32_t ph) -> int32_t {
         const int32_t part = q >> (cpplog + MTLOG - 2), within = q & ((1 << (cpplog + MTLOG - 2)) - 1);
         const int32_t cg = ((part * chunks) >> kslog) + ph * cpp + (within >> (MTLOG - 2));
@@ -291,7 +300,7 @@ __global__ void __launch_bounds__(64 * W)
             }
         }
     };
-    float* pl = reinterpret_cast<float*>(smem + rows_lds_p(ks, cpp, MT));  // [ks cpp][MT]: 2^-s
+    float* pl = reinterpret_cast<float*>(smem + rows_lds_p(kin, cpp, MT));  // [kin cpp][MT]: 2^-s
     auto store_x = [&](int32_t ph, int32_t rd) {
         if constexpr (COPY)
             if (rd == 0 && tid < factor_pieces) reinterpret_cast<float4*>(pl)[tid] = fv;
@@ -369,7 +378,7 @@ __global__ void __launch_bounds__(64 * W)
         load_x(0, rd, 0, MAX_PASSES);
         store_x(0, rd);
     }
-    unsigned char* stg = smem + rows_lds_stage(ks, cpp, MT) + wave * rows * STAGE_ROW_BYTES;
+    unsigned char* stg = smem + rows_lds_stage(kin, cpp, MT) + wave * rows * STAGE_ROW_BYTES;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         if (16 * i + (ln >> 2) < rows) *reinterpret_cast<u32x4*>(stg + i * 1024 + 16 * ln) = sst[i];
@@ -433,7 +442,7 @@ __global__ void __launch_bounds__(64 * W)
         // a chunk past the wave's range adds nothing; its reads stay in the phase's tiles
         // and the wave's staged rows (the phase's first chunk is below nmax)
         const int32_t cc = live ? cl : ph * cpp;
-        const int32_t chl = kp * cpp + (cc - ph * cpp);  // the chunk's place in the phase
+        const int32_t chl = kpl * cpp + (cc - ph * cpp);  // the chunk's place in the phase
         const unsigned char* tc = smem + chl * 4 * tile + a_lane;
         float sc[NGC];
         uint32_t zc[NGC];
@@ -550,6 +559,58 @@ __global__ void __launch_bounds__(64 * W)
     // ---- the last sub-parts; the K-parts of each column set (the tree's top), a row's
     // hi and lo sums; the stores. The meeting area takes the x tiles' place.
     while (sp < sp_count) close_sub_part();
+    auto store_row = [&](int32_t m, float sum) {
+        float* dst = out + static_cast<size_t>(m) * N + col;
+        float o = accumulate ? *dst : 0.0f;
+        o = fmaf(alpha, sum, o);
+        if (bias) o += bias[col];
+        *dst = o;
+    };
+    if constexpr (SPLIT) {
+        // [K-part][column-set group][wave][NT][16 A rows][16 columns]: this wave's subtree,
+        // written through the caches; once every wave's stores are complete the workgroup
+        // counts itself in, and the last of the K-parts reads them all past the caches.
+        const size_t stride = static_cast<size_t>(gridDim.x) * W * NT * 256;  // one K-part
+        float* mine = partials + kp * stride + (static_cast<size_t>(blockIdx.x) * W + wave) * NT * 256 + nl;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __hip_atomic_store(mine + (tt * 16 + 4 * kb + i) * 16, part[tt][i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // every wave's stores are in memory; the tiles are free
+        uint32_t* flag = reinterpret_cast<uint32_t*>(smem);
+        if (tid == 0) {
+            const uint32_t before =
+                __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = before == static_cast<uint32_t>(ks - 1);
+            if (last) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last ? 1u : 0u;
+        }
+        __syncthreads();
+        if (*flag == 0u || !set_live) return;
+        const float* base = partials + (static_cast<size_t>(blockIdx.x) * W + wave) * NT * 256 + nl;
+#pragma unroll
+        for (int j = 0; j < MT / 4; ++j) {
+            const int32_t m = 4 * j + kb;  // lane group kb stores rows kb, kb + 4, ...
+            if (m >= M) continue;
+            const int32_t ah = PK ? m : m % HR, al = HR + m % HR;  // the row's A rows (hi, lo)
+            float vh[SUB_PARTS], vl[SUB_PARTS];
+#pragma unroll
+            for (int q = 0; q < SUB_PARTS; ++q) {
+                vh[q] = vl[q] = 0.0f;
+                if (q < ks) {
+                    const float* pq = base + q * stride + (m / HR) * 256;
+                    vh[q] = __hip_atomic_load(pq + ah * 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    if (!PK) vl[q] = __hip_atomic_load(pq + al * 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+            }
+            store_row(m, PK ? tree_top(vh, 1, kslog) : tree_top(vh, 1, kslog) + tree_top(vl, 1, kslog));
+        }
+        return;
+    }
     __syncthreads();  // every wave is done with the tiles
     float* red = reinterpret_cast<float*>(smem);  // [W][NT][16 A rows][16 columns]
 #pragma unroll
@@ -564,61 +625,109 @@ __global__ void __launch_bounds__(64 * W)
         const int32_t m = 4 * j + kb;  // lane group kb stores rows kb, kb + 4, ...
         if (m >= M) continue;
         const float* base = red + (my_cs * NT + m / HR) * 256 + nl;
-        const float sum = PK ? tree_top(base + m * 16, cs * NT * 256, kslog)
-                             : tree_top(base + (m % HR) * 16, cs * NT * 256, kslog) +
-                                   tree_top(base + (HR + m % HR) * 16, cs * NT * 256, kslog);  // hi + lo
-        float* dst = out + static_cast<size_t>(m) * N + col;
-        float o = accumulate ? *dst : 0.0f;
-        o = fmaf(alpha, sum, o);
-        if (bias) o += bias[col];
-        *dst = o;
+        store_row(m, PK ? tree_top(base + m * 16, cs * NT * 256, kslog)
+                        : tree_top(base + (m % HR) * 16, cs * NT * 256, kslog) +
+                              tree_top(base + (HR + m % HR) * 16, cs * NT * 256, kslog));  // hi + lo
     }
 }
 
 }  // namespace
 
-// The launch: the one-row kernel's K split (plan_packed), or the largest smaller one
-// whose x tiles fit (the result does not depend on the split); the x tiles a phase holds
-// (chunks per phase: a power of two, at least R, at most what the waves convert in
-// MAX_PASSES tasks each, no more than the wave's range needs, within what LDS
-// the staged rows leave); the LDS. ks = 0: none fits.
+// The launch. Inside the workgroup (split = false): the one-row kernel's K split
+// (plan_packed), or the largest smaller one whose x tiles fit. Across workgroups (split):
+// the smallest power of two that keeps a wave's range within MAX_WAVE_CHUNKS, doubled up
+// to SUB_PARTS while the workgroups (eight column sets each, one per K-part) number fewer
+// than 4/5 of the CUs and every part keeps four chunks. The result does not depend on
+// either. Then the x tiles a phase holds (chunks per phase: a power of two, at least R, at
+// most what the waves convert in MAX_PASSES tasks each, no more than the wave's range
+// needs, within what LDS the staged rows leave) and the LDS. ks = 0: none fits.
 struct RowsPlan {
     int32_t ks = 0, cpp = 0;
+    bool split = false;
     size_t lds = 0;
 };
 // Rows of the x tiles for M rows: 4, 8 or 16.
 static int32_t tile_rows(int32_t M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
-static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets) {
-    RowsPlan r;
-    const PackedPlan plan = plan_packed(K, g, sets);
-    const int32_t gshift = log2_exact(g / RUN), chunks = ceil_div(K, CHUNK);
+// The x tiles of one K-part per phase, for kin K-parts in the workgroup: false when none fits.
+static bool rows_phase(int32_t M, int32_t chunks, int32_t gshift, int32_t ks, int32_t kin, RowsPlan& r) {
     const int32_t mt = tile_rows(M), quads = ceil_div(M, 4);
     const int32_t tile = run_tile_bytes(mt);
-    for (int32_t ks = plan.ks; ks >= 1; ks /= 2) {
-        const int32_t nmax = ceil_div(chunks, ks);
-        if (nmax > MAX_WAVE_CHUNKS) break;
-        const int32_t rows = stage_rows(nmax, gshift);
-        const int32_t fixed = rows_lds_bytes(ks, 0, mt, rows);
-        if (fixed >= static_cast<int32_t>(LDS_MAX)) continue;
-        int32_t cap = (static_cast<int32_t>(LDS_MAX) - fixed) / (ks * (4 * tile + mt * 4));
-        cap = std::min(cap, W * MAX_PASSES / (quads * ks));
-        int32_t cpp = R;
-        while (cpp * 2 <= cap && cpp < nmax) cpp *= 2;
-        if (cpp > cap) continue;
-        r.ks = ks;
-        r.cpp = cpp;
-        r.lds = static_cast<size_t>(rows_lds_bytes(ks, cpp, mt, rows));
+    const int32_t nmax = ceil_div(chunks, ks);
+    if (nmax > MAX_WAVE_CHUNKS) return false;
+    const int32_t rows = stage_rows(nmax, gshift);
+    const int32_t fixed = rows_lds_bytes(kin, 0, mt, rows);
+    if (fixed >= static_cast<int32_t>(LDS_MAX)) return false;
+    int32_t cap = (static_cast<int32_t>(LDS_MAX) - fixed) / (kin * (4 * tile + mt * 4));
+    cap = std::min(cap, W * MAX_PASSES / (quads * kin));
+    int32_t cpp = R;
+    while (cpp * 2 <= cap && cpp < nmax) cpp *= 2;
+    if (cpp > cap) return false;
+    r.ks = ks;
+    r.cpp = cpp;
+    r.lds = static_cast<size_t>(rows_lds_bytes(kin, cpp, mt, rows));
+    return true;
+}
+
+static RowsPlan rows_plan(int32_t M, int32_t K, int32_t g, int32_t sets, bool split) {
+    RowsPlan r;
+    r.split = split;
+    const int32_t gshift = log2_exact(g / RUN), chunks = ceil_div(K, CHUNK);
+    if (split) {
+        int32_t ks = 1;
+        while (ks < SUB_PARTS && ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) ks *= 2;
+        const int64_t groups = ceil_div(sets, W);
+        if (const int32_t f = packed_forced_ks()) {  // a forced split, where it covers K
+            if (f < ks || f > chunks) return r;
+            ks = f;
+        } else {
+            while (ks < SUB_PARTS && groups * ks * 5 < static_cast<int64_t>(cu_count()) * 4 && chunks >= 8 * ks)
+                ks *= 2;
+        }
+        if (!rows_phase(M, chunks, gshift, ks, 1, r)) r.ks = 0;
         return r;
     }
+    const PackedPlan plan = plan_packed(K, g, sets);
+    for (int32_t ks = plan.ks; ks >= 1; ks /= 2) {
+        if (ceil_div(chunks, ks) > MAX_WAVE_CHUNKS) break;
+        if (rows_phase(M, chunks, gshift, ks, ks, r)) return r;
+    }
+    r.ks = 0;
     return r;
 }
 
-// The automatic choice: wide weights only. With column sets at least 16 times the 128-k
-// chunks (the 8B gate/up, the heads) this kernel is well ahead of the row-block kernel;
-// for narrow ones (8192 -> 2048, 14336 -> 4096, 4096 -> 4096) its grid is small and its x
-// tiles take several phases, and the row-block kernel is faster (measured at M = 2..16).
-bool gemv_rows_packed_preferred(const WeightView& w) { return w.N / SET >= 16 * ceil_div(w.K, CHUNK); }
+// How the K-parts meet: 0 automatic, 1 inside the workgroup, 2 across workgroups
+// (kt_set_kernel_config's gemv_reduce).
+static int32_t g_rows_reduce = 0;
+void set_gemv_rows_packed_reduce(int32_t mode) { g_rows_reduce = mode; }
+// Automatic: across workgroups from K = 4096 on (32 chunks), for the wide weights from 5
+// rows on and for narrower ones of at least 256 column sets. A workgroup holding every
+// K-part of its sets converts and reads all of x (M K floats: at M = 8 and K = 4096 as
+// many bytes as its weights), and beyond K = 8192 its x tiles take several phases; split,
+// each workgroup converts only its part, and the parts meet through memory, one more
+// round trip. Measured (INT4 g64, us, M = 2 / 4 / 8 / 16): 14336 -> 4096 split 14.6 /
+// 14.8 / 16.6 / 20.8, the row-block kernel 19.6 / 25.3 / 25.7 / 26.8; 4096 -> 14336
+// split 13.5 / 13.8 / 15.4 / 18.8, inside 12.8 / 13.4 / 16.3 / 22.1; 4096 -> 4096 split
+// 9.7 / - / 10.6 / 12.2, row-block 11.9 / - / 11.5 / 11.9; 8192 -> 2048 (128 sets) at
+// M = 16 split 15.1, row-block 12.2.
+static bool rows_wide(const WeightView& w) { return w.N / SET >= 16 * ceil_div(w.K, CHUNK); }
+static bool rows_split_preferred(const WeightView& w, int32_t m) {
+    if (ceil_div(w.K, CHUNK) < 32) return false;
+    return rows_wide(w) ? m > 4 : w.N / SET >= 256;
+}
+static bool rows_split(const WeightView& w, int32_t m) {
+    if (g_rows_reduce != 0) return g_rows_reduce == 2;
+    return rows_split_preferred(w, m);
+}
+
+// The automatic choice: wide weights (column sets at least 16 times the 128-k chunks: the
+// 8B gate/up, the heads), and the long-K weights of at least 256 column sets, which split
+// across workgroups (14336 -> 4096, 4096 -> 4096). For the rest (fewer column sets,
+// shorter K: 8192 -> 2048, 4864 -> 896) the row-block kernel is as fast or faster
+// (measured at M = 2..16).
+bool gemv_rows_packed_preferred(const WeightView& w) {
+    return rows_wide(w) || (ceil_div(w.K, CHUNK) >= 32 && w.N / SET >= 256);
+}
 
 bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, const float* c) {
     if (m < 2 || m > MAX_ROWS || !w.p) return false;
@@ -627,48 +736,54 @@ bool gemv_rows_packed_supported(const float* a, int32_t m, const WeightView& w, 
     if (w.N % SET != 0) return false;
     if (static_cast<int64_t>(w.G) * w.N * 4 > INT32_MAX) return false;
     if (!aligned(w.p, 16) || !aligned(a, 16) || !aligned(c, 4)) return false;
-    return rows_plan(m, w.K, w.g, w.N / SET).ks != 0;
+    return rows_plan(m, w.K, w.g, w.N / SET, rows_split(w, m)).ks != 0;
 }
 
-template <int GS, int MT, bool COPY>
-static int32_t launch_rows(int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st, const uint8_t* p,
-                           const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts, float alpha, float* c,
-                           int32_t accumulate, const float* bias) {
-    if (bits == 4) {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<4, true, GS, MT, COPY>>(lds)) return ls;
-        gemv_rows_packed_kernel<4, true, GS, MT, COPY>
-            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    } else if (zp) {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, true, GS, MT, COPY>>(lds)) return ls;
-        gemv_rows_packed_kernel<8, true, GS, MT, COPY>
-            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    } else {
-        if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<8, false, GS, MT, COPY>>(lds)) return ls;
-        gemv_rows_packed_kernel<8, false, GS, MT, COPY>
-            <<<grid, 64 * W, lds, st>>>(p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    }
+// What every launch of a call shares.
+struct RowsLaunch {
+    dim3 grid;
+    size_t lds;
+    hipStream_t st;
+    const uint8_t* p;
+    const float* a;
+    int32_t m, N, K, shifts;
+    float alpha;
+    float* c;
+    int32_t accumulate;
+    const float* bias;
+    float* partials;
+    uint32_t* counters;
+};
+
+template <int BITS, bool ZP, int GS, int MT, bool COPY, bool SPLIT>
+static int32_t launch_rows_kernel(const RowsLaunch& L) {
+    if (const int32_t ls = allow_lds<&gemv_rows_packed_kernel<BITS, ZP, GS, MT, COPY, SPLIT>>(L.lds)) return ls;
+    gemv_rows_packed_kernel<BITS, ZP, GS, MT, COPY, SPLIT><<<L.grid, 64 * W, L.lds, L.st>>>(
+        L.p, L.a, L.m, L.N, L.K, L.shifts, L.alpha, L.c, L.accumulate, L.bias, L.partials, L.counters);
     return KT_OK;
 }
 
-template <int MT, bool COPY>
-static int32_t launch_rows_g(int32_t gshift, int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st,
-                             const uint8_t* p, const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts,
-                             float alpha, float* c, int32_t accumulate, const float* bias) {
-    if (gshift == 0)
-        return launch_rows<0, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    if (gshift == 1)
-        return launch_rows<1, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    return launch_rows<2, MT, COPY>(bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
+template <int GS, int MT, bool COPY, bool SPLIT>
+static int32_t launch_rows(int32_t bits, bool zp, const RowsLaunch& L) {
+    if (bits == 4) return launch_rows_kernel<4, true, GS, MT, COPY, SPLIT>(L);
+    if (zp) return launch_rows_kernel<8, true, GS, MT, COPY, SPLIT>(L);
+    return launch_rows_kernel<8, false, GS, MT, COPY, SPLIT>(L);
 }
 
+template <int MT, bool COPY, bool SPLIT>
+static int32_t launch_rows_g(int32_t gshift, int32_t bits, bool zp, const RowsLaunch& L) {
+    if (gshift == 0) return launch_rows<0, MT, COPY, SPLIT>(bits, zp, L);
+    if (gshift == 1) return launch_rows<1, MT, COPY, SPLIT>(bits, zp, L);
+    return launch_rows<2, MT, COPY, SPLIT>(bits, zp, L);
+}
+
+// 16 rows copy prepared tiles unless the K-parts are split across workgroups (each then
+// converts only its own part).
 template <int MT>
-static int32_t launch_rows_mt(bool copy, int32_t gshift, int32_t bits, bool zp, dim3 grid, size_t lds, hipStream_t st,
-                              const uint8_t* p, const float* a, int32_t m, int32_t N, int32_t K, int32_t shifts,
-                              float alpha, float* c, int32_t accumulate, const float* bias) {
-    if (MT == 16 || copy)  // 16 rows always copy
-        return launch_rows_g<MT, true>(gshift, bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
-    if constexpr (MT != 16)
-        return launch_rows_g<MT, false>(gshift, bits, zp, grid, lds, st, p, a, m, N, K, shifts, alpha, c, accumulate, bias);
+static int32_t launch_rows_mt(bool copy, bool split, int32_t gshift, int32_t bits, bool zp, const RowsLaunch& L) {
+    if (split) return launch_rows_g<MT, false, true>(gshift, bits, zp, L);
+    if (MT == 16 || copy) return launch_rows_g<MT, true, false>(gshift, bits, zp, L);
+    if constexpr (MT != 16) return launch_rows_g<MT, false, false>(gshift, bits, zp, L);
     return KT_OK;
 }
 
@@ -680,13 +795,30 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
                                 hipStream_t st) {
     const WeightView& w0 = ws[0];
     const int32_t mt = tile_rows(m);
+    bool split = true;  // every weight of the call meets its K-parts across workgroups
+    for (int32_t i = 0; i < count; ++i) split = split && rows_split(ws[i], m);
     int64_t wgs = 0;
+    size_t part_floats = 0;
+    int64_t groups = 0;
     for (int32_t i = 0; i < count; ++i) {
-        const RowsPlan plan = rows_plan(m, ws[i].K, ws[i].g, ws[i].N / SET);
-        if (plan.ks) wgs = std::max<int64_t>(wgs, ceil_div(ws[i].N / SET, W / plan.ks));
+        const RowsPlan plan = rows_plan(m, ws[i].K, ws[i].g, ws[i].N / SET, split);
+        if (!plan.ks) continue;
+        wgs = std::max<int64_t>(wgs, ceil_div(ws[i].N / SET, W / plan.ks));
+        const int64_t gi = ceil_div(ws[i].N / SET, W);
+        groups = std::max(groups, gi);
+        part_floats = std::max(part_floats, static_cast<size_t>(plan.ks) * gi * W * 256);
     }
-    const bool copy = mt == 16 || wgs > cu_count();
+    const bool copy = !split && (mt == 16 || wgs > cu_count());
     const float* src = a;
+    float* partials = nullptr;
+    uint32_t* counters = nullptr;
+    if (split) {  // the K-parts' sums and one counter per column-set group (launches run in turn)
+        void* general = nullptr;
+        if (const int32_t status = workspace_counters(st, part_floats * sizeof(float), static_cast<size_t>(groups),
+                                                      &general, &counters))
+            return status;
+        partials = static_cast<float*>(general);
+    }
     if (copy) {  // one preparation of x for every weight of the call (same K, bits)
         const int32_t chunks = ceil_div(w0.K, CHUNK);
         void* general = nullptr;
@@ -709,24 +841,20 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
     }
     for (int32_t i = 0; i < count; ++i) {
         const WeightView& w = ws[i];
-        const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET);
+        const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET, split);
         const int32_t gshift = log2_exact(w.g / RUN);
         if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
         const int32_t kslog = log2_exact(plan.ks);
-        const dim3 grid(static_cast<uint32_t>(ceil_div(w.N / SET, W / plan.ks)));
+        const dim3 grid = split ? dim3(static_cast<uint32_t>(ceil_div(w.N / SET, W)), static_cast<uint32_t>(plan.ks))
+                                : dim3(static_cast<uint32_t>(ceil_div(w.N / SET, W / plan.ks)));
         const int32_t shifts = kslog | gshift << 4 | log2_exact(plan.cpp) << 8;
-        const float* bias = biases ? biases[i] : nullptr;
-        int32_t status;
+        const RowsLaunch L{grid,  plan.lds, st,    w.p,        src, m,          w.N, w.K, shifts, alpha, cs[i],
+                           accumulate, biases ? biases[i] : nullptr, partials, counters};
         const bool zp = w.z != nullptr;
-        if (mt == 4)
-            status = launch_rows_mt<4>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
-                                       alpha, cs[i], accumulate, bias);
-        else if (mt == 8)
-            status = launch_rows_mt<8>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
-                                       alpha, cs[i], accumulate, bias);
-        else
-            status = launch_rows_mt<16>(copy, gshift, w.bits, zp, grid, plan.lds, st, w.p, src, m, w.N, w.K, shifts,
-                                        alpha, cs[i], accumulate, bias);
+        int32_t status;
+        if (mt == 4) status = launch_rows_mt<4>(copy, split, gshift, w.bits, zp, L);
+        else if (mt == 8) status = launch_rows_mt<8>(copy, split, gshift, w.bits, zp, L);
+        else status = launch_rows_mt<16>(copy, split, gshift, w.bits, zp, L);
         if (status) return status;
         KT_LAUNCHED("qmatmul: packed rows gemv kernel");
     }

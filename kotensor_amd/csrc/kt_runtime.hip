@@ -383,6 +383,7 @@ int32_t kt_set_kernel_config(int32_t gemv_kind, int32_t gemv_vec, int32_t gemv_s
     set_gemv_mfma_config(gemv_splits, gemv_waves, gemv_reduce, gemv_kind == 1);
     set_gemv_wide_config(gemv_splits, gemv_waves);
     set_gemv_packed_config(gemv_splits, gemv_waves, gemv_vec);
+    set_gemv_rows_packed_reduce(gemv_reduce);
     g_gemv_kind = gemv_kind;
     return KT_OK;
 }

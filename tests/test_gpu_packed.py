@@ -402,10 +402,10 @@ def _grouped_rows_cases(kt, oracle_lib, rng):
 
 
 def test_packed_rows_work_splits_agree(kt, oracle_lib):
-    """Every split of a column set's K range over 1, 2, 4 or 8 waves (and the x tiles in
-    one phase or several) gives the same bits at 4 and 16 rows, within the oracle's
-    bound (a split whose x tiles do not fit LDS runs as the largest smaller one that
-    does)."""
+    """Every split of a column set's K range over 1, 2, 4 or 8 waves of one workgroup (and
+    the x tiles in one phase or several) or over as many workgroups gives the same bits at
+    4 and 16 rows, within the oracle's bound (inside a workgroup, a split whose x tiles do
+    not fit LDS runs as the largest smaller one that does)."""
     rng = np.random.default_rng(43)
     try:
         for k, n, bits in [(4096, 14336, 4), (2048, 2048, 8), (8192, 2048, 4)]:
@@ -415,14 +415,82 @@ def test_packed_rows_work_splits_agree(kt, oracle_lib):
                 x = rng.standard_normal((m, k), dtype=np.float32)
                 want = oracle_lib.multiply_quantized(x, q, m, threads=16)
                 first = None
-                for ks in (1, 2, 4, 8):
-                    if -(-k // 128) > 16 * ks or ks > -(-k // 128):
-                        continue
-                    banner("packed-rows-split", k, n, bits, m, ks)
-                    kt.MatMul.set_kernel_config(5, 0, ks, 0, 0)
-                    got = gpu_matmul(kt, x, qt, m)
-                    assert normwise_rel(got, want) <= TOL, (m, ks)
-                    first = got if first is None else first
-                    assert same_bits(got, first), (k, n, bits, m, ks)
+                for reduce in (1, 2):
+                    for ks in (1, 2, 4, 8):
+                        if -(-k // 128) > 16 * ks or ks > -(-k // 128):
+                            continue
+                        banner("packed-rows-split", k, n, bits, m, reduce, ks)
+                        kt.MatMul.set_kernel_config(5, 0, ks, 0, reduce)
+                        got = gpu_matmul(kt, x, qt, m)
+                        assert normwise_rel(got, want) <= TOL, (m, reduce, ks)
+                        first = got if first is None else first
+                        assert same_bits(got, first), (k, n, bits, m, reduce, ks)
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("k,n,bits,g", [(14336, 4096, 4, 64), (4096, 4096, 4, 64), (4096, 1024, 8, 64),
+                                        (8192, 2048, 8, 32), (2048, 8192, 4, 128), (896, 4864, 4, 32),
+                                        (4096, 14336, 4, 64)])
+def test_packed_rows_split_across_workgroups(kt, oracle_lib, k, n, bits, g):
+    """The K-parts of a column set as separate workgroups that meet through memory (a
+    write-through partial per wave, a counter per group of column sets, the last
+    workgroup adding the parts in the tree's fixed order) against the K-parts meeting
+    inside one workgroup: the same bits at every row count (one quad, two, four; hi and lo
+    parts in the rows or in K), and within the oracle's bound. Two calls in a row check
+    that the counters are left at zero. Inside one workgroup, 9..16 rows of K >= 8192 do
+    not fit LDS (the call goes to another kernel): there the split rows are checked
+    against the oracle and for not depending on the other rows of the call."""
+    q = _weights(oracle_lib, k, n, bits, g, 61)
+    qt = _packed(kt, q)
+    rng = np.random.default_rng(k + n + bits + g + 7)
+    try:
+        for m in (2, 3, 5, 8, 9, 12, 16):
+            x = rng.standard_normal((m, k), dtype=np.float32)
+            banner("packed-rows-split-wg", k, n, bits, g, m)
+            kt.MatMul.set_kernel_config(5, 0, 0, 0, 2)
+            across = gpu_matmul(kt, x, qt, m)
+            again = gpu_matmul(kt, x, qt, m)
+            assert same_bits(again, across), (k, n, bits, g, m)
+            if m <= 8 or k < 8192:
+                kt.MatMul.set_kernel_config(5, 0, 0, 0, 1)
+                inside = gpu_matmul(kt, x, qt, m)
+                assert same_bits(across, inside), (k, n, bits, g, m)
+            else:  # three of the rows, with six others, in a call of nine (the same class)
+                rows = [m - 1, 0, m // 2]
+                nine = gpu_matmul(kt, np.concatenate([x[rows], x[:6]]), qt, 9)
+                assert all(same_bits(nine[i], across[r]) for i, r in enumerate(rows)), (k, n, m)
+            if m in (3, 16):
+                want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+                errs = [normwise_rel(across[r], want[r]) for r in range(m)]
+                print(f"  worst row normwise={max(errs):.2e}", flush=True)
+                assert max(errs) <= TOL, errs
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
+
+
+def test_packed_rows_split_grouped_accumulate_and_bias(kt, oracle_lib):
+    """Grouped weights of one input across split workgroups (the counters and partials
+    reused launch after launch): accumulate, alpha and biases against the oracle."""
+    rng = np.random.default_rng(62)
+    try:
+        for m, k, ns, bits, g in [(5, 14336, (4096, 1024), 4, 64), (16, 4096, (4096, 4096, 1024), 8, 32)]:
+            banner("packed-rows-split-group", m, k, ns, bits, g)
+            qs = [_weights(oracle_lib, k, n, bits, g, 70 + i) for i, n in enumerate(ns)]
+            qts = [_packed(kt, q) for q in qs]
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            biases = [rng.standard_normal(n).astype(np.float32) for n in ns]
+            c0 = [rng.standard_normal((m, n)).astype(np.float32) for n in ns]
+            outs = [kt.DeviceBuffer.from_numpy(c) for c in c0]
+            dbias = [kt.DeviceBuffer.from_numpy(b) for b in biases]
+            kt.MatMul.set_kernel_config(5, 0, 0, 0, 2)
+            kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(x), qts, outs, m, accumulate=True,
+                                               alpha=-0.75, biases=dbias)
+            kt.synchronize()
+            kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
+            for q, o, b, c, n in zip(qs, outs, biases, c0, ns):
+                got = o.download(np.float32).reshape(m, n)
+                want = oracle_lib.multiply_quantized(x, q, m, c=c, accumulate=True, alpha=-0.75, threads=16) + b[None, :]
+                assert normwise_rel(got, want) <= TOL
     finally:
         kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
