@@ -746,6 +746,54 @@ __global__ void __launch_bounds__(256)
     if (ln == 0) er[m] = e;
 }
 
+// The same for rows of 4096 < K <= 16384: a workgroup of four waves per row, each wave a
+// quarter of it in registers (float4 f = 1024 w + ln + 64 j), the row's maximum through
+// LDS, so the row is read once and in one round trip. (One wave per row read such a row
+// twice, in rounds of 16 loads per lane: 22 us for 64 rows of 14336 against 4 at 4096.)
+template <int BITS, int TM>
+__global__ void __launch_bounds__(256)
+    gemm_prep_tiled_long(const float* __restrict__ a, int32_t M, int32_t K, int32_t S, int32_t vec_rows,
+                         _Float16* __restrict__ a16t, int32_t* __restrict__ er) {
+    __shared__ float red[4];
+    const int32_t m = blockIdx.x, t = threadIdx.x, ln = t & 63, w = t >> 6;
+    const int32_t tm = m / TM, r = m % TM, rb = r / 32, rl = r % 32;
+    auto piece = [&](int32_t sp, int32_t o8) -> u32x4* {
+        const int32_t q = o8 >> 1, i = o8 & 1;
+        const int32_t slab = BITS == 8 ? sp : 2 * (sp >> 1) + q;
+        const int32_t hl = BITS == 8 ? q : (sp & 1);
+        return reinterpret_cast<u32x4*>(a16t) + ((static_cast<size_t>(tm) * S + slab) * (TM / 16) + rb * 2 + i) * 64 +
+               rl + 32 * hl;
+    };
+    if (m >= M) {
+        for (int32_t sp = t; sp < S; sp += 256)
+#pragma unroll
+            for (int o8 = 0; o8 < 4; ++o8) *piece(sp, o8) = u32x4{0u, 0u, 0u, 0u};
+        if (t == 0) er[m] = 0;
+        return;
+    }
+    const float* row = a + static_cast<size_t>(m) * K;
+    const bool vec = vec_rows != 0;
+    auto absmax = [](const f32x4& v) { return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))); };
+    f32x4 v[16];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int32_t f = 1024 * w + ln + 64 * j;
+        v[j] = f < 8 * S ? row_chunk(row, f, K, vec) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        mx = fmaxf(mx, absmax(v[j]));
+    }
+    const int32_t e = scale_exponent(block_max<4>(mx, red), 15);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int32_t f = 1024 * w + ln + 64 * j;
+        if (f < 8 * S)
+            *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(piece(f >> 3, (f & 7) >> 1)) + 8 * (f & 1)) =
+                u32x2{pack_half2(ldexpf(v[j][0], -e), ldexpf(v[j][1], -e)),
+                      pack_half2(ldexpf(v[j][2], -e), ldexpf(v[j][3], -e))};
+    }
+    if (t == 0) er[m] = e;
+}
+
 // One slab of a wave: a pieces (2 rb + i), the weight bytes of its CB column blocks, and
 // their scales and zero points.
 template <int BITS, int RB, int CB>
@@ -1142,11 +1190,16 @@ static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightV
         part += static_cast<size_t>(splits) * m * ws[i].N;
     }
     const int32_t vec_rows = (w.K % 4 == 0 && aligned(a, 16)) ? 1 : 0;
-    const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4);
-    if (w.bits == 4)
-        gemm_prep_tiled<4, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
-    else
-        gemm_prep_tiled<8, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
+    if (S > 128 && S <= 512) {  // a workgroup per row
+        if (w.bits == 4) gemm_prep_tiled_long<4, TM><<<Mp, 256, 0, st>>>(a, m, w.K, S, vec_rows, a16t, er);
+        else gemm_prep_tiled_long<8, TM><<<Mp, 256, 0, st>>>(a, m, w.K, S, vec_rows, a16t, er);
+    } else {
+        const uint32_t prep_blocks = static_cast<uint32_t>(Mp / 4);
+        if (w.bits == 4)
+            gemm_prep_tiled<4, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
+        else
+            gemm_prep_tiled<8, TM><<<prep_blocks, 256, 0, st>>>(a, m, w.K, S, vec_rows, Mp, a16t, er);
+    }
     KT_LAUNCHED("qmatmul: tiled gemm prep");
     constexpr size_t lds = plds_bytes(TN);
     static bool raised = false;

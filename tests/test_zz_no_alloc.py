@@ -43,23 +43,28 @@ def _run(kt, entry, x, qt, c0=None, accumulate=0, alpha=1.0, stream=None):
     return c.download(np.float32).reshape(m, qt.columns)
 
 
-# (k, n, bits, g, m) of the first and the second (smaller) call, and whether the
-# kernels' reduction order is fixed (bit-identical results expected)
+# (k, n, bits, g, m) of the first and the second (smaller) call, whether the kernels'
+# reduction order is fixed (bit-identical results expected), and whether the weight has
+# its column-run copy (2..16 rows: K-parts meeting across workgroups through the
+# array's partials and counters)
 CASES = [
-    ("gemm", (2048, 8192, 8, 32, 512), (2048, 8192, 8, 32, 64), True),
-    ("row mode", (4096, 14336, 4, 64, 16), (4096, 14336, 4, 64, 5), True),
-    ("one row", (4096, 14336, 4, 64, 1), (896, 4864, 4, 64, 1), False),
-    ("one row int8", (8192, 2048, 8, 32, 1), (2048, 2048, 8, 32, 1), False),
+    ("gemm", (2048, 8192, 8, 32, 512), (2048, 8192, 8, 32, 64), True, False),
+    ("row mode", (4096, 14336, 4, 64, 16), (4096, 14336, 4, 64, 5), True, False),
+    ("one row", (4096, 14336, 4, 64, 1), (896, 4864, 4, 64, 1), False, False),
+    ("one row int8", (8192, 2048, 8, 32, 1), (2048, 2048, 8, 32, 1), False, False),
+    ("packed rows", (14336, 4096, 4, 64, 16), (4096, 4096, 8, 64, 3), True, True),
 ]
 
 
-@pytest.mark.parametrize("label,first,second,exact", CASES, ids=[c[0] for c in CASES])
-def test_noalloc_equals_qmatmul_on_two_calls(kt, oracle_lib, label, first, second, exact):
+@pytest.mark.parametrize("label,first,second,exact,packed", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_equals_qmatmul_on_two_calls(kt, oracle_lib, label, first, second, exact, packed):
     rng = np.random.default_rng(61)
     for k, n, bits, g, m in (first, second):
         banner("noalloc", label, k, n, bits, g, m)
         q = _weights(oracle_lib, k, n, bits, g, k + n + m)
         qt = upload_quantized(kt, q)
+        if packed:
+            qt = qt.pack()
         x = rng.standard_normal((m, k), dtype=np.float32)
         c0 = rng.standard_normal((m, n), dtype=np.float32)
         for acc, alpha in ((0, 1.0), (1, -0.5)):
