@@ -708,9 +708,12 @@ int32_t launch_k(dim3 grid, size_t lds, hipStream_t st, const float* x, const fl
 template <int BITS, bool ZP, int XMODE, bool GLU>
 int32_t launch_g(dim3 grid, size_t lds, hipStream_t st, const float* x, const float* aux, float eps, int32_t K,
                  int32_t gshift, const PJobs& jobs, int32_t kslog, float alpha, int32_t accumulate, int32_t nmax) {
-    // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short ranges)
+    // the ring: 4 KB of weights in flight per wave (8 KB when forced, 2 KB for short
+    // ranges); INT8 ranges of 8 chunks or more take 8 KB (measured: 4096 -> 14336 g64 /
+    // g32 12.8 / 14.3 -> 12.5 / 13.4 us, 4096 -> 128256 g32 95.3 -> 91.8; INT4 slower with
+    // 8 KB, 8.4 -> 9.0; 2048 -> 8192 INT8, 4-chunk ranges, 5.4 -> 5.5)
     constexpr int RS = BITS == 4 ? 4 : 2;
-    if (g_forced.ring == 2)
+    if (g_forced.ring == 2 || (g_forced.ring == 0 && BITS == 8 && nmax >= 8))
         return launch_k<BITS, 2 * RS, ZP, XMODE, GLU>(grid, lds, st, x, aux, eps, K, gshift, jobs, kslog, alpha,
                                                       accumulate, nmax);
     if (g_forced.ring == 1 || nmax > RS / 2)
