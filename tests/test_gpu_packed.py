@@ -429,18 +429,22 @@ def test_packed_rows_work_splits_agree(kt, oracle_lib):
         kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
 
-@pytest.mark.parametrize("k,n,bits,g", [(14336, 4096, 4, 64), (4096, 4096, 4, 64), (4096, 1024, 8, 64),
-                                        (8192, 2048, 8, 32), (2048, 8192, 4, 128), (896, 4864, 4, 32),
-                                        (4096, 14336, 4, 64)])
-def test_packed_rows_split_across_workgroups(kt, oracle_lib, k, n, bits, g):
+# (k, n, bits, g, the most rows whose x tiles fit one workgroup holding every K-part)
+@pytest.mark.parametrize("k,n,bits,g,inside_rows", [(14336, 4096, 4, 64, 8), (4096, 4096, 4, 64, 16),
+                                               (4096, 1024, 8, 64, 16), (8192, 2048, 8, 32, 8),
+                                               (2048, 8192, 4, 128, 16), (896, 4864, 4, 32, 16),
+                                               (4096, 14336, 4, 64, 16), (14336, 4096, 4, 32, 4)])
+def test_packed_rows_split_across_workgroups(kt, oracle_lib, k, n, bits, g, inside_rows):
     """The K-parts of a column set as separate workgroups that meet through memory (a
     write-through partial per wave, a counter per group of column sets, the last
     workgroup adding the parts in the tree's fixed order) against the K-parts meeting
     inside one workgroup: the same bits at every row count (one quad, two, four; hi and lo
     parts in the rows or in K), and within the oracle's bound. Two calls in a row check
-    that the counters are left at zero. Inside one workgroup, 9..16 rows of K >= 8192 do
-    not fit LDS (the call goes to another kernel): there the split rows are checked
-    against the oracle and for not depending on the other rows of the call."""
+    that the counters are left at zero. Where the x tiles and staged rows do not fit one
+    workgroup holding every K-part (9..16 rows of K >= 8192, 5..16 rows of 14336 at g32;
+    the call then goes to another kernel), the split rows are checked against the oracle
+    and for not depending on the other rows of the call. 14336 -> 4096 at g32 with 9..16
+    rows holds its x tiles in two phases."""
     q = _weights(oracle_lib, k, n, bits, g, 61)
     qt = _packed(kt, q)
     rng = np.random.default_rng(k + n + bits + g + 7)
@@ -452,15 +456,16 @@ def test_packed_rows_split_across_workgroups(kt, oracle_lib, k, n, bits, g):
             across = gpu_matmul(kt, x, qt, m)
             again = gpu_matmul(kt, x, qt, m)
             assert same_bits(again, across), (k, n, bits, g, m)
-            if m <= 8 or k < 8192:
+            if m <= inside_rows:
                 kt.MatMul.set_kernel_config(5, 0, 0, 0, 1)
                 inside = gpu_matmul(kt, x, qt, m)
                 assert same_bits(across, inside), (k, n, bits, g, m)
-            else:  # three of the rows, with six others, in a call of nine (the same class)
+            else:  # three of the rows, with others, in a call of the same class (2..8 or 9..16)
                 rows = [m - 1, 0, m // 2]
-                nine = gpu_matmul(kt, np.concatenate([x[rows], x[:6]]), qt, 9)
-                assert all(same_bits(nine[i], across[r]) for i, r in enumerate(rows)), (k, n, m)
-            if m in (3, 16):
+                fill = 6 if m > 8 else 2
+                other = gpu_matmul(kt, np.concatenate([x[rows], x[:fill]]), qt, 3 + fill)
+                assert all(same_bits(other[i], across[r]) for i, r in enumerate(rows)), (k, n, m)
+            if m in (3, 5, 16):
                 want = oracle_lib.multiply_quantized(x, q, m, threads=16)
                 errs = [normwise_rel(across[r], want[r]) for r in range(m)]
                 print(f"  worst row normwise={max(errs):.2e}", flush=True)
