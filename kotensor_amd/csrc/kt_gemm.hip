@@ -1230,12 +1230,18 @@ static int32_t launch_gemm_packed_tiles(const float* a, int32_t m, const WeightV
 }
 
 constexpr int GEMM_NARROW_DEPTH = 5;  // the 64 x 64 tile's ring (3, 5, 8 measured alike; 5 a little ahead)
-// Tile shape: 64-row tiles when M <= 64 (a 128-row tile would be half padding), 64-column
-// tiles when 128-column ones number fewer than the CUs.
+// Tile shape: 64-row tiles when M <= 64 (a 128-row tile would be half padding), and up to
+// M = 128 while 64 x 64 tiles make one round of workgroups with K <= 8192 (2048 -> 8192
+// INT8 g32 M = 128: 20.5 -> 15.6 us, 128-row tiles needing a K split there; 4096 -> 4096
+// 20.9 -> 19.9; two rounds, 4096 -> 14336, 31.5 -> 35.4, and K = 14336, 35.4 -> 36.2,
+// stay with 128 rows); 64-column tiles when 128-column ones number fewer than the CUs.
 static int32_t launch_gemm_packed(const float* a, int32_t m, const WeightView* ws, float* const* cs,
                                   const float* const* biases, int32_t count, int32_t accumulate, float alpha,
                                   hipStream_t st) {
-    const bool rows64 = m <= 64;
+    int64_t tiles64 = 0;
+    for (int32_t i = 0; i < count; ++i) tiles64 += ceil_div(ws[i].N, 64);
+    tiles64 *= ceil_div(m, 64);
+    const bool rows64 = m <= 64 || (m <= 128 && tiles64 <= cu_count() && ws[0].K <= 8192);
     int64_t tiles128 = 0;
     for (int32_t i = 0; i < count; ++i) tiles128 += ceil_div(ws[i].N, 128);
     tiles128 *= ceil_div(m, rows64 ? 64 : 128);
