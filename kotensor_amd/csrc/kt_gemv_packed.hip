@@ -681,6 +681,32 @@ __global__ void __launch_bounds__(64 * W)
                                                        blockIdx.x, 0, ChainLink{});
 }
 
+// 2..16 rows of a small weight as one-row products in one launch: workgroup row
+// blockIdx.y takes x row y and writes output row y, so each row's result is its one-row
+// result bit for bit. The weight is read once per row (the later reads mostly from the
+// caches); this pays where the rows' reads and workgroups cost less than the row kernels'
+// fixed costs (the rule is gemv_packed_rows_rep_preferred).
+template <int BITS, int R, bool ZP>
+__global__ void __launch_bounds__(64 * W)
+    gemv_packed_rows_rep(const uint8_t* __restrict__ packed, const float* __restrict__ x, int32_t N, int32_t K,
+                         int32_t shifts, float alpha, float* out, int32_t accumulate, const float* bias) {
+    const int32_t kslog = shifts & 15, gshift = shifts >> 4;
+    const int32_t sets = N >> 4, chunks = (K + CHUNK - 1) >> 7, G = (K + (RUN << gshift) - 1) >> (gshift + 5);
+    PJobs jobs;
+    jobs.count = 1;
+    PJob& jb = jobs.job[0];
+    jb.packed = packed;
+    jb.s = reinterpret_cast<const float*>(packed + static_cast<int64_t>(sets) * chunks * block_bytes(BITS));
+    jb.z = ZP ? reinterpret_cast<const int8_t*>(jb.s + static_cast<int64_t>(sets) * G * SET) : nullptr;
+    jb.out = out + static_cast<size_t>(blockIdx.y) * N;
+    jb.bias = bias;
+    jb.N = N;
+    jb.sets = sets;
+    gemv_packed_body<BITS, R, ZP, X_PLAIN, false, false>(x + static_cast<size_t>(blockIdx.y) * K, nullptr, 0.0f, K,
+                                                         gshift, jobs, kslog, alpha, accumulate, blockIdx.x, 0,
+                                                         ChainLink{});
+}
+
 struct Forced {
     int ks = 0;
     int ring = 0;  // 1: 4 KB of weights in flight per wave, 2: 8 KB, 0: automatic
@@ -1034,6 +1060,52 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
                                          L.alpha, L.accumulate, L.nmax, L.glu ? 1 : 0);
     if (launched) return launched;
     KT_LAUNCHED("qmatmul: packed gemv kernel");
+    return KT_OK;
+}
+
+// Rows as one-row products where the extra rows cost little: (m - 1) times the larger of a
+// row's workgroups at 5 ns each and its weight bytes at 7.5 TB/s (the extra rows' reads
+// come mostly from the caches) within 5 us, and not for the wide weights, whose row kernel
+// is already near its one-row cost. Measured (INT4 g64, M = 2 / 4 / 8 / 16, us, against
+// the kernel taken before): 4096 -> 1024 4.1 / 4.3 / 5.7 / 8.5 (10.6 / 9.0 / 9.2 / 9.5);
+// 2048 -> 2048 M = 3 / 8 5.0 / 7.5 (7.9 / 8.6), M = 16 12.7 (9.2, not taken); 8192 -> 2048
+// M = 2 / 4 5.6 / 7.8 (12.8 / 11.3), M = 8 12.9 (11.7, not taken); 4096 -> 4096 M = 2 / 4
+// 6.2 / 8.9 (9.7 / 9.8); 896 -> 896 M = 8 / 16 4.0 / 4.9 (7.9 / 8.0); INT8 g32 2048 ->
+// 2048 M = 8 6.5 (9.1), 8192 -> 2048 M = 2 6.6 (13.4); 896 -> 4864 (wide) M = 8 8.3 (7.9).
+bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView& w) {
+    if (m < 2 || m > 16) return false;
+    const int64_t sets = w.N / SET, chunks = ceil_div(w.K, CHUNK);
+    if (sets >= 16 * chunks) return false;  // wide: the row kernel
+    const PackedPlan plan = plan_packed(w.K, w.g, sets);
+    if (!plan.ks) return false;
+    const double wgs = static_cast<double>(ceil_div(sets, static_cast<int64_t>(W / plan.ks)));
+    const double bytes = static_cast<double>(packed_weight_bytes(w.K, w.N, w.bits));
+    const double per_row_us = std::max(wgs * 0.005, bytes / 7.5e6);
+    return (m - 1) * per_row_us <= 5.0;
+}
+
+int32_t launch_gemv_packed_rows_rep(const float* a, int32_t m, const WeightView& w, float* c, const float* bias,
+                                    int32_t accumulate, float alpha, hipStream_t st) {
+    const float* biases[1] = {bias};
+    PackedLaunch L;
+    const int32_t status = prepare_gemv_packed(a, &w, &c, biases, 1, accumulate, alpha, nullptr, nullptr, 0.0f, false, &L);
+    if (status) return status;
+    const dim3 grid(L.grid.x, static_cast<uint32_t>(m));
+    const int32_t shifts = L.kslog | L.gshift << 4;
+    if (L.bits == 4) {
+        if (const int32_t ls = allow_lds<&gemv_packed_rows_rep<4, 4, true>>(L.lds)) return ls;
+        gemv_packed_rows_rep<4, 4, true>
+            <<<grid, dim3(64 * W), L.lds, st>>>(w.p, a, w.N, L.K, shifts, alpha, c, accumulate, bias);
+    } else if (L.zp) {
+        if (const int32_t ls = allow_lds<&gemv_packed_rows_rep<8, 2, true>>(L.lds)) return ls;
+        gemv_packed_rows_rep<8, 2, true>
+            <<<grid, dim3(64 * W), L.lds, st>>>(w.p, a, w.N, L.K, shifts, alpha, c, accumulate, bias);
+    } else {
+        if (const int32_t ls = allow_lds<&gemv_packed_rows_rep<8, 2, false>>(L.lds)) return ls;
+        gemv_packed_rows_rep<8, 2, false>
+            <<<grid, dim3(64 * W), L.lds, st>>>(w.p, a, w.N, L.K, shifts, alpha, c, accumulate, bias);
+    }
+    KT_LAUNCHED("qmatmul: packed rows as one-row products");
     return KT_OK;
 }
 

@@ -602,6 +602,8 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
     const float* biases[1] = {bias};
     if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_packed_supported(a, m, v, c))
         return launch_gemv_packed(a, &v, &c, biases, 1, accumulate, alpha, st);
+    if (g_gemv_kind == 0 && m >= 2 && gemv_packed_supported(a, 1, v, c) && gemv_packed_rows_rep_preferred(m, v))
+        return launch_gemv_packed_rows_rep(a, m, v, c, bias, accumulate, alpha, st);
     if ((g_gemv_kind == 5 || (g_gemv_kind == 0 && gemv_rows_packed_preferred(v))) &&
         gemv_rows_packed_supported(a, m, v, c))
         return launch_gemv_rows_packed(a, m, &v, &c, biases, 1, accumulate, alpha, st);

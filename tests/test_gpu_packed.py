@@ -499,3 +499,28 @@ def test_packed_rows_split_grouped_accumulate_and_bias(kt, oracle_lib):
                 assert normwise_rel(got, want) <= TOL
     finally:
         kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("k,n,bits,g,counts", [(4096, 1024, 4, 64, (2, 5, 8, 16)), (2048, 2048, 8, 32, (2, 3, 8)),
+                                               (896, 896, 4, 64, (2, 7, 16)), (8192, 2048, 4, 64, (2, 4)),
+                                               (4864, 896, 4, 32, (3, 8))])
+def test_packed_small_weights_rows_as_one_row_products(kt, oracle_lib, k, n, bits, g, counts):
+    """Small weights at 2..16 rows run as one-row products in one launch (the automatic
+    choice where the extra rows' reads cost less than the row kernels' fixed costs): each
+    row's bits are its one-row result's, with accumulate and alpha, and the rows meet the
+    oracle."""
+    q = _weights(oracle_lib, k, n, bits, g, 81)
+    qt = _packed(kt, q)
+    rng = np.random.default_rng(k + n + bits + g + 9)
+    for m in counts:
+        banner("packed-rows-as-one-row", k, n, bits, g, m)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        c0 = rng.standard_normal((m, n), dtype=np.float32)
+        got = gpu_matmul(kt, x, qt, m, c0, accumulate=True, alpha=-0.5)
+        for r in range(m):
+            one = gpu_matmul(kt, x[r:r + 1], qt, 1, c0[r:r + 1], accumulate=True, alpha=-0.5)
+            assert same_bits(got[r], one[0]), (k, n, m, r)
+        want = oracle_lib.multiply_quantized(x, q, m, c=c0, accumulate=True, alpha=-0.5, threads=16)
+        errs = [normwise_rel(got[r], want[r]) for r in range(m)]
+        print(f"  worst row normwise={max(errs):.2e}", flush=True)
+        assert max(errs) <= TOL, errs
