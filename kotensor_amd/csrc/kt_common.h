@@ -200,11 +200,15 @@ int32_t launch_gemv_chain(const ChainStep* steps, int32_t n, hipStream_t st);
 void set_gemv_packed_config(int32_t ks, int32_t waves, int32_t ring);
 void set_gemv_rows_packed_reduce(int32_t mode);  // 0 automatic, 1 K-parts meet in the workgroup, 2 across
 int32_t packed_forced_ks();  // the K-parts set by set_gemv_packed_config (0: automatic)
-// 2..16 rows of a small weight as one-row products in one launch (each row's bits are its
-// one-row result): the automatic choice's rule, and the launch (one weight).
-bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView& w);
+// 2..16 rows of small weights as one-row products in one launch (each row's bits are its
+// one-row result): the automatic choice's rule, and the launches (one weight; up to four
+// sharing x).
+bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView* ws, int32_t count);
 int32_t launch_gemv_packed_rows_rep(const float* a, int32_t m, const WeightView& w, float* c, const float* bias,
                                     int32_t accumulate, float alpha, hipStream_t st);
+int32_t launch_gemv_packed_group_rep(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                     const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                     hipStream_t st);
 
 // 2 to 16 rows on the column-run copy (kt_gemv_rows_packed.hip): support check and launch
 // (up to four weights sharing the input: one preparation of x, one launch per weight).

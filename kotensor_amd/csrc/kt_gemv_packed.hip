@@ -323,7 +323,7 @@ template <int BITS, int R, bool ZP, int XMODE, bool GLU, bool CHAIN, int XS = X_
 __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, const float* __restrict__ aux, float eps,
                                                  int32_t K, int32_t gshift, const PJobs& jobs, int32_t kslog,
                                                  float alpha, int32_t accumulate, int32_t bx, int32_t by,
-                                                 const ChainLink& link) {
+                                                 const ChainLink& link, int32_t out_row = 0) {
     constexpr int BB = block_bytes(BITS);
     constexpr int NB = BITS == 4 ? 1 : 2;  // 16-byte loads per lane and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -333,8 +333,9 @@ __device__ __forceinline__ void gemv_packed_body(const float* __restrict__ x, co
     // GLU: set slot my_cs holds weight my_cs % 2, column set my_cs / 2 of the pair range.
     // The job's fields are the first loads (first in the source: otherwise they wait for
     // kslog and the start costs a second scalar round trip).
-    const PJob jb = jobs.job[GLU ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & ((1 << (3 - kslog)) - 1) & 1)
-                                 : by];
+    PJob jb = jobs.job[GLU ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & ((1 << (3 - kslog)) - 1) & 1)
+                           : by];
+    jb.out += static_cast<size_t>(out_row) * jb.N;  // (row out_row of a call's outputs)
     const int32_t tid = threadIdx.x, ln = tid & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t cslog = 3 - kslog;  // column sets per workgroup: 1 << cslog
@@ -707,6 +708,16 @@ __global__ void __launch_bounds__(64 * W)
                                                          ChainLink{});
 }
 
+// The same for up to four weights sharing x (blockIdx.y the weight, blockIdx.z the row).
+template <int BITS, int R, bool ZP>
+__global__ void __launch_bounds__(64 * W)
+    gemv_packed_group_rep(const float* __restrict__ x, int32_t K, int32_t gshift, PJobs jobs, int32_t kslog, float alpha,
+                          int32_t accumulate) {
+    gemv_packed_body<BITS, R, ZP, X_PLAIN, false, false>(x + static_cast<size_t>(blockIdx.z) * K, nullptr, 0.0f, K,
+                                                         gshift, jobs, kslog, alpha, accumulate, blockIdx.x,
+                                                         blockIdx.y, ChainLink{}, blockIdx.z);
+}
+
 struct Forced {
     int ks = 0;
     int ring = 0;  // 1: 4 KB of weights in flight per wave, 2: 8 KB, 0: automatic
@@ -1072,16 +1083,47 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
 // M = 2 / 4 5.6 / 7.8 (12.8 / 11.3), M = 8 12.9 (11.7, not taken); 4096 -> 4096 M = 2 / 4
 // 6.2 / 8.9 (9.7 / 9.8); 896 -> 896 M = 8 / 16 4.0 / 4.9 (7.9 / 8.0); INT8 g32 2048 ->
 // 2048 M = 8 6.5 (9.1), 8192 -> 2048 M = 2 6.6 (13.4); 896 -> 4864 (wide) M = 8 8.3 (7.9).
-bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView& w) {
+bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView* ws, int32_t count) {
     if (m < 2 || m > 16) return false;
-    const int64_t sets = w.N / SET, chunks = ceil_div(w.K, CHUNK);
-    if (sets >= 16 * chunks) return false;  // wide: the row kernel
-    const PackedPlan plan = plan_packed(w.K, w.g, sets);
+    int64_t sets_total = 0;
+    double bytes = 0.0;
+    for (int32_t i = 0; i < count; ++i) {
+        const int64_t sets = ws[i].N / SET;
+        if (sets >= 16 * ceil_div(ws[i].K, CHUNK)) return false;  // wide: the row kernel
+        sets_total += sets;
+        bytes += static_cast<double>(packed_weight_bytes(ws[i].K, ws[i].N, ws[i].bits));
+    }
+    const PackedPlan plan = plan_packed(ws[0].K, ws[0].g, sets_total);
     if (!plan.ks) return false;
-    const double wgs = static_cast<double>(ceil_div(sets, static_cast<int64_t>(W / plan.ks)));
-    const double bytes = static_cast<double>(packed_weight_bytes(w.K, w.N, w.bits));
+    double wgs = 0.0;  // the workgroups that hold column sets (a grouped launch's others exit at once)
+    for (int32_t i = 0; i < count; ++i) wgs += static_cast<double>(ceil_div(ws[i].N / SET, static_cast<int64_t>(W / plan.ks)));
     const double per_row_us = std::max(wgs * 0.005, bytes / 7.5e6);
     return (m - 1) * per_row_us <= 5.0;
+}
+
+int32_t launch_gemv_packed_group_rep(const float* a, int32_t m, const WeightView* ws, float* const* cs,
+                                     const float* const* biases, int32_t count, int32_t accumulate, float alpha,
+                                     hipStream_t st) {
+    PackedLaunch L;
+    const int32_t status = prepare_gemv_packed(a, ws, cs, biases, count, accumulate, alpha, nullptr, nullptr, 0.0f,
+                                               false, &L);
+    if (status) return status;
+    const dim3 grid(L.grid.x, static_cast<uint32_t>(count), static_cast<uint32_t>(m));
+    if (L.bits == 4) {
+        if (const int32_t ls = allow_lds<&gemv_packed_group_rep<4, 4, true>>(L.lds)) return ls;
+        gemv_packed_group_rep<4, 4, true>
+            <<<grid, dim3(64 * W), L.lds, st>>>(a, L.K, L.gshift, L.jobs, L.kslog, alpha, accumulate);
+    } else if (L.zp) {
+        if (const int32_t ls = allow_lds<&gemv_packed_group_rep<8, 2, true>>(L.lds)) return ls;
+        gemv_packed_group_rep<8, 2, true>
+            <<<grid, dim3(64 * W), L.lds, st>>>(a, L.K, L.gshift, L.jobs, L.kslog, alpha, accumulate);
+    } else {
+        if (const int32_t ls = allow_lds<&gemv_packed_group_rep<8, 2, false>>(L.lds)) return ls;
+        gemv_packed_group_rep<8, 2, false>
+            <<<grid, dim3(64 * W), L.lds, st>>>(a, L.K, L.gshift, L.jobs, L.kslog, alpha, accumulate);
+    }
+    KT_LAUNCHED("qmatmul: packed grouped rows as one-row products");
+    return KT_OK;
 }
 
 int32_t launch_gemv_packed_rows_rep(const float* a, int32_t m, const WeightView& w, float* c, const float* bias,

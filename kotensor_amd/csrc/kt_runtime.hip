@@ -602,7 +602,7 @@ static int32_t qmatmul_impl(const float* a, int32_t m, const kt_qweight* w, floa
     const float* biases[1] = {bias};
     if ((g_gemv_kind == 0 || g_gemv_kind == 5) && gemv_packed_supported(a, m, v, c))
         return launch_gemv_packed(a, &v, &c, biases, 1, accumulate, alpha, st);
-    if (g_gemv_kind == 0 && m >= 2 && gemv_packed_supported(a, 1, v, c) && gemv_packed_rows_rep_preferred(m, v))
+    if (g_gemv_kind == 0 && m >= 2 && gemv_packed_supported(a, 1, v, c) && gemv_packed_rows_rep_preferred(m, &v, 1))
         return launch_gemv_packed_rows_rep(a, m, v, c, bias, accumulate, alpha, st);
     if ((g_gemv_kind == 5 || (g_gemv_kind == 0 && gemv_rows_packed_preferred(v))) &&
         gemv_rows_packed_supported(a, m, v, c))
@@ -633,6 +633,7 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         bool strip = (g_gemv_kind == 0 || g_gemv_kind == 4) && a != nullptr;
         bool packed = (g_gemv_kind == 0 || g_gemv_kind == 5) && a != nullptr;
         bool rows_packed = packed && m >= 2;
+        bool rep = g_gemv_kind == 0 && m >= 2 && a != nullptr;  // rows as one-row products
         bool gemm = m > 2 && a != nullptr;
         for (int32_t i = 0; i < n; ++i) {
             int32_t status = view_weight(&weights[start + i], &views[i]);
@@ -647,6 +648,8 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
             wide = wide && gemv_wide_supported(a, m, v, outputs[start + i]);
             strip = strip && gemv_strip_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 4));
             packed = packed && gemv_packed_supported(a, m, v, outputs[start + i]);
+            rep = rep && gemv_packed_supported(a, 1, v, outputs[start + i]) &&
+                  (v.z != nullptr) == (views[0].z != nullptr);
             rows_packed = rows_packed && gemv_rows_packed_supported(a, m, v, outputs[start + i]) &&
                           (g_gemv_kind == 5 || gemv_rows_packed_preferred(v));
             gemm = gemm && gemm_supported(a, m, v, outputs[start + i]) && (!b || aligned(b, 16)) &&
@@ -658,9 +661,13 @@ int32_t kt_qmatmul_group(const float* a, int32_t m, const kt_qweight* weights, i
         int32_t status = KT_OK;
         if (strip && g_gemv_kind == 0 && !gemv_strip_preferred(views, n)) strip = false;
         if (wide && g_gemv_kind == 0 && !gemv_wide_preferred(views, n)) wide = false;
+        if (rep && !gemv_packed_rows_rep_preferred(m, views, n)) rep = false;
         if (packed) {
             status = launch_gemv_packed(a, views, outputs + start, biases ? biases + start : nullptr, n, accumulate,
                                         alpha, st);
+        } else if (rep) {
+            status = launch_gemv_packed_group_rep(a, m, views, outputs + start, biases ? biases + start : nullptr, n,
+                                                  accumulate, alpha, st);
         } else if (rows_packed) {
             status = launch_gemv_rows_packed(a, m, views, outputs + start, biases ? biases + start : nullptr, n,
                                              accumulate, alpha, st);

@@ -524,3 +524,35 @@ def test_packed_small_weights_rows_as_one_row_products(kt, oracle_lib, k, n, bit
         errs = [normwise_rel(got[r], want[r]) for r in range(m)]
         print(f"  worst row normwise={max(errs):.2e}", flush=True)
         assert max(errs) <= TOL, errs
+
+
+def test_packed_small_weights_grouped_rows_as_one_row_products(kt, oracle_lib):
+    """Grouped small weights sharing x (q/k/v of the 1B and Qwen2 decoders) at 2..8 rows,
+    as one-row products in one launch: each row's bits are its one-row grouped result's,
+    with accumulate, alpha and biases, and they meet the oracle."""
+    rng = np.random.default_rng(83)
+    for k, ns, bits, g, counts in [(2048, (2048, 512, 512), 4, 64, (2, 4)), (896, (896, 128, 128), 4, 64, (3, 8)),
+                                   (2048, (2048, 512, 512), 8, 32, (2, 3))]:
+        qs = [_weights(oracle_lib, k, n, bits, g, 90 + i) for i, n in enumerate(ns)]
+        qts = [_packed(kt, q) for q in qs]
+        biases = [rng.standard_normal(n).astype(np.float32) for n in ns]
+        dbias = [kt.DeviceBuffer.from_numpy(b) for b in biases]
+        for m in counts:
+            banner("packed-group-rows-as-one-row", k, ns, bits, g, m)
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            c0 = [rng.standard_normal((m, n)).astype(np.float32) for n in ns]
+
+            def run(xs, cs, rows):
+                outs = [kt.DeviceBuffer.from_numpy(np.ascontiguousarray(c)) for c in cs]
+                kt.MatMul.multiply_quantized_group(kt.DeviceBuffer.from_numpy(np.ascontiguousarray(xs)), qts, outs,
+                                                   rows, accumulate=True, alpha=-0.75, biases=dbias)
+                kt.synchronize()
+                return [o.download(np.float32).reshape(rows, n) for o, n in zip(outs, ns)]
+
+            got = run(x, c0, m)
+            for r in range(m):
+                one = run(x[r:r + 1], [c[r:r + 1] for c in c0], 1)
+                assert all(same_bits(gw[r], ow[0]) for gw, ow in zip(got, one)), (k, ns, m, r)
+            for q, o, b, c in zip(qs, got, biases, c0):
+                want = oracle_lib.multiply_quantized(x, q, m, c=c, accumulate=True, alpha=-0.75, threads=16) + b[None, :]
+                assert normwise_rel(o, want) <= TOL
