@@ -83,9 +83,11 @@ int32_t kt_set_device(int32_t device);
  * (K/MatMul.kt:30-82: numThreads, parallelThreshold, lookupInt4): they choose how the
  * small-M kernels split their work, never their result beyond fp32 rounding order.
  * gemv_kind: 0 = automatic (the column-run kernel for one row when the weight has a
- *            packed copy, and for 2 to 16 rows when it also has at least 16 column sets
- *            of 16 per 128 rows of K, or K >= 4096 and at least 256 column sets;
- *            otherwise for one row the column-strip kernel up to
+ *            packed copy; for 2 to 16 rows of small weights that are not wide, the
+ *            one-row kernel once per row in one launch (each row's bits its one-row
+ *            result); for 2 to 16 rows when the weight also has at least 16 column sets
+ *            of 16 per 128 rows of K, or K >= 4096 and at least 256 column sets, the
+ *            column-run rows kernel; otherwise for one row the column-strip kernel up to
  *            a size and the wide-strip MFMA kernel above it, and the row-block MFMA kernel
  *            for 2 to 16 rows, where the layout allows), 1 = vector-ALU kernel for M == 1 (and no MFMA
  *            GEMV for M > 1: those go to the GEMM), 2 = row-block MFMA kernel for M <= 16,
