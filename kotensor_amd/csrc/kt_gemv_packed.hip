@@ -1074,22 +1074,26 @@ int32_t launch_gemv_packed(const float* a, const WeightView* ws, float* const* c
     return KT_OK;
 }
 
-// Rows as one-row products where the extra rows cost little: (m - 1) times the larger of a
-// row's workgroups at 5 ns each and its weight bytes at 7.5 TB/s (the extra rows' reads
-// come mostly from the caches) within 5 us, and not for the wide weights, whose row kernel
-// is already near its one-row cost. Measured (INT4 g64, M = 2 / 4 / 8 / 16, us, against
-// the kernel taken before): 4096 -> 1024 4.1 / 4.3 / 5.7 / 8.5 (10.6 / 9.0 / 9.2 / 9.5);
-// 2048 -> 2048 M = 3 / 8 5.0 / 7.5 (7.9 / 8.6), M = 16 12.7 (9.2, not taken); 8192 -> 2048
-// M = 2 / 4 5.6 / 7.8 (12.8 / 11.3), M = 8 12.9 (11.7, not taken); 4096 -> 4096 M = 2 / 4
-// 6.2 / 8.9 (9.7 / 9.8); 896 -> 896 M = 8 / 16 4.0 / 4.9 (7.9 / 8.0); INT8 g32 2048 ->
-// 2048 M = 8 6.5 (9.1), 8192 -> 2048 M = 2 6.6 (13.4); 896 -> 4864 (wide) M = 8 8.3 (7.9).
+// Rows as one-row products where the extra rows cost little: (m - 1) times the larger of
+// a row's workgroups that hold column sets at 5 ns each and its weight bytes at 10 TB/s
+// (the extra rows' reads come mostly from the caches) within 5 us, or within 3 us per
+// weight for the wide weights (their row kernel, one launch per weight, is nearer its
+// one-row cost). Measured (INT4 g64, us, against the kernel taken before): 4096 -> 1024
+// M = 2 / 4 / 8 / 16 4.1 / 4.3 / 5.6 / 8.5 (10.6 / 9.0 / 9.2 / 9.5); 2048 -> 2048 M = 3 / 8
+// 5.0 / 7.5 (7.9 / 8.6), M = 16 12.7 (9.2, not taken); 8192 -> 2048 M = 2 / 4 5.6 / 7.8
+// (12.8 / 11.3), M = 8 12.9 (11.7, not taken); 4096 -> 4096 M = 2 / 4 6.2 / 8.9 (9.7 /
+// 9.8); 14336 -> 4096 M = 2 12.9 (15.1); 896 -> 896 M = 8 / 16 4.0 / 4.9 (7.9 / 8.0); wide:
+// 2048 -> 8192 M = 2 / 3 5.9 / 7.0 (7.0 / 7.2), M = 4 8.6 (7.2, not taken); 896 -> 4864
+// M = 2 / 4 4.7 / 5.8 (6.4 / 6.6); 4096 -> 14336 M = 2 11.4 (12.8); gate/up pairs 2048 ->
+// 8192 M = 2 7.8 (13.4), 896 -> 4864 M = 3 7.4 (12.7).
 bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView* ws, int32_t count) {
     if (m < 2 || m > 16) return false;
     int64_t sets_total = 0;
     double bytes = 0.0;
+    bool wide = false;
     for (int32_t i = 0; i < count; ++i) {
         const int64_t sets = ws[i].N / SET;
-        if (sets >= 16 * ceil_div(ws[i].K, CHUNK)) return false;  // wide: the row kernel
+        wide = wide || sets >= 16 * ceil_div(ws[i].K, CHUNK);
         sets_total += sets;
         bytes += static_cast<double>(packed_weight_bytes(ws[i].K, ws[i].N, ws[i].bits));
     }
@@ -1097,8 +1101,8 @@ bool gemv_packed_rows_rep_preferred(int32_t m, const WeightView* ws, int32_t cou
     if (!plan.ks) return false;
     double wgs = 0.0;  // the workgroups that hold column sets (a grouped launch's others exit at once)
     for (int32_t i = 0; i < count; ++i) wgs += static_cast<double>(ceil_div(ws[i].N / SET, static_cast<int64_t>(W / plan.ks)));
-    const double per_row_us = std::max(wgs * 0.005, bytes / 7.5e6);
-    return (m - 1) * per_row_us <= 5.0;
+    const double per_row_us = std::max(wgs * 0.005, bytes / 10.0e6);
+    return (m - 1) * per_row_us <= (wide ? 3.0 * count : 5.0);
 }
 
 int32_t launch_gemv_packed_group_rep(const float* a, int32_t m, const WeightView* ws, float* const* cs,

@@ -311,35 +311,42 @@ def test_packed_rows_match_the_oracle(kt, oracle_lib, k, n, bits, g):
 def test_packed_rows_do_not_depend_on_the_other_rows(kt, oracle_lib):
     """QuantizationTest.kt:110-134: a and W ~ U(-0.5, 0.5), INT4 g64; m copies of one row
     give its one-row result within 1e-4 (absolute) -- here within normwise 1e-6, since
-    both sides are exact products with fp32 sums. Beyond the reference's bound, a row's
-    bits on the copy do not depend on what the other rows of the call hold: they are the
-    same for every call of 2..8 rows and for every call of 9..16 rows (the two tile
-    arrangements add x's hi and lo parts in different orders)."""
+    both sides are exact products with fp32 sums (the automatic choice, which takes small
+    row counts of these weights as one-row products, and the rows kernel). Beyond the
+    reference's bound, a row's bits from the rows kernel do not depend on what the other
+    rows of the call hold: they are the same for every call of 2..8 rows and for every call
+    of 9..16 rows (the two tile arrangements add x's hi and lo parts in different orders)."""
     rng = np.random.default_rng(41)
-    for k, n in ((320, 2112), (4096, 14336)):
-        a = (rng.random((1, k), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
-        w = (rng.random((k, n), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
-        st, q = oracle_lib.quantize(w, 4, 64)
-        assert st == 0
-        qt = _packed(kt, q)
-        single = gpu_matmul(kt, a, qt, 1)
-        ref = {}
-        for m in (2, 3, 5, 8, 9, 12, 16):
-            banner("packed-rows-batched", k, n, m)
-            batched = gpu_matmul(kt, np.tile(a, (m, 1)), qt, m)
-            diff = float(np.abs(batched - single).max())
-            print(f"  max |batched - single| = {diff:.2e}", flush=True)
-            assert diff < 1e-4 and normwise_rel(batched, np.tile(single, (m, 1))) <= 1e-6, (k, n, m, diff)
-            cls = m > 8
-            ref.setdefault(cls, batched[0])
-            assert all(same_bits(batched[r], ref[cls]) for r in range(m)), m
-        x = rng.standard_normal((16, k)).astype(np.float32)
-        full16 = gpu_matmul(kt, x, qt, 16)
-        full8 = gpu_matmul(kt, x[:8], qt, 8)
-        for rows, full in (([0, 5, 7], full8), ([7, 3], full8), ([2, 6, 1, 4, 0], full8),
-                           ([9, 0, 15, 3, 11, 4, 8, 13, 1, 6], full16), ([14, 2, 5, 10, 12, 7, 0, 9, 11], full16)):
-            part = gpu_matmul(kt, x[rows], qt, len(rows))
-            assert all(same_bits(part[i], full[r]) for i, r in enumerate(rows)), rows
+    try:
+        for k, n in ((320, 2112), (4096, 14336)):
+            a = (rng.random((1, k), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+            w = (rng.random((k, n), dtype=np.float32) - np.float32(0.5)).astype(np.float32)
+            st, q = oracle_lib.quantize(w, 4, 64)
+            assert st == 0
+            qt = _packed(kt, q)
+            single = gpu_matmul(kt, a, qt, 1)
+            for kind in (0, 5):
+                kt.MatMul.set_kernel_config(kind, 0, 0, 0, 0)
+                ref = {}
+                for m in (2, 3, 5, 8, 9, 12, 16):
+                    banner("packed-rows-batched", k, n, kind, m)
+                    batched = gpu_matmul(kt, np.tile(a, (m, 1)), qt, m)
+                    diff = float(np.abs(batched - single).max())
+                    print(f"  max |batched - single| = {diff:.2e}", flush=True)
+                    assert diff < 1e-4 and normwise_rel(batched, np.tile(single, (m, 1))) <= 1e-6, (k, n, m, diff)
+                    if kind == 5:
+                        cls = m > 8
+                        ref.setdefault(cls, batched[0])
+                        assert all(same_bits(batched[r], ref[cls]) for r in range(m)), m
+            x = rng.standard_normal((16, k)).astype(np.float32)
+            full16 = gpu_matmul(kt, x, qt, 16)
+            full8 = gpu_matmul(kt, x[:8], qt, 8)
+            for rows, full in (([0, 5, 7], full8), ([7, 3], full8), ([2, 6, 1, 4, 0], full8),
+                               ([9, 0, 15, 3, 11, 4, 8, 13, 1, 6], full16), ([14, 2, 5, 10, 12, 7, 0, 9, 11], full16)):
+                part = gpu_matmul(kt, x[rows], qt, len(rows))
+                assert all(same_bits(part[i], full[r]) for i, r in enumerate(rows)), rows
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
 
 @pytest.mark.parametrize("bits,g", [(4, 64), (8, 32)])
@@ -357,15 +364,19 @@ def test_packed_rows_many_workgroups_copy_prepared_tiles(kt, oracle_lib, bits, g
     assert st == 0
     del w
     qt, qtp = _packed(kt, q), _packed(kt, qp)
-    for m in (2, 5, 8):
-        banner("packed-rows-copy", k, n, bits, g, m)
-        x = rng.standard_normal((m, k), dtype=np.float32)
-        got = gpu_matmul(kt, x, qt, m)
-        want = oracle_lib.multiply_quantized(x, q, m, threads=16)
-        errs = [normwise_rel(got[r], want[r]) for r in range(m)]
-        print(f"  worst row normwise={max(errs):.2e}", flush=True)
-        assert max(errs) <= TOL, errs
-        assert same_bits(gpu_matmul(kt, x, qtp, m), np.ascontiguousarray(got[:, :part])), m
+    try:
+        kt.MatMul.set_kernel_config(5, 0, 0, 0, 0)  # the rows kernel (the 4096 columns alone are a small weight)
+        for m in (2, 5, 8):
+            banner("packed-rows-copy", k, n, bits, g, m)
+            x = rng.standard_normal((m, k), dtype=np.float32)
+            got = gpu_matmul(kt, x, qt, m)
+            want = oracle_lib.multiply_quantized(x, q, m, threads=16)
+            errs = [normwise_rel(got[r], want[r]) for r in range(m)]
+            print(f"  worst row normwise={max(errs):.2e}", flush=True)
+            assert max(errs) <= TOL, errs
+            assert same_bits(gpu_matmul(kt, x, qtp, m), np.ascontiguousarray(got[:, :part])), m
+    finally:
+        kt.MatMul.set_kernel_config(0, 0, 0, 0, 0)
 
 
 def test_packed_rows_grouped_accumulate_and_bias(kt, oracle_lib):
