@@ -14,18 +14,21 @@
 //     [2^14, 2^15)), and x 2^s splits into two fp16 parts, hi = fp16(x 2^s) and
 //     lo = fp16(x 2^s - hi): 22 significant bits. The parts of up to eight rows make the
 //     16 rows of one MFMA A tile (rows 0..7 hi, 8..15 lo; four rows: 0..3 and 4..7), so one
-//     MFMA per run covers both parts; sixteen rows take an A tile per part, two MFMAs per
+//     MFMA per 32 k covers both parts; sixteen rows take an A tile per part, two MFMAs per
 //     run into one accumulator. The workgroup converts the chunks of its K range into LDS
 //     once for all its waves, or (sixteen rows, or more workgroups than CUs) copies them
 //     from one conversion launch before the product;
 //   * weights: the exact integers q - z as fp16 (the bits of 1024 + q from the nibble or
 //     byte, minus 1024 + z in one packed fp16 add). The chunk's 16-byte lane pieces hold
-//     one run each (lane group kb: run kb); four lane swaps across the lane groups
-//     (v_permlane32_swap, v_permlane16_swap) transpose them so that lane group kb holds
-//     k 8 kb .. 8 kb + 7 of every run. INT4 takes the nibbles as they lie (low nibbles of
-//     bytes 0 and 2, high nibbles of 0 and 2, then bytes 1 and 3 after a shift), so the A
-//     tiles hold x in that order: k 0, 2, 4, 6, 1, 3, 5, 7 of the eight;
-//   * v_mfma_f32_16x16x32_f16, one per run and A tile into one accumulator per group:
+//     one run each (lane group kb: run kb, dword j its 8-k slice j); each MFMA takes 8 k
+//     per lane group of one quantization group only: g = 32 transposes the pieces with four
+//     lane swaps (v_permlane32_swap, v_permlane16_swap: MFMA m = run m), g = 64 swaps halves
+//     with two (MFMA m = two slices of each of the group's two runs), g >= 128 takes them as
+//     they lie (MFMA m = slice m of every run); the A tiles hold x in the same places. INT4
+//     takes the nibbles as they lie (low nibbles of bytes 0 and 2, high nibbles of 0 and 2,
+//     then bytes 1 and 3 after a shift), so the A tiles hold x in that order: k 0, 2, 4, 6,
+//     1, 3, 5, 7 of the eight;
+//   * v_mfma_f32_16x16x32_f16, four per chunk and A tile into one accumulator per group:
 //     every product is exact in fp32 (11-bit x part times an integer of at most 9 bits);
 //     INT4 high nibbles enter as 16 (q - z), so x's parts at those positions carry 2^(s-4).
 //     Lane (kb, n) gets A rows 4 kb .. 4 kb + 3 of column n, and per chunk
@@ -60,7 +63,7 @@ constexpr int MAX_ROWS = 16;
 constexpr int MAX_PASSES = 8;  // x conversion tasks a wave takes per phase
 
 // Two arrangements of x's parts. Up to eight rows: both parts in the rows of one A tile
-// (rows 0..7 hi, 8..15 lo; four rows: 0..3 and 4..7), one MFMA per run. Sixteen rows: an
+// (rows 0..7 hi, 8..15 lo; four rows: 0..3 and 4..7), one MFMA per 32 k. Sixteen rows: an
 // A tile per part, [part][lane group kb][row][8 halves], both MFMAs into one accumulator
 // (half the values per lane to combine that two tiles of eight rows would hold).
 __host__ __device__ constexpr bool parts_in_k(int32_t MT) { return MT == 16; }
@@ -97,6 +100,12 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 }
 __device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
 __device__ __forceinline__ uint32_t as_u(half2v v) { return __builtin_bit_cast(uint32_t, v); }
+// a b + c for a, b < 2^24 in one instruction
+__device__ __forceinline__ uint32_t mad24(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 // (a & m) | o in one instruction (the compiler emits two)
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
     uint32_t r;
@@ -117,6 +126,36 @@ __device__ __forceinline__ void transpose4(uint32_t (&v)[4]) {
     v[3] = d[1];
 }
 
+// A chunk's weights as the MFMAs take them: on exit v[m] feeds MFMA m, which must not mix
+// quantization groups. On entry lane group r holds run r, v[j] its 8-k slice j. g = 32 (a
+// group per run): the full transpose, MFMA m = run m, lane group kb its slice kb. g = 64:
+// only the halves swap, MFMA m = runs 2 (m / 2) and 2 (m / 2) + 1 (one group), lane group kb
+// run 2 (m / 2) + kb % 2, slice 2 (kb / 2) + m % 2. g >= 128 (one group per chunk): as they
+// lie, MFMA m = slice m, lane group kb run kb.
+template <int GS>
+__device__ __forceinline__ void arrange(uint32_t (&v)[4]) {
+    if constexpr (GS == 0) {
+        transpose4(v);
+    } else if constexpr (GS == 1) {
+        auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+        auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+        v[0] = a[0];
+        v[1] = b[0];
+        v[2] = a[1];
+        v[3] = b[1];
+    }
+}
+// The run and the 8-k slice that MFMA m's lane group kb takes after arrange<GS>: what x's
+// A tile m holds for lane group kb.
+template <int GS>
+__device__ __forceinline__ int32_t run_of(int32_t m, int32_t kb) {
+    return GS == 0 ? m : GS == 1 ? 2 * (m >> 1) + (kb & 1) : kb;
+}
+template <int GS>
+__device__ __forceinline__ int32_t slice_of(int32_t m, int32_t kb) {
+    return GS == 0 ? kb : GS == 1 ? 2 * (kb >> 1) + (m & 1) : m;
+}
+
 // hi and lo fp16 parts of two floats (RNE; the differences are exact in fp32)
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
     const half2v h = __builtin_convertvector(f32x2{a, b}, half2v);
@@ -126,8 +165,8 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 }
 
 // x conversion, a task at a time: a task is four rows' one chunk, a wave's lane (row
-// 4 q + (ln & 3), 8-k slice (ln >> 2) & 3, run ln >> 4) holding its 8 floats (zeros past M
-// and K). Returns 2^-s of the lane's row and chunk and its hi and lo parts in the A order:
+// 4 q + (ln & 3); the run and 8-k slice that A tile ln / 16 holds for lane group
+// (ln / 4) % 4) holding its 8 floats (zeros past M and K). Returns 2^-s of the lane's row and chunk and its hi and lo parts in the A order:
 // INT4 k 0, 2, 4, 6, 1, 3, 5, 7 of the eight (4..7 meet high nibbles: 2^(s - 4)), INT8
 // k 0..7.
 template <int BITS>
@@ -163,7 +202,7 @@ __device__ __forceinline__ int32_t tile_offset(int32_t row, int32_t kb, int32_t 
 // [chunks][MT] floats: a task per wave, once per call, for the products that copy tiles
 // instead of converting x themselves. Quads past M are not written (their A rows reach only
 // output rows that are never stored).
-template <int BITS, int MT>
+template <int BITS, int MT, int GS>
 __global__ void __launch_bounds__(64 * W)
     rows_prep_kernel(const float* __restrict__ x, int32_t M, int32_t K, unsigned char* __restrict__ xt) {
     constexpr int32_t tile = run_tile_bytes(MT);
@@ -171,8 +210,9 @@ __global__ void __launch_bounds__(64 * W)
     const int32_t j = blockIdx.x * W + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (j >= ((M + 3) >> 2) * chunks) return;
     const int32_t quad = j / chunks, c = j - quad * chunks;
-    const int32_t xrow = ln & 3, xsl = (ln >> 2) & 3, xrun = ln >> 4;
-    const int32_t row = 4 * quad + xrow, k = c * CHUNK + xrun * RUN + xsl * 8;
+    // lane: x row ln % 4 of the quad for A tile ln / 16, lane group (ln / 4) % 4
+    const int32_t xrow = ln & 3, xkb = (ln >> 2) & 3, xm = ln >> 4;
+    const int32_t row = 4 * quad + xrow, k = c * CHUNK + run_of<GS>(xm, xkb) * RUN + slice_of<GS>(xm, xkb) * 8;
     const int32_t xoob = M * K * 4;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, xoob, 0x00020000);
     const int32_t off = row < M && k < K ? (row * K + k) * 4 : xoob;
@@ -180,9 +220,9 @@ __global__ void __launch_bounds__(64 * W)
     const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 16, 0));
     uint32_t hw[4], lw[4];
     const float f = convert_task<BITS>(a, b, hw, lw);
-    unsigned char* d = xt + static_cast<size_t>(c * 4 + xrun) * tile;
-    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    unsigned char* d = xt + static_cast<size_t>(c * 4 + xm) * tile;
+    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xkb, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xkb, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
     if ((ln >> 2) == 0) reinterpret_cast<float*>(xt + static_cast<size_t>(chunks) * 4 * tile)[c * MT + row] = f;
 }
 
@@ -237,7 +277,9 @@ __global__ void __launch_bounds__(64 * W)
     // chunks of the phase contiguous there and here.
     const int32_t ppr = kin * cpp;              // a phase's chunks over the workgroup's K-parts
     const int32_t tasks = ((M + 3) >> 2) * ppr;  // quads past M are not converted
-    const int32_t xrow = ln & 3, xsl = (ln >> 2) & 3, xrun = ln >> 4;
+    // lane: x row ln % 4 of the task's quad for A tile ln / 16, lane group (ln / 4) % 4
+    const int32_t xrow = ln & 3, xkb = (ln >> 2) & 3, xm = ln >> 4;
+    const int32_t xk = run_of<GS>(xm, xkb) * RUN + slice_of<GS>(xm, xkb) * 8;  // its k in the chunk
     const int32_t xoob = COPY ? chunks * (4 * tile + MT * 4) : M * K * 4;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, xoob, 0x00020000);
     float4 xv[MAX_PASSES][2];
@@ -250,7 +292,7 @@ __global__ void __launch_bounds__(64 * W)
         const int32_t c = ph * cpp + (ch & (cpp - 1));
         const int32_t cg = ((part * chunks) >> kslog) + c;
         const int32_t ce = ((part + 1) * chunks) >> kslog;
-        const int32_t row = 4 * quad + xrow, k = cg * CHUNK + xrun * RUN + xsl * 8;
+        const int32_t row = 4 * quad + xrow, k = cg * CHUNK + xk;
         return cg < ce && row < M && k < K ? (row * K + k) * 4 : xoob;
     };
     // copy pieces: a part's phase is 2^(cpplog + 5 + log2 MT) pieces of tiles (32 MT per
@@ -321,9 +363,9 @@ __global__ void __launch_bounds__(64 * W)
                 uint32_t hw[4], lw[4];
                 const float f = convert_task<BITS>(xv[i][0], xv[i][1], hw, lw);
                 const int32_t row = 4 * quad + xrow;  // < MT
-                unsigned char* d = smem + (ch * 4 + xrun) * tile;
-                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xsl, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                unsigned char* d = smem + (ch * 4 + xm) * tile;
+                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xkb, 0)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4*>(d + tile_offset<MT>(row, xkb, 1)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
                 if ((ln >> 2) == 0) pl[ch * MT + row] = f;
             }
         }
@@ -410,16 +452,20 @@ __global__ void __launch_bounds__(64 * W)
         sp_end = (((sp0 + sp + 1) * chunks) >> SUB_LOG) - c_begin;
     };
     const int32_t run0 = k0 >> 5;  // the wave's first run
-    // the slot's weights, transposed: t[r] = k 8 kb .. 8 kb + 7 of run r of the chunk
-    // (INT8: t[r] k 8 kb .. 8 kb + 3, t2[r] the next 4) -- taken out of the ring so the
-    // slot refills at once
+    // the slot's weights as the MFMAs take them (arrange: t[m] feeds MFMA m; INT4 a slice's
+    // 8 k, INT8 t[m] its first 4 k and t2[m] the next 4) -- taken out of the ring so the slot
+    // refills at once
+    // (the copies are forced: left to itself the compiler works on the ring's registers
+    // and delays their refill until the chunk is converted, measured slower)
     auto take = [&](int s, uint32_t (&t)[4], uint32_t (&t2)[4]) {
         if constexpr (BITS == 4) {
             t[0] = wb[s][0][0];
             t[1] = wb[s][0][1];
             t[2] = wb[s][0][2];
             t[3] = wb[s][0][3];
-            transpose4(t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]));
+            arrange<GS>(t);
         } else {
             // 8-byte pieces p = k 8p .. 8p + 7: dwords (2p, 2p + 1) of the lane's 32 bytes
             t[0] = wb[s][0][0];
@@ -430,8 +476,10 @@ __global__ void __launch_bounds__(64 * W)
             t2[1] = wb[s][0][3];
             t2[2] = wb[s][1][1];
             t2[3] = wb[s][1][3];
-            transpose4(t);
-            transpose4(t2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]), "+v"(t2[i]));
+            arrange<GS>(t);
+            arrange<GS>(t2);
         }
     };
     constexpr int NGC = GS == 0 ? 4 : GS == 1 ? 2 : 1;  // quantization groups a chunk touches
@@ -468,13 +516,13 @@ __global__ void __launch_bounds__(64 * W)
         half2v ol[NGC], oh[NGC];
 #pragma unroll
         for (int gi = 0; gi < NGC; ++gi) {
+            // (z (2^16 + 1) + 0x64006400 in one 24-bit multiply-add: z <= 255 never carries
+            // into the exponent bits)
             if constexpr (BITS == 4) {
-                const uint32_t zz = zc[gi] | (zc[gi] << 16);
-                ol[gi] = as_h2(zz | 0x64006400u);
-                oh[gi] = as_h2((zz << 4) | 0x64006400u);
+                ol[gi] = as_h2(mad24(zc[gi], 0x00010001u, 0x64006400u));
+                oh[gi] = as_h2(mad24(zc[gi], 0x00100010u, 0x64006400u));
             } else {
-                const uint32_t zz = (zc[gi] ^ 0x80u) | ((zc[gi] ^ 0x80u) << 16);
-                ol[gi] = as_h2(zz | 0x64006400u);
+                ol[gi] = as_h2(mad24(zc[gi] ^ 0x80u, 0x00010001u, 0x64006400u));
                 oh[gi] = ol[gi];
             }
         }
@@ -543,13 +591,27 @@ __global__ void __launch_bounds__(64 * W)
             __syncthreads();
         }
         const int32_t c_end = min((ph + 1) * cpp, nmax);
+        // groups of R chunks all below n first (no per-chunk select), then the rest
+        const int32_t c_live = min(c_end, n);
+        int32_t c0 = ph * cpp;
 #pragma nounroll
-        for (int32_t c0 = ph * cpp; c0 < c_end; c0 += R) {
+        for (; c0 + R <= c_live; c0 += R) {
             static_for<0, R>([&](auto si) {
                 constexpr int sl = decltype(si)::value;
                 uint32_t t[4], t2[4];
                 take(sl, t, t2);
                 issue(sl, c0 + sl + R);  // the slot refills before its chunk is computed
+                process(t, t2, c0 + sl, true, ph);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+#pragma nounroll
+        for (; c0 < c_end; c0 += R) {
+            static_for<0, R>([&](auto si) {
+                constexpr int sl = decltype(si)::value;
+                uint32_t t[4], t2[4];
+                take(sl, t, t2);
+                issue(sl, c0 + sl + R);
                 process(t, t2, c0 + sl, c0 + sl < n, ph);
                 __builtin_amdgcn_sched_barrier(0);
             });
@@ -787,6 +849,23 @@ static int32_t launch_rows_mt(bool copy, bool split, int32_t gshift, int32_t bit
     return KT_OK;
 }
 
+// The group size's class: 0 g = 32, 1 g = 64, 2 g >= 128.
+static int32_t gs_class(int32_t g) { return g == RUN ? 0 : g == 2 * RUN ? 1 : 2; }
+
+template <int GS>
+static void launch_rows_prep(int32_t bits, int32_t mt, uint32_t blocks, const float* a, int32_t m, int32_t K,
+                             unsigned char* xt, hipStream_t st) {
+    if (bits == 4) {
+        if (mt == 4) rows_prep_kernel<4, 4, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+        else if (mt == 8) rows_prep_kernel<4, 8, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+        else rows_prep_kernel<4, 16, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+    } else {
+        if (mt == 4) rows_prep_kernel<8, 4, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+        else if (mt == 8) rows_prep_kernel<8, 8, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+        else rows_prep_kernel<8, 16, GS><<<blocks, 64 * W, 0, st>>>(a, m, K, xt);
+    }
+}
+
 // Converting x in every workgroup saves the prep's launch; copying prepared tiles is
 // cheaper for 16 rows (two phases of conversion per workgroup) and when the workgroups
 // outnumber the CUs (the conversion repeats per round of workgroups).
@@ -809,7 +888,6 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
         part_floats = std::max(part_floats, static_cast<size_t>(plan.ks) * gi * W * 256);
     }
     const bool copy = !split && (mt == 16 || wgs > cu_count());
-    const float* src = a;
     float* partials = nullptr;
     uint32_t* counters = nullptr;
     if (split) {  // the K-parts' sums and one counter per column-set group (launches run in turn)
@@ -819,30 +897,35 @@ int32_t launch_gemv_rows_packed(const float* a, int32_t m, const WeightView* ws,
             return status;
         partials = static_cast<float*>(general);
     }
-    if (copy) {  // one preparation of x for every weight of the call (same K, bits)
+    // the x tiles are arranged as the weights' MFMAs take them, which depends on the group
+    // size's class (arrange): copying, one preparation per class among the call's weights
+    const float* srcs[3] = {a, a, a};
+    if (copy) {
         const int32_t chunks = ceil_div(w0.K, CHUNK);
+        const size_t bytes = (static_cast<size_t>(chunks) * (4 * run_tile_bytes(mt) + mt * 4) + 255) & ~size_t{255};
+        bool used[3] = {false, false, false};
+        for (int32_t i = 0; i < count; ++i) used[gs_class(ws[i].g)] = true;
+        const size_t classes = static_cast<size_t>(used[0]) + used[1] + used[2];
         void* general = nullptr;
-        const size_t bytes = static_cast<size_t>(chunks) * (4 * run_tile_bytes(mt) + mt * 4);
-        if (const int32_t status = workspace(st, bytes + 256, &general)) return status;
+        if (const int32_t status = workspace(st, classes * bytes + 256, &general)) return status;
         unsigned char* xt =
             reinterpret_cast<unsigned char*>((reinterpret_cast<uintptr_t>(general) + 255) & ~uintptr_t{255});
         const uint32_t blocks = static_cast<uint32_t>(ceil_div(ceil_div(m, 4) * chunks, W));
-        if (w0.bits == 4) {
-            if (mt == 4) rows_prep_kernel<4, 4><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
-            else if (mt == 8) rows_prep_kernel<4, 8><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
-            else rows_prep_kernel<4, 16><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
-        } else {
-            if (mt == 4) rows_prep_kernel<8, 4><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
-            else if (mt == 8) rows_prep_kernel<8, 8><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
-            else rows_prep_kernel<8, 16><<<blocks, 64 * W, 0, st>>>(a, m, w0.K, xt);
+        for (int32_t gc = 0; gc < 3; ++gc) {
+            if (!used[gc]) continue;
+            if (gc == 0) launch_rows_prep<0>(w0.bits, mt, blocks, a, m, w0.K, xt, st);
+            else if (gc == 1) launch_rows_prep<1>(w0.bits, mt, blocks, a, m, w0.K, xt, st);
+            else launch_rows_prep<2>(w0.bits, mt, blocks, a, m, w0.K, xt, st);
+            KT_LAUNCHED("qmatmul: rows prep kernel");
+            srcs[gc] = reinterpret_cast<const float*>(xt);
+            xt += bytes;
         }
-        KT_LAUNCHED("qmatmul: rows prep kernel");
-        src = reinterpret_cast<const float*>(xt);
     }
     for (int32_t i = 0; i < count; ++i) {
         const WeightView& w = ws[i];
         const RowsPlan plan = rows_plan(m, w.K, w.g, w.N / SET, split);
         const int32_t gshift = log2_exact(w.g / RUN);
+        const float* src = srcs[gs_class(w.g)];
         if (!plan.ks) return fail(KT_ERR_ARGUMENT, "packed rows gemv: no work split fits K = %d, M = %d", w.K, m);
         const int32_t kslog = log2_exact(plan.ks);
         const dim3 grid = split ? dim3(static_cast<uint32_t>(ceil_div(w.N / SET, W)), static_cast<uint32_t>(plan.ks))
