@@ -496,13 +496,16 @@ __global__ void __launch_bounds__(64 * W)
         uint32_t zc[NGC];
         half8 a[NA][4];  // [A tile or part][run]
         f32x4 pf[NT];
+        // the chunk's first group row; group gi is row gr + gi (the staged rows cover every
+        // group of the wave's chunks, those past G, the padding of the last chunk, as zeros:
+        // their x is zero, so they add nothing)
+        const int32_t gr = ((run0 + cc * 4) >> gshift) - g0;
+        const unsigned char* srow = stg + gr * (SET * 4) + nl * 4;
+        const unsigned char* zrow = stg + rows * SET * 4 + gr * SET + nl;
 #pragma unroll
         for (int gi = 0; gi < NGC; ++gi) {
-            // the group row of runs gi RPG .. (a run past K, the padding of the last chunk,
-            // takes the last group's; its x is zero)
-            const int32_t gr = min((run0 + cc * 4 + gi * RPG) >> gshift, G - 1) - g0;
-            sc[gi] = *reinterpret_cast<const float*>(stg + gr * (SET * 4) + nl * 4);
-            zc[gi] = ZP ? stg[rows * SET * 4 + gr * SET + nl] : 0u;
+            sc[gi] = *reinterpret_cast<const float*>(srow + gi * (SET * 4));
+            zc[gi] = ZP ? zrow[gi * SET] : 0u;
         }
 #pragma unroll
         for (int u = 0; u < NA; ++u)
