@@ -102,15 +102,7 @@ __device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(
 __device__ __forceinline__ uint32_t as_u(half2v v) { return __builtin_bit_cast(uint32_t, v); }
 // a b + c for a, b < 2^24 in one instruction
 __device__ __forceinline__ uint32_t mad24(uint32_t a, uint32_t b, uint32_t c) {
-    uint32_t r;
-    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-// (a & m) | o in one instruction (the compiler emits two)
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-    return r;
+    return __umul24(a, b) + c;  // (v_mad_u32_u24)
 }
 
 // 4 x 4 transpose of dwords across the lane groups: on entry lane group r holds V[r][d]
@@ -484,6 +476,11 @@ __global__ void __launch_bounds__(64 * W)
     };
     constexpr int NGC = GS == 0 ? 4 : GS == 1 ? 2 : 1;  // quantization groups a chunk touches
     constexpr int RPG = 4 / NGC;                        // runs per group
+    // the nibble masks and 1024's bits held in registers: with register operands the
+    // compiler makes each (w & m) | o one v_and_or_b32 that it can schedule (literal
+    // operands give two instructions; an inline-asm form cost hazard nops and SALU work)
+    uint32_t k_lo = 0x000F000Fu, k_hi = 0x00F000F0u, k_or = 0x64006400u;
+    asm volatile("" : "+v"(k_lo), "+v"(k_hi), "+v"(k_or));
     auto process = [&](const uint32_t (&t)[4], const uint32_t (&t2)[4], int32_t cl, bool live, int32_t ph) {
         if (live)
             while (cl >= sp_end) close_sub_part();
@@ -538,10 +535,10 @@ __global__ void __launch_bounds__(64 * W)
                 // halves: the bits of 1024 + q (low nibbles) or 1024 + 16 q (high nibbles),
                 // minus 1024 + z or 1024 + 16 z: bytes 0 and 2, then 1 and 3
                 const uint32_t w = t[r], w8 = t[r] >> 8;
-                bw[0] = as_u(as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) - o_lo);   // k 0, 2
-                bw[1] = as_u(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)) - o_hi);   // k 4, 6
-                bw[2] = as_u(as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)) - o_lo);  // k 1, 3
-                bw[3] = as_u(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)) - o_hi);  // k 5, 7
+                bw[0] = as_u(as_h2(((w & k_lo) | k_or)) - o_lo);   // k 0, 2
+                bw[1] = as_u(as_h2(((w & k_hi) | k_or)) - o_hi);   // k 4, 6
+                bw[2] = as_u(as_h2(((w8 & k_lo) | k_or)) - o_lo);  // k 1, 3
+                bw[3] = as_u(as_h2(((w8 & k_hi) | k_or)) - o_hi);  // k 5, 7
             } else {
                 // byte b (signed q): 0x64 above b ^ 0x80 is 1152 + q; minus 1152 + z
                 const uint32_t u0 = t[r] ^ 0x80808080u, u1 = t2[r] ^ 0x80808080u;
