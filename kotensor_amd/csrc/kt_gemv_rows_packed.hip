@@ -393,13 +393,14 @@ __global__ void __launch_bounds__(64 * W)
     }
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(packed + (static_cast<int64_t>(set) * chunks + c_begin) * BB), 0, n * BB, 0x00020000);
-    u32x4 wb[R][NB];
-    auto issue = [&](int slot, int32_t cc) {
+    u32x4 wb[R][NB], wb2[R][NB];
+    auto issue_to = [&](u32x4 (&ring)[R][NB], int slot, int32_t cc) {
 #pragma unroll
         for (int h = 0; h < NB; ++h)
-            wb[slot][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            ring[slot][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                         wr, cc * BB + h * 1024 + 16 * ln, 0, NONTEMPORAL));
     };
+    auto issue = [&](int slot, int32_t cc) { issue_to(wb, slot, cc); };
 #pragma unroll
     for (int s = 0; s < R / 2; ++s) issue(s, s);
     load_x(0, 0, MAX_PASSES / 2, MAX_PASSES);
@@ -449,31 +450,34 @@ __global__ void __launch_bounds__(64 * W)
     // refills at once
     // (the copies are forced: left to itself the compiler works on the ring's registers
     // and delays their refill until the chunk is converted, measured slower)
-    auto take = [&](int s, uint32_t (&t)[4], uint32_t (&t2)[4]) {
+    auto take_from = [&](const u32x4 (&ring)[R][NB], int s, uint32_t (&t)[4], uint32_t (&t2)[4], bool copy) {
         if constexpr (BITS == 4) {
-            t[0] = wb[s][0][0];
-            t[1] = wb[s][0][1];
-            t[2] = wb[s][0][2];
-            t[3] = wb[s][0][3];
+            t[0] = ring[s][0][0];
+            t[1] = ring[s][0][1];
+            t[2] = ring[s][0][2];
+            t[3] = ring[s][0][3];
+            if (copy)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]));
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]));
             arrange<GS>(t);
         } else {
             // 8-byte pieces p = k 8p .. 8p + 7: dwords (2p, 2p + 1) of the lane's 32 bytes
-            t[0] = wb[s][0][0];
-            t[1] = wb[s][0][2];
-            t[2] = wb[s][1][0];
-            t[3] = wb[s][1][2];
-            t2[0] = wb[s][0][1];
-            t2[1] = wb[s][0][3];
-            t2[2] = wb[s][1][1];
-            t2[3] = wb[s][1][3];
+            t[0] = ring[s][0][0];
+            t[1] = ring[s][0][2];
+            t[2] = ring[s][1][0];
+            t[3] = ring[s][1][2];
+            t2[0] = ring[s][0][1];
+            t2[1] = ring[s][0][3];
+            t2[2] = ring[s][1][1];
+            t2[3] = ring[s][1][3];
+            if (copy)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]), "+v"(t2[i]));
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(t[i]), "+v"(t2[i]));
             arrange<GS>(t);
             arrange<GS>(t2);
         }
     };
+    auto take = [&](int s, uint32_t (&t)[4], uint32_t (&t2)[4]) { take_from(wb, s, t, t2, true); };
     constexpr int NGC = GS == 0 ? 4 : GS == 1 ? 2 : 1;  // quantization groups a chunk touches
     constexpr int RPG = 4 / NGC;                        // runs per group
     // the nibble masks and 1024's bits held in registers: with register operands the
@@ -581,40 +585,71 @@ __global__ void __launch_bounds__(64 * W)
     };
     // The ring over each phase's chunks (refills cross the loop's back edge, as in the
     // one-row kernel; cpp is a multiple of R, so the ring's slots line up with phases).
-    for (int32_t ph = 0; ph < phases; ++ph) {
-        if (ph > 0) {
-            __syncthreads();  // every wave is done with the previous phase's tiles
-            for (int32_t rd = 0; rd < x_rounds; ++rd) {
-                load_x(ph, rd, 0, MAX_PASSES);
-                store_x(ph, rd);
+    if (phases == 1 && nmax >= 4 * R) {
+        // one phase of at least 4 R chunks: two register sets, chunk c in set (c / R) % 2,
+        // each refill going to the other set, so a chunk's registers are worked on in place
+        // (no copies) while its refill is already in flight (8B FFN M = 8 14.4 -> 13.3 us;
+        // with 8 chunks per wave, 4096 x 4096, it measured slower: 10.2 -> 10.9)
+        const int32_t c_end = nmax, c_live = min(nmax, n);
+        int32_t c0 = 0;
+#pragma nounroll
+        for (; c0 + 2 * R <= c_live; c0 += 2 * R) {
+            static_for<0, 2 * R>([&](auto si) {
+                constexpr int q = decltype(si)::value, sl = q % R;
+                uint32_t t[4], t2[4];
+                take_from(q < R ? wb : wb2, sl, t, t2, false);
+                issue_to(q < R ? wb2 : wb, sl, c0 + q + R);
+                process(t, t2, c0 + q, true, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+#pragma nounroll
+        for (; c0 < c_end; c0 += 2 * R) {
+            static_for<0, 2 * R>([&](auto si) {
+                constexpr int q = decltype(si)::value, sl = q % R;
+                uint32_t t[4], t2[4];
+                take_from(q < R ? wb : wb2, sl, t, t2, false);
+                issue_to(q < R ? wb2 : wb, sl, c0 + q + R);
+                process(t, t2, c0 + q, c0 + q < n, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+    } else {
+        for (int32_t ph = 0; ph < phases; ++ph) {
+            if (ph > 0) {
+                __syncthreads();  // every wave is done with the previous phase's tiles
+                for (int32_t rd = 0; rd < x_rounds; ++rd) {
+                    load_x(ph, rd, 0, MAX_PASSES);
+                    store_x(ph, rd);
+                }
+                __syncthreads();
             }
-            __syncthreads();
-        }
-        const int32_t c_end = min((ph + 1) * cpp, nmax);
-        // groups of R chunks all below n first (no per-chunk select), then the rest
-        const int32_t c_live = min(c_end, n);
-        int32_t c0 = ph * cpp;
+            const int32_t c_end = min((ph + 1) * cpp, nmax);
+            // groups of R chunks all below n first (no per-chunk select), then the rest
+            const int32_t c_live = min(c_end, n);
+            int32_t c0 = ph * cpp;
 #pragma nounroll
-        for (; c0 + R <= c_live; c0 += R) {
-            static_for<0, R>([&](auto si) {
-                constexpr int sl = decltype(si)::value;
-                uint32_t t[4], t2[4];
-                take(sl, t, t2);
-                issue(sl, c0 + sl + R);  // the slot refills before its chunk is computed
-                process(t, t2, c0 + sl, true, ph);
-                __builtin_amdgcn_sched_barrier(0);
-            });
-        }
+            for (; c0 + R <= c_live; c0 += R) {
+                static_for<0, R>([&](auto si) {
+                    constexpr int sl = decltype(si)::value;
+                    uint32_t t[4], t2[4];
+                    take(sl, t, t2);
+                    issue(sl, c0 + sl + R);  // the slot refills before its chunk is computed
+                    process(t, t2, c0 + sl, true, ph);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            }
 #pragma nounroll
-        for (; c0 < c_end; c0 += R) {
-            static_for<0, R>([&](auto si) {
-                constexpr int sl = decltype(si)::value;
-                uint32_t t[4], t2[4];
-                take(sl, t, t2);
-                issue(sl, c0 + sl + R);
-                process(t, t2, c0 + sl, c0 + sl < n, ph);
-                __builtin_amdgcn_sched_barrier(0);
-            });
+            for (; c0 < c_end; c0 += R) {
+                static_for<0, R>([&](auto si) {
+                    constexpr int sl = decltype(si)::value;
+                    uint32_t t[4], t2[4];
+                    take(sl, t, t2);
+                    issue(sl, c0 + sl + R);
+                    process(t, t2, c0 + sl, c0 + sl < n, ph);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            }
         }
     }
 
