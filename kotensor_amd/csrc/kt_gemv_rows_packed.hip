@@ -585,7 +585,9 @@ __global__ void __launch_bounds__(64 * W)
     };
     // The ring over each phase's chunks (refills cross the loop's back edge, as in the
     // one-row kernel; cpp is a multiple of R, so the ring's slots line up with phases).
-    if (phases == 1 && nmax >= 4 * R) {
+    bool two_sets = false;  // (not where x tiles are copied: their registers would spill)
+    if constexpr (!COPY) two_sets = phases == 1 && nmax >= 4 * R;
+    if (two_sets) {
         // one phase of at least 4 R chunks: two register sets, chunk c in set (c / R) % 2,
         // each refill going to the other set, so a chunk's registers are worked on in place
         // (no copies) while its refill is already in flight (8B FFN M = 8 14.4 -> 13.3 us;
