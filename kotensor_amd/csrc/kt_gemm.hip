@@ -936,9 +936,11 @@ __global__ void __launch_bounds__(PTHREADS, 1)
                 uint32_t h[4];
 #pragma unroll
                 for (int dw = 0; dw < 2; ++dw) {
-                    const uint32_t wv = d.w[j][2 * i + dw];
-                    const uint32_t p0 = (__builtin_amdgcn_perm(0u, wv, SEL01) ^ 0x00800080u) + 0x64006400u;
-                    const uint32_t p1 = (__builtin_amdgcn_perm(0u, wv, SEL23) ^ 0x00800080u) + 0x64006400u;
+                    // the bytes b ^ 0x80 under 0x64: the halves 1152 + q (one XOR for four bytes,
+                    // then one permute a pair)
+                    const uint32_t wv = d.w[j][2 * i + dw] ^ 0x80808080u;
+                    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, wv, 0x04010400u);
+                    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, wv, 0x04030402u);
                     h[2 * dw] = __builtin_bit_cast(uint32_t, (as_h2(p0) + ofv) * scv);
                     h[2 * dw + 1] = __builtin_bit_cast(uint32_t, (as_h2(p1) + ofv) * scv);
                 }
